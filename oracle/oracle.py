@@ -1,0 +1,382 @@
+"""TEST INFRASTRUCTURE, NOT PRODUCT CODE.
+
+The CPU oracle for the per-matrix quantization hot path: a restatement of the reference's
+algorithm (ShinMegamiBoson/lookatmyquant) in plain C (lamq_oracle.c, loaded here through ctypes)
+and numpy. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import it,
+and only as the checker or the timed CPU baseline; the product (lookatmyquant_amd) never does.
+
+Parity status of each function (what pins it is listed in the test named beside it):
+  viterbi            brute force over all paths incl. exact-arithmetic tie cases (tests/test_oracle.py)
+                     and the reference's own vectors (tests/golden)
+  ldlq_trellis       least-squares refit identity, H = c*I composition, reference vectors
+  ldlq_scalar        least-squares refit identity, eager GPTQ identity, reference vectors
+  environment        LAPACK closed form; U^T U = H_damped^-1
+  hadamard / rht     orthogonality, |H_ij| = 1/sqrt(n), Kronecker closed forms
+  hessian            fp64 closed form X^T diag(w) X / N
+  kl_rows            fp64 closed form; KL(p||p) = 0; Gaussian-logit closed form
+  lloyd_max          Max (1960) MSE table; GAUSS2 levels; reference vectors
+  pack_symbols etc.  round trip and the reference's byte layout spelled out bit by bit
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+_LIB = None
+
+_i64, _i32, _dbl = ctypes.c_int64, ctypes.c_int, ctypes.c_double
+_p = ctypes.c_void_p
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def build():
+    """Compile lamq_oracle.c with gcc (no reference sources are involved: the reference is Python)."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        so = HERE / "liblamq_oracle.so"
+        if not so.exists() or so.stat().st_mtime < (HERE / "lamq_oracle.c").stat().st_mtime:
+            build()
+        L = ctypes.CDLL(str(so))
+        L.orc_viterbi.argtypes = [_p, _i64, _i32, _i64, _p, _i32, _i32, _p, _p]
+        L.orc_ldlq_trellis.argtypes = [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _p, _p]
+        L.orc_ldlq_scalar.argtypes = [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _i32, _i32, _i32, _p, _p, _p]
+        L.orc_kl_rows.argtypes = [_p, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _p]
+        for f in (L.orc_viterbi, L.orc_ldlq_trellis, L.orc_ldlq_scalar, L.orc_kl_rows):
+            f.restype = _i32
+        _LIB = L
+    return _LIB
+
+
+def _check(rc, what):
+    if rc != 0:
+        raise ValueError(f"{what}: oracle returned {rc}")
+
+
+# ----------------------------------------------------------------------------- Viterbi (codes.py:151-181)
+
+
+def viterbi(X, values, L: int, k: int, start=None) -> np.ndarray:
+    """States (rows, T) of the nearest trellis path, as opgraph/codes.py:151-181: X and the values are cast to float32."""
+    x = np.ascontiguousarray(np.asarray(X, dtype=np.float64).astype(np.float32))
+    if x.ndim != 2:
+        raise ValueError("X must be (rows, T)")
+    C = np.ascontiguousarray(np.asarray(values, dtype=np.float64).astype(np.float32))
+    if len(C) != 1 << L:
+        raise ValueError("values must have 2^L entries")
+    st = None if start is None else np.ascontiguousarray(np.asarray(start, dtype=np.int64))
+    out = np.empty(x.shape, dtype=np.int32)
+    _check(lib().orc_viterbi(_ptr(x), x.shape[0], x.shape[1], x.shape[1], _ptr(C), L, k, _ptr(st), _ptr(out)), "viterbi")
+    return out.astype(np.int64)
+
+
+# ----------------------------------------------------------------------------- sweeps (syntax.py:86-124)
+
+
+def ldlq_trellis(X, U, S, table64, L: int, k: int, width: int = 16, look: int = 8, lazy: int = 128, dead=None,
+                 want_before: bool = False):
+    """Row-trellis block LDLQ of X (rows in the rotated basis, not yet divided by S): the states, and optionally
+    each column as it stood before it was settled. opgraph/codes.py:397-404,442-452 inside syntax.py:86-124."""
+    T = np.array(X, dtype=np.float64, order="C", copy=True)
+    m, n = T.shape
+    U = np.ascontiguousarray(U, dtype=np.float64)
+    S = np.ascontiguousarray(S, dtype=np.float64)
+    tb = np.ascontiguousarray(table64, dtype=np.float64)
+    dd = None if dead is None else np.ascontiguousarray(dead, dtype=np.uint8)
+    states = np.empty((m, n), dtype=np.int32)
+    before = np.empty((m, n), dtype=np.float64) if want_before else None
+    _check(lib().orc_ldlq_trellis(_ptr(T), m, n, n, _ptr(U), U.shape[1], _ptr(S), _ptr(tb), L, k, width, look, lazy,
+                                  _ptr(dd), _ptr(states), _ptr(before)), "ldlq_trellis")
+    return (states, before) if want_before else states
+
+
+def ldlq_scalar(T0, U, levels, mode: int = 0, S=None, lazy: int = 128, dead=None, want_before: bool = False):
+    """Width-1 LDLQ onto a scalar set. mode 0: nested.multirate_sweep with one rate (T0 already X/S, argmin with the
+    first minimum); mode 1: ldlq_words with a ScalarCode (T0 = X, bucketize(t/S) on midpoints, q*S)."""
+    T = np.array(T0, dtype=np.float64, order="C", copy=True)
+    m, n = T.shape
+    U = np.ascontiguousarray(U, dtype=np.float64)
+    lv = np.ascontiguousarray(levels, dtype=np.float64)
+    Sv = None if S is None else np.ascontiguousarray(S, dtype=np.float64)
+    dd = None if dead is None else np.ascontiguousarray(dead, dtype=np.uint8)
+    idx = np.empty((m, n), dtype=np.int32)
+    before = np.empty((m, n), dtype=np.float64) if want_before else None
+    _check(lib().orc_ldlq_scalar(_ptr(T), m, n, n, _ptr(U), U.shape[1], _ptr(Sv), _ptr(lv), len(lv), mode, lazy,
+                                 _ptr(dd), _ptr(idx), _ptr(before)), "ldlq_scalar")
+    return (idx, before) if want_before else idx
+
+
+# ----------------------------------------------------------------------------- environment (frame.py:508-522)
+
+
+def environment(H, damp: float = 0.01):
+    """(H damped, U, dead): dead = diag(H) == 0 gets a unit diagonal, H += damp*mean(diag H)*I, and U is the upper
+    Cholesky factor of H^-1 (torch.linalg.cholesky(torch.cholesky_inverse(torch.linalg.cholesky(H)), upper=True))."""
+    H = np.array(H, dtype=np.float64, copy=True)
+    dead = np.diag(H) == 0
+    idx = np.nonzero(dead)[0]
+    H[idx, idx] = 1.0
+    H = H + damp * np.mean(np.diag(H)) * np.eye(len(H))
+    Lc = np.linalg.cholesky(H)
+    Li = np.linalg.inv(Lc)
+    Hinv = Li.T @ Li
+    U = np.linalg.cholesky(Hinv).T
+    return H, U, dead
+
+
+# ----------------------------------------------------------------------------- Hadamard and RHT (codes.py:83-132)
+
+
+def _is_prime(q: int) -> bool:
+    return q > 1 and all(q % d for d in range(2, math.isqrt(q) + 1))
+
+
+def _sylvester(a: int) -> np.ndarray:
+    H = np.ones((1, 1))
+    while H.shape[0] < 2**a:
+        H = np.block([[H, H], [H, -H]])
+    return H
+
+
+def _paley(q: int) -> np.ndarray:
+    """Paley's first construction, order q + 1, q prime and q = 3 mod 4 (codes.py:87-94)."""
+    squares = {(x * x) % q for x in range(1, q)}
+    chi = np.array([0.0] + [1.0 if a in squares else -1.0 for a in range(1, q)])
+    Q = chi[(np.arange(q)[None, :] - np.arange(q)[:, None]) % q]
+    S = np.zeros((q + 1, q + 1))
+    S[0, 1:], S[1:, 0], S[1:, 1:] = 1, -1, Q
+    return S + np.eye(q + 1)
+
+
+def hadamard_factors(n: int):
+    """A, B with hadamard(n) = kron(A, B)/sqrt(n) (codes.py:104-119)."""
+    for a in range(int(math.log2(n)), -1, -1):
+        if n % 2**a:
+            continue
+        p = n // 2**a
+        if p in (1, 2) or (_is_prime(p - 1) and (p - 1) % 4 == 3):
+            if p == 1 and a > 1:
+                return _sylvester(a // 2), _sylvester(a - a // 2)
+            P = np.array([[1.0, 1.0], [1.0, -1.0]]) if p == 2 else np.ones((1, 1)) if p == 1 else _paley(p - 1)
+            return _sylvester(a), P
+    raise ValueError(f"no Hadamard construction here for order {n}")
+
+
+def hadamard(n: int) -> np.ndarray:
+    A, B = hadamard_factors(n)
+    return np.kron(A, B) / math.sqrt(n)
+
+
+def rht_signs(n: int, seed: int) -> np.ndarray:
+    """s = -1 where torch.rand(n, Generator(seed), float64) < 0.5 (codes.py:131): the library RNG the reference calls."""
+    import torch
+    u = torch.rand(n, generator=torch.Generator().manual_seed(int(seed)), dtype=torch.float64).numpy()
+    return np.where(u < 0.5, -1.0, 1.0)
+
+
+def rht(n: int, seed: int) -> np.ndarray:
+    return hadamard(n) * rht_signs(n, seed)[None, :]
+
+
+# ----------------------------------------------------------------------------- statistics and scales
+
+
+def hessian(X, w=None) -> np.ndarray:
+    """H = (1/N) sum_t w_t x_t x_t^T in float64 (quantize.py:1465,1470 with the token weights of :1389-1391)."""
+    X = np.asarray(X, dtype=np.float64)
+    Xw = X if w is None else X * np.asarray(w, dtype=np.float64)[:, None]
+    return (X.T @ Xw) / X.shape[0]
+
+
+def cross_gram(Xr, Xq, w=None) -> np.ndarray:
+    """D = (1/N) X_ref^T (w * X_q) in float64 (quantize.py:1457)."""
+    Xr = np.asarray(Xr, dtype=np.float64)
+    Xq = np.asarray(Xq, dtype=np.float64)
+    Xw = Xq if w is None else Xq * np.asarray(w, dtype=np.float64)[:, None]
+    return (Xr.T @ Xw) / Xr.shape[0]
+
+
+def row_scale(X) -> np.ndarray:
+    """S_r = max(sqrt(mean_j X_rj^2), 1e-12) (codes.py:436; nested.py:168)."""
+    X = np.asarray(X, dtype=np.float64)
+    return np.maximum(np.sqrt((X * X).mean(1)), 1e-12)
+
+
+# ----------------------------------------------------------------------------- Lloyd-Max (nested.py:36-82)
+
+
+def _phi(x):
+    return np.exp(-0.5 * x * x) / math.sqrt(2 * math.pi)
+
+
+def _Phi(x):
+    from scipy.special import erf
+    return 0.5 * (1 + erf(x / math.sqrt(2)))
+
+
+def gaussian_centroids(bounds) -> np.ndarray:
+    a, b = bounds[:-1], bounds[1:]
+    with np.errstate(invalid="ignore"):
+        pa = np.where(np.isinf(a), 0.0, _phi(a))
+        pb = np.where(np.isinf(b), 0.0, _phi(b))
+    return (pa - pb) / (_Phi(b) - _Phi(a))
+
+
+def lloyd_max_levels(n: int, iters: int = 500) -> np.ndarray:
+    from scipy.special import ndtri
+    lv = gaussian_centroids(ndtri(np.arange(n + 1, dtype=np.float64) / n) * math.sqrt(3))
+    for _ in range(iters):
+        mid = (lv[1:] + lv[:-1]) / 2
+        lv = gaussian_centroids(np.concatenate([[-math.inf], mid, [math.inf]]))
+    return lv
+
+
+def lloyd_max(bits: int, iters: int = 500) -> np.ndarray:
+    return lloyd_max_levels(2**bits, iters)
+
+
+def gaussian_mse(bounds, levels) -> float:
+    """E[(x - q(x))^2] for x ~ N(0,1) (nested.py:51-59)."""
+    a, b = bounds[:-1], bounds[1:]
+    P = _Phi(b) - _Phi(a)
+    with np.errstate(invalid="ignore"):
+        fa = lambda t: np.where(np.isinf(t), 0.0, t * _phi(t))
+        pa = lambda t: np.where(np.isinf(t), 0.0, _phi(t))
+        m1 = pa(a) - pa(b)
+        m2 = P + fa(a) - fa(b)
+    return float((m2 - 2 * levels * m1 + levels**2 * P).sum())
+
+
+# ----------------------------------------------------------------------------- KL (compiler.py:177-188)
+
+
+def kl_rows(ref_bf16, q_bf16, w=None):
+    """Per-token KL(p_ref || p_q) in float64 from bfloat16 logits given as uint16 bit patterns; returns (kl per token,
+    sum_t w_t kl_t / sum_t w_t)."""
+    r = np.ascontiguousarray(ref_bf16, dtype=np.uint16)
+    q = np.ascontiguousarray(q_bf16, dtype=np.uint16)
+    T, V = r.shape
+    ww = None if w is None else np.ascontiguousarray(w, dtype=np.float32)
+    kl = np.empty(T, dtype=np.float64)
+    sw, st = ctypes.c_double(), ctypes.c_double()
+    _check(lib().orc_kl_rows(_ptr(r), _ptr(q), T, V, V, V, _ptr(ww), _ptr(kl), ctypes.byref(sw), ctypes.byref(st)), "kl")
+    return kl, (sw.value / st.value if st.value else 0.0)
+
+
+def bf16_bits(x) -> np.ndarray:
+    """float32 -> bfloat16 bit patterns, round to nearest even (what torch's .to(bfloat16) does)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return r
+
+
+def bf16_to_f32(h) -> np.ndarray:
+    return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# ----------------------------------------------------------------------------- packing (compiler_artifact.py:225-297)
+
+
+def pack_symbols(q, bits: int) -> np.ndarray:
+    """Symbols (m, n) < 2^bits, each row padded to a multiple of 32 and packed little-endian: symbol i of a group of
+    32 starts at bit i*bits of the group's `bits` 32-bit words (compiler_artifact.py:225-240)."""
+    q = np.asarray(q)
+    m, n = q.shape
+    npad = (n + 31) // 32 * 32
+    out = np.zeros((m, npad // 32 * bits), dtype=np.uint32)
+    for r in range(m):
+        for g in range(npad // 32):
+            acc = 0
+            for i in range(32):
+                c = g * 32 + i
+                v = int(q[r, c]) if c < n else 0
+                acc |= v << (i * bits)
+            for wd in range(bits):
+                out[r, g * bits + wd] = (acc >> (32 * wd)) & 0xFFFFFFFF
+    return out
+
+
+def unpack_symbols(codes, bits: int, columns: int) -> np.ndarray:
+    codes = np.asarray(codes, dtype=np.uint32)
+    m = codes.shape[0]
+    blocks = (columns + 31) // 32
+    out = np.zeros((m, blocks * 32), dtype=np.uint32)
+    for r in range(m):
+        for g in range(blocks):
+            acc = 0
+            for wd in range(bits):
+                acc |= int(codes[r, g * bits + wd]) << (32 * wd)
+            for i in range(32):
+                out[r, g * 32 + i] = (acc >> (i * bits)) & ((1 << bits) - 1)
+    return out[:, :columns]
+
+
+def valid_path(states, bits: int, state_bits: int = 12) -> bool:
+    s = np.asarray(states, dtype=np.int64)
+    return bool(s.ndim == 2 and s.shape[1] > 0 and np.all((s >= 0) & (s < (1 << state_bits))) and np.all(s[:, 0] < (1 << bits))
+                and np.all((s[:, 1:] >> bits) == (s[:, :-1] & ((1 << (state_bits - bits)) - 1))))
+
+
+def pack_trellis(states, bits: int, state_bits: int = 12) -> np.ndarray:
+    """Symbols = state & (2^bits - 1), padded forward to 32, the row reversed, then packed (compiler_artifact.py:276-284)."""
+    s = np.asarray(states, dtype=np.int64)
+    if not valid_path(s, bits, state_bits):
+        raise ValueError("states are not a row trellis from zero")
+    sym = s & ((1 << bits) - 1)
+    sym = np.pad(sym, ((0, 0), (0, (-sym.shape[1]) % 32)))
+    return pack_symbols(sym[:, ::-1], bits)
+
+
+def unpack_trellis(codes, bits: int, columns: int, state_bits: int = 12) -> np.ndarray:
+    padded = (columns + 31) // 32 * 32
+    sym = unpack_symbols(codes, bits, padded)[:, ::-1]
+    state = np.zeros(len(sym), dtype=np.int64)
+    out = np.empty((len(sym), columns), dtype=np.int64)
+    for i in range(columns):
+        state = ((state << bits) | sym[:, i]) & ((1 << state_bits) - 1)
+        out[:, i] = state
+    return out
+
+
+# ----------------------------------------------------------------------------- end-to-end words
+
+
+def ldlq_words_trellis(W, H, table64, L: int, k: int, in_seed: int, width: int = 16, look: int = 8, lazy: int = 128):
+    """ldlq_words([W], H, RowTrellisCode(L, k), [seed], in_seed=in_seed, out_rot=False) (codes.py:413-462): the
+    states, the row scales and the reconstruction diag(S) table[states] R_in."""
+    W = np.asarray(W, dtype=np.float64)
+    R = rht(W.shape[1], in_seed)
+    X = W @ R.T
+    S = row_scale(X)
+    Hr = R @ np.asarray(H, dtype=np.float64) @ R.T
+    _, U, dead = environment(Hr)
+    st = ldlq_trellis(X, U, S, table64, L, k, width, look, lazy, dead if dead.any() else None)
+    What = (S[:, None] * np.asarray(table64)[st]) @ R
+    return st, S, What
+
+
+def nested_lm(W, H, levels, in_seed: int, lazy: int = 128):
+    """nested_words([W], H, [seed], b, [b], 0.4, [1.0], lloyd_max(b), in_seed=in_seed, out_rot=False)[b][0]
+    (nested.py:155-192): the level indices, the row scales and the reconstruction."""
+    W = np.asarray(W, dtype=np.float64)
+    R = rht(W.shape[1], in_seed)
+    X = W @ R.T
+    S = row_scale(X)
+    Hr = R @ np.asarray(H, dtype=np.float64) @ R.T
+    _, U, dead = environment(Hr)
+    idx = ldlq_scalar(X / S[:, None], U, levels, 0, None, lazy, dead if dead.any() else None)
+    What = (S[:, None] * np.asarray(levels)[idx]) @ R
+    return idx, S, What
