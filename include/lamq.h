@@ -1,0 +1,184 @@
+/*
+ * lamq.h -- C ABI of the MI355X (gfx950) per-matrix quantization hot path.
+ *
+ * Every entry point takes caller-owned device pointers with explicit leading dimensions
+ * (in elements) and a hipStream_t (passed as void*), enqueues its kernels on that stream and
+ * returns an int status:
+ *     0                 success
+ *     LAMQ_EINVAL (-1)  an argument is out of range or a pointer is NULL (nothing was launched)
+ *     LAMQ_EUNSUP (-2)  a shape or parameter this build does not support (nothing was launched)
+ *     > 0               the hipError_t of a failed launch
+ * Results that depend on the data (a pivot that is not positive, an invalid trellis path) are
+ * reported through device-side outputs named in each declaration. Nothing here allocates device
+ * memory; entry points that need scratch take a workspace whose size a *_workspace_size query
+ * returns. No entry point keeps state between calls, and calls on distinct streams with
+ * distinct buffers are independent.
+ *
+ * Data types: bf16 is passed as uint16_t bit patterns; fp64 as double; fp32 as float.
+ * Matrices are row-major.
+ */
+#ifndef LAMQ_H
+#define LAMQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LAMQ_OK 0
+#define LAMQ_EINVAL (-1)
+#define LAMQ_EUNSUP (-2)
+
+/* Version of this ABI (major * 100 + minor). */
+int lamq_abi_version(void);
+
+/* ------------------------------------------------------------------------------------------------
+ * Viterbi over a bitshift trellis, one path per row.
+ * Replaces opgraph/codes.py:151-181 viterbi(X, values, L, k, chunk=None, start=None).
+ *   x       [B, T] float32 targets (row stride ldx); the reference casts its float64 inputs to float32
+ *   C       [2^L] float32 state values
+ *   start   NULL (first state free) or [B] int32 previous states (codes.py:165-167)
+ *   states  [B, T] int32 output (row stride lds)
+ * Ties: the lowest predecessor h and the lowest final state win, as torch's min/argmin do.
+ * Supported: 2 <= L <= 12 with 1 <= k <= min(4, L-1). Paths longer than 32 steps keep their
+ * back-pointers in the workspace: lamq_viterbi_workspace_size(B, T, L, k) bytes (0 otherwise).
+ * ---------------------------------------------------------------------------------------------- */
+size_t lamq_viterbi_workspace_size(int64_t B, int T, int L, int k);
+int lamq_viterbi_rows(const float* x, int64_t B, int T, int64_t ldx, const float* C, int L, int k,
+                      const int32_t* start, int32_t* states, int64_t lds, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * One lazy block [b0, b1) of the row-trellis block-LDLQ sweep, for every row.
+ * Replaces the inner loop of opgraph/syntax.py:106-121 (sweep) driven by the project closure of
+ * opgraph/codes.py:442-450 and RowTrellisCode.step (codes.py:397-404).
+ *   T        [m, n] float64 running target (row stride ldT), rows in the rotated basis, not divided
+ *            by S; columns [b0, b1) are settled and receive the in-block refit; columns >= b1 are
+ *            read (look-ahead) but not written
+ *   U        [n, n] float64 upper Cholesky factor of H^-1 (row stride ldU)
+ *   S        [m] float64 row scales
+ *   table64  [2^L] float64 state values; table32 the same values cast to float32
+ *   state    [m] int32, the state before column b0 on entry (0 at b0 = 0), after b1-1 on return
+ *   states   [m, n] int32 output for columns [b0, b1) (row stride lds)
+ *   Z        [m, b1-b0] float64 output: the block's refit coefficients z = E U_BB^-1 (row stride ldZ),
+ *            the left operand of the trailing update
+ * width divides lazy = b1-b0 except in the last block; width + look <= 32; b1 - b0 <= 256.
+ * Supported: 2 <= L <= 12 with 1 <= k <= min(4, L-1).
+ * ---------------------------------------------------------------------------------------------- */
+int lamq_ldlq_trellis_block(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU,
+                            const double* S, const double* table64, const float* table32, int L, int k,
+                            int64_t b0, int64_t b1, int width, int look, int32_t* state, int32_t* states,
+                            int64_t lds, double* Z, int64_t ldZ, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * One lazy block [b0, b1) of the width-1 LDLQ sweep onto a scalar set of K levels.
+ * Replaces opgraph/syntax.py:106-121 with the project of opgraph/nested.py:127-140 (mode 0: T is
+ * already X/S, index = first argmin_i (t - lv_i)^2, q = lv[index]) or of opgraph/codes.py:322-332,
+ * 442-450 (mode 1: T is X, index = bucketize(t/S, midpoints) with halfway ties to the lower level,
+ * q = lv[index]*S; S must be given). idx [m, n] int32 output for [b0, b1) (row stride ldi); Z as
+ * above. K <= 256, b1 - b0 <= 128.
+ * ---------------------------------------------------------------------------------------------- */
+int lamq_ldlq_scalar_block(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU,
+                           const double* S, const double* levels, int K, int mode, int64_t b0, int64_t b1,
+                           int32_t* idx, int64_t ldi, double* Z, int64_t ldZ, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * The lazy trailing update T[:, b1:n] -= Z @ U[b0:b1, b1:n] on fp64 MFMA.
+ * Replaces opgraph/syntax.py:122-123 (and opgraph/ldlq_gpu.py:48).
+ *   Z [m, b1-b0] (row stride ldZ), b1 - b0 <= 256.
+ * ---------------------------------------------------------------------------------------------- */
+int lamq_trailing_update_f64(double* T, int64_t m, int64_t n, int64_t ldT, const double* Z, int64_t ldZ,
+                             const double* U, int64_t ldU, int64_t b0, int64_t b1, void* stream);
+
+/* T[:, dead] = 0 before a sweep (opgraph/syntax.py:101); dead [n] uint8. */
+int lamq_zero_columns(double* T, int64_t m, int64_t n, int64_t ldT, const uint8_t* dead, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Damped Hessian and the upper Cholesky factor of its inverse.
+ * Replaces opgraph/frame.py:515-522 (Environment.__init__):
+ *   dead = diag(H) == 0;  H[dead, dead] = 1;  H += damp * mean(diag H) * I;
+ *   U = torch.linalg.cholesky(torch.cholesky_inverse(torch.linalg.cholesky(H)), upper=True)
+ * computed as U = J inv(chol(J H J)) J (J the order reversal), the same unique factor.
+ *   H     [n, n] float64 input (row stride ldH; the lower triangle is read)
+ *   Hd    NULL or [n, n] float64 output of the damped H (row stride ldHd)
+ *   U     [n, n] float64 output (row stride ldU), zero below the diagonal
+ *   dead  NULL or [n] uint8 output
+ *   info  [1] int32 device output: 0, or j+1 when the leading minor of order j+1 of J H J is not
+ *         positive definite (torch.linalg.LinAlgError in the reference)
+ *   workspace: lamq_chol_inv_upper_workspace_size(n) bytes
+ * ---------------------------------------------------------------------------------------------- */
+size_t lamq_chol_inv_upper_workspace_size(int64_t n);
+int lamq_chol_inv_upper(const double* H, int64_t n, int64_t ldH, double damp, double* Hd, int64_t ldHd,
+                        double* U, int64_t ldU, uint8_t* dead, int32_t* info, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Randomized Hadamard transform of rows: out[r, :] = in[r, :] @ R^T with R = (A (x) B)/sqrt(n) diag(s).
+ * Replaces the dense products W @ R_in.T and R_in @ H @ R_in.T of opgraph/codes.py:129-132, 430,
+ * 439 (rht, incoherence_in) with the Kronecker-factored form of hadamard_factors (codes.py:104-119).
+ *   A [a, a], B [b, b] int8 (+1/-1), a*b = n <= 16384; signs [n] int8 (+1/-1)
+ *   in/out may alias. rms: NULL or [rows] float64 output max(sqrt(mean_j out[r, j]^2), 1e-12)
+ *   (codes.py:436).
+ * inverse != 0 applies R instead of R^T: out = in @ R (the reconstruction diag(S) Q R_in of a Net).
+ * R H R^T is two row passes with a transpose between them (lamq_transpose_f64, out = in^T, no aliasing).
+ * ---------------------------------------------------------------------------------------------- */
+int lamq_rht_rows(const double* in, int64_t rows, int64_t n, int64_t ldi, double* out, int64_t ldo,
+                  const int8_t* signs, const int8_t* A, int a, const int8_t* B, int b, int inverse, double* rms,
+                  void* stream);
+int lamq_transpose_f64(const double* in, int64_t rows, int64_t cols, int64_t ldi, double* out, int64_t ldo,
+                       void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Token-weighted Gram matrix on bf16 MFMA with fp32 accumulation:
+ *   H[i, j] += scale * sum_t w_t X[t, i] X[t, j]     (lower triangle i >= j written; upper untouched)
+ * Replaces the capture accumulation of quantize.py:1465 (H += X^T (w * X)), compiler.py:244 and
+ * opgraph/frame.py:498-505.
+ *   X [N, n] bf16 (row stride ldx; n and ldx even, X 4-byte aligned);  w NULL (every w_t = 1) or
+ *   [N] float32;  H [n, n] float32 (row stride ldH).
+ * With w the weighted operand is split into two bf16 parts (hi + lo) so the products keep float32
+ * precision. Small n splits the tokens over workgroups; the partial sums then go through the
+ * workspace (lamq_gram_workspace_size(N, n, 1) bytes, possibly 0) and are added in a fixed order.
+ * lamq_hessian_finalize mirrors the lower triangle, divides by ntok (quantize.py:1470) and, if H64
+ * is given, writes the float64 copy the sweep consumes.
+ * ---------------------------------------------------------------------------------------------- */
+size_t lamq_gram_workspace_size(int64_t N, int64_t n, int sym);
+int lamq_hessian_accum(const uint16_t* X, int64_t N, int64_t n, int64_t ldx, const float* w, float scale,
+                       float* H, int64_t ldH, void* workspace, size_t workspace_bytes, void* stream);
+int lamq_hessian_finalize(float* H, int64_t n, int64_t ldH, float ntok, double* H64, int64_t ldH64,
+                          void* stream);
+
+/* QEP cross-Gram D[i, j] += scale * sum_t w_t Xr[t, i] Xq[t, j] (all of D), quantize.py:1457.
+ * Workspace: lamq_gram_workspace_size(N, n, 0) bytes. */
+int lamq_cross_gram(const uint16_t* Xr, const uint16_t* Xq, int64_t N, int64_t n, int64_t ldx, const float* w,
+                    float scale, float* D, int64_t ldD, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Per-token KL(p_ref || p_q) of two bf16 logit matrices in one streaming pass.
+ * Replaces compiler.py:177-188 (kl()), quantize.py:904-920 and text_kl.py:57-61:
+ *   kl_t = sum_v softmax(ref_t)_v (log_softmax(ref_t)_v - log_softmax(q_t)_v)
+ *   ref, q  [T, V] bf16 (row strides ldr, ldq);  w NULL or [T] float32 token weights
+ *   kl      [T] float32 output;  sums [2] float64 output: sum_t w_t kl_t and sum_t w_t
+ * workspace: lamq_kl_workspace_size(T) bytes.
+ * ---------------------------------------------------------------------------------------------- */
+size_t lamq_kl_workspace_size(int64_t T);
+int lamq_kl_rows(const uint16_t* ref, const uint16_t* q, int64_t T, int64_t V, int64_t ldr, int64_t ldq,
+                 const float* w, float* kl, double* sums, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Pack row-trellis states into the opgraph-packed-1 bitstream.
+ * Replaces compiler_artifact.py:225-240 (pack_symbols) and :261-284 (valid_path, pack_trellis):
+ *   symbols = state & (2^k - 1), each row padded forward to a multiple of 32, reversed, then
+ *   packed little-endian, k uint32 words per 32 symbols.
+ *   states [m, n] int32 (row stride lds);  codes [m, ceil(n/32)*k] uint32 (row stride ldc)
+ *   bad    [1] int32 device output, set to 1 if any row is not a trellis path from state 0
+ *          (the reference raises ValueError); must be zero on entry. 1 <= k <= 4, k < L <= 16.
+ * ---------------------------------------------------------------------------------------------- */
+int lamq_pack_trellis(const int32_t* states, int64_t m, int64_t n, int64_t lds, int k, int L, uint32_t* codes,
+                      int64_t ldc, int32_t* bad, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LAMQ_H */

@@ -1,0 +1,115 @@
+// Width-1 block-LDLQ onto a scalar set, the lazy trailing update, and dead-column zeroing.
+#include "gemm_f64.h"
+
+// ------------------------------------------------------------------------------------------------
+// ldlq_scalar_block: one wave per row walks the columns of the lazy block [b0, b1), b1-b0 <= 128;
+// lane c holds columns b0+c and b0+64+c of the row in registers.
+//   mode 0 (opgraph/nested.py:127-140): t = T[j] (T is X/S), index = first argmin_i (t - lv_i)^2,
+//          q = lv[index]
+//   mode 1 (opgraph/codes.py:322-332, 442-450): index = bucketize(t/S, midpoints) (halfway to the
+//          lower level), q = lv[index]*S
+//   z = (t - q) / U[j][j];  T[col] = T[col] - z*U[j][col] for col in (j, b1)   (syntax.py:117-121,
+//   a K = 1 product: rounded, then subtracted)
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void ldlq_scalar_block_kernel(const double* __restrict__ T, int64_t m, int64_t ldT,
+                                                                const double* __restrict__ U, int64_t ldU,
+                                                                const double* __restrict__ S,
+                                                                const double* __restrict__ levels, int K, int mode,
+                                                                int64_t b0, int64_t b1, int32_t* __restrict__ idx,
+                                                                int64_t ldi, double* __restrict__ Z, int64_t ldZ)
+{
+    __shared__ double lv[256];
+    __shared__ double mid[256];
+    for (int i = threadIdx.x; i < K; i += 256) lv[i] = levels[i];
+    __syncthreads();
+    for (int i = threadIdx.x; i + 1 < K; i += 256) mid[i] = (lv[i + 1] + lv[i]) / 2;
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= m) return;
+    const int bw = (int)(b1 - b0);
+    const double* Tr = T + row * ldT + b0;
+    double t0 = lane < bw ? Tr[lane] : 0.0;
+    double t1 = lane + 64 < bw ? Tr[lane + 64] : 0.0;
+    const double Sr = mode == 1 ? S[row] : 1.0;
+    for (int c = 0; c < bw; ++c) {
+        const double t = c < 64 ? __shfl(t0, c) : __shfl(t1, c - 64);
+        int best = 0;
+        double q;
+        if (mode == 0) {
+            const double d0 = t - lv[0];
+            double bd = d0 * d0;
+            for (int i = 1; i < K; ++i) {
+                double d = t - lv[i];
+                d = d * d;
+                if (d < bd) { bd = d; best = i; }
+            }
+            q = lv[best];
+        } else {
+            const double ts = t / Sr;
+            while (best < K - 1 && ts > mid[best]) ++best;
+            q = lv[best] * Sr;
+        }
+        const int64_t j = b0 + c;
+        const double zj = (t - q) / U[j * ldU + j];
+        const double* Uj = U + j * ldU + b0;
+        if (lane > c && lane < bw) {
+            const double p = zj * Uj[lane];
+            t0 = t0 - p;
+        }
+        if (lane + 64 > c && lane + 64 < bw) {
+            const double p = zj * Uj[lane + 64];
+            t1 = t1 - p;
+        }
+        if (lane == (c & 63)) {
+            idx[row * ldi + j] = best;
+            Z[row * ldZ + c] = zj;
+        }
+    }
+}
+
+extern "C" int lamq_ldlq_scalar_block(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU,
+                                      const double* S, const double* levels, int K, int mode, int64_t b0, int64_t b1,
+                                      int32_t* idx, int64_t ldi, double* Z, int64_t ldZ, void* stream)
+{
+    if (!T || !U || !levels || !idx || !Z || (mode == 1 && !S) || (mode != 0 && mode != 1)) return LAMQ_EINVAL;
+    if (m < 0 || n < 1 || ldT < n || ldU < n || ldi < n || b0 < 0 || b1 <= b0 || b1 > n || K < 1 || K > 256)
+        return LAMQ_EINVAL;
+    if (ldZ < b1 - b0) return LAMQ_EINVAL;
+    if (b1 - b0 > 128) return LAMQ_EUNSUP;
+    if (m == 0) return LAMQ_OK;
+    hipLaunchKernelGGL(ldlq_scalar_block_kernel, dim3((unsigned)cdiv(m, 4)), dim3(256), 0, as_stream(stream), T, m, ldT, U,
+                       ldU, S, levels, K, mode, b0, b1, idx, ldi, Z, ldZ);
+    LAMQ_LAUNCH_CHECK();
+    return LAMQ_OK;
+}
+
+extern "C" int lamq_trailing_update_f64(double* T, int64_t m, int64_t n, int64_t ldT, const double* Z, int64_t ldZ,
+                                        const double* U, int64_t ldU, int64_t b0, int64_t b1, void* stream)
+{
+    if (!T || !Z || !U || m < 0 || n < 1 || ldT < n || ldU < n || b0 < 0 || b1 <= b0 || b1 > n || ldZ < b1 - b0)
+        return LAMQ_EINVAL;
+    if (b1 - b0 > 256) return LAMQ_EUNSUP;
+    if (m == 0 || b1 == n) return LAMQ_OK;
+    return gemm_sub_f64<false, false>(T + b1, ldT, Z, ldZ, U + b0 * ldU + b1, ldU, m, n - b1, b1 - b0, nullptr,
+                                      as_stream(stream));
+}
+
+// T[:, dead] = 0 at the start of a sweep (opgraph/syntax.py:101).
+__global__ void zero_columns_kernel(double* __restrict__ T, int64_t m, int64_t n, int64_t ldT, const uint8_t* __restrict__ dead)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= m * n) return;
+    const int64_t r = i / n, c = i - r * n;
+    if (dead[c]) T[r * ldT + c] = 0.0;
+}
+
+extern "C" int lamq_zero_columns(double* T, int64_t m, int64_t n, int64_t ldT, const uint8_t* dead, void* stream)
+{
+    if (!T || !dead || m < 0 || n < 1 || ldT < n) return LAMQ_EINVAL;
+    if (m == 0) return LAMQ_OK;
+    hipLaunchKernelGGL(zero_columns_kernel, dim3((unsigned)cdiv(m * n, 256)), dim3(256), 0, as_stream(stream), T, m, n, ldT,
+                       dead);
+    LAMQ_LAUNCH_CHECK();
+    return LAMQ_OK;
+}

@@ -1,0 +1,278 @@
+"""Tensor-level entry points of the gfx950 kernels: every function takes and returns torch tensors on the GPU and
+enqueues HIP kernels on torch's current stream (no host synchronisation unless a result is read back). These
+are what the reference-compatible modules (codes, frame, nested, quantize, compiler, artifact) are built on."""
+
+from __future__ import annotations
+
+from functools import lru_cache
+
+import torch
+
+from . import _abi
+from ._abi import check, ld, lib, need, ptr, stream, workspace
+from .hadamard import hadamard_factors, rht_signs
+
+
+class LinAlgError(torch.linalg.LinAlgError if hasattr(torch.linalg, "LinAlgError") else RuntimeError):
+    pass
+
+
+# ----------------------------------------------------------------------------- Viterbi (codes.py:151-181)
+
+
+def viterbi_rows(x: torch.Tensor, C: torch.Tensor, L: int, k: int, start: torch.Tensor | None = None) -> torch.Tensor:
+    """x [B, T] float32, C [2^L] float32, start None or [B] int32 -> states [B, T] int32."""
+    need(x, torch.float32, "x", 2)
+    need(C, torch.float32, "C", 1)
+    if C.numel() != 1 << L:
+        raise ValueError("the table must have 2^L entries")
+    B, T = x.shape
+    out = torch.empty(B, T, dtype=torch.int32, device=x.device)
+    st = None
+    if start is not None:
+        st = start.to(device=x.device, dtype=torch.int32).contiguous()
+        if st.numel() != B:
+            raise ValueError("one start state per row")
+    nbytes = lib().lamq_viterbi_workspace_size(B, T, L, k)
+    ws = workspace(nbytes, x.device)
+    check(lib().lamq_viterbi_rows(ptr(x), B, T, ld(x), ptr(C), L, k, ptr(st), ptr(out), T, ptr(ws), nbytes,
+                                  stream(x.device)), "viterbi")
+    return out
+
+
+# ----------------------------------------------------------------------------- randomized Hadamard transforms
+
+
+@lru_cache(maxsize=64)
+def _factors(n: int, dev: str):
+    A, B = hadamard_factors(n)
+    return A.to(torch.int8).to(dev).contiguous(), B.to(torch.int8).to(dev).contiguous()
+
+
+@lru_cache(maxsize=256)
+def _signs(n: int, seed: int, dev: str):
+    return rht_signs(n, seed).to(torch.int8).to(dev).contiguous()
+
+
+def rht_rows(X: torch.Tensor, seed: int, inverse: bool = False, want_rms: bool = False, out: torch.Tensor | None = None):
+    """X @ R^T (or X @ R with inverse) for R = rht(n, seed), row by row in Kronecker-factored form; optionally the
+    row RMS max(sqrt(mean x^2), 1e-12) of the result (codes.py:436)."""
+    need(X, torch.float64, "X", 2)
+    rows, n = X.shape
+    dev = str(X.device)
+    A, B = _factors(n, dev)
+    s = _signs(n, seed, dev)
+    y = torch.empty_like(X, memory_format=torch.contiguous_format) if out is None else out
+    rms = torch.empty(rows, dtype=torch.float64, device=X.device) if want_rms else None
+    check(lib().lamq_rht_rows(ptr(X), rows, n, ld(X), ptr(y), ld(y), ptr(s), ptr(A), A.shape[0], ptr(B), B.shape[0],
+                              1 if inverse else 0, ptr(rms), stream(X.device)), "rht_rows")
+    return (y, rms) if want_rms else y
+
+
+def transpose(X: torch.Tensor) -> torch.Tensor:
+    need(X, torch.float64, "X", 2)
+    r, c = X.shape
+    out = torch.empty(c, r, dtype=torch.float64, device=X.device)
+    check(lib().lamq_transpose_f64(ptr(X), r, c, ld(X), ptr(out), r, stream(X.device)), "transpose")
+    return out
+
+
+def rotate_hessian(H: torch.Tensor, seed: int) -> torch.Tensor:
+    """R H R^T for R = rht(n, seed) (codes.py:439): the rows of H, a transpose, the rows again."""
+    Y = rht_rows(H, seed)
+    return rht_rows(transpose(Y), seed)
+
+
+def rotate_columns(X: torch.Tensor, seed: int) -> torch.Tensor:
+    """R X for R = rht(rows, seed): the output-side rotation of incoherence (codes.py:253-263)."""
+    return transpose(rht_rows(transpose(X), seed))
+
+
+def unrotate_columns(X: torch.Tensor, seed: int) -> torch.Tensor:
+    """R^T X."""
+    return transpose(rht_rows(transpose(X), seed, inverse=True))
+
+
+# ----------------------------------------------------------------------------- environment (frame.py:515-522)
+
+
+def chol_inv_upper(H: torch.Tensor, damp: float = 0.01, raise_on_fail: bool = True):
+    """(Hd, U, dead, info): the damped H, the upper Cholesky factor of its inverse, the dead-column mask and the
+    failing pivot (0 when H is positive definite after damping; raises LinAlgError then unless told not to)."""
+    need(H, torch.float64, "H", 2)
+    n = H.shape[0]
+    if H.shape[1] != n:
+        raise ValueError("H must be square")
+    Hd = torch.empty(n, n, dtype=torch.float64, device=H.device)
+    U = torch.empty(n, n, dtype=torch.float64, device=H.device)
+    dead = torch.empty(n, dtype=torch.uint8, device=H.device)
+    info = torch.empty(1, dtype=torch.int32, device=H.device)
+    nbytes = lib().lamq_chol_inv_upper_workspace_size(n)
+    ws = workspace(nbytes, H.device)
+    check(lib().lamq_chol_inv_upper(ptr(H), n, ld(H), float(damp), ptr(Hd), n, ptr(U), n, ptr(dead), ptr(info), ptr(ws),
+                                    nbytes, stream(H.device)), "chol_inv_upper")
+    if raise_on_fail:
+        bad = int(info.item())
+        if bad:
+            raise LinAlgError(f"linalg.cholesky: the leading minor of order {bad} is not positive-definite")
+    return Hd, U, dead.bool(), info
+
+
+# ----------------------------------------------------------------------------- the sweeps (syntax.py:86-124)
+
+
+def ldlq_trellis(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, table64: torch.Tensor, L: int, k: int,
+                 width: int = 16, look: int = 8, lazy: int = 128, dead: torch.Tensor | None = None,
+                 table32: torch.Tensor | None = None) -> torch.Tensor:
+    """States [m, n] int32 of the row-trellis block LDLQ of X (rotated rows, not divided by S) under U."""
+    need(X, torch.float64, "X", 2)
+    need(U, torch.float64, "U", 2)
+    need(S, torch.float64, "S", 1)
+    need(table64, torch.float64, "table64", 1)
+    m, n = X.shape
+    if lazy % width:
+        raise ValueError("lazy must be a multiple of width and of block")
+    T = X.clone(memory_format=torch.contiguous_format)
+    dev = X.device
+    s = stream(dev)
+    if dead is not None and bool(dead.any()):
+        dd = dead.to(device=dev, dtype=torch.uint8).contiguous()
+        check(lib().lamq_zero_columns(ptr(T), m, n, n, ptr(dd), s), "zero_columns")
+    t32 = table64.to(torch.float32) if table32 is None else table32
+    state = torch.zeros(m, dtype=torch.int32, device=dev)
+    states = torch.empty(m, n, dtype=torch.int32, device=dev)
+    Z = torch.empty(m, lazy, dtype=torch.float64, device=dev)
+    for b0 in range(0, n, lazy):
+        b1 = min(b0 + lazy, n)
+        check(lib().lamq_ldlq_trellis_block(ptr(T), m, n, n, ptr(U), ld(U), ptr(S), ptr(table64), ptr(t32), L, k, b0, b1,
+                                            width, look, ptr(state), ptr(states), n, ptr(Z), lazy, s), "ldlq_trellis_block")
+        if b1 < n:
+            check(lib().lamq_trailing_update_f64(ptr(T), m, n, n, ptr(Z), lazy, ptr(U), ld(U), b0, b1, s), "trailing_update")
+    return states
+
+
+def ldlq_scalar(T0: torch.Tensor, U: torch.Tensor, levels: torch.Tensor, mode: int = 0, S: torch.Tensor | None = None,
+                lazy: int = 128, dead: torch.Tensor | None = None) -> torch.Tensor:
+    """Level indices [m, n] int32 of the width-1 LDLQ onto `levels` (mode 0: T0 = X/S and the first argmin of the
+    squared distance; mode 1: T0 = X and bucketize(t/S) on midpoints, q*S)."""
+    need(T0, torch.float64, "T0", 2)
+    need(U, torch.float64, "U", 2)
+    need(levels, torch.float64, "levels", 1)
+    if mode == 1:
+        need(S, torch.float64, "S", 1)
+    m, n = T0.shape
+    lazy = min(lazy, 128) if lazy > 128 else lazy
+    T = T0.clone(memory_format=torch.contiguous_format)
+    dev = T0.device
+    s = stream(dev)
+    if dead is not None and bool(dead.any()):
+        dd = dead.to(device=dev, dtype=torch.uint8).contiguous()
+        check(lib().lamq_zero_columns(ptr(T), m, n, n, ptr(dd), s), "zero_columns")
+    idx = torch.empty(m, n, dtype=torch.int32, device=dev)
+    Z = torch.empty(m, lazy, dtype=torch.float64, device=dev)
+    for b0 in range(0, n, lazy):
+        b1 = min(b0 + lazy, n)
+        check(lib().lamq_ldlq_scalar_block(ptr(T), m, n, n, ptr(U), ld(U), ptr(S), ptr(levels), levels.numel(), mode, b0,
+                                           b1, ptr(idx), n, ptr(Z), lazy, s), "ldlq_scalar_block")
+        if b1 < n:
+            check(lib().lamq_trailing_update_f64(ptr(T), m, n, n, ptr(Z), lazy, ptr(U), ld(U), b0, b1, s), "trailing_update")
+    return idx
+
+
+def trailing_update(T: torch.Tensor, Z: torch.Tensor, U: torch.Tensor, b0: int, b1: int):
+    """T[:, b1:] -= Z @ U[b0:b1, b1:] in place (syntax.py:123)."""
+    need(T, torch.float64, "T", 2)
+    need(Z, torch.float64, "Z", 2)
+    need(U, torch.float64, "U", 2)
+    m, n = T.shape
+    check(lib().lamq_trailing_update_f64(ptr(T), m, n, ld(T), ptr(Z), ld(Z), ptr(U), ld(U), b0, b1, stream(T.device)),
+          "trailing_update")
+    return T
+
+
+# ----------------------------------------------------------------------------- statistics
+
+
+def hessian_accum(H: torch.Tensor, X: torch.Tensor, w: torch.Tensor | None = None, scale: float = 1.0) -> torch.Tensor:
+    """H (float32 [n, n], lower triangle) += scale * X^T diag(w) X for bf16 X [N, n]."""
+    need(H, torch.float32, "H", 2)
+    need(X, torch.bfloat16, "X", 2)
+    N, n = X.shape
+    wv = None
+    if w is not None:
+        wv = w.to(device=X.device, dtype=torch.float32).contiguous()
+    nbytes = lib().lamq_gram_workspace_size(N, n, 1)
+    ws = workspace(nbytes, X.device)
+    check(lib().lamq_hessian_accum(ptr(X), N, n, ld(X), ptr(wv), float(scale), ptr(H), ld(H), ptr(ws), nbytes,
+                                   stream(X.device)), "hessian_accum")
+    return H
+
+
+def hessian_finalize(H: torch.Tensor, ntok: float, want64: bool = True):
+    need(H, torch.float32, "H", 2)
+    n = H.shape[0]
+    H64 = torch.empty(n, n, dtype=torch.float64, device=H.device) if want64 else None
+    check(lib().lamq_hessian_finalize(ptr(H), n, ld(H), float(ntok), ptr(H64), n, stream(H.device)), "hessian_finalize")
+    return H64 if want64 else H
+
+
+def hessian(X: torch.Tensor, w: torch.Tensor | None = None) -> torch.Tensor:
+    """H = (1/N) X^T diag(w) X as float64 [n, n] from bf16 activations [N, n] (quantize.py:1465,1470)."""
+    N, n = X.shape
+    H = torch.zeros(n, n, dtype=torch.float32, device=X.device)
+    hessian_accum(H, X, w)
+    return hessian_finalize(H, float(N))
+
+
+def cross_gram_accum(D: torch.Tensor, Xr: torch.Tensor, Xq: torch.Tensor, w: torch.Tensor | None = None,
+                     scale: float = 1.0) -> torch.Tensor:
+    """D (float32 [n, n]) += scale * Xr^T diag(w) Xq (quantize.py:1457)."""
+    need(D, torch.float32, "D", 2)
+    need(Xr, torch.bfloat16, "Xr", 2)
+    need(Xq, torch.bfloat16, "Xq", 2)
+    if Xr.shape != Xq.shape or ld(Xr) != ld(Xq):
+        raise ValueError("Xr and Xq must have the same shape and row stride")
+    N, n = Xr.shape
+    wv = None if w is None else w.to(device=Xr.device, dtype=torch.float32).contiguous()
+    nbytes = lib().lamq_gram_workspace_size(N, n, 0)
+    ws = workspace(nbytes, Xr.device)
+    check(lib().lamq_cross_gram(ptr(Xr), ptr(Xq), N, n, ld(Xr), ptr(wv), float(scale), ptr(D), ld(D), ptr(ws), nbytes,
+                                stream(Xr.device)), "cross_gram")
+    return D
+
+
+# ----------------------------------------------------------------------------- KL (compiler.py:177-188)
+
+
+def kl_rows(ref: torch.Tensor, q: torch.Tensor, w: torch.Tensor | None = None):
+    """(kl [T] float32, sums [2] float64 = (sum w kl, sum w)) for bf16 logits [T, V]."""
+    need(ref, torch.bfloat16, "ref", 2)
+    need(q, torch.bfloat16, "q", 2)
+    if ref.shape != q.shape:
+        raise ValueError("ref and q must have the same shape")
+    T, V = ref.shape
+    wv = None if w is None else w.to(device=ref.device, dtype=torch.float32).contiguous()
+    kl = torch.empty(T, dtype=torch.float32, device=ref.device)
+    sums = torch.empty(2, dtype=torch.float64, device=ref.device)
+    nbytes = lib().lamq_kl_workspace_size(T)
+    ws = workspace(nbytes, ref.device)
+    check(lib().lamq_kl_rows(ptr(ref), ptr(q), T, V, ld(ref), ld(q), ptr(wv), ptr(kl), ptr(sums), ptr(ws), nbytes,
+                             stream(ref.device)), "kl_rows")
+    return kl, sums
+
+
+# ----------------------------------------------------------------------------- packing (compiler_artifact.py:276-284)
+
+
+def pack_trellis(states: torch.Tensor, k: int, L: int = 12) -> torch.Tensor:
+    """uint32 code words [m, ceil(n/32)*k] of row-trellis states; raises ValueError if a row is not a path from 0."""
+    need(states, torch.int32, "states", 2)
+    m, n = states.shape
+    words = (n + 31) // 32 * k
+    codes = torch.empty(m, words, dtype=torch.int32, device=states.device)
+    bad = torch.zeros(1, dtype=torch.int32, device=states.device)
+    check(lib().lamq_pack_trellis(ptr(states), m, n, ld(states), k, L, ptr(codes), words, ptr(bad), stream(states.device)),
+          "pack_trellis")
+    if int(bad.item()):
+        raise ValueError("states are not a row trellis from zero")
+    return codes.view(torch.uint32) if hasattr(torch, "uint32") else codes

@@ -1,0 +1,299 @@
+"""GPU parity of each kernel against the reference's own vectors (tests/golden) and the CPU oracle, through the
+C ABI (lookatmyquant_amd.engine wraps include/lamq.h one to one). Codes and states must be bit-exact; floating
+point results meet the tolerance written in each test."""
+
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def E():
+    from lookatmyquant_amd import engine
+
+    assert torch.cuda.is_available(), "the GPU tests need an MI355X"
+    return engine
+
+
+def cuda(a, dtype=None):
+    t = torch.as_tensor(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.cuda()
+
+
+# ----------------------------------------------------------------------------- Viterbi
+
+
+@pytest.mark.parametrize("k", [1, 2, 3, 4])
+def test_viterbi_L12_matches_reference(E, golden, tables, k):
+    g = golden("viterbi")
+    x = g[f"L12_k{k}_x"].astype(np.float32)
+    C = cuda(tables[k].astype(np.float32))
+    say(f"viterbi L=12 k={k} rows={len(x)}")
+    free = E.viterbi_rows(cuda(x), C, 12, k).cpu().numpy()
+    fixed = E.viterbi_rows(cuda(x), C, 12, k, start=cuda(g[f"L12_k{k}_start"], torch.int32)).cpu().numpy()
+    assert np.array_equal(free, g[f"L12_k{k}_free"])
+    assert np.array_equal(fixed, g[f"L12_k{k}_fixed"])
+
+
+@pytest.mark.parametrize("L,k", [(8, 2), (6, 1), (9, 3)])
+def test_viterbi_ties_match_reference(E, golden, L, k):
+    g = golden("viterbi")
+    p = f"ties_L{L}_k{k}_"
+    C = cuda(g[p + "table"].astype(np.float32))
+    x = cuda(g[p + "x"].astype(np.float32))
+    say(f"viterbi ties L={L} k={k}")
+    assert np.array_equal(E.viterbi_rows(x, C, L, k).cpu().numpy(), g[p + "free"])
+    st = cuda(g[p + "start"], torch.int32)
+    assert np.array_equal(E.viterbi_rows(x, C, L, k, start=st).cpu().numpy(), g[p + "fixed"])
+
+
+def test_viterbi_long_paths_use_workspace(E, tables):
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((6, 200)).astype(np.float32)
+    say("viterbi L=12 k=2 T=200")
+    got = E.viterbi_rows(cuda(x), cuda(tables[2].astype(np.float32)), 12, 2).cpu().numpy()
+    assert np.array_equal(got, O.viterbi(x, tables[2], 12, 2))
+
+
+# ----------------------------------------------------------------------------- fp64 building blocks
+
+
+def test_trailing_update_matches_oracle_order(E):
+    rng = np.random.default_rng(5)
+    m, n, b0, b1 = 200, 300, 64, 192
+    T = rng.standard_normal((m, n))
+    Z = rng.standard_normal((m, b1 - b0))
+    U = np.triu(rng.standard_normal((n, n)))
+    say("trailing update")
+    got = E.trailing_update(cuda(T), cuda(Z), cuda(U), b0, b1).cpu().numpy()
+    ref = T.copy()
+    acc = np.zeros((m, n - b1))
+    for c in range(b1 - b0):  # fma chain in c order, as the oracle spells it
+        acc = acc + Z[:, c : c + 1] * U[b0 + c, b1:][None, :]
+    ref[:, b1:] = T[:, b1:] - acc
+    assert np.array_equal(got[:, :b1], T[:, :b1])
+    err = np.abs(got - ref).max() / np.abs(ref).max()
+    say(f"  max relative difference {err:.3e}")
+    assert err < 1e-14
+
+
+@pytest.mark.parametrize("n", [64, 100, 960])
+def test_chol_inv_upper(E, n):
+    rng = np.random.default_rng(n)
+    X = rng.standard_normal((2 * n + 50, n))
+    H = X.T @ X / len(X)
+    if n == 100:
+        H[7, :] = 0
+        H[:, 7] = 0  # a dead column
+    say(f"chol_inv_upper n={n}")
+    Hd, U, dead, info = E.chol_inv_upper(cuda(H))
+    Hd_o, U_o, dead_o = O.environment(H)
+    assert int(info.item()) == 0
+    assert np.array_equal(dead.cpu().numpy(), dead_o)
+    assert np.allclose(Hd.cpu().numpy(), Hd_o, rtol=0, atol=1e-12 * np.abs(Hd_o).max())
+    Ug = U.cpu().numpy()
+    assert np.all(np.tril(Ug, -1) == 0)
+    assert np.all(np.diag(Ug) > 0)
+    err = np.abs(Ug - U_o).max() / np.abs(U_o).max()
+    say(f"  |U - U_lapack| / |U| = {err:.3e}")
+    assert err < 1e-10
+    # U^T U = Hd^-1
+    assert np.abs(Ug.T @ Ug @ Hd_o - np.eye(n)).max() < 1e-9
+
+
+def test_chol_inv_upper_reports_non_pd(E):
+    H = -np.eye(40)
+    say("chol_inv_upper not positive definite")
+    _, _, _, info = E.chol_inv_upper(cuda(H), raise_on_fail=False)
+    assert int(info.item()) > 0
+    with pytest.raises(E.LinAlgError):
+        E.chol_inv_upper(cuda(H))
+
+
+@pytest.mark.parametrize("m,n,seed", [(48, 960, 201), (20, 2560, 1301), (8, 4096, 7), (4, 9728, 3301)])
+def test_rht_rows(E, m, n, seed):
+    rng = np.random.default_rng(n)
+    W = rng.standard_normal((m, n))
+    R = O.rht(n, seed)
+    say(f"rht rows m={m} n={n}")
+    Xg, S = E.rht_rows(cuda(W), seed, want_rms=True)
+    X = W @ R.T
+    assert np.abs(Xg.cpu().numpy() - X).max() < 1e-12 * np.abs(X).max()
+    assert np.allclose(S.cpu().numpy(), O.row_scale(X), rtol=1e-13, atol=0)
+    back = E.rht_rows(Xg, seed, inverse=True).cpu().numpy()
+    assert np.abs(back - W).max() < 1e-12 * np.abs(W).max()
+
+
+def test_rotate_hessian(E, config12):
+    _, H = config12
+    say("rotate hessian n=960")
+    Hr = E.rotate_hessian(cuda(H), 201).cpu().numpy()
+    R = O.rht(960, 201)
+    ref = R @ H @ R.T
+    assert np.abs(Hr - ref).max() < 1e-12 * np.abs(ref).max()
+
+
+# ----------------------------------------------------------------------------- the sweeps
+
+
+def _rotated(W, H, seed):
+    R = O.rht(W.shape[1], seed)
+    X = np.asarray(W, dtype=np.float64) @ R.T
+    S = O.row_scale(X)
+    _, U, dead = O.environment(R @ H @ R.T)
+    return X, S, U, dead
+
+
+def test_ldlq_trellis_block_matches_reference_config2(E, golden, tables, config12):
+    """Config 2 (960 x 960, L = 12, k = 2): the sweep kernels on the oracle's U reproduce the reference states."""
+    W, H = config12
+    g = golden("ldlq_trellis_c2_L12_k2")
+    X, S, U, dead = _rotated(W, H, 201)
+    say("ldlq trellis config 2 L=12 k=2 (960 rows)")
+    st = E.ldlq_trellis(cuda(X), cuda(S), cuda(U), cuda(tables[2]), 12, 2).cpu().numpy()
+    agree = (st == g["states"]).mean()
+    say(f"  state agreement with the reference {agree:.6f}")
+    assert np.array_equal(st, g["states"])
+
+
+@pytest.mark.parametrize("k", [1, 3, 4])
+def test_ldlq_trellis_other_widths_match_reference(E, golden, tables, config12, k):
+    W, H = config12
+    g = golden(f"ldlq_trellis_L12_k{k}_rows128")
+    X, S, U, dead = _rotated(W[:128], H, 201)
+    say(f"ldlq trellis L=12 k={k} (128 rows)")
+    st = E.ldlq_trellis(cuda(X), cuda(S), cuda(U), cuda(tables[k]), 12, k).cpu().numpy()
+    assert np.array_equal(st, g["states"])
+
+
+def test_ldlq_trellis_ragged_matches_oracle(E, tables):
+    """n not a multiple of the lazy block or of the width, m not a multiple of anything."""
+    rng = np.random.default_rng(11)
+    m, n = 37, 200
+    Xa = rng.standard_normal((500, n))
+    H = Xa.T @ Xa / 500
+    _, U, _ = O.environment(H)
+    X = rng.standard_normal((m, n))
+    S = O.row_scale(X)
+    say("ldlq trellis ragged 37 x 200, width 12, look 5, lazy 96")
+    st = E.ldlq_trellis(cuda(X), cuda(S), cuda(U), cuda(tables[3]), 12, 3, width=12, look=5, lazy=96).cpu().numpy()
+    ref = O.ldlq_trellis(X, U, S, tables[3], 12, 3, width=12, look=5, lazy=96)
+    assert np.array_equal(st, ref)
+
+
+def test_ldlq_scalar_matches_reference_config1(E, golden, config12):
+    """Config 1 (960 x 960, 3-bit Lloyd-Max, nested_words path): indices equal the reference's."""
+    W, H = config12
+    g = golden("nested_lm3_c1")
+    X, S, U, dead = _rotated(W, H, 201)
+    say("ldlq scalar config 1 lm3")
+    idx = E.ldlq_scalar(cuda(X / S[:, None]), cuda(U), cuda(g["levels"]), mode=0).cpu().numpy()
+    assert np.array_equal(idx, g["idx"].astype(np.int32))
+
+
+def test_ldlq_scalar_bucketize_mode_matches_oracle(E):
+    rng = np.random.default_rng(2)
+    m, n = 50, 170
+    Xa = rng.standard_normal((400, n))
+    _, U, _ = O.environment(Xa.T @ Xa / 400)
+    X = rng.standard_normal((m, n)) * 0.02
+    S = O.row_scale(X)
+    lv = np.array([-1.5104, -0.4528, 0.4528, 1.5104])
+    say("ldlq scalar bucketize mode")
+    idx = E.ldlq_scalar(cuda(X), cuda(U), cuda(lv), mode=1, S=cuda(S)).cpu().numpy()
+    assert np.array_equal(idx, O.ldlq_scalar(X, U, lv, 1, S))
+
+
+def test_end_to_end_gpu_factor_config2(E, golden, tables, config12):
+    """Hessian rotation and U on the GPU too: the reference states at config 2, bit for bit."""
+    W, H = config12
+    g = golden("ldlq_trellis_c2_L12_k2")
+    say("end to end config 2 with GPU rotation and factor")
+    X, S = E.rht_rows(cuda(W.astype(np.float64)), 201, want_rms=True)
+    Hr = E.rotate_hessian(cuda(H), 201)
+    _, U, dead, _ = E.chol_inv_upper(Hr)
+    st = E.ldlq_trellis(X, S, U, cuda(tables[2]), 12, 2, dead=dead).cpu().numpy()
+    agree = (st == g["states"]).mean()
+    say(f"  state agreement with the reference {agree:.6f}")
+    assert agree == 1.0
+
+
+# ----------------------------------------------------------------------------- statistics and KL
+
+
+@pytest.mark.parametrize("N,n,weighted", [(4096, 960, False), (3000, 256, True), (2048, 2560, True)])
+def test_hessian(E, N, n, weighted):
+    from lookatmyquant_amd import synthetic
+
+    X = synthetic.calibration(N, n, 12, 13)
+    w = synthetic.digit_weights(N, 14) if weighted else None
+    say(f"hessian N={N} n={n} weighted={weighted}")
+    Xb = torch.from_numpy(X).to(torch.bfloat16).cuda()
+    Hg = E.hessian(Xb, None if w is None else torch.from_numpy(w).cuda()).cpu().numpy()
+    ref = O.hessian(X, w)
+    err = np.abs(Hg - ref).max() / np.abs(ref).max()
+    say(f"  max |H - H64| / max |H64| = {err:.3e}")
+    assert err < 1e-4
+    assert np.array_equal(Hg, Hg.T)
+
+
+def test_cross_gram(E):
+    from lookatmyquant_amd import synthetic
+
+    N, n = 2500, 192
+    Xr = synthetic.calibration(N, n, 21, 22)
+    Xq = synthetic.bf16_round(Xr + 0.05 * np.random.default_rng(23).standard_normal(Xr.shape).astype(np.float32))
+    w = synthetic.digit_weights(N, 24)
+    say("cross gram")
+    D = torch.zeros(n, n, dtype=torch.float32, device="cuda")
+    E.cross_gram_accum(D, torch.from_numpy(Xr).to(torch.bfloat16).cuda(), torch.from_numpy(Xq).to(torch.bfloat16).cuda(),
+                       torch.from_numpy(w).cuda(), scale=1.0 / N)
+    ref = O.cross_gram(Xr, Xq, w)
+    err = np.abs(D.cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err < 1e-4
+
+
+@pytest.mark.parametrize("T,V", [(64, 151936), (33, 1000), (5, 77)])
+def test_kl_rows(E, T, V):
+    from lookatmyquant_amd import synthetic
+
+    r, q = synthetic.logits(T, V, 401 + V, 402 + V)
+    w = np.random.default_rng(V).uniform(0.5, 2.0, T).astype(np.float32)
+    say(f"kl T={T} V={V}")
+    kl, sums = E.kl_rows(cuda(r.view(np.int16)).view(torch.bfloat16), cuda(q.view(np.int16)).view(torch.bfloat16),
+                         torch.from_numpy(w).cuda())
+    ref, mean = O.kl_rows(r, q, w)
+    kl = kl.cpu().numpy().astype(np.float64)
+    err = np.abs(kl - ref).max() / np.abs(ref).max()
+    say(f"  max relative KL error {err:.3e}")
+    assert err < 1e-4
+    s = sums.cpu().numpy()
+    assert abs(s[0] / s[1] - mean) < 1e-4 * abs(mean)
+
+
+def test_pack_trellis_matches_reference(E, golden):
+    g = golden("misc")
+    for bits in (1, 2, 3, 4):
+        st = g[f"pack_{bits}_states"].astype(np.int32)
+        say(f"pack bits={bits}")
+        codes = E.pack_trellis(cuda(st), bits).cpu()
+        codes = codes.view(torch.int32).numpy().view(np.uint32)
+        assert np.array_equal(codes, g[f"pack_{bits}_codes"])
+    bad = g["pack_2_states"].astype(np.int32).copy()
+    bad[3, 10] ^= 0x100
+    with pytest.raises(ValueError):
+        E.pack_trellis(cuda(bad), 2)
