@@ -123,8 +123,10 @@ def chol_inv_upper(H: torch.Tensor, damp: float = 0.01, raise_on_fail: bool = Tr
 
 def ldlq_trellis(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, table64: torch.Tensor, L: int, k: int,
                  width: int = 16, look: int = 8, lazy: int = 128, dead: torch.Tensor | None = None,
-                 table32: torch.Tensor | None = None) -> torch.Tensor:
-    """States [m, n] int32 of the row-trellis block LDLQ of X (rotated rows, not divided by S) under U."""
+                 table32: torch.Tensor | None = None, events: dict | None = None) -> torch.Tensor:
+    """States [m, n] int32 of the row-trellis block LDLQ of X (rotated rows, not divided by S) under U.
+    events: optional dict; each launch of the block kernel and of the trailing update is bracketed by a pair of
+    torch.cuda.Event on this stream, appended to events["block"] and events["trailing"]."""
     need(X, torch.float64, "X", 2)
     need(U, torch.float64, "U", 2)
     need(S, torch.float64, "S", 1)
@@ -135,7 +137,7 @@ def ldlq_trellis(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, table64: tor
     T = X.clone(memory_format=torch.contiguous_format)
     dev = X.device
     s = stream(dev)
-    if dead is not None and bool(dead.any()):
+    if dead is not None:
         dd = dead.to(device=dev, dtype=torch.uint8).contiguous()
         check(lib().lamq_zero_columns(ptr(T), m, n, n, ptr(dd), s), "zero_columns")
     t32 = table64.to(torch.float32) if table32 is None else table32
@@ -144,11 +146,34 @@ def ldlq_trellis(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, table64: tor
     Z = torch.empty(m, lazy, dtype=torch.float64, device=dev)
     for b0 in range(0, n, lazy):
         b1 = min(b0 + lazy, n)
+        ev = _event_pair(events, "block")
         check(lib().lamq_ldlq_trellis_block(ptr(T), m, n, n, ptr(U), ld(U), ptr(S), ptr(table64), ptr(t32), L, k, b0, b1,
                                             width, look, ptr(state), ptr(states), n, ptr(Z), lazy, s), "ldlq_trellis_block")
+        _event_end(ev)
         if b1 < n:
+            ev = _event_pair(events, "trailing")
             check(lib().lamq_trailing_update_f64(ptr(T), m, n, n, ptr(Z), lazy, ptr(U), ld(U), b0, b1, s), "trailing_update")
+            _event_end(ev)
     return states
+
+
+def _event_pair(events: dict | None, key: str):
+    if events is None:
+        return None
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    events.setdefault(key, []).append((a, b))
+    return b
+
+
+def _event_end(ev):
+    if ev is not None:
+        ev.record()
+
+
+def event_ms(events: dict, key: str) -> list[float]:
+    """Durations in ms of the launches recorded under `key` (synchronise first)."""
+    return [a.elapsed_time(b) for a, b in events.get(key, [])]
 
 
 def ldlq_scalar(T0: torch.Tensor, U: torch.Tensor, levels: torch.Tensor, mode: int = 0, S: torch.Tensor | None = None,
@@ -161,11 +186,12 @@ def ldlq_scalar(T0: torch.Tensor, U: torch.Tensor, levels: torch.Tensor, mode: i
     if mode == 1:
         need(S, torch.float64, "S", 1)
     m, n = T0.shape
-    lazy = min(lazy, 128) if lazy > 128 else lazy
+    if lazy > 128:
+        raise NotImplementedError("the width-1 block kernel keeps at most 128 columns of a row in registers")
     T = T0.clone(memory_format=torch.contiguous_format)
     dev = T0.device
     s = stream(dev)
-    if dead is not None and bool(dead.any()):
+    if dead is not None:
         dd = dead.to(device=dev, dtype=torch.uint8).contiguous()
         check(lib().lamq_zero_columns(ptr(T), m, n, n, ptr(dd), s), "zero_columns")
     idx = torch.empty(m, n, dtype=torch.int32, device=dev)
@@ -264,8 +290,10 @@ def kl_rows(ref: torch.Tensor, q: torch.Tensor, w: torch.Tensor | None = None):
 # ----------------------------------------------------------------------------- packing (compiler_artifact.py:276-284)
 
 
-def pack_trellis(states: torch.Tensor, k: int, L: int = 12) -> torch.Tensor:
-    """uint32 code words [m, ceil(n/32)*k] of row-trellis states; raises ValueError if a row is not a path from 0."""
+def pack_trellis(states: torch.Tensor, k: int, L: int = 12, check_paths: bool = True):
+    """int32 tensor holding the uint32 code words [m, ceil(n/32)*k] of row-trellis states. With check_paths a row
+    that is not a path from state 0 raises ValueError (one host synchronisation); without it (codes, bad) is
+    returned, bad a device flag."""
     need(states, torch.int32, "states", 2)
     m, n = states.shape
     words = (n + 31) // 32 * k
@@ -273,6 +301,8 @@ def pack_trellis(states: torch.Tensor, k: int, L: int = 12) -> torch.Tensor:
     bad = torch.zeros(1, dtype=torch.int32, device=states.device)
     check(lib().lamq_pack_trellis(ptr(states), m, n, ld(states), k, L, ptr(codes), words, ptr(bad), stream(states.device)),
           "pack_trellis")
+    if not check_paths:
+        return codes, bad
     if int(bad.item()):
         raise ValueError("states are not a row trellis from zero")
-    return codes.view(torch.uint32) if hasattr(torch, "uint32") else codes
+    return codes

@@ -290,8 +290,7 @@ def test_pack_trellis_matches_reference(E, golden):
     for bits in (1, 2, 3, 4):
         st = g[f"pack_{bits}_states"].astype(np.int32)
         say(f"pack bits={bits}")
-        codes = E.pack_trellis(cuda(st), bits).cpu()
-        codes = codes.view(torch.int32).numpy().view(np.uint32)
+        codes = E.pack_trellis(cuda(st), bits).cpu().numpy().view(np.uint32)
         assert np.array_equal(codes, g[f"pack_{bits}_codes"])
     bad = g["pack_2_states"].astype(np.int32).copy()
     bad[3, 10] ^= 0x100
