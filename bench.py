@@ -114,7 +114,7 @@ def main():
     Wg = torch.from_numpy(W.astype(np.float64)).to(dev)
     Hg = torch.from_numpy(H).to(dev)
     tab64 = torch.from_numpy(np.array(table)).to(dev)
-    tab32 = tab64.to(torch.float32)
+    tab32 = E.half_bits(tab64) if L >= E.BIG_L else tab64.to(torch.float32)
 
     def step(events=None):
         X, S = E.rht_rows(Wg, in_seed, want_rms=True)
@@ -157,7 +157,7 @@ def main():
                    "table": "reference e-means L=12 table" if L == 12 else f"fp16 Gaussian quantiles, 2^{L} entries"},
         "viterbi_rows_per_s": round(rows_per_s, 1),
         "viterbi_row_steps_per_s": round(m * sum(per_block) / (ms * 1e-3), 1),
-        "roofline": {"kernel": "ldlq_trellis_block_kernel", "bound": "valu", "achieved": round(achieved, 3),
+        "roofline": {"kernel": "ldlq_trellis_block_big_kernel" if L >= E.BIG_L else "ldlq_trellis_block_kernel", "bound": "valu", "achieved": round(achieved, 3),
                      "peak": round(VALU_PEAK_TOPS, 1), "unit": "TOP/s", "frac": round(achieved / VALU_PEAK_TOPS, 4),
                      "traffic": None, "launches_per_step": len(per_block),
                      "avg_launch_us": round(1e3 * sum(blk) / len(blk), 2),

@@ -85,6 +85,24 @@ int lamq_ldlq_scalar_block(double* T, int64_t m, int64_t n, int64_t ldT, const d
                            int32_t* idx, int64_t ldi, double* Z, int64_t ldZ, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
+ * The 16-bit-state trellis (13 <= L <= 16, 1 <= k <= 4 with 2^L/1024 >= 2^k): the same two operations as
+ * lamq_viterbi_rows and lamq_ldlq_trellis_block (the same references, the same arithmetic and tie rules)
+ * for tables whose values are exactly representable in fp16, passed as their fp16 bit patterns
+ * (table16, 4-byte aligned; table64 holds the same values in float64 for the settled values).
+ * One 1024-thread workgroup per row. The fused block needs width + look <= 24 and b1 - b0 <= 256; the
+ * standalone search keeps back-pointers of paths longer than 24 steps in the workspace:
+ * lamq_viterbi16_workspace_size(B, T, L, k) bytes.
+ * ---------------------------------------------------------------------------------------------- */
+size_t lamq_viterbi16_workspace_size(int64_t B, int T, int L, int k);
+int lamq_viterbi16_rows(const float* x, int64_t B, int T, int64_t ldx, const uint16_t* table16, int L, int k,
+                        const int32_t* start, int32_t* states, int64_t lds, void* workspace,
+                        size_t workspace_bytes, void* stream);
+int lamq_ldlq_trellis16_block(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU,
+                              const double* S, const double* table64, const uint16_t* table16, int L, int k,
+                              int64_t b0, int64_t b1, int width, int look, int32_t* state, int32_t* states,
+                              int64_t lds, double* Z, int64_t ldZ, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
  * The lazy trailing update T[:, b1:n] -= Z @ U[b0:b1, b1:n] on fp64 MFMA.
  * Replaces opgraph/syntax.py:122-123 (and opgraph/ldlq_gpu.py:48).
  *   Z [m, b1-b0] (row stride ldZ), b1 - b0 <= 256.

@@ -1,0 +1,331 @@
+// Trellis search with 2^13 .. 2^16 states (the 16-bit-state configurations), standalone and fused into the
+// row-trellis LDLQ block.
+//
+// One 1024-thread workgroup per row. Thread t owns the SPT = 2^L/1024 consecutive states [t*SPT, t*SPT+SPT):
+// their float32 path costs stay in VGPRs, their state values in VGPRs as packed fp16 (the kernels take tables
+// whose values are fp16-exact, as the 16-bit configurations' Gaussian-quantile table is; x - C is formed in
+// float32 from the fp16 value, which is exact). A step needs, for each of the thread's predecessor groups
+// r = s >> k, the costs of the states h*2^(L-k) + r owned by other threads; these are exchanged through an LDS
+// window of one quarter of the states (2^(L-2) floats) in four phases, quarter q written by threads
+// [256q, 256q+256). Predecessors are folded in increasing h (quarters are visited in increasing order and
+// h*2^(L-k) + r grows with h), so the strict comparison keeps the lowest h on ties as torch's min does.
+// Back-pointers are one 32-bit word per thread and step (G*k <= 32 bits), in LDS.
+#include "common.h"
+
+#define BIG_NT 1024
+#define BIG_TV 24       // longest fused search: width + look
+#define BIG_LAZY 256
+
+template <int L, int K>
+struct VBig {
+    static constexpr int NS = 1 << L;
+    static constexpr int R = 1 << (L - K);
+    static constexpr int NB = 1 << K;
+    static constexpr int SPT = NS / BIG_NT;
+    static constexpr int G = SPT / NB;  // predecessor groups per thread
+    static constexpr int QS = NS / 4;   // states per exchange quarter
+    static_assert(SPT >= NB && G * K <= 32, "layout");
+    static constexpr int F = G < 4 ? G : 4;  // groups folded per LDS load
+    static_assert(SPT % 2 == 0, "fp16 pairs");
+};
+
+__device__ __forceinline__ float h2f_lo(uint32_t u) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(u & 0xFFFFu)); }
+__device__ __forceinline__ float h2f_hi(uint32_t u) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(u >> 16)); }
+
+// state value i of this thread from the packed registers
+template <int SPT>
+__device__ __forceinline__ float cval(const uint32_t (&Ch)[SPT / 2], int i)
+{
+    return (i & 1) ? h2f_hi(Ch[i >> 1]) : h2f_lo(Ch[i >> 1]);
+}
+
+// Search one path of TV steps; thread 0 writes path[0..TV). xs: TV float32 targets. start < 0: free first state.
+// xbuf: QS floats of LDS. back: (TV-1)*1024 words (LDS or global). red: 32 words of LDS.
+// Between steps a thread keeps only the minimum of each of its predecessor groups (bprev) and the previous
+// target: the path cost of its state g*2^K + b is bprev[g] + (x_prev - C)^2, formed again (with the same three
+// rounded operations, hence bit for bit the same value) when the thread writes it to the exchange window.
+template <int L, int K>
+__device__ void viterbi_big(const float* xs, int TV, uint32_t (&Ch)[VBig<L, K>::SPT / 2], int start, float* xbuf,
+                            uint32_t* back, int* path, float* red)
+{
+    using V = VBig<L, K>;
+    const int tid = threadIdx.x;
+    float bprev[V::G];
+    {
+        const int rs = start >= 0 ? (start & (V::R - 1)) : -1;
+#pragma unroll
+        for (int g = 0; g < V::G; ++g) bprev[g] = (rs >= 0 && tid * V::G + g != rs) ? __builtin_inff() : 0.0f;
+    }
+    float xprev = xs[0];
+    for (int t = 1; t < TV; ++t) {
+        float best[V::G];
+        uint32_t bits = 0;  // the winning h of group g in bits [g*K, g*K+K)
+#pragma unroll
+        for (int g = 0; g < V::G; ++g) best[g] = __builtin_inff();
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if ((tid >> 8) == q) {
+#pragma unroll
+                for (int i = 0; i < V::SPT / 2; ++i) asm volatile("" : "+v"(Ch[i]));
+                float* dst = xbuf + (tid & 255) * V::SPT;  // tid - 256q: one base, small immediates
+#pragma unroll
+                for (int i = 0; i < V::SPT; i += 4) {
+                    float c4[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float d = xprev - cval<V::SPT>(Ch, i + e);
+                        const float dd = d * d;
+                        c4[e] = bprev[(i + e) / V::NB] + dd;
+                    }
+                    *reinterpret_cast<float4*>(dst + i) = make_float4(c4[0], c4[1], c4[2], c4[3]);
+                }
+            }
+            __syncthreads();
+            // the predecessors h*R + r of this thread's groups that lie in quarter q: for K >= 2 the
+            // quarter of h*R + r is h*R/QS whatever r is; for K = 1 it is 2h plus the half of r
+#pragma unroll
+            for (int h = 0; h < V::NB; ++h) {
+                bool here;
+                if constexpr (V::R >= 2 * V::QS)
+                    here = (h * (V::R / V::QS) + ((tid * V::G) / V::QS)) == q;
+                else
+                    here = (h * V::R) / V::QS == q;
+                if (here) {
+                    const float* src = xbuf + ((h * V::R + tid * V::G) & (V::QS - 1));
+#pragma unroll
+                    for (int g0 = 0; g0 < V::G; g0 += V::F) {
+                        float c[V::F];
+                        lds_load<V::F>(src + g0, c);
+#pragma unroll
+                        for (int e = 0; e < V::F; ++e) {
+                            const int g = g0 + e;
+                            const uint32_t mk = (uint32_t)(V::NB - 1) << (g * K);
+                            const uint32_t with_h = (bits & ~mk) | ((uint32_t)h << (g * K));
+                            if (c[e] < best[g]) { best[g] = c[e]; bits = with_h; }
+                        }
+                    }
+                }
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int g = 0; g < V::G; ++g) bprev[g] = best[g];
+        back[(t - 1) * BIG_NT + tid] = bits;
+        xprev = xs[t];
+    }
+    // final argmin, lowest state on ties
+    float bv = __builtin_inff();
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < V::SPT / 2; ++i) asm volatile("" : "+v"(Ch[i]));
+#pragma unroll
+    for (int i = 0; i < V::SPT; ++i) {
+        const float d = xprev - cval<V::SPT>(Ch, i);
+        const float dd = d * d;
+        const float c = bprev[i / V::NB] + dd;
+        if (i == 0 || c < bv) { bv = c; bi = tid * V::SPT + i; }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        if (ov < bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    int* redi = reinterpret_cast<int*>(red + 16);
+    if ((tid & 63) == 0) { red[tid >> 6] = bv; redi[tid >> 6] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+        float v = red[0];
+        int s = redi[0];
+        for (int w = 1; w < BIG_NT / 64; ++w)
+            if (red[w] < v || (red[w] == v && redi[w] < s)) { v = red[w]; s = redi[w]; }
+        path[TV - 1] = s;
+        for (int t = TV - 1; t > 0; --t) {
+            const int r = s >> K;
+            const int owner = r / V::G;
+            const int g = r - owner * V::G;
+            const int h = (int)((back[(t - 1) * BIG_NT + owner] >> (g * K)) & (uint32_t)(V::NB - 1));
+            s = r + h * V::R;
+            path[t - 1] = s;
+        }
+    }
+    __syncthreads();
+}
+
+template <int L, int K>
+__device__ __forceinline__ void load_half_table(const uint16_t* __restrict__ table16, uint32_t (&Ch)[VBig<L, K>::SPT / 2])
+{
+    using V = VBig<L, K>;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(table16 + threadIdx.x * V::SPT);
+#pragma unroll
+    for (int i = 0; i < V::SPT / 2; ++i) Ch[i] = src[i];
+}
+
+// ------------------------------------------------------------------------------------------------ standalone
+template <int L, int K, bool BACK_GLOBAL>
+__global__ __launch_bounds__(BIG_NT) void viterbi_rows_big_kernel(const float* __restrict__ x, int T, int64_t ldx,
+                                                                  const uint16_t* __restrict__ table16,
+                                                                  const int32_t* __restrict__ start,
+                                                                  int32_t* __restrict__ states, int64_t lds,
+                                                                  uint32_t* __restrict__ back_ws)
+{
+    using V = VBig<L, K>;
+    __shared__ __align__(16) float xbuf[V::QS];
+    __shared__ uint32_t back_lds[BACK_GLOBAL ? 1 : (BIG_TV - 1) * BIG_NT];
+    __shared__ float red[32];
+    const int64_t row = blockIdx.x;
+    uint32_t Ch[V::SPT / 2];
+    load_half_table<L, K>(table16, Ch);
+    uint32_t* back = BACK_GLOBAL ? back_ws + row * (int64_t)(T - 1) * BIG_NT : back_lds;
+    viterbi_big<L, K>(x + row * ldx, T, Ch, start ? start[row] : -1, xbuf, back, states + row * lds, red);
+}
+
+template <int L, int K>
+struct ViterbiRowsBig {
+    static int run(const float* x, int64_t B, int T, int64_t ldx, const uint16_t* table16, const int32_t* start,
+                   int32_t* states, int64_t lds, void* ws, size_t ws_bytes, hipStream_t s)
+    {
+        if (T <= BIG_TV) {
+            hipLaunchKernelGGL((viterbi_rows_big_kernel<L, K, false>), dim3((unsigned)B), dim3(BIG_NT), 0, s, x, T, ldx,
+                               table16, start, states, lds, (uint32_t*)nullptr);
+        } else {
+            const size_t need = (size_t)B * (size_t)(T - 1) * BIG_NT * sizeof(uint32_t);
+            if (!ws || ws_bytes < need) return LAMQ_EINVAL;
+            hipLaunchKernelGGL((viterbi_rows_big_kernel<L, K, true>), dim3((unsigned)B), dim3(BIG_NT), 0, s, x, T, ldx,
+                               table16, start, states, lds, (uint32_t*)ws);
+        }
+        LAMQ_LAUNCH_CHECK();
+        return LAMQ_OK;
+    }
+};
+
+template <template <int, int> class F, typename... Args>
+static int dispatch_big(int L, int K, Args&&... args)
+{
+#define BIG_CASE(l, k) \
+    if (L == l && K == k) return F<l, k>::run(args...);
+    BIG_CASE(16, 1) BIG_CASE(16, 2) BIG_CASE(16, 3) BIG_CASE(16, 4)
+    BIG_CASE(15, 1) BIG_CASE(15, 2) BIG_CASE(15, 3) BIG_CASE(15, 4)
+    BIG_CASE(14, 1) BIG_CASE(14, 2) BIG_CASE(14, 3) BIG_CASE(14, 4)
+    BIG_CASE(13, 1) BIG_CASE(13, 2) BIG_CASE(13, 3)
+#undef BIG_CASE
+    return LAMQ_EUNSUP;
+}
+
+extern "C" size_t lamq_viterbi16_workspace_size(int64_t B, int T, int L, int k)
+{
+    (void)L;
+    (void)k;
+    if (B < 0 || T <= BIG_TV) return 0;
+    return (size_t)B * (size_t)(T - 1) * BIG_NT * sizeof(uint32_t);
+}
+
+extern "C" int lamq_viterbi16_rows(const float* x, int64_t B, int T, int64_t ldx, const uint16_t* table16, int L, int k,
+                                   const int32_t* start, int32_t* states, int64_t lds, void* workspace,
+                                   size_t workspace_bytes, void* stream)
+{
+    if (!x || !table16 || !states || B < 0 || T < 1 || ldx < T || lds < T) return LAMQ_EINVAL;
+    if (((uintptr_t)table16 % 4) != 0) return LAMQ_EINVAL;
+    if (B == 0) return LAMQ_OK;
+    if (B > 0x7fffffff) return LAMQ_EUNSUP;
+    return dispatch_big<ViterbiRowsBig>(L, k, x, B, T, ldx, table16, start, states, lds, workspace, workspace_bytes,
+                                        as_stream(stream));
+}
+
+// ------------------------------------------------------------------------------------------------ fused block
+// The same per-step arithmetic as ldlq_trellis_block_kernel (viterbi.hip), with the 16-bit-state search.
+template <int L, int K>
+__global__ __launch_bounds__(BIG_NT) void ldlq_trellis_block_big_kernel(
+    const double* __restrict__ T, int64_t n, int64_t ldT, const double* __restrict__ U, int64_t ldU,
+    const double* __restrict__ S, const double* __restrict__ table64, const uint16_t* __restrict__ table16,
+    int64_t b0, int64_t b1, int width, int look, int32_t* __restrict__ state, int32_t* __restrict__ states,
+    int64_t lds, double* __restrict__ Z, int64_t ldZ)
+{
+    using V = VBig<L, K>;
+    __shared__ __align__(16) float xbuf[V::QS];
+    __shared__ uint32_t back[(BIG_TV - 1) * BIG_NT];
+    __shared__ double trow[BIG_LAZY + BIG_TV];
+    __shared__ float xs[BIG_TV];
+    __shared__ int path[BIG_TV];
+    __shared__ double es[BIG_TV];
+    __shared__ double zs[BIG_TV];
+    __shared__ float red[32];
+
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x;
+    uint32_t Ch[V::SPT / 2];
+    load_half_table<L, K>(table16, Ch);
+    const int64_t cend = (b1 + look < n) ? b1 + look : n;
+    const double* Tr = T + row * ldT;
+    for (int64_t c = tid; c < cend - b0; c += BIG_NT) trow[c] = Tr[b0 + c];
+    const double Sr = S[row];
+    int st = state[row];
+    __syncthreads();
+
+    for (int64_t j = b0; j < b1; j += width) {
+        const int w = (int)((j + width <= b1) ? width : (b1 - j));
+        const int64_t ahead = n - (j + w);
+        const int a = (int)(ahead < look ? ahead : look);
+        const int TV = w + a;
+        const int jo = (int)(j - b0);
+        if (tid < TV) xs[tid] = (float)(trow[jo + tid] / Sr);
+        __syncthreads();
+        viterbi_big<L, K>(xs, TV, Ch, st, xbuf, back, path, red);
+        if (tid < w) {
+            const int p = path[tid];
+            states[row * lds + j + tid] = p;
+            const double qs = table64[p] * Sr;
+            es[tid] = trow[jo + tid] - qs;
+        }
+        __syncthreads();
+        if (tid < 64) {
+            double acc = tid < w ? es[tid] : 0.0;
+            for (int l = 0; l < w; ++l) {
+                double zl = 0.0;
+                if (tid == l) zl = acc / U[(j + l) * ldU + j + l];
+                zl = __shfl(zl, l);
+                if (tid > l && tid < w) acc = fma(-zl, U[(j + l) * ldU + j + tid], acc);
+                if (tid == l) zs[l] = zl;
+            }
+        }
+        __syncthreads();
+        for (int64_t col = j + w + tid; col < b1; col += BIG_NT) {
+            double acc = 0.0;
+            for (int l = 0; l < w; ++l) acc = fma(zs[l], U[(j + l) * ldU + col], acc);
+            trow[col - b0] = trow[col - b0] - acc;
+        }
+        if (tid < w) Z[row * ldZ + jo + tid] = zs[tid];
+        st = path[w - 1];
+        __syncthreads();
+    }
+    if (tid == 0) state[row] = st;
+}
+
+template <int L, int K>
+struct TrellisBlockBig {
+    static int run(const double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU, const double* S,
+                   const double* table64, const uint16_t* table16, int64_t b0, int64_t b1, int width, int look,
+                   int32_t* state, int32_t* states, int64_t lds, double* Z, int64_t ldZ, hipStream_t s)
+    {
+        hipLaunchKernelGGL((ldlq_trellis_block_big_kernel<L, K>), dim3((unsigned)m), dim3(BIG_NT), 0, s, T, n, ldT, U, ldU,
+                           S, table64, table16, b0, b1, width, look, state, states, lds, Z, ldZ);
+        LAMQ_LAUNCH_CHECK();
+        return LAMQ_OK;
+    }
+};
+
+extern "C" int lamq_ldlq_trellis16_block(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU,
+                                         const double* S, const double* table64, const uint16_t* table16, int L, int k,
+                                         int64_t b0, int64_t b1, int width, int look, int32_t* state, int32_t* states,
+                                         int64_t lds, double* Z, int64_t ldZ, void* stream)
+{
+    if (!T || !U || !S || !table64 || !table16 || !state || !states || !Z) return LAMQ_EINVAL;
+    if (((uintptr_t)table16 % 4) != 0) return LAMQ_EINVAL;
+    if (m < 0 || n < 1 || ldT < n || ldU < n || lds < n || b0 < 0 || b1 <= b0 || b1 > n || width < 1 || look < 0)
+        return LAMQ_EINVAL;
+    if (ldZ < b1 - b0) return LAMQ_EINVAL;
+    if (width + look > BIG_TV || b1 - b0 > BIG_LAZY || m > 0x7fffffff) return LAMQ_EUNSUP;
+    if (m == 0) return LAMQ_OK;
+    return dispatch_big<TrellisBlockBig>(L, k, T, m, n, ldT, U, ldU, S, table64, table16, b0, b1, width, look, state,
+                                         states, lds, Z, ldZ, as_stream(stream));
+}

@@ -20,7 +20,20 @@ class LinAlgError(torch.linalg.LinAlgError if hasattr(torch.linalg, "LinAlgError
 # ----------------------------------------------------------------------------- Viterbi (codes.py:151-181)
 
 
-def viterbi_rows(x: torch.Tensor, C: torch.Tensor, L: int, k: int, start: torch.Tensor | None = None) -> torch.Tensor:
+BIG_L = 13  # tables of 2^13 states and more go to the 1024-thread kernels (fp16-exact tables)
+
+
+def half_bits(C: torch.Tensor) -> torch.Tensor:
+    """The fp16 bit patterns (int16 tensor) of a table whose values fp16 represents exactly; raises otherwise."""
+    c32 = C.to(torch.float32)
+    h = c32.to(torch.float16)
+    if not torch.equal(h.to(torch.float32), c32):
+        raise NotImplementedError("the 2^13..2^16-state kernels take tables whose values are exact in fp16")
+    return h.view(torch.int16).contiguous()
+
+
+def viterbi_rows(x: torch.Tensor, C: torch.Tensor, L: int, k: int, start: torch.Tensor | None = None,
+                 C16: torch.Tensor | None = None) -> torch.Tensor:
     """x [B, T] float32, C [2^L] float32, start None or [B] int32 -> states [B, T] int32."""
     need(x, torch.float32, "x", 2)
     need(C, torch.float32, "C", 1)
@@ -33,6 +46,13 @@ def viterbi_rows(x: torch.Tensor, C: torch.Tensor, L: int, k: int, start: torch.
         st = start.to(device=x.device, dtype=torch.int32).contiguous()
         if st.numel() != B:
             raise ValueError("one start state per row")
+    if L >= BIG_L:
+        h = half_bits(C) if C16 is None else C16
+        nbytes = lib().lamq_viterbi16_workspace_size(B, T, L, k)
+        ws = workspace(nbytes, x.device)
+        check(lib().lamq_viterbi16_rows(ptr(x), B, T, ld(x), ptr(h), L, k, ptr(st), ptr(out), T, ptr(ws), nbytes,
+                                        stream(x.device)), "viterbi16")
+        return out
     nbytes = lib().lamq_viterbi_workspace_size(B, T, L, k)
     ws = workspace(nbytes, x.device)
     check(lib().lamq_viterbi_rows(ptr(x), B, T, ld(x), ptr(C), L, k, ptr(st), ptr(out), T, ptr(ws), nbytes,
@@ -140,15 +160,20 @@ def ldlq_trellis(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, table64: tor
     if dead is not None:
         dd = dead.to(device=dev, dtype=torch.uint8).contiguous()
         check(lib().lamq_zero_columns(ptr(T), m, n, n, ptr(dd), s), "zero_columns")
-    t32 = table64.to(torch.float32) if table32 is None else table32
+    if L >= BIG_L:
+        t32 = half_bits(table64) if table32 is None or table32.dtype != torch.int16 else table32
+        block = lib().lamq_ldlq_trellis16_block
+    else:
+        t32 = table64.to(torch.float32) if table32 is None else table32
+        block = lib().lamq_ldlq_trellis_block
     state = torch.zeros(m, dtype=torch.int32, device=dev)
     states = torch.empty(m, n, dtype=torch.int32, device=dev)
     Z = torch.empty(m, lazy, dtype=torch.float64, device=dev)
     for b0 in range(0, n, lazy):
         b1 = min(b0 + lazy, n)
         ev = _event_pair(events, "block")
-        check(lib().lamq_ldlq_trellis_block(ptr(T), m, n, n, ptr(U), ld(U), ptr(S), ptr(table64), ptr(t32), L, k, b0, b1,
-                                            width, look, ptr(state), ptr(states), n, ptr(Z), lazy, s), "ldlq_trellis_block")
+        check(block(ptr(T), m, n, n, ptr(U), ld(U), ptr(S), ptr(table64), ptr(t32), L, k, b0, b1, width, look, ptr(state),
+                    ptr(states), n, ptr(Z), lazy, s), "ldlq_trellis_block")
         _event_end(ev)
         if b1 < n:
             ev = _event_pair(events, "trailing")

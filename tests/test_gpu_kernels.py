@@ -61,6 +61,40 @@ def test_viterbi_ties_match_reference(E, golden, L, k):
     assert np.array_equal(E.viterbi_rows(x, C, L, k, start=st).cpu().numpy(), g[p + "fixed"])
 
 
+def test_viterbi_L16_matches_reference(E, golden):
+    g = golden("viterbi")
+    x = cuda(g["L16_k2_x"].astype(np.float32))
+    C = cuda(g["L16_k2_table"].astype(np.float32))
+    say("viterbi L=16 k=2 (fp16 quantile table, with duplicate values)")
+    got = E.viterbi_rows(x, C, 16, 2, start=cuda(g["L16_k2_start"], torch.int32)).cpu().numpy()
+    assert np.array_equal(got, g["L16_k2_fixed"])
+
+
+@pytest.mark.parametrize("L,k", [(16, 1), (16, 3), (16, 4), (14, 2), (13, 3)])
+def test_viterbi_big_tables_match_oracle(E, L, k):
+    from lookatmyquant_amd.tables import quantile_table
+
+    tab = quantile_table(L, 0)
+    rng = np.random.default_rng(L * 10 + k)
+    x = rng.standard_normal((5, 24)).astype(np.float32)
+    st = rng.integers(0, 1 << L, 5)
+    say(f"viterbi L={L} k={k}")
+    got = E.viterbi_rows(cuda(x), cuda(tab.astype(np.float32)), L, k, start=cuda(st, torch.int32)).cpu().numpy()
+    assert np.array_equal(got, O.viterbi(x, tab, L, k, start=st))
+    free = E.viterbi_rows(cuda(x[:2]), cuda(tab.astype(np.float32)), L, k).cpu().numpy()
+    assert np.array_equal(free, O.viterbi(x[:2], tab, L, k))
+
+
+def test_viterbi_L16_long_paths_use_workspace(E):
+    from lookatmyquant_amd.tables import quantile_table
+
+    tab = quantile_table(16, 0)
+    x = np.random.default_rng(4).standard_normal((2, 40)).astype(np.float32)
+    say("viterbi L=16 k=2 T=40")
+    got = E.viterbi_rows(cuda(x), cuda(tab.astype(np.float32)), 16, 2).cpu().numpy()
+    assert np.array_equal(got, O.viterbi(x, tab, 16, 2))
+
+
 def test_viterbi_long_paths_use_workspace(E, tables):
     rng = np.random.default_rng(3)
     x = rng.standard_normal((6, 200)).astype(np.float32)
@@ -177,6 +211,20 @@ def test_ldlq_trellis_other_widths_match_reference(E, golden, tables, config12, 
     X, S, U, dead = _rotated(W[:128], H, 201)
     say(f"ldlq trellis L=12 k={k} (128 rows)")
     st = E.ldlq_trellis(cuda(X), cuda(S), cuda(U), cuda(tables[k]), 12, k).cpu().numpy()
+    assert np.array_equal(st, g["states"])
+
+
+def test_ldlq_trellis_L16_matches_reference(E, golden, config12):
+    """The 16-bit-state configuration (fp16 quantile table with repeated values): states of the first 32 rows of
+    config 2 equal the states the reference's sweep records."""
+    W, H = config12
+    g = golden("ldlq_trellis_L16_k2_rows32")
+    tab = golden("viterbi")["L16_k2_table"]
+    X, S, U, dead = _rotated(W[:32], H, 201)
+    say("ldlq trellis L=16 k=2 (32 rows)")
+    st = E.ldlq_trellis(cuda(X), cuda(S), cuda(U), cuda(tab), 16, 2).cpu().numpy()
+    agree = (st == g["states"]).mean()
+    say(f"  state agreement with the reference {agree:.6f}")
     assert np.array_equal(st, g["states"])
 
 
