@@ -85,7 +85,7 @@ int lamq_ldlq_scalar_block(double* T, int64_t m, int64_t n, int64_t ldT, const d
                            int32_t* idx, int64_t ldi, double* Z, int64_t ldZ, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
- * The 16-bit-state trellis (13 <= L <= 16, 1 <= k <= 4 with 2^L/1024 >= 2^k): the same two operations as
+ * The 16-bit-state trellis (13 <= L <= 16, 1 <= k <= min(4, L-12)): the same two operations as
  * lamq_viterbi_rows and lamq_ldlq_trellis_block (the same references, the same arithmetic and tie rules)
  * for tables whose values are exactly representable in fp16, passed as their fp16 bit patterns
  * (table16, 4-byte aligned; table64 holds the same values in float64 for the settled values).

@@ -37,6 +37,43 @@ struct Vit {
     static_assert(G * K <= 8, "one back-pointer byte per thread and step");
 };
 
+// LDS float index -> bank-spread index: the 16-byte chunk index (x >> 2) has its low two bits xor'ed with bits
+// 4-5 of itself, a bijection within every 64 floats. Writes of consecutive threads at a stride of 16 floats then
+// fall on 16 different 16-byte bank groups, and reads of consecutive 16-byte chunks stay conflict-free.
+__device__ __forceinline__ int swz(int x) { return x ^ (((x >> 6) & 3) << 2); }
+
+// N floats at logical index x (x a multiple of min(N, 4)), chunk by chunk through swz.
+template <int N>
+__device__ __forceinline__ void lds_load_swz(const float* __restrict__ base, int x, float (&dst)[N])
+{
+    if constexpr (N >= 4) {
+#pragma unroll
+        for (int i = 0; i < N; i += 4) {
+            float4 v = *reinterpret_cast<const float4*>(base + swz(x + i));
+            dst[i] = v.x; dst[i + 1] = v.y; dst[i + 2] = v.z; dst[i + 3] = v.w;
+        }
+    } else if constexpr (N == 2) {
+        float2 v = *reinterpret_cast<const float2*>(base + swz(x));
+        dst[0] = v.x; dst[1] = v.y;
+    } else {
+        dst[0] = base[swz(x)];
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void lds_store_swz(float* __restrict__ base, int x, const float (&src)[N])
+{
+    if constexpr (N >= 4) {
+#pragma unroll
+        for (int i = 0; i < N; i += 4)
+            *reinterpret_cast<float4*>(base + swz(x + i)) = make_float4(src[i], src[i + 1], src[i + 2], src[i + 3]);
+    } else if constexpr (N == 2) {
+        *reinterpret_cast<float2*>(base + swz(x)) = make_float2(src[0], src[1]);
+    } else {
+        base[swz(x)] = src[0];
+    }
+}
+
 template <int N>
 __device__ __forceinline__ void lds_load(const float* __restrict__ src, float (&dst)[N])
 {
@@ -75,7 +112,7 @@ __device__ __forceinline__ void lds_store(float* __restrict__ dst, const float (
 
 // Search one path of TV steps. xs: TV float32 targets (any address space); Cr: this thread's state
 // values; start < 0 leaves the first state free, else only states (start << K | b) & (2^L-1) may
-// begin (opgraph/codes.py:164-167). cost0/cost1: 2*2^L floats of LDS. back: TV*ACT bytes (LDS or
+// begin (opgraph/codes.py:164-167). cost0/cost1: 2*2^L floats of LDS, indexed through swz. back: TV*ACT bytes (LDS or
 // global). path: TV ints written by thread 0. red: 8 words of LDS. Every thread of the workgroup
 // must call this; it ends with a barrier after which path[] is complete.
 //   forward step  (codes.py:170-172): best(r) = min_h cost[h*R + r] (lowest h on ties),
@@ -100,7 +137,7 @@ __device__ void viterbi_wg(const float* xs, int TV, const float (&Cr)[Vit<L, K>:
             c[i] = d * d;
             if (rs >= 0 && ((tid * V::SPT + i) >> K) != rs) c[i] = __builtin_inff();
         }
-        lds_store<V::SPT>(cost0 + tid * V::SPT, c);
+        lds_store_swz<V::SPT>(cost0, tid * V::SPT, c);
     }
     __syncthreads();
     float* cur = cost0;
@@ -110,13 +147,13 @@ __device__ void viterbi_wg(const float* xs, int TV, const float (&Cr)[Vit<L, K>:
             const float xt = xs[t];
             float best[V::G];
             int arg[V::G];
-            lds_load<V::G>(cur + tid * V::G, best);
+            lds_load_swz<V::G>(cur, tid * V::G, best);
 #pragma unroll
             for (int g = 0; g < V::G; ++g) arg[g] = 0;
 #pragma unroll
             for (int h = 1; h < V::NB; ++h) {
                 float c[V::G];
-                lds_load<V::G>(cur + h * V::R + tid * V::G, c);
+                lds_load_swz<V::G>(cur, h * V::R + tid * V::G, c);
 #pragma unroll
                 for (int g = 0; g < V::G; ++g)
                     if (c[g] < best[g]) { best[g] = c[g]; arg[g] = h; }
@@ -133,7 +170,7 @@ __device__ void viterbi_wg(const float* xs, int TV, const float (&Cr)[Vit<L, K>:
                     o[g * V::NB + b] = best[g] + dd;
                 }
             }
-            lds_store<V::SPT>(nxt + tid * V::SPT, o);
+            lds_store_swz<V::SPT>(nxt, tid * V::SPT, o);
             back[t * V::ACT + tid] = (uint8_t)bits;
         }
         __syncthreads();
@@ -146,7 +183,7 @@ __device__ void viterbi_wg(const float* xs, int TV, const float (&Cr)[Vit<L, K>:
     int bi = 0x7fffffff;
     if (act) {
         float c[V::SPT];
-        lds_load<V::SPT>(cur + tid * V::SPT, c);
+        lds_load_swz<V::SPT>(cur, tid * V::SPT, c);
         bv = c[0];
         bi = tid * V::SPT;
 #pragma unroll

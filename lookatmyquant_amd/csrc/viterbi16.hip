@@ -1,15 +1,19 @@
 // Trellis search with 2^13 .. 2^16 states (the 16-bit-state configurations), standalone and fused into the
 // row-trellis LDLQ block.
 //
-// One 1024-thread workgroup per row. Thread t owns the SPT = 2^L/1024 consecutive states [t*SPT, t*SPT+SPT):
-// their float32 path costs stay in VGPRs, their state values in VGPRs as packed fp16 (the kernels take tables
-// whose values are fp16-exact, as the 16-bit configurations' Gaussian-quantile table is; x - C is formed in
-// float32 from the fp16 value, which is exact). A step needs, for each of the thread's predecessor groups
-// r = s >> k, the costs of the states h*2^(L-k) + r owned by other threads; these are exchanged through an LDS
-// window of one quarter of the states (2^(L-2) floats) in four phases, quarter q written by threads
-// [256q, 256q+256). Predecessors are folded in increasing h (quarters are visited in increasing order and
-// h*2^(L-k) + r grows with h), so the strict comparison keeps the lowest h on ties as torch's min does.
-// Back-pointers are one 32-bit word per thread and step (G*k <= 32 bits), in LDS.
+// One 1024-thread workgroup per row. The states are cut into four quarters of QS = 2^(L-2); thread t owns the
+// SQ = 2^L/4096 consecutive states [q*QS + SQ*t, q*QS + SQ*t + SQ) of every quarter q. Those are exactly the
+// successors of its predecessor groups r = q*QS/2^k + SQ*t/2^k + g (g < SQ/2^k), so a thread needs, per step,
+// the path costs of the states h*2^(L-k) + r of its groups, which other threads own. They are exchanged
+// through an LDS window of one quarter: in phase p every thread writes its own states of quarter p and then
+// folds those of its predecessors that lie in quarter p, so all 16 waves work in every phase. Predecessors
+// reach a group in increasing h (a quarter index never decreases with h, and within a phase h is visited in
+// increasing order), so the strict comparison keeps the lowest h on ties, as torch's min does.
+// A thread keeps its state values as packed fp16 in VGPRs (the kernels take tables whose values fp16 holds
+// exactly, as the 16-bit configurations' Gaussian-quantile table; x - C is then exact in float32) and, between
+// steps, only the minimum of each of its groups: the path cost of its state (g, b) is bprev[g] +
+// (x_prev - C)^2, formed again when written to the window with the same three rounded operations, hence the
+// same float32 value. Back-pointers are one 32-bit word per thread and step (G*k <= 32 bits), in LDS.
 #include "common.h"
 
 #define BIG_NT 1024
@@ -21,12 +25,16 @@ struct VBig {
     static constexpr int NS = 1 << L;
     static constexpr int R = 1 << (L - K);
     static constexpr int NB = 1 << K;
-    static constexpr int SPT = NS / BIG_NT;
-    static constexpr int G = SPT / NB;  // predecessor groups per thread
-    static constexpr int QS = NS / 4;   // states per exchange quarter
-    static_assert(SPT >= NB && G * K <= 32, "layout");
-    static constexpr int F = G < 4 ? G : 4;  // groups folded per LDS load
-    static_assert(SPT % 2 == 0, "fp16 pairs");
+    static constexpr int SPT = NS / BIG_NT;  // states per thread
+    static constexpr int SQ = SPT / 4;       // states per thread and quarter
+    static constexpr int QS = NS / 4;        // states per quarter (the exchange window)
+    static constexpr int GQ = SQ / NB;       // predecessor groups per thread and quarter
+    static constexpr int G = 4 * GQ;         // predecessor groups per thread
+    static constexpr int RQ = QS / NB;       // group indices per quarter of states
+    static_assert(SQ >= NB && SQ >= 2 && G * K <= 32, "layout");
+    // quarter of the predecessors h*R + r of the groups of quarter q (independent of the thread, see above)
+    static constexpr int quarter(int h, int q) { return (h * R + q * RQ) / QS; }
+    static constexpr int offset(int h, int q) { return (h * R + q * RQ) % QS; }
 };
 
 __device__ __forceinline__ float h2f_lo(uint32_t u) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(u & 0xFFFFu)); }
@@ -40,91 +48,79 @@ __device__ __forceinline__ float cval(const uint32_t (&Ch)[SPT / 2], int i)
 }
 
 // Search one path of TV steps; thread 0 writes path[0..TV). xs: TV float32 targets. start < 0: free first state.
-// xbuf: QS floats of LDS. back: (TV-1)*1024 words (LDS or global). red: 32 words of LDS.
-// Between steps a thread keeps only the minimum of each of its predecessor groups (bprev) and the previous
-// target: the path cost of its state g*2^K + b is bprev[g] + (x_prev - C)^2, formed again (with the same three
-// rounded operations, hence bit for bit the same value) when the thread writes it to the exchange window.
+// xbuf: QS floats of LDS (indexed through swz). back: (TV-1)*1024 words (LDS or global). red: 32 words of LDS.
 template <int L, int K>
 __device__ void viterbi_big(const float* xs, int TV, uint32_t (&Ch)[VBig<L, K>::SPT / 2], int start, float* xbuf,
                             uint32_t* back, int* path, float* red)
 {
     using V = VBig<L, K>;
     const int tid = threadIdx.x;
-    float bprev[V::G];
+    float bprev[V::G];  // index q*GQ + g
     {
         const int rs = start >= 0 ? (start & (V::R - 1)) : -1;
 #pragma unroll
-        for (int g = 0; g < V::G; ++g) bprev[g] = (rs >= 0 && tid * V::G + g != rs) ? __builtin_inff() : 0.0f;
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int g = 0; g < V::GQ; ++g)
+                bprev[q * V::GQ + g] = (rs >= 0 && q * V::RQ + V::GQ * tid + g != rs) ? __builtin_inff() : 0.0f;
     }
     float xprev = xs[0];
     for (int t = 1; t < TV; ++t) {
         float best[V::G];
-        uint32_t bits = 0;  // the winning h of group g in bits [g*K, g*K+K)
+        uint32_t bits = 0;  // the winning h of group j = q*GQ + g in bits [j*K, j*K+K)
 #pragma unroll
-        for (int g = 0; g < V::G; ++g) best[g] = __builtin_inff();
+        for (int j = 0; j < V::G; ++j) best[j] = __builtin_inff();
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            if ((tid >> 8) == q) {
+        for (int p = 0; p < 4; ++p) {
 #pragma unroll
-                for (int i = 0; i < V::SPT / 2; ++i) asm volatile("" : "+v"(Ch[i]));
-                float* dst = xbuf + (tid & 255) * V::SPT;  // tid - 256q: one base, small immediates
+            for (int i = 0; i < V::SPT / 2; ++i) asm volatile("" : "+v"(Ch[i]));
+            {
+                float c[V::SQ];
 #pragma unroll
-                for (int i = 0; i < V::SPT; i += 4) {
-                    float c4[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float d = xprev - cval<V::SPT>(Ch, i + e);
-                        const float dd = d * d;
-                        c4[e] = bprev[(i + e) / V::NB] + dd;
-                    }
-                    *reinterpret_cast<float4*>(dst + i) = make_float4(c4[0], c4[1], c4[2], c4[3]);
+                for (int i = 0; i < V::SQ; ++i) {
+                    const float d = xprev - cval<V::SPT>(Ch, p * V::SQ + i);
+                    const float dd = d * d;
+                    c[i] = bprev[p * V::GQ + i / V::NB] + dd;
                 }
+                lds_store_swz<V::SQ>(xbuf, V::SQ * tid, c);
             }
             __syncthreads();
-            // the predecessors h*R + r of this thread's groups that lie in quarter q: for K >= 2 the
-            // quarter of h*R + r is h*R/QS whatever r is; for K = 1 it is 2h plus the half of r
 #pragma unroll
-            for (int h = 0; h < V::NB; ++h) {
-                bool here;
-                if constexpr (V::R >= 2 * V::QS)
-                    here = (h * (V::R / V::QS) + ((tid * V::G) / V::QS)) == q;
-                else
-                    here = (h * V::R) / V::QS == q;
-                if (here) {
-                    const float* src = xbuf + ((h * V::R + tid * V::G) & (V::QS - 1));
+            for (int q = 0; q < 4; ++q)
 #pragma unroll
-                    for (int g0 = 0; g0 < V::G; g0 += V::F) {
-                        float c[V::F];
-                        lds_load<V::F>(src + g0, c);
+                for (int h = 0; h < V::NB; ++h) {
+                    if (V::quarter(h, q) != p) continue;
+                    float c[V::GQ];
+                    lds_load_swz<V::GQ>(xbuf, V::offset(h, q) + V::GQ * tid, c);
 #pragma unroll
-                        for (int e = 0; e < V::F; ++e) {
-                            const int g = g0 + e;
-                            const uint32_t mk = (uint32_t)(V::NB - 1) << (g * K);
-                            const uint32_t with_h = (bits & ~mk) | ((uint32_t)h << (g * K));
-                            if (c[e] < best[g]) { best[g] = c[e]; bits = with_h; }
-                        }
+                    for (int g = 0; g < V::GQ; ++g) {
+                        const int j = q * V::GQ + g;
+                        const uint32_t mk = (uint32_t)(V::NB - 1) << (j * K);
+                        const uint32_t with_h = (bits & ~mk) | ((uint32_t)h << (j * K));
+                        if (c[g] < best[j]) { best[j] = c[g]; bits = with_h; }
                     }
                 }
-            }
             __syncthreads();
         }
 #pragma unroll
-        for (int g = 0; g < V::G; ++g) bprev[g] = best[g];
+        for (int j = 0; j < V::G; ++j) bprev[j] = best[j];
         back[(t - 1) * BIG_NT + tid] = bits;
         xprev = xs[t];
     }
-    // final argmin, lowest state on ties
+    // final argmin, lowest state on ties (a thread's states increase with (q, i))
     float bv = __builtin_inff();
     int bi = 0x7fffffff;
 #pragma unroll
     for (int i = 0; i < V::SPT / 2; ++i) asm volatile("" : "+v"(Ch[i]));
 #pragma unroll
-    for (int i = 0; i < V::SPT; ++i) {
-        const float d = xprev - cval<V::SPT>(Ch, i);
-        const float dd = d * d;
-        const float c = bprev[i / V::NB] + dd;
-        if (i == 0 || c < bv) { bv = c; bi = tid * V::SPT + i; }
-    }
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int i = 0; i < V::SQ; ++i) {
+            const float d = xprev - cval<V::SPT>(Ch, q * V::SQ + i);
+            const float dd = d * d;
+            const float c = bprev[q * V::GQ + i / V::NB] + dd;
+            if ((q == 0 && i == 0) || c < bv) { bv = c; bi = q * V::QS + V::SQ * tid + i; }
+        }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         const float ov = __shfl_xor(bv, off);
@@ -142,9 +138,10 @@ __device__ void viterbi_big(const float* xs, int TV, uint32_t (&Ch)[VBig<L, K>::
         path[TV - 1] = s;
         for (int t = TV - 1; t > 0; --t) {
             const int r = s >> K;
-            const int owner = r / V::G;
-            const int g = r - owner * V::G;
-            const int h = (int)((back[(t - 1) * BIG_NT + owner] >> (g * K)) & (uint32_t)(V::NB - 1));
+            const int q = r / V::RQ, rem = r - q * V::RQ;
+            const int owner = rem / V::GQ, g = rem - owner * V::GQ;
+            const int j = q * V::GQ + g;
+            const int h = (int)((back[(t - 1) * BIG_NT + owner] >> (j * K)) & (uint32_t)(V::NB - 1));
             s = r + h * V::R;
             path[t - 1] = s;
         }
@@ -152,13 +149,17 @@ __device__ void viterbi_big(const float* xs, int TV, uint32_t (&Ch)[VBig<L, K>::
     __syncthreads();
 }
 
+// this thread's state values: quarter q, states q*QS + SQ*t + i, packed two per register in (q, i) order
 template <int L, int K>
 __device__ __forceinline__ void load_half_table(const uint16_t* __restrict__ table16, uint32_t (&Ch)[VBig<L, K>::SPT / 2])
 {
     using V = VBig<L, K>;
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(table16 + threadIdx.x * V::SPT);
 #pragma unroll
-    for (int i = 0; i < V::SPT / 2; ++i) Ch[i] = src[i];
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(table16 + q * V::QS + V::SQ * threadIdx.x);
+#pragma unroll
+        for (int i = 0; i < V::SQ / 2; ++i) Ch[q * V::SQ / 2 + i] = src[i];
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ standalone
@@ -205,9 +206,9 @@ static int dispatch_big(int L, int K, Args&&... args)
 #define BIG_CASE(l, k) \
     if (L == l && K == k) return F<l, k>::run(args...);
     BIG_CASE(16, 1) BIG_CASE(16, 2) BIG_CASE(16, 3) BIG_CASE(16, 4)
-    BIG_CASE(15, 1) BIG_CASE(15, 2) BIG_CASE(15, 3) BIG_CASE(15, 4)
-    BIG_CASE(14, 1) BIG_CASE(14, 2) BIG_CASE(14, 3) BIG_CASE(14, 4)
-    BIG_CASE(13, 1) BIG_CASE(13, 2) BIG_CASE(13, 3)
+    BIG_CASE(15, 1) BIG_CASE(15, 2) BIG_CASE(15, 3)
+    BIG_CASE(14, 1) BIG_CASE(14, 2)
+    BIG_CASE(13, 1)
 #undef BIG_CASE
     return LAMQ_EUNSUP;
 }
