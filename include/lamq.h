@@ -110,6 +110,12 @@ int lamq_ldlq_trellis16_block(double* T, int64_t m, int64_t n, int64_t ldT, cons
 int lamq_trailing_update_f64(double* T, int64_t m, int64_t n, int64_t ldT, const double* Z, int64_t ldZ,
                              const double* U, int64_t ldU, int64_t b0, int64_t b1, void* stream);
 
+/* One step of the generic sweep for a projection Q [m, w] computed by the caller (opgraph/syntax.py:117-121):
+ * E = T[:, j:j+w] - Q, z = E U_BB^-1, T[:, j+w:b1] -= z @ U[j:j+w, j+w:b1], Z[:, j-b0 : j-b0+w] = z.
+ * The same arithmetic as the fused block kernels; w <= 64. */
+int lamq_refit_step(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU, const double* Q,
+                    int64_t ldq, int64_t j, int w, int64_t b0, int64_t b1, double* Z, int64_t ldZ, void* stream);
+
 /* T[:, dead] = 0 before a sweep (opgraph/syntax.py:101); dead [n] uint8. */
 int lamq_zero_columns(double* T, int64_t m, int64_t n, int64_t ldT, const uint8_t* dead, void* stream);
 
@@ -147,6 +153,8 @@ int lamq_rht_rows(const double* in, int64_t rows, int64_t n, int64_t ldi, double
                   void* stream);
 int lamq_transpose_f64(const double* in, int64_t rows, int64_t cols, int64_t ldi, double* out, int64_t ldo,
                        void* stream);
+/* Row scales S_r = max(sqrt(mean_j X[r, j]^2), 1e-12) (opgraph/codes.py:436, nested.py:168). */
+int lamq_row_rms(const double* X, int64_t rows, int64_t n, int64_t ldx, double* S, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
  * Token-weighted Gram matrix on bf16 MFMA with fp32 accumulation:

@@ -29,11 +29,14 @@ SIGNATURES = {
     "lamq_ldlq_trellis16_block": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _p, _p, _c_int, _c_int, _c_i64,
                                            _c_i64, _c_int, _c_int, _p, _p, _c_i64, _p, _c_i64, _p]),
     "lamq_trailing_update_f64": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _c_i64, _c_i64, _c_i64, _p]),
+    "lamq_refit_step": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _c_i64, _c_i64, _c_int, _c_i64, _c_i64, _p,
+                                 _c_i64, _p]),
     "lamq_zero_columns": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _p]),
     "lamq_chol_inv_upper_workspace_size": (_c_size, [_c_i64]),
     "lamq_chol_inv_upper": (_c_int, [_p, _c_i64, _c_i64, _c_dbl, _p, _c_i64, _p, _c_i64, _p, _p, _p, _c_size, _p]),
     "lamq_rht_rows": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _p, _c_int, _p, _c_int, _c_int, _p, _p]),
     "lamq_transpose_f64": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p]),
+    "lamq_row_rms": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _p]),
     "lamq_gram_workspace_size": (_c_size, [_c_i64, _c_i64, _c_int]),
     "lamq_hessian_accum": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_flt, _p, _c_i64, _p, _c_size, _p]),
     "lamq_hessian_finalize": (_c_int, [_p, _c_i64, _c_i64, _c_flt, _p, _c_i64, _p]),

@@ -113,3 +113,57 @@ extern "C" int lamq_zero_columns(double* T, int64_t m, int64_t n, int64_t ldT, c
     LAMQ_LAUNCH_CHECK();
     return LAMQ_OK;
 }
+
+// ------------------------------------------------------------------------------------------------
+// One step of the generic sweep (opgraph/syntax.py:117-121) for a projection computed elsewhere:
+//   E = T[:, j:j+w] - Q;  z = E U_BB^-1 (forward substitution, an fma chain in l);
+//   T[:, col] = T[:, col] - sum_l z[l] U[j+l][col] for col in [j+w, b1);  Z[:, j-b0+c] = z[c]
+// One wave per row (w <= 64), four rows per workgroup. The arithmetic is the fused kernels'.
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void refit_step_kernel(double* __restrict__ T, int64_t m, int64_t ldT,
+                                                         const double* __restrict__ U, int64_t ldU,
+                                                         const double* __restrict__ Q, int64_t ldq, int64_t j, int w,
+                                                         int64_t b0, int64_t b1, double* __restrict__ Z, int64_t ldZ)
+{
+    __shared__ double zsh[4][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+    if (row >= m) return;  // whole waves leave; no workgroup barrier follows
+    double* Tr = T + row * ldT;
+    double acc = 0.0;
+    if (lane < w) {
+        const double q = Q[row * ldq + lane];
+        acc = Tr[j + lane] - q;
+    }
+    double zmine = 0.0;
+    for (int l = 0; l < w; ++l) {
+        double zl = 0.0;
+        if (lane == l) zl = acc / U[(j + l) * ldU + j + l];
+        zl = __shfl(zl, l);
+        if (lane > l && lane < w) acc = fma(-zl, U[(j + l) * ldU + j + lane], acc);
+        if (lane == l) zmine = zl;
+    }
+    // the coefficients go through this wave's LDS slot: the column loop below has a trip count per lane
+    zsh[wave][lane] = zmine;
+    __builtin_amdgcn_wave_barrier();
+    for (int64_t col = j + w + lane; col < b1; col += 64) {
+        double a2 = 0.0;
+        for (int l = 0; l < w; ++l) a2 = fma(zsh[wave][l], U[(j + l) * ldU + col], a2);
+        Tr[col] = Tr[col] - a2;
+    }
+    if (lane < w) Z[row * ldZ + (j - b0) + lane] = zmine;
+}
+
+extern "C" int lamq_refit_step(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU, const double* Q,
+                               int64_t ldq, int64_t j, int w, int64_t b0, int64_t b1, double* Z, int64_t ldZ, void* stream)
+{
+    if (!T || !U || !Q || !Z || m < 0 || n < 1 || ldT < n || ldU < n || w < 1 || ldq < w || b0 < 0 || j < b0 ||
+        b1 > n || j + w > b1 || ldZ < b1 - b0)
+        return LAMQ_EINVAL;
+    if (w > 64) return LAMQ_EUNSUP;
+    if (m == 0) return LAMQ_OK;
+    hipLaunchKernelGGL(refit_step_kernel, dim3((unsigned)cdiv(m, 4)), dim3(256), 0, as_stream(stream), T, m, ldT, U, ldU, Q,
+                       ldq, j, w, b0, b1, Z, ldZ);
+    LAMQ_LAUNCH_CHECK();
+    return LAMQ_OK;
+}

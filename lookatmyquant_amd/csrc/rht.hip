@@ -131,3 +131,34 @@ extern "C" int lamq_transpose_f64(const double* in, int64_t rows, int64_t cols, 
     LAMQ_LAUNCH_CHECK();
     return LAMQ_OK;
 }
+
+// S_r = max(sqrt(mean_j X[r, j]^2), 1e-12) (opgraph/codes.py:436, nested.py:168), one workgroup per row,
+// summed in a fixed order.
+__global__ __launch_bounds__(256) void row_rms_kernel(const double* __restrict__ X, int64_t n, int64_t ldx,
+                                                      double* __restrict__ S)
+{
+    __shared__ double part[256];
+    const double* x = X + (int64_t)blockIdx.x * ldx;
+    double ss = 0.0;
+    for (int64_t j = threadIdx.x; j < n; j += 256) ss += x[j] * x[j];
+    part[threadIdx.x] = ss;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const double r = sqrt(part[0] / (double)n);
+        S[blockIdx.x] = r > 1e-12 ? r : 1e-12;
+    }
+}
+
+extern "C" int lamq_row_rms(const double* X, int64_t rows, int64_t n, int64_t ldx, double* S, void* stream)
+{
+    if (!X || !S || rows < 0 || n < 1 || ldx < n) return LAMQ_EINVAL;
+    if (rows == 0) return LAMQ_OK;
+    if (rows > 0x7fffffff) return LAMQ_EUNSUP;
+    hipLaunchKernelGGL(row_rms_kernel, dim3((unsigned)rows), dim3(256), 0, as_stream(stream), X, n, ldx, S);
+    LAMQ_LAUNCH_CHECK();
+    return LAMQ_OK;
+}

@@ -89,6 +89,14 @@ def rht_rows(X: torch.Tensor, seed: int, inverse: bool = False, want_rms: bool =
     return (y, rms) if want_rms else y
 
 
+def row_rms(X: torch.Tensor) -> torch.Tensor:
+    """S_r = max(sqrt(mean_j X_rj^2), 1e-12) (codes.py:436)."""
+    need(X, torch.float64, "X", 2)
+    S = torch.empty(X.shape[0], dtype=torch.float64, device=X.device)
+    check(lib().lamq_row_rms(ptr(X), X.shape[0], X.shape[1], ld(X), ptr(S), stream(X.device)), "row_rms")
+    return S
+
+
 def transpose(X: torch.Tensor) -> torch.Tensor:
     need(X, torch.float64, "X", 2)
     r, c = X.shape
@@ -228,6 +236,27 @@ def ldlq_scalar(T0: torch.Tensor, U: torch.Tensor, levels: torch.Tensor, mode: i
         if b1 < n:
             check(lib().lamq_trailing_update_f64(ptr(T), m, n, n, ptr(Z), lazy, ptr(U), ld(U), b0, b1, s), "trailing_update")
     return idx
+
+
+def refit_step(T: torch.Tensor, U: torch.Tensor, Q: torch.Tensor, j: int, b0: int, b1: int, Z: torch.Tensor):
+    """E = T[:, j:j+w] - Q, z = E U_BB^-1, T[:, j+w:b1] -= z U[j:j+w, j+w:b1], Z[:, j-b0:j-b0+w] = z (in place)."""
+    need(T, torch.float64, "T", 2)
+    need(U, torch.float64, "U", 2)
+    need(Q, torch.float64, "Q", 2)
+    need(Z, torch.float64, "Z", 2)
+    m, n = T.shape
+    w = Q.shape[1]
+    check(lib().lamq_refit_step(ptr(T), m, n, ld(T), ptr(U), ld(U), ptr(Q), ld(Q), j, w, b0, b1, ptr(Z), ld(Z),
+                                stream(T.device)), "refit_step")
+    return T
+
+
+def zero_columns(T: torch.Tensor, dead: torch.Tensor):
+    need(T, torch.float64, "T", 2)
+    m, n = T.shape
+    dd = dead.to(device=T.device, dtype=torch.uint8).contiguous()
+    check(lib().lamq_zero_columns(ptr(T), m, n, ld(T), ptr(dd), stream(T.device)), "zero_columns")
+    return T
 
 
 def trailing_update(T: torch.Tensor, Z: torch.Tensor, U: torch.Tensor, b0: int, b1: int):

@@ -1,0 +1,130 @@
+"""Lloyd-Max and compander level sets, and the one-rate LDLQ onto them (opgraph/nested.py), on the gfx950 kernels.
+
+    gaussian_centroids, gaussian_mse, compander_bounds, compander_levels      nested.py:44-68
+    lloyd_max(bits, iters=500), lloyd_max_levels(n, iters=500)                nested.py:71-82
+    nested_tables(top, rates, alpha)                                          nested.py:150-152
+    multirate_sweep(X, H, tables, weights, G=None, block=32)                  nested.py:104-147 (one rate)
+    nested_words(Ws, H, seeds, top, rates, alpha, weights, levels=None, in_seed=None, out_rot=True)   nested.py:155
+
+The level tables are small host computations in float64 with torch's special functions, as the reference does
+them (so the levels are the same bits). The sweep is the width-1 LDLQ kernel: each column's index is the first
+minimum of (t - level)^2 over the levels, then the later columns are re-solved under U. Several rates at once
+and output-side shaping (G) are not part of this path."""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import engine as E
+from .codes import SET, _nets, _prepare
+from .frame import Domain
+
+OUTPUT_DAMP = 0.03
+
+
+def _phi(x):
+    return torch.exp(-0.5 * x * x) / math.sqrt(2 * math.pi)
+
+
+def _Phi(x):
+    return 0.5 * (1 + torch.erf(x / math.sqrt(2)))
+
+
+def gaussian_centroids(bounds: torch.Tensor) -> torch.Tensor:
+    """The mean of a unit Gaussian on each cell [bounds[j], bounds[j+1]]."""
+    a, b = bounds[:-1], bounds[1:]
+    pa = torch.where(torch.isinf(a), torch.zeros_like(a), _phi(a))
+    pb = torch.where(torch.isinf(b), torch.zeros_like(b), _phi(b))
+    return (pa - pb) / (_Phi(b) - _Phi(a))
+
+
+def gaussian_mse(bounds: torch.Tensor, levels: torch.Tensor) -> float:
+    """E[(x - q(x))^2] for x ~ N(0, 1) by the truncated-moment formulas."""
+    a, b = bounds[:-1], bounds[1:]
+    P = _Phi(b) - _Phi(a)
+    fa = lambda t: torch.where(torch.isinf(t), torch.zeros_like(t), t * _phi(t))
+    pa = lambda t: torch.where(torch.isinf(t), torch.zeros_like(t), _phi(t))
+    m1 = pa(a) - pa(b)
+    m2 = P + fa(a) - fa(b)
+    return float((m2 - 2 * levels * m1 + levels**2 * P).sum())
+
+
+def compander_bounds(bits: int, alpha: float) -> torch.Tensor:
+    u = torch.arange(2**bits + 1, dtype=torch.float64) / 2**bits
+    return torch.special.ndtri(u) / math.sqrt(alpha)
+
+
+def compander_levels(bits: int, alpha: float) -> torch.Tensor:
+    return gaussian_centroids(compander_bounds(bits, alpha))
+
+
+def lloyd_max_levels(n: int, iters: int = 500) -> torch.Tensor:
+    """The best n levels for a unit Gaussian: Lloyd iterations from the centroids of equal-probability cells
+    widened by sqrt(3)."""
+    lv = gaussian_centroids(torch.special.ndtri(torch.arange(n + 1, dtype=torch.float64) / n) * math.sqrt(3))
+    inf = torch.tensor([math.inf], dtype=torch.float64)
+    for _ in range(iters):
+        mid = (lv[1:] + lv[:-1]) / 2
+        lv = gaussian_centroids(torch.cat([-inf, mid, inf]))
+    return lv
+
+
+def lloyd_max(bits: int, iters: int = 500) -> torch.Tensor:
+    return lloyd_max_levels(2**bits, iters)
+
+
+def NESTED(bits: int, alpha: float) -> Domain:
+    return SET(compander_levels(bits, alpha).tolist())
+
+
+def nested_tables(top: int, rates: list[int], alpha: float) -> torch.Tensor:
+    i = torch.arange(2**top)
+    return torch.stack([compander_levels(b, alpha)[i >> (top - b)] for b in rates])
+
+
+def multirate_sweep(X: torch.Tensor, H: torch.Tensor | None, tables: torch.Tensor, weights: torch.Tensor,
+                    G: torch.Tensor | None = None, block: int = 32) -> torch.Tensor:
+    """One index per entry of X (already in units of the row scale) for one rate (nested.py:104-147): with H, the
+    width-1 LDLQ sweep under U; without H, the nearest level. Returns int64 indices on the CPU."""
+    tables = torch.as_tensor(tables, dtype=torch.float64)
+    if tables.dim() != 2 or tables.shape[0] != 1 or G is not None:
+        raise NotImplementedError("several rates at once and output shaping are not part of this path")
+    dev = E._abi.device()
+    lv = tables[0].to(dev).contiguous()
+    x = torch.as_tensor(X).to(dev, torch.float64).contiguous()
+    if H is None:
+        # first minimum of (t - lv)^2 per entry: a zero-row environment is not needed, every column alone
+        d = (x[:, :, None] - lv[None, None, :]) ** 2
+        return d.argmin(-1).cpu()
+    _, U, dead, _ = E.chol_inv_upper(torch.as_tensor(H).to(dev, torch.float64).contiguous())
+    return E.ldlq_scalar(x, U, lv, mode=0, dead=dead).to(torch.int64).cpu()
+
+
+def nested_words(Ws: list, H: torch.Tensor | None, seeds: list[int], top: int, rates: list[int], alpha: float,
+                 weights: list[float], levels: torch.Tensor | None = None, in_seed: int | None = None,
+                 out_rot: bool = True, G: torch.Tensor | None = None, block: int = 32) -> dict:
+    """Incoherence (shared input transform) -> per-row RMS scale -> LDLQ onto one rate's levels -> {rate: [Net]}
+    (nested.py:155-192). With `levels` the code is that set (a dedicated code, as quantize.word's lm<b>)."""
+    if len(rates) != 1 or G is not None:
+        raise NotImplementedError("several rates at once and output shaping are not part of this path")
+    dev, X, S, rin = _prepare(Ws, seeds, True, in_seed, out_rot)
+    if levels is None:
+        tab = nested_tables(top, rates, alpha)[0]
+        dom = NESTED(rates[0], alpha)
+    else:
+        tab = torch.as_tensor(levels, dtype=torch.float64)
+        dom = SET(tab.tolist(), bits=math.log2(len(tab)))
+    lv = tab.to(dev).contiguous()
+    x = X / S[:, None]
+    if H is None:
+        idx = ((x[:, :, None] - lv[None, None, :]) ** 2).argmin(-1).to(torch.int32)
+    else:
+        Hr = E.rotate_hessian(torch.as_tensor(H).to(dev, torch.float64).contiguous(), rin)
+        _, U, dead, _ = E.chol_inv_upper(Hr)
+        idx = E.ldlq_scalar(x.contiguous(), U, lv, mode=0, dead=dead)
+    idx = idx.cpu()
+    values = tab[idx.long()]
+    rows_label = "u" if out_rot else "o"
+    return {rates[0]: _nets(Ws, seeds, X, values, S.cpu(), dom, rows_label, rin, out_rot, True, idx)}

@@ -1,0 +1,241 @@
+"""The build harness's per-matrix entry points (quantize.py of the reference) on the gfx950 path.
+
+    parse(program)                                                          quantize.py:276-285
+    word(program, W, H, seed, trellis, in_seed=None, out_rot=True, G=None)  quantize.py:332-347
+    trellis_states(values, table), trellis_code_entry(net, shape, bits, in_seed)    quantize.py:502-527
+    quantize_row_groups(target, groups, round_group, in_seed, keep_codes)   quantize.py:530-565
+    lamq_codes(values, levels)                                              quantize.py:491-493
+    trellis_code(k, T, rows=(16, 8), L=12)                                  quantize.py:588-590
+    token_weights_from_kinds(kinds, floor, ceiling, gamma)                  quantize.py:593-629 ("digits")
+    cross_target(H, D, alpha, lam)                                          quantize.py:1330-1335
+    block_seed(name), matrix_seeds(i, names, j, seed_set, first)            quantize.py:1492-1493, compiler_arch.py:33,75-77
+    stage_statistics(...)                                                   quantize.py:1404-1470 (H and the QEP D)
+    quantize_stage_row_groups(...)                                          the batched form of quantize_row_groups
+
+quantize_stage_row_groups is the production form of the per-stage loop: every matrix of a stage shares H and the
+input rotation, so R_in H R_in^T and U are computed once for all its matrices and row groups (the reference
+recomputes them inside every ldlq_words call; the factor is the same) and all rows of one bit width go through
+one sweep. The results are those of quantize_row_groups with the trellis word, row for row.
+"""
+
+from __future__ import annotations
+
+import re
+import zlib
+
+import torch
+
+from . import codes as C
+from . import engine as E
+from . import nested as N
+from .frame import Dense
+
+PROGRAM = re.compile(r"orig|(rtn|gptq|gptaq|lm|tr|higgs|ter)(\d)(x?)")
+LAM = 0.1
+KNOWN_BLOCKS = {"linear_attn": 1, "self_attn": 2, "mlp": 3}
+
+
+def parse(program: str):
+    """(family, bits, cross-term target) of a program name (quantize.py:276-285)."""
+    if program == "fp16":
+        return "fp", 16, False
+    if program in ("mean", "prng", "zero"):
+        return program, 0, False
+    m = PROGRAM.fullmatch(program)
+    if not m or (m.group(1) in ("gptaq",) and m.group(3)) or (m.group(1) in ("rtn", "gptq", "higgs") and m.group(3)):
+        raise ValueError(f"unknown program {program}")
+    return m.group(1), int(m.group(2)), m.group(1) == "gptaq" or m.group(3) == "x"
+
+
+def trellis_code(k: int, T: int = 256, rows: tuple | None = (16, 8), L: int = 12, values=None):
+    """The code of a tr<k> program: the row trellis (width, look) = rows (quantize.py:588-590 with --trellis-rows);
+    the column trellis (rows=None) is not part of this path."""
+    if rows is None:
+        raise NotImplementedError("the column-wise TrellisCode layout is not part of this path")
+    return C.RowTrellisCode(L, k, T=256, width=rows[0], look=rows[1], values=values)
+
+
+def word(program, W, H, seed, trellis, in_seed=None, out_rot=True, G=None):
+    """One matrix's quantized word for its target W and input statistics H (quantize.py:332-347): lm<b> and ter<b>
+    are one-rate nested words on Lloyd-Max levels, tr<b> the trellis code trellis[b], fp16 the bf16 values."""
+    fam, b, _ = parse(program)
+    if fam == "fp":
+        return Dense(torch.as_tensor(W).to(torch.bfloat16).double(), 16 * W.numel())
+    if fam == "lm":
+        return N.nested_words([W], H, [seed], b, [b], 0.4, [1.0], N.lloyd_max(b), in_seed=in_seed, out_rot=out_rot, G=G)[b][0]
+    if fam == "ter":
+        return N.nested_words([W], H, [seed], 2, [2], 0.4, [1.0], N.lloyd_max_levels(b), in_seed=in_seed, out_rot=out_rot)[2][0]
+    if fam == "tr":
+        return C.ldlq_words([W], H, trellis[b], [seed], in_seed=in_seed, out_rot=out_rot)[0]
+    raise NotImplementedError(f"program family {fam!r} is not part of this path")
+
+
+def lamq_codes(values: torch.Tensor, levels: torch.Tensor) -> torch.Tensor:
+    """The index of the nearest level for each value (quantize.py:491-493)."""
+    levels = torch.as_tensor(levels, dtype=torch.float64)
+    return torch.searchsorted(((levels[1:] + levels[:-1]) / 2).contiguous(), torch.as_tensor(values).double().contiguous())
+
+
+def trellis_states(values: torch.Tensor, table: torch.Tensor) -> torch.Tensor:
+    """Each entry's state: the index of its value in the table (quantize.py:502-510). Ambiguous for tables with
+    repeated values; words built here carry their states (net.codes) instead."""
+    t = torch.as_tensor(table).double().flatten()
+    st, order = t.sort()
+    v = torch.as_tensor(values).double().contiguous()
+    pos = torch.searchsorted(st, v).clamp(1, len(st) - 1)
+    pos = torch.where((v - st[pos - 1]).abs() <= (st[pos] - v).abs(), pos - 1, pos)
+    assert float((st[pos] - v).abs().max()) < 1e-9, "a trellis value not in its table"
+    return order[pos].to(torch.int16)
+
+
+def trellis_code_entry(net, shape, bits, in_seed):
+    """A one-sided row-trellis word in the saved codes format (quantize.py:513-527): int16 states, f32 row scales,
+    the input seed, the f32 table and one row group."""
+    if in_seed is None or "I[u]" in net.cores:
+        raise ValueError("saved trellis codes require an input-only rotation with a recorded seed")
+    core = net.cores["W"]
+    table = torch.as_tensor(core.domain.levels, dtype=torch.float64)
+    if len(table) != 4096:
+        raise ValueError("saved row-group codes require a 12-bit state table")
+    states = net.codes.reshape(shape).to(torch.int16) if getattr(net, "codes", None) is not None else \
+        trellis_states(core.data.reshape(shape), table)
+    entry = {"states": states, "scales": net.cores["W.S"].data.float().flatten(), "in_seed": int(in_seed),
+             "table": table.float(), "trellis_layout": "row" if core.domain.fixed_start else "column"}
+    if core.domain.fixed_start:
+        entry["row_groups"] = [{"rows": torch.arange(shape[0], dtype=torch.long), "bits": int(bits), "table_index": 0}]
+    return entry
+
+
+def quantize_row_groups(target, groups, round_group, in_seed, keep_codes):
+    """Apply validated original-row groups (quantize.py:530-565): one to eight non-empty groups of widths 1-4 that
+    cover every row exactly once; each group is round_group(rows, bits), a word; returns (W_hat, bits, entry)."""
+    groups = [(torch.as_tensor(g["rows"], dtype=torch.long), int(g["bits"])) for g in groups]
+    if not groups or len(groups) > 8 or any(not len(rows) or bits not in (1, 2, 3, 4) for rows, bits in groups):
+        raise ValueError("row groups need one to eight nonempty groups at widths 1–4")
+    all_rows = torch.cat([rows for rows, _ in groups])
+    if not torch.equal(all_rows.sort().values, torch.arange(target.shape[0])):
+        raise ValueError("row groups must cover every matrix row exactly once")
+    Wq, rate = torch.empty(target.shape, dtype=torch.float64), 0.0
+    states = torch.empty(target.shape, dtype=torch.int16) if keep_codes else None
+    scales = torch.empty(target.shape[0], dtype=torch.float32) if keep_codes else None
+    tables, saved_groups, layouts = [], [], set()
+    for rows, bits in groups:
+        net = round_group(rows, bits)
+        Wq[rows] = net.matrix(dtype=torch.float64)
+        rate += net.rate_bits()
+        if keep_codes:
+            entry = trellis_code_entry(net, (len(rows), target.shape[1]), bits, in_seed)
+            table_index = len(tables)
+            states[rows] = entry["states"] + table_index * 4096
+            scales[rows] = entry["scales"]
+            tables.append(entry["table"])
+            layouts.add(entry["trellis_layout"])
+            saved_groups.append({"rows": rows.clone(), "bits": bits, "table_index": table_index})
+    if not keep_codes:
+        return Wq, rate, None
+    if len(layouts) != 1:
+        raise ValueError("mixed trellis layouts are not a saved row-group representation")
+    return Wq, rate, {"states": states, "scales": scales, "in_seed": int(in_seed), "table": torch.cat(tables),
+                      "row_groups": saved_groups, "trellis_layout": next(iter(layouts))}
+
+
+# ----------------------------------------------------------------------------- seeds, weights and statistics
+
+
+def block_seed(path: str) -> int:
+    """compiler_arch.block_seed (compiler_arch.py:75-77): the known blocks' fixed seeds, else 4 + crc32 % 5."""
+    head = path.split(".")[0]
+    return KNOWN_BLOCKS.get(head, 4 + zlib.crc32(head.encode()) % 5)
+
+
+def matrix_seeds(layer: int, name: str, j: int, first: str, seed_set: int = 0, stage_j: int = 0):
+    """(seed, in_seed) of a matrix (quantize.py:1492-1493 with --rot in-shared)."""
+    shift = 100000 * seed_set
+    seed = 1000 * layer + 100 * block_seed(name) + j + stage_j + shift
+    in_seed = 1000 * layer + 100 * block_seed(first) + 1 + shift
+    return seed, in_seed
+
+
+def token_weights_from_kinds(kinds: torch.Tensor, floor: float = 0.1, ceiling: float = 100.0, gamma: float = 1.0):
+    """Per-token weights of the "digits" rule (quantize.py:593-629) from the token kinds of the next position
+    (0: a digit of a computed result, 1: another digit, else other; the last position of a window has none):
+    2 / 1 / 0, over their mean, raised to gamma, kept within [floor, ceiling] times the mean, mean 1, float32."""
+    k = torch.as_tensor(kinds)
+    v = torch.zeros(k.shape, dtype=torch.float64)
+    v[..., :-1] = 2.0 * (k[..., :-1] == 0) + 1.0 * (k[..., :-1] == 1)
+    w = (v / v.mean()).clamp(min=1e-9) ** gamma
+    w = (w / w.mean()).clamp(floor, ceiling)
+    return (w / w.mean()).float()
+
+
+def cross_target(H: torch.Tensor, D: torch.Tensor, alpha: float, lam: float = LAM) -> torch.Tensor:
+    """M = I + alpha ((H + lam mean(diag H) I)^-1 D^T)^T (quantize.py:1330-1335), D = X_ref^T X_q / N - H. The
+    damped H is symmetric positive definite, so the solve is the Cholesky solve of lamq_chol_inv_upper's factor:
+    (H + d I)^-1 = U^T U. Returned on the CPU in float64."""
+    dev = E._abi.device()
+    Hg = torch.as_tensor(H).to(dev, torch.float64).contiguous()
+    Dg = torch.as_tensor(D).to(dev, torch.float64).contiguous()
+    n = Hg.shape[0]
+    _, U, _, _ = E.chol_inv_upper(Hg, damp=lam)
+    # (H + d I)^-1 D^T = U^T (U D^T); then M = I + alpha (.)^T
+    Y = U.T @ (U @ Dg.T)
+    return (torch.eye(n, dtype=torch.float64, device=dev) + alpha * Y.T).cpu()
+
+
+def stage_statistics(Xq_chunks, w_chunks=None, Xr_chunks=None):
+    """H = (1/N) sum_t w_t x_t x_t^T and, for a cross-term stage, D = (1/N) sum_t w_t x_ref,t x_q,t^T, from bf16
+    activation chunks [tokens, n] on the GPU (quantize.py:1416-1470). Returns float64 (H, D or None)."""
+    dev = E._abi.device()
+    n = Xq_chunks[0].shape[-1]
+    H = torch.zeros(n, n, dtype=torch.float32, device=dev)
+    D = torch.zeros(n, n, dtype=torch.float32, device=dev) if Xr_chunks is not None else None
+    ntok = 0
+    for c, xq in enumerate(Xq_chunks):
+        xq = xq.reshape(-1, n).to(dev, torch.bfloat16).contiguous()
+        w = None if w_chunks is None else w_chunks[c].reshape(-1).to(dev, torch.float32)
+        E.hessian_accum(H, xq, w)
+        if D is not None:
+            xr = Xr_chunks[c].reshape(-1, n).to(dev, torch.bfloat16).contiguous()
+            E.cross_gram_accum(D, xr, xq, w)
+        ntok += xq.shape[0]
+    H64 = E.hessian_finalize(H, float(ntok))
+    D64 = None if D is None else (D / ntok).double()
+    return H64, D64
+
+
+# ----------------------------------------------------------------------------- the batched stage path
+
+
+def quantize_stage_row_groups(targets: dict, groups: dict, H: torch.Tensor, in_seed: int, L: int = 12,
+                              width: int = 16, look: int = 8, tables: dict | None = None, events: dict | None = None):
+    """Every matrix of a stage, row group by row group, with the row trellis at the group's width: the same result
+    as quantize_row_groups(target, groups, round_group) with round_group = the tr<bits> word of (target[rows], H,
+    in_seed, out_rot=False), for each matrix. targets: {name: W [m, n]}; groups: {name: [{"rows", "bits"}]};
+    tables: {bits: float64 table} (default: the cached L = 12 tables). Returns {name: (states int32 [m, n] on the
+    GPU, S float64 [m] on the GPU)}; the codes entries and reconstructions follow from them."""
+    dev = E._abi.device()
+    names = list(targets)
+    Hr = E.rotate_hessian(torch.as_tensor(H).to(dev, torch.float64).contiguous(), in_seed)
+    _, U, dead, _ = E.chol_inv_upper(Hr)
+    X_all, S_all = {}, {}
+    for nm in names:
+        W = torch.as_tensor(targets[nm]).to(dev, torch.float64).contiguous()
+        X_all[nm], S_all[nm] = E.rht_rows(W, in_seed, want_rms=True)
+    # rows of one width across the stage's matrices go through one sweep
+    by_bits: dict = {}
+    for nm in names:
+        for g in groups[nm]:
+            by_bits.setdefault(int(g["bits"]), []).append((nm, torch.as_tensor(g["rows"], dtype=torch.long)))
+    out = {nm: torch.empty(X_all[nm].shape, dtype=torch.int32, device=dev) for nm in names}
+    for bits, parts in sorted(by_bits.items()):
+        table = (tables or {}).get(bits)
+        table = torch.from_numpy(C.load_table(12, bits).copy()) if table is None else torch.as_tensor(table, dtype=torch.float64)
+        idx = [(nm, rows.to(dev)) for nm, rows in parts]
+        X = torch.cat([X_all[nm].index_select(0, r) for nm, r in idx])
+        S = torch.cat([S_all[nm].index_select(0, r) for nm, r in idx])
+        st = E.ldlq_trellis(X, S, U, table.to(dev), L, bits, width, look, 128, dead=dead, events=events)
+        r0 = 0
+        for nm, r in idx:
+            out[nm].index_copy_(0, r, st[r0 : r0 + len(r)])
+            r0 += len(r)
+    return {nm: (out[nm], S_all[nm]) for nm in names}

@@ -1,0 +1,206 @@
+"""The reference-compatible API on the GPU (lookatmyquant_amd.codes / nested / quantize / syntax / compiler /
+artifact): the words the reference's callers build give the reference's codes and reconstructions."""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    assert torch.cuda.is_available(), "the GPU tests need an MI355X"
+
+
+def test_ldlq_words_row_trellis_config2(golden, config12):
+    """quantize.word('tr2', ...) with the LM2 flags: ldlq_words([W], H, RowTrellisCode(12, 2), [seed],
+    in_seed=201, out_rot=False) -- the reference's states, scales and reconstruction."""
+    from lookatmyquant_amd import codes as C
+
+    W, H = config12
+    g = golden("ldlq_trellis_c2_L12_k2")
+    say("ldlq_words tr2 config 2")
+    net = C.ldlq_words([torch.from_numpy(W.astype(np.float64))], torch.from_numpy(H), C.RowTrellisCode(12, 2), [200],
+                       in_seed=201, out_rot=False)[0]
+    assert np.array_equal(net.codes.numpy(), g["states"])
+    S = net.cores["W.S"].data.numpy()
+    assert np.abs(S / g["S"] - 1).max() < 1e-13
+    What = net.matrix(dtype=torch.float64)[:8].numpy()
+    assert np.abs(What - g["what_rows"]).max() < 1e-4 * np.abs(g["what_rows"]).max()
+    assert net.rate_bits() == 960 * 960 * 2 + 16 * 960 + 960
+    assert net.cores["W"].domain.fixed_start and net.cores["W"].domain.state_bits == 12
+    assert C.is_trellis_path(net.codes, 12, 2)
+
+
+def test_word_lm3_config1(golden, config12):
+    from lookatmyquant_amd import quantize as Q
+
+    W, H = config12
+    g = golden("nested_lm3_c1")
+    say("word lm3 config 1")
+    net = Q.word("lm3", torch.from_numpy(W.astype(np.float64)), torch.from_numpy(H), 200, None, in_seed=201, out_rot=False)
+    assert np.array_equal(net.codes.numpy(), g["idx"].astype(np.int32))
+    codes = Q.lamq_codes(net.cores["W"].data, torch.from_numpy(g["levels"]))
+    assert np.array_equal(codes.numpy(), g["idx"])
+    What = net.matrix(dtype=torch.float64)[:8].numpy()
+    assert np.abs(What - g["what_rows"]).max() < 1e-4 * np.abs(g["what_rows"]).max()
+    assert net.rate_bits() == 960 * 960 * 3 + 16 * 960 + 960
+
+
+def test_row_trellis_16bit_states(golden, config12):
+    from lookatmyquant_amd import codes as C
+
+    W, H = config12
+    g = golden("ldlq_trellis_L16_k2_rows32")
+    say("ldlq_words L=16 k=2, 32 rows")
+    code = C.RowTrellisCode(16, 2, values=C.trellis_init_values(16, 0, "float16"))
+    net = C.ldlq_words([torch.from_numpy(W[:32].astype(np.float64))], torch.from_numpy(H), code, [200], in_seed=201,
+                       out_rot=False)[0]
+    assert np.array_equal(net.codes.numpy(), g["states"])
+
+
+def test_quantize_row_groups_and_the_batched_stage(config12, tables):
+    """A rowgroup plan over one matrix through quantize_row_groups (one word per group, as the reference) and
+    through quantize_stage_row_groups (one factor, one sweep per width): the same states; each group's states
+    equal the oracle's for that group's rows."""
+    from lookatmyquant_amd import codes as C
+    from lookatmyquant_amd import quantize as Q
+    from lookatmyquant_amd import synthetic
+
+    W, H = config12
+    Wt, Ht = torch.from_numpy(W.astype(np.float64)), torch.from_numpy(H)
+    groups = synthetic.row_plan(960, 11)
+    trellis = {b: C.RowTrellisCode(12, b) for b in (1, 2, 3, 4)}
+    say("quantize_row_groups config 2 with a 2.3 bpw row plan")
+
+    def round_group(rows, bits):
+        return Q.word(f"tr{bits}", Wt[rows], Ht, 200, trellis, in_seed=201, out_rot=False)
+
+    Wq, rate, entry = Q.quantize_row_groups(Wt, groups, round_group, 201, True)
+    assert rate == sum(len(g["rows"]) * 960 * g["bits"] + 16 * len(g["rows"]) + 960 for g in groups)
+    states = entry["states"].numpy().astype(np.int64) % 4096
+    for g in groups[:3]:
+        rows = np.array(g["rows"])
+        ref, _, _ = O.ldlq_words_trellis(W[rows[:16]], H, tables[g["bits"]], 12, g["bits"], 201)
+        assert np.array_equal(states[rows[:16]], ref)
+    say("quantize_stage_row_groups")
+    out = Q.quantize_stage_row_groups({"q": Wt}, {"q": groups}, Ht, 201)
+    st, S = out["q"]
+    assert np.array_equal(st.cpu().numpy(), states)
+    assert torch.equal(entry["scales"], S.cpu().float())
+
+
+def test_viterbi_api(golden, tables):
+    from lookatmyquant_amd import codes as C
+
+    g = golden("viterbi")
+    x = torch.from_numpy(g["L12_k3_x"])
+    say("codes.viterbi")
+    st = C.viterbi(x, torch.from_numpy(tables[3].copy()), 12, 3, start=torch.from_numpy(g["L12_k3_start"]))
+    assert st.dtype == torch.int64 and st.device == x.device
+    assert np.array_equal(st.numpy(), g["L12_k3_fixed"])
+
+
+def test_generic_sweep_matches_the_fused_scalar_kernel(config12):
+    """syntax.sweep with a Python projection (the ScalarCode project of ldlq_words) settles the same levels as the
+    fused width-1 kernel."""
+    from lookatmyquant_amd import engine as E
+    from lookatmyquant_amd.frame import Environment
+    from lookatmyquant_amd.syntax import sweep
+
+    W, H = config12
+    X = (torch.from_numpy(W[:64].astype(np.float64)) @ torch.from_numpy(O.rht(960, 201)).T).cuda()
+    S = E.row_rms(X)
+    env = Environment(E.rotate_hessian(torch.from_numpy(H).cuda(), 201))
+    lv = torch.tensor([-1.5104, -0.4528, 0.4528, 1.5104], dtype=torch.float64, device="cuda")
+    mids = (lv[1:] + lv[:-1]) / 2
+    chosen = torch.empty(X.shape, dtype=torch.long, device="cuda")
+
+    def project(j, col, T):
+        i = torch.bucketize((col / S).contiguous(), mids)
+        chosen[:, j] = i
+        return lv[i] * S
+
+    say("generic sweep, width 1")
+    sweep(X, env, project)
+    fused = E.ldlq_scalar(X, env.U, lv, mode=1, S=S, dead=env.dead)
+    assert torch.equal(chosen.to(torch.int32), fused)
+
+
+def test_kl_api():
+    from lookatmyquant_amd import compiler
+    from lookatmyquant_amd import synthetic
+
+    r, q = synthetic.logits(12, 5000, 5, 6)
+    w = np.linspace(0.5, 2.0, 12).astype(np.float32)
+    ref, mean = O.kl_rows(r, q, w)
+    rt = torch.from_numpy(r.view(np.int16)).view(torch.bfloat16).reshape(3, 4, 5000)
+    qt = torch.from_numpy(q.view(np.int16)).view(torch.bfloat16).reshape(3, 4, 5000)
+    say("compiler.kl")
+    assert abs(compiler.kl(rt, qt, torch.from_numpy(w).reshape(3, 4)) - mean) < 1e-4 * mean
+    per = compiler.kl_per_token(rt, qt)
+    assert per.shape == (3, 4)
+    assert np.abs(per.cpu().numpy().reshape(-1) - ref).max() < 1e-4 * ref.max()
+
+
+def test_artifact_packing(golden):
+    from lookatmyquant_amd import artifact
+
+    g = golden("misc")
+    for bits in (1, 3):
+        st = g[f"pack_{bits}_states"]
+        codes = artifact.pack_trellis(st, bits)
+        assert np.array_equal(codes, g[f"pack_{bits}_codes"])
+        assert np.array_equal(artifact.unpack_trellis(codes, bits, st.shape[1]), st)
+
+
+def test_environment_and_covariance(config12):
+    from lookatmyquant_amd import synthetic
+    from lookatmyquant_amd.frame import Environment, covariance
+
+    X = synthetic.calibration(3000, 320, 31, 32)
+    say("covariance and Environment")
+    H = covariance(torch.from_numpy(X).to(torch.bfloat16))
+    ref = O.hessian(X) * 3000
+    assert (H.cpu().numpy() - ref).__abs__().max() < 1e-4 * np.abs(ref).max()
+    env = Environment(H)
+    _, U, _ = O.environment(H.cpu().numpy())
+    assert np.abs(env.U.cpu().numpy() - U).max() < 1e-9 * np.abs(U).max()
+
+
+def test_cross_target_is_the_damped_solve():
+    from lookatmyquant_amd.quantize import cross_target
+
+    rng = np.random.default_rng(12)
+    Xa = rng.standard_normal((500, 48))
+    H = Xa.T @ Xa / 500
+    D = 0.01 * rng.standard_normal((48, 48))
+    M = cross_target(torch.from_numpy(H), torch.from_numpy(D), 0.5).numpy()
+    ref = np.eye(48) + 0.5 * np.linalg.solve(H + 0.1 * np.diag(H).mean() * np.eye(48), D.T).T
+    assert np.abs(M - ref).max() < 1e-9
+
+
+def test_error_paths():
+    from lookatmyquant_amd import codes as C
+    from lookatmyquant_amd import engine as E
+    from lookatmyquant_amd.frame import Environment
+
+    with pytest.raises(E.LinAlgError):
+        Environment(-torch.eye(16, dtype=torch.float64))
+    with pytest.raises(NotImplementedError):  # a 17-bit state is beyond the kernels
+        C.viterbi(torch.zeros(2, 4), torch.zeros(1 << 17), 17, 2)
+    with pytest.raises(NotImplementedError):  # search longer than the fused kernel's window
+        C.ldlq_words([torch.randn(4, 64, dtype=torch.float64)], torch.eye(64, dtype=torch.float64),
+                     C.RowTrellisCode(12, 2, width=16, look=20), [1], in_seed=2, out_rot=False)
+    with pytest.raises(NotImplementedError):  # a 16-bit table that fp16 cannot hold
+        C.viterbi(torch.zeros(2, 4), torch.randn(1 << 16, dtype=torch.float64), 16, 2)

@@ -1,0 +1,194 @@
+"""Host-side logic of the product, CPU only: the C ABI library loads and binds every symbol include/lamq.h
+declares (no compute calls), the host tables (Hadamard factors, rotation signs, Lloyd-Max levels) equal the
+reference's, and the plan/row-plan/program validation behaves like the reference's."""
+
+import json
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import REPO
+
+
+def declared_symbols():
+    text = (REPO / "include" / "lamq.h").read_text()
+    return sorted(set(re.findall(r"^(?:int|size_t)\s+(lamq_\w+)\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    from lookatmyquant_amd import _abi
+
+    names = declared_symbols()
+    assert len(names) >= 20
+    assert sorted(_abi.SIGNATURES) == names, "the ctypes bindings must be exactly the header's declarations"
+    lib = _abi.lib()  # loads the gfx950 library; binding fails on a missing symbol
+    for n in names:
+        assert hasattr(lib, n)
+    assert lib.lamq_abi_version() == 100
+
+
+def test_library_symbols_are_c_abi():
+    so = REPO / "lookatmyquant_amd" / "liblamq_hip.so"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(so)], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r" T (lamq_\w+)$", out, flags=re.M))
+    assert set(declared_symbols()) <= exported
+
+
+def test_argument_errors_are_reported_without_a_gpu():
+    """Entry points validate their arguments before touching a device: NULL pointers and bad shapes return
+    LAMQ_EINVAL, unsupported parameters LAMQ_EUNSUP."""
+    from lookatmyquant_amd import _abi
+
+    L = _abi.lib()
+    assert L.lamq_viterbi_rows(None, 4, 8, 8, None, 12, 2, None, None, 8, None, 0, None) == -1
+    assert L.lamq_trailing_update_f64(None, 1, 1, 1, None, 1, None, 1, 0, 1, None) == -1
+    assert L.lamq_kl_rows(None, None, 1, 1, 1, 1, None, None, None, None, 0, None) == -1
+    p = torch.empty(64, dtype=torch.float64)
+    q = torch.empty(64, dtype=torch.int32)
+    ptr = lambda t: t.data_ptr()
+    # width + look beyond the fused search's limit: unsupported, not a crash
+    assert L.lamq_ldlq_trellis_block(ptr(p), 1, 8, 8, ptr(p), 8, ptr(p), ptr(p), ptr(p), 12, 2, 0, 8, 30, 8, ptr(q), ptr(q),
+                                     8, ptr(p), 8, None) == -2
+    # a trellis width the kernels are not built for
+    assert L.lamq_viterbi_rows(ptr(p), 1, 4, 4, ptr(p), 12, 7, None, ptr(q), 4, None, 0, None) == -2
+    assert L.lamq_chol_inv_upper_workspace_size(10) >= 800
+    assert L.lamq_viterbi_workspace_size(3, 100, 12, 2) == 3 * 100 * 256
+
+
+def test_hadamard_factors_and_signs_equal_the_reference(golden):
+    from lookatmyquant_amd import hadamard as Hd
+
+    g = golden("misc")
+    for n in (960, 2560, 4096, 9728):
+        A, B = Hd.hadamard_factors(n)
+        assert np.array_equal(A.numpy().astype(np.int8), g[f"had_{n}_A"])
+        assert np.array_equal(B.numpy().astype(np.int8), g[f"had_{n}_B"])
+    for n, s in ((960, 201), (2560, 1301), (9728, 3301)):
+        assert np.array_equal(Hd.rht_signs(n, s).numpy().astype(np.int8), g[f"signs_{n}_{s}"])
+    for n in (2, 12, 20, 64, 1024):
+        H = Hd.hadamard(n)
+        assert float((H @ H.T - torch.eye(n, dtype=torch.float64)).abs().max()) < 1e-12
+
+
+def test_lloyd_max_levels_equal_the_reference_bits(golden):
+    from lookatmyquant_amd import nested as N
+
+    for b in (1, 2, 3, 4):
+        assert np.array_equal(N.lloyd_max(b).numpy(), golden("misc")[f"lloyd_max_{b}"])
+
+
+def test_tables():
+    from lookatmyquant_amd.tables import load_table, quantile_table
+
+    t = load_table(12, 2)
+    assert t.shape == (4096,) and abs(t[0] - 1.056634) < 1e-6 and len(set(t.tolist())) == 4096
+    with pytest.raises(FileNotFoundError):
+        load_table(12, 5)
+    q = quantile_table(16, 0)
+    assert q.shape == (65536,)
+    assert np.array_equal(q.astype(np.float16).astype(np.float64), q)
+    assert len(set(q.tolist())) < 65536  # fp16 collapses neighbouring quantiles: ties are decided by the tie rules
+
+
+def test_program_parsing():
+    from lookatmyquant_amd.quantize import parse
+
+    assert parse("tr2") == ("tr", 2, False)
+    assert parse("lm3x") == ("lm", 3, True)
+    assert parse("fp16") == ("fp", 16, False)
+    for bad in ("tr", "gptaq3x", "rtn4x", "q4"):
+        with pytest.raises(ValueError):
+            parse(bad)
+
+
+def test_seeds_follow_the_reference_rule():
+    from lookatmyquant_amd.quantize import block_seed, matrix_seeds
+
+    assert block_seed("self_attn.q_proj") == 2 and block_seed("mlp.down_proj") == 3 and block_seed("linear_attn.x") == 1
+    assert 4 <= block_seed("vision.proj") <= 8
+    assert matrix_seeds(0, "self_attn.q_proj", 0, "self_attn.q_proj") == (200, 201)
+    assert matrix_seeds(3, "mlp.up_proj", 1, "mlp.gate_proj", seed_set=1) == (100000 + 3301, 100000 + 3301)
+
+
+def test_token_weights_digits():
+    from lookatmyquant_amd.quantize import token_weights_from_kinds
+
+    kinds = torch.tensor([[0, 1, 2, 2, 2, 2, 2, 2, 2, 0]])
+    w = token_weights_from_kinds(kinds)
+    assert abs(float(w.mean()) - 1.0) < 1e-6
+    assert float(w[0, 0]) > float(w[0, 1]) > float(w[0, 2])
+    assert float(w.min()) > 0  # the floor keeps every token's pull
+
+
+def _plan(tmp_path, groups, name="model.layers.0.mlp.down_proj.weight", cols=128):
+    p = tmp_path / "plan.json"
+    p.write_text(json.dumps({"format": "rowgroup-plan-1", "groups": [dict(g, matrix=name, columns=cols) for g in groups]}))
+    return p
+
+
+def test_row_plan_validation(tmp_path):
+    from lookatmyquant_amd.rowplan import load_row_plan, write_row_plan
+
+    shape = {"model.layers.0.mlp.down_proj.weight": (128, 128)}
+    ok = _plan(tmp_path, [{"group": 0, "rows": list(range(64)), "bits": 2}, {"group": 1, "rows": list(range(64, 128)), "bits": 3}])
+    plan, manifest = load_row_plan(ok, shape)
+    assert [g["bits"] for g in plan["model.layers.0.mlp.down_proj.weight"]] == [2, 3] and manifest["groups"] == 2
+    bad_cases = [
+        [{"group": 0, "rows": list(range(64)), "bits": 2}],                                     # rows not covered
+        [{"group": 0, "rows": list(range(100)), "bits": 2}, {"group": 1, "rows": list(range(100, 128)), "bits": 2}],  # not x64
+        [{"group": 0, "rows": list(range(128)), "bits": 5}],                                    # width
+        [{"group": 1, "rows": list(range(128)), "bits": 2}],                                    # group ids
+        [{"group": 0, "rows": list(range(64)), "bits": 2}, {"group": 1, "rows": list(range(64)), "bits": 2}],  # overlap
+    ]
+    for groups in bad_cases:
+        with pytest.raises(ValueError):
+            load_row_plan(_plan(tmp_path, groups), shape)
+    with pytest.raises(ValueError):
+        load_row_plan(_plan(tmp_path, [{"group": 0, "rows": list(range(128)), "bits": 2}], name="unknown"), shape)
+    from lookatmyquant_amd import synthetic
+
+    plans = {"m": synthetic.row_plan(960, 7)}
+    write_row_plan(tmp_path / "w.json", plans, {"m": (960, 960)})
+    back, _ = load_row_plan(tmp_path / "w.json", {"m": (960, 960)})
+    bpw = sum(len(g["rows"]) * g["bits"] for g in back["m"]) / 960
+    assert 1.0 <= bpw <= 4.0
+
+
+def test_quantize_row_groups_rejects_bad_groups():
+    from lookatmyquant_amd.quantize import quantize_row_groups
+
+    W = torch.zeros(128, 8, dtype=torch.float64)
+    never = lambda rows, bits: (_ for _ in ()).throw(AssertionError("must not be called"))
+    with pytest.raises(ValueError):
+        quantize_row_groups(W, [{"rows": list(range(64)), "bits": 2}], never, 1, False)
+    with pytest.raises(ValueError):
+        quantize_row_groups(W, [{"rows": list(range(128)), "bits": 6}], never, 1, False)
+    with pytest.raises(ValueError):
+        quantize_row_groups(W, [{"rows": list(range(16)), "bits": 2}] * 9, never, 1, False)
+
+
+def test_trellis_states_recovers_distinct_values():
+    from lookatmyquant_amd.quantize import trellis_states
+    from lookatmyquant_amd.tables import load_table
+
+    t = torch.from_numpy(load_table(12, 3).copy())
+    st = torch.randint(0, 4096, (5, 7))
+    assert torch.equal(trellis_states(t[st], t).long(), st)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    r = subprocess.run([sys.executable, str(REPO / "bench.py"), "--gpus", "2"], capture_output=True, text=True)
+    assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_bench_workload_counts():
+    sys.path.insert(0, str(REPO))
+    import bench
+
+    assert sum(bench.row_steps(960, 16, 8, 128)) == 1432  # (n/16 - 1) * 24 + 16
+    assert sum(bench.row_steps(9728, 16, 8, 128)) == 14584
+    assert bench.viterbi_ops_per_row_step(16, 2) == 245760

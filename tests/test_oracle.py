@@ -1,0 +1,262 @@
+"""The CPU oracle pinned: against the reference's own vectors (tests/golden, written from the reference by
+tests/golden/make_golden.py), against brute force on tiny trellises, and against identities the mathematics fixes
+(least-squares refit, the H = c*I composition, closed-form KL, Max 1960). CPU only."""
+
+import itertools
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+
+# ----------------------------------------------------------------------------- Viterbi
+
+
+@pytest.mark.parametrize("k", [1, 2, 3, 4])
+def test_viterbi_matches_reference_vectors(golden, tables, k):
+    g = golden("viterbi")
+    x = g[f"L12_k{k}_x"]
+    assert np.array_equal(O.viterbi(x, tables[k], 12, k), g[f"L12_k{k}_free"])
+    assert np.array_equal(O.viterbi(x, tables[k], 12, k, start=g[f"L12_k{k}_start"]), g[f"L12_k{k}_fixed"])
+
+
+def test_viterbi_L16_fp16_table_matches_reference(golden):
+    g = golden("viterbi")
+    got = O.viterbi(g["L16_k2_x"], g["L16_k2_table"], 16, 2, start=g["L16_k2_start"])
+    assert np.array_equal(got, g["L16_k2_fixed"])
+
+
+@pytest.mark.parametrize("L,k", [(8, 2), (6, 1), (9, 3)])
+def test_viterbi_tie_rules_match_reference(golden, L, k):
+    g = golden("viterbi")
+    p = f"ties_L{L}_k{k}_"
+    assert np.array_equal(O.viterbi(g[p + "x"], g[p + "table"], L, k), g[p + "free"])
+    assert np.array_equal(O.viterbi(g[p + "x"], g[p + "table"], L, k, start=g[p + "start"]), g[p + "fixed"])
+
+
+def _paths(L, k, T, start=None):
+    """Every path of T states (first state free, or continuing from `start`)."""
+    firsts = range(1 << L) if start is None else [((start << k) | b) & ((1 << L) - 1) for b in range(1 << k)]
+    for s0 in firsts:
+        for bits in itertools.product(range(1 << k), repeat=T - 1):
+            s, path = s0, [s0]
+            for b in bits:
+                s = ((s << k) | b) & ((1 << L) - 1)
+                path.append(s)
+            yield path
+
+
+def test_viterbi_is_optimal_by_brute_force():
+    """tests/test_codes.py:101-117 of the reference: the path cost equals the best over all paths."""
+    rng = np.random.default_rng(0)
+    L, k, T = 4, 1, 7
+    v = rng.standard_normal(1 << L)
+    X = rng.standard_normal((5, T))
+    st = O.viterbi(X, v, L, k)
+    v32, X32 = v.astype(np.float32), X.astype(np.float32)
+    for r in range(len(X)):
+        best = min(sum((float(X32[r, t]) - float(v32[s])) ** 2 for t, s in enumerate(p)) for p in _paths(L, k, T))
+        got = sum((float(X32[r, t]) - float(v32[s])) ** 2 for t, s in enumerate(st[r]))
+        assert abs(got - best) < 1e-5
+        assert all((st[r][t] >> k) == (st[r][t - 1] & ((1 << (L - k)) - 1)) for t in range(1, T))
+
+
+@pytest.mark.parametrize("L,k,start", [(4, 1, None), (5, 2, None), (4, 2, 9), (6, 2, 17)])
+def test_viterbi_ties_by_brute_force(L, k, start):
+    """With small-integer values every float32 sum is exact, so the path the search keeps is determined by its
+    rules alone: among minimal-cost paths the lowest final state, then at each earlier step the predecessor with
+    the lowest top bits (torch's min returns the first minimum). Brute force over all paths with that order."""
+    rng = np.random.default_rng(L * 100 + k)
+    T = 6
+    v = rng.integers(-2, 3, 1 << L).astype(np.float64)
+    R = 1 << (L - k)
+    for _ in range(6):
+        x = rng.integers(-3, 4, T).astype(np.float64)
+        st = O.viterbi(x[None], v, L, k, start=None if start is None else [start])[0]
+
+        def key(p):
+            cost = sum((x[t] - v[s]) ** 2 for t, s in enumerate(p))
+            tops = tuple(p[t - 1] // R for t in range(T - 1, 0, -1))  # h of each step, last step first
+            return (cost, p[-1]) + tops
+
+        want = min(_paths(L, k, T, start), key=key)
+        assert list(st) == list(want), (list(st), want)
+
+
+# ----------------------------------------------------------------------------- the sweeps
+
+
+def _spd(n, seed, N=None):
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((N or 3 * n, n)) * np.abs(rng.standard_t(4, n))
+    return X.T @ X / len(X)
+
+
+def test_ldlq_trellis_matches_reference_vectors(golden, tables, config12):
+    """Config 2 rows (rows are independent given H): the reference's states, bit for bit."""
+    W, H = config12
+    g = golden("ldlq_trellis_c2_L12_k2")
+    st, S, What = O.ldlq_words_trellis(W[:96], H, tables[2], 12, 2, 201)
+    assert np.array_equal(st, g["states"][:96])
+    assert np.allclose(S, g["S"][:96], rtol=1e-14, atol=0)
+    assert np.abs(What[:8] - g["what_rows"]).max() < 1e-12 * np.abs(g["what_rows"]).max()
+
+
+@pytest.mark.parametrize("k", [1, 3, 4])
+def test_ldlq_trellis_widths_match_reference_vectors(golden, tables, config12, k):
+    W, H = config12
+    g = golden(f"ldlq_trellis_L12_k{k}_rows128")
+    st, _, _ = O.ldlq_words_trellis(W[:32], H, tables[k], 12, k, 201)
+    assert np.array_equal(st, g["states"][:32])
+
+
+def test_nested_lm3_matches_reference_vectors(golden, config12):
+    W, H = config12
+    g = golden("nested_lm3_c1")
+    idx, S, What = O.nested_lm(W, H, g["levels"], 201)
+    assert np.array_equal(idx, g["idx"].astype(np.int32))
+    assert np.abs(What[:8] - g["what_rows"]).max() < 1e-12 * np.abs(g["what_rows"]).max()
+
+
+def _refit_exact(H, W, fixed_cols, values):
+    """The least-squares form of the refit (opgraph/frame.py:539-546): given the fixed columns, the free columns
+    minimising ||(W - W_hat) X||."""
+    free = [j for j in range(W.shape[1]) if j not in set(fixed_cols)]
+    out = W.copy()
+    out[:, fixed_cols] = values
+    out[:, free] = W[:, free] + (W[:, fixed_cols] - values) @ H[np.ix_(fixed_cols, free)] @ np.linalg.inv(H[np.ix_(free, free)])
+    return out
+
+
+@pytest.mark.parametrize("kind", ["scalar", "trellis"])
+def test_sweep_is_the_least_squares_refit(kind, tables):
+    """Each column just before it is settled equals the least-squares refit of W given the columns settled before
+    it: the lazy block refit (in-block and trailing) is exact, whatever the projection chose."""
+    n, m = 40, 6
+    H = _spd(n, 1)
+    Hd, U, _ = O.environment(H)
+    rng = np.random.default_rng(2)
+    W = rng.standard_normal((m, n))
+    if kind == "scalar":
+        width = 1
+        lv = O.lloyd_max(2)
+        idx, before = O.ldlq_scalar(W, U, lv, mode=0, lazy=16, want_before=True)
+        Q = lv[idx]
+    else:
+        width = 4
+        S = O.row_scale(W)
+        st, before = O.ldlq_trellis(W, U, S, tables[2], 12, 2, width=width, look=2, lazy=16, want_before=True)
+        Q = tables[2][st] * S[:, None]
+    for j in (1, 7, 16, 23, 39):
+        j0 = j - j % width  # a block of `width` columns is settled together
+        ref = _refit_exact(Hd, W, list(range(j0)), Q[:, :j0])
+        assert np.abs(before[:, j] - ref[:, j]).max() < 1e-9
+
+
+def test_trellis_sweep_with_diagonal_H_is_the_chained_search(tables):
+    """With H = c*I the refit moves nothing, so the sweep is the chain of searches: each step's path starts from
+    the previous step's last state and sees `look` further targets, as RowTrellisCode.step does (codes.py:397-404)."""
+    m, n, width, look, lazy = 4, 70, 16, 8, 32
+    rng = np.random.default_rng(3)
+    X = rng.standard_normal((m, n))
+    S = O.row_scale(X)
+    _, U, _ = O.environment(np.eye(n) * 2.0)
+    st = O.ldlq_trellis(X, U, S, tables[2], 12, 2, width, look, lazy)
+    want = np.empty((m, n), dtype=np.int64)
+    state = np.zeros(m, dtype=np.int64)
+    for b0 in range(0, n, lazy):
+        b1 = min(b0 + lazy, n)
+        for j in range(b0, b1, width):
+            w = min(width, b1 - j)
+            a = min(look, n - j - w)
+            p = O.viterbi(X[:, j : j + w + a] / S[:, None], tables[2], 12, 2, start=state)[:, :w]
+            want[:, j : j + w] = p
+            state = p[:, -1]
+    assert np.array_equal(st, want)
+
+
+def test_sweep_lazy_equals_eager_for_scalar():
+    """The lazy run only reorders floating-point work (tests/test_grammar.py:76-91): lazy 1 (eager) and lazy 128
+    settle the same levels on a well-conditioned H."""
+    n, m = 60, 10
+    H = _spd(n, 5)
+    _, U, _ = O.environment(H)
+    W = np.random.default_rng(6).standard_normal((m, n))
+    lv = O.lloyd_max(3)
+    a = O.ldlq_scalar(W, U, lv, mode=0, lazy=1)
+    b = O.ldlq_scalar(W, U, lv, mode=0, lazy=128)
+    assert (a == b).mean() > 0.99
+
+
+def test_environment_is_the_cholesky_factor_of_the_inverse():
+    H = _spd(30, 7)
+    H[4, :] = 0
+    H[:, 4] = 0
+    Hd, U, dead = O.environment(H)
+    assert dead[4] and dead.sum() == 1 and Hd[4, 4] > 1.0
+    assert np.allclose(U, np.triu(U)) and np.all(np.diag(U) > 0)
+    assert np.abs(U.T @ U @ Hd - np.eye(30)).max() < 1e-10
+
+
+# ----------------------------------------------------------------------------- tables, transforms, statistics
+
+
+def test_lloyd_max_matches_max_1960_and_reference_bits(golden):
+    inf = np.array([math.inf])
+    for b, mse in ((1, 0.3634), (2, 0.1175), (3, 0.03455), (4, 0.009497)):  # Max (1960)
+        lv = O.lloyd_max(b)
+        bounds = np.concatenate([-inf, (lv[1:] + lv[:-1]) / 2, inf])
+        assert abs(O.gaussian_mse(bounds, lv) - mse) < 2e-4
+        assert np.abs(lv - golden("misc")[f"lloyd_max_{b}"]).max() < 1e-12
+    assert np.allclose(O.lloyd_max(2), [-1.5104, -0.4528, 0.4528, 1.5104], atol=1e-4)
+
+
+@pytest.mark.parametrize("n", [64, 320, 960, 2560])
+def test_hadamard_orders(n, golden):
+    H = O.hadamard(n)
+    assert np.abs(H @ H.T - np.eye(n)).max() < 1e-10
+    assert np.abs(np.abs(H) - 1 / math.sqrt(n)).max() < 1e-12
+    if n in (960, 2560):
+        A, B = O.hadamard_factors(n)
+        assert np.array_equal(A, golden("misc")[f"had_{n}_A"]) and np.array_equal(B, golden("misc")[f"had_{n}_B"])
+
+
+def test_hessian_is_the_weighted_sum_of_outer_products():
+    rng = np.random.default_rng(8)
+    X = rng.standard_normal((9, 5))
+    w = rng.uniform(0.1, 3, 9)
+    ref = sum(w[t] * np.outer(X[t], X[t]) for t in range(9)) / 9
+    assert np.abs(O.hessian(X, w) - ref).max() < 1e-14
+
+
+def test_kl_closed_forms():
+    """KL(p || p) = 0; for two logits the KL of two Bernoulli distributions; and KL >= 0."""
+    rng = np.random.default_rng(9)
+    r = O.bf16_bits(rng.standard_normal((4, 300)).astype(np.float32) * 3)
+    kl, mean = O.kl_rows(r, r)
+    assert np.abs(kl).max() < 1e-12
+    a = np.array([[0.5, -1.25], [2.0, 0.0]], dtype=np.float32)
+    b = np.array([[-0.75, 0.25], [1.0, 1.5]], dtype=np.float32)
+    kl, _ = O.kl_rows(O.bf16_bits(a), O.bf16_bits(b))
+    for t in range(2):
+        p = 1 / (1 + math.exp(-(a[t, 0] - a[t, 1])))
+        q = 1 / (1 + math.exp(-(b[t, 0] - b[t, 1])))
+        assert abs(kl[t] - (p * math.log(p / q) + (1 - p) * math.log((1 - p) / (1 - q)))) < 1e-12
+    q = O.bf16_bits(O.bf16_to_f32(r) + rng.standard_normal(r.shape).astype(np.float32))
+    kl, _ = O.kl_rows(r, q)
+    assert np.all(kl > 0)
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+def test_pack_trellis_matches_reference_bytes(golden, bits):
+    g = golden("misc")
+    st = g[f"pack_{bits}_states"].astype(np.int64)
+    codes = O.pack_trellis(st, bits)
+    assert np.array_equal(codes, g[f"pack_{bits}_codes"])
+    assert np.array_equal(O.unpack_trellis(codes, bits, st.shape[1]), st)
+    bad = st.copy()
+    bad[1, 5] ^= 1 << 11
+    with pytest.raises(ValueError):
+        O.pack_trellis(bad, bits)
