@@ -64,7 +64,7 @@ int lamq_viterbi_rows(const float* x, int64_t B, int T, int64_t ldx, const float
  *   states   [m, n] int32 output for columns [b0, b1) (row stride lds)
  *   Z        [m, b1-b0] float64 output: the block's refit coefficients z = E U_BB^-1 (row stride ldZ),
  *            the left operand of the trailing update
- * width divides lazy = b1-b0 except in the last block; width + look <= 32; b1 - b0 <= 256.
+ * width divides lazy = b1-b0 except in the last block; width + look <= 24; b1 - b0 <= 128.
  * Supported: 2 <= L <= 12 with 1 <= k <= min(4, L-1).
  * ---------------------------------------------------------------------------------------------- */
 int lamq_ldlq_trellis_block(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU,

@@ -12,11 +12,13 @@ typedef double lamq_d4 __attribute__((ext_vector_type(4)));
 // TRANSB: op(B)[k][j] = B[j*ldb + k]; otherwise B[k*ldb + j].
 // LOWER: C is a square diagonal block; tiles wholly above the diagonal are skipped and only
 // entries with col <= row are written.
-template <bool TRANSB, bool LOWER>
-__global__ __launch_bounds__(256) void gemm_sub_f64_kernel(double* __restrict__ C, int64_t ldc,
-                                                           const double* __restrict__ A, int64_t lda,
-                                                           const double* __restrict__ B, int64_t ldb, int64_t M,
-                                                           int64_t N, int64_t K, const int32_t* __restrict__ info)
+// OVERWRITE: C = A @ op(B) instead of C -= A @ op(B). C may then alias A (a workgroup's output rows are the rows
+// it reads, when N fits one tile column) or B (its output columns are the columns it reads, when M fits one tile
+// row): every wave finishes its reads before any wave writes.
+template <bool TRANSB, bool LOWER, bool OVERWRITE = false>
+__global__ __launch_bounds__(256) void gemm_sub_f64_kernel(double* C, int64_t ldc, const double* A, int64_t lda,
+                                                           const double* B, int64_t ldb, int64_t M, int64_t N,
+                                                           int64_t K, const int32_t* __restrict__ info)
 {
     if (info && *info != 0) return;
     const int64_t tr = (int64_t)blockIdx.y * 64, tc = (int64_t)blockIdx.x * 64;
@@ -49,6 +51,7 @@ __global__ __launch_bounds__(256) void gemm_sub_f64_kernel(double* __restrict__ 
         acc[1][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b0, acc[1][0], 0, 0, 0);
         acc[1][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc[1][1], 0, 0, 0);
     }
+    if (OVERWRITE) __syncthreads();
 #pragma unroll
     for (int ti = 0; ti < 2; ++ti)
 #pragma unroll
@@ -59,18 +62,22 @@ __global__ __launch_bounds__(256) void gemm_sub_f64_kernel(double* __restrict__ 
                 const int64_t col = wc + tj * 16 + li;
                 if (row < M && col < N && (!LOWER || col <= row)) {
                     double* p = C + row * ldc + col;
-                    *p = *p - acc[ti][tj][v];
+                    if (OVERWRITE)
+                        *p = acc[ti][tj][v];
+                    else
+                        *p = *p - acc[ti][tj][v];
                 }
             }
 }
 
-template <bool TRANSB, bool LOWER>
+template <bool TRANSB, bool LOWER, bool OVERWRITE = false>
 static int gemm_sub_f64(double* C, int64_t ldc, const double* A, int64_t lda, const double* B, int64_t ldb, int64_t M,
                         int64_t N, int64_t K, const int32_t* info, hipStream_t s)
 {
     if (M <= 0 || N <= 0 || K <= 0) return LAMQ_OK;
     dim3 grid((unsigned)cdiv(N, 64), (unsigned)cdiv(M, 64));
-    hipLaunchKernelGGL((gemm_sub_f64_kernel<TRANSB, LOWER>), grid, dim3(256), 0, s, C, ldc, A, lda, B, ldb, M, N, K, info);
+    hipLaunchKernelGGL((gemm_sub_f64_kernel<TRANSB, LOWER, OVERWRITE>), grid, dim3(256), 0, s, C, ldc, A, lda, B, ldb, M, N,
+                       K, info);
     LAMQ_LAUNCH_CHECK();
     return LAMQ_OK;
 }

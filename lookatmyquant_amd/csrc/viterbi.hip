@@ -2,8 +2,10 @@
 // block-LDLQ sweep (the search fused with the block's fp64 refit).
 #include "common.h"
 
-#define LAMQ_TV_LDS 32  // longest path whose back-pointers stay in LDS
-#define LAMQ_LAZY_MAX 256
+#define LAMQ_TV_LDS 32  // longest standalone path whose back-pointers stay in LDS
+#define LAMQ_TV_BLK 24  // longest search of the fused block (width + look): with lazy <= 128 the block kernel's
+                        // LDS stays under 40 KB, four workgroups per CU
+#define LAMQ_LAZY_MAX 128
 
 // ------------------------------------------------------------------------------------------------
 // viterbi_rows: one workgroup per row (opgraph/codes.py:151-181).
@@ -95,12 +97,12 @@ __global__ __launch_bounds__(LAMQ_NT) void ldlq_trellis_block_kernel(
 {
     using V = Vit<L, K>;
     __shared__ __align__(16) float cost[2][V::NS];
-    __shared__ uint8_t back[LAMQ_TV_LDS * V::ACT];
-    __shared__ double trow[LAMQ_LAZY_MAX + LAMQ_TV_LDS];
-    __shared__ float xs[LAMQ_TV_LDS];
-    __shared__ int path[LAMQ_TV_LDS];
-    __shared__ double es[LAMQ_TV_LDS];
-    __shared__ double zs[LAMQ_TV_LDS];
+    __shared__ uint8_t back[LAMQ_TV_BLK * V::ACT];
+    __shared__ double trow[LAMQ_LAZY_MAX + LAMQ_TV_BLK];
+    __shared__ float xs[LAMQ_TV_BLK];
+    __shared__ int path[LAMQ_TV_BLK];
+    __shared__ double es[LAMQ_TV_BLK];
+    __shared__ double zs[LAMQ_TV_BLK];
     __shared__ float red[8];
 
     const int64_t row = blockIdx.x;
@@ -178,7 +180,7 @@ extern "C" int lamq_ldlq_trellis_block(double* T, int64_t m, int64_t n, int64_t 
     if (m < 0 || n < 1 || ldT < n || ldU < n || lds < n || b0 < 0 || b1 <= b0 || b1 > n || width < 1 || look < 0)
         return LAMQ_EINVAL;
     if (ldZ < b1 - b0) return LAMQ_EINVAL;
-    if (width + look > LAMQ_TV_LDS || b1 - b0 > LAMQ_LAZY_MAX || m > 0x7fffffff) return LAMQ_EUNSUP;
+    if (width + look > LAMQ_TV_BLK || b1 - b0 > LAMQ_LAZY_MAX || m > 0x7fffffff) return LAMQ_EUNSUP;
     if (m == 0) return LAMQ_OK;
     return dispatch_lk<TrellisBlock>(L, k, T, m, n, ldT, U, ldU, S, table64, table32, b0, b1, width, look, state,
                                      states, lds, Z, ldZ, as_stream(stream));
