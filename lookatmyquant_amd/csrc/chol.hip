@@ -54,61 +54,69 @@ __global__ void prep_kernel(const double* __restrict__ H, int64_t n, int64_t ldH
 }
 
 // The nb x nb diagonal block at (k0, k0) of A (lower): its Cholesky factor Lkk, written back into A, and
-// Lkk^-1 (lower), written to Linv (ld NBK). One wave; lane i owns row i of the factorization and column i of
-// the inverse. Factorization, column c: l = sqrt(a[c][c]); a[i][c] /= l (i > c);
-// a[i][j] -= a[i][c] a[j][c] for c < j <= i. Inverse, column c: x[c] = 1/L[c][c];
-// x[i] = -(sum_{l=c}^{i-1} L[i][l] x[l]) / L[i][i] for i > c.
+// Lkk^-1 (lower), written to Linv (ld NBK). One wave, everything in registers and fully unrolled (register
+// arrays need compile-time indices); a block shorter than NBK is padded with the identity.
+// Factorization: lane i holds row i, r[j] = a[i][j]. Column c: d = a[c][c]; l[i][c] = a[i][c] / sqrt(d)
+// (l[c][c] = sqrt(d)); a[i][j] -= l[i][c] l[j][c] for j > c. Column c of L is published through LDS
+// (lt[c][i] = l[i][c]) and read back as broadcasts.
+// Inverse: lane c holds column c of X = L^-1, x = e_c initially; for l = 0..: x[l] /= l[l][l];
+// x[i] -= l[i][l] x[l] for i > l (the l[i][l] broadcast from lt).
 __global__ __launch_bounds__(64) void diag_block_kernel(double* __restrict__ A, int64_t n, int64_t k0, int nb,
                                                         double* __restrict__ Linv, int32_t* __restrict__ info)
 {
-    __shared__ double a[NBK][NBK + 1];
-    __shared__ double x[NBK][NBK + 1];
+    __shared__ __align__(16) double lt[NBK][NBK];  // lt[c][i] = L[i][c]
     if (*info != 0) return;
     const int lane = threadIdx.x;
-    for (int e = lane; e < nb * nb; e += 64) {
-        const int i = e / nb, j = e - i * nb;
-        a[i][j] = j <= i ? A[(k0 + i) * n + k0 + j] : 0.0;
+    const bool live = lane < nb;
+    double r[NBK];
+    // branch-free loads: rows and columns clamped into the block, padding selected afterwards
+    const double* Ar = A + (k0 + (live ? lane : 0)) * n + k0;
+#pragma unroll
+    for (int j = 0; j < NBK; ++j) {
+        const double v = Ar[j < nb ? j : nb - 1];
+        r[j] = (live && j < nb) ? (j <= lane ? v : 0.0) : (j == lane ? 1.0 : 0.0);
     }
-    __builtin_amdgcn_wave_barrier();
-    for (int c = 0; c < nb; ++c) {
-        const double d = a[c][c];
-        if (!(d > 0.0)) {  // uniform: every lane read the same value
-            if (lane == 0) *info = (int32_t)(k0 + c + 1);
-            return;
-        }
-        const double l = sqrt(d);
-        __builtin_amdgcn_wave_barrier();
-        double lic = 0.0;
-        if (lane > c && lane < nb) {
-            lic = a[lane][c] / l;
-            a[lane][c] = lic;
-        }
-        if (lane == c) a[c][c] = l;
-        __builtin_amdgcn_wave_barrier();
-        if (lane > c && lane < nb)
-            for (int j = c + 1; j <= lane; ++j) a[lane][j] = fma(-lic, a[j][c], a[lane][j]);
-        __builtin_amdgcn_wave_barrier();
+    int fail = 0;  // the first non-positive pivot; the loop runs on without branching, its output unused
+#pragma unroll
+    for (int c = 0; c < NBK; ++c) {
+        lt[c][lane] = r[c];
+        const double d = lt[c][c];
+        fail = (fail == 0 && !(d > 0.0)) ? (int)(k0 + c + 1) : fail;
+        const double sd = sqrt(d);
+        const double lic = lane > c ? r[c] / sd : (lane == c ? sd : 0.0);
+        r[c] = lic;
+        lt[c][lane] = lic;
+#pragma unroll
+        for (int j = c + 1; j < NBK; ++j) r[j] = fma(-lic, lt[c][j], r[j]);
+        // the empty asm pins this step's updates here: without it the compiler sinks them into per-column dot
+        // products (a left-looking order) that keep every broadcast value live. One group per step, after all of
+        // the step's loads, so the loads still issue back to back.
+#pragma unroll
+        for (int j = c + 1; j < NBK; ++j) asm volatile("" : "+v"(r[j]));
     }
-    // inverse: lane c computes column c
-    if (lane < nb) {
-        const int c = lane;
-        x[c][c] = 1.0 / a[c][c];
-        for (int i = c + 1; i < nb; ++i) {
-            double acc = 0.0;
-            for (int l = c; l < i; ++l) acc = fma(a[i][l], x[l][c], acc);
-            x[i][c] = -acc / a[i][i];
-        }
+    if (fail != 0) {  // uniform
+        if (lane == 0) *info = fail;
+        return;
     }
-    __builtin_amdgcn_wave_barrier();
-    for (int e = lane; e < nb * nb; e += 64) {
-        const int i = e / nb, j = e - i * nb;
-        if (j <= i) {
-            A[(k0 + i) * n + k0 + j] = a[i][j];
-            Linv[i * NBK + j] = x[i][j];
-        } else {
-            Linv[i * NBK + j] = 0.0;
-        }
+    if (live) {
+        double* Aw = A + (k0 + lane) * n + k0;
+#pragma unroll
+        for (int j = 0; j < NBK; ++j)
+            if (j < nb && j <= lane) Aw[j] = r[j];
     }
+    double x[NBK];
+#pragma unroll
+    for (int i = 0; i < NBK; ++i) x[i] = i == lane ? 1.0 : 0.0;
+#pragma unroll
+    for (int l = 0; l < NBK; ++l) {
+        x[l] = x[l] / lt[l][l];
+#pragma unroll
+        for (int i = l + 1; i < NBK; ++i) x[i] = fma(-lt[l][i], x[l], x[i]);
+#pragma unroll
+        for (int i = l + 1; i < NBK; ++i) asm volatile("" : "+v"(x[i]));
+    }
+#pragma unroll
+    for (int i = 0; i < NBK; ++i) Linv[i * NBK + lane] = x[i];
 }
 
 __global__ void identity_kernel(double* __restrict__ X, int64_t n, int64_t ldX)

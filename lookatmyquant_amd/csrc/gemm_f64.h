@@ -33,23 +33,44 @@ __global__ __launch_bounds__(256) void gemm_sub_f64_kernel(double* C, int64_t ld
         for (int j = 0; j < 2; ++j) acc[i][j] = lamq_d4{0.0, 0.0, 0.0, 0.0};
     const int64_t r0 = wr + li, r1 = wr + 16 + li, c0 = wc + li, c1 = wc + 16 + li;
     const bool vr0 = r0 < M, vr1 = r1 < M, vc0 = c0 < N, vc1 = c1 < N;
-    for (int64_t k0 = 0; k0 < K; k0 += 4) {
-        const int64_t kk = k0 + lk;
-        const bool vk = kk < K;
-        const double a0 = (vr0 && vk) ? A[r0 * lda + kk] : 0.0;
-        const double a1 = (vr1 && vk) ? A[r1 * lda + kk] : 0.0;
-        double b0, b1;
-        if (TRANSB) {
-            b0 = (vc0 && vk) ? B[c0 * ldb + kk] : 0.0;
-            b1 = (vc1 && vk) ? B[c1 * ldb + kk] : 0.0;
-        } else {
-            b0 = (vc0 && vk) ? B[kk * ldb + c0] : 0.0;
-            b1 = (vc1 && vk) ? B[kk * ldb + c1] : 0.0;
+    // k advances in chunks of KC = 16 (four MFMA steps); the next chunk's operands are loaded into registers
+    // while the current chunk's MFMAs run, so one memory latency is paid per chunk, overlapped.
+    constexpr int KC = 16;
+    double pa0[4], pa1[4], pb0[4], pb1[4];
+    auto load = [&](int64_t kb) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int64_t kk = kb + 4 * s + lk;
+            const bool vk = kk < K;
+            pa0[s] = (vr0 && vk) ? A[r0 * lda + kk] : 0.0;
+            pa1[s] = (vr1 && vk) ? A[r1 * lda + kk] : 0.0;
+            if (TRANSB) {
+                pb0[s] = (vc0 && vk) ? B[c0 * ldb + kk] : 0.0;
+                pb1[s] = (vc1 && vk) ? B[c1 * ldb + kk] : 0.0;
+            } else {
+                pb0[s] = (vc0 && vk) ? B[kk * ldb + c0] : 0.0;
+                pb1[s] = (vc1 && vk) ? B[kk * ldb + c1] : 0.0;
+            }
         }
-        acc[0][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b0, acc[0][0], 0, 0, 0);
-        acc[0][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b1, acc[0][1], 0, 0, 0);
-        acc[1][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b0, acc[1][0], 0, 0, 0);
-        acc[1][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc[1][1], 0, 0, 0);
+    };
+    load(0);
+    for (int64_t k0 = 0; k0 < K; k0 += KC) {
+        double a0[4], a1[4], b0[4], b1[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            a0[s] = pa0[s];
+            a1[s] = pa1[s];
+            b0[s] = pb0[s];
+            b1[s] = pb1[s];
+        }
+        if (k0 + KC < K) load(k0 + KC);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            acc[0][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0[s], b0[s], acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0[s], b1[s], acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1[s], b0[s], acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1[s], b1[s], acc[1][1], 0, 0, 0);
+        }
     }
     if (OVERWRITE) __syncthreads();
 #pragma unroll

@@ -125,7 +125,7 @@ def test_trailing_update_matches_oracle_order(E):
     assert err < 1e-14
 
 
-@pytest.mark.parametrize("n", [64, 100, 960])
+@pytest.mark.parametrize("n", [64, 100, 200, 960])
 def test_chol_inv_upper(E, n):
     rng = np.random.default_rng(n)
     X = rng.standard_normal((2 * n + 50, n))
@@ -149,13 +149,18 @@ def test_chol_inv_upper(E, n):
     assert np.abs(Ug.T @ Ug @ Hd_o - np.eye(n)).max() < 1e-9
 
 
-def test_chol_inv_upper_reports_non_pd(E):
-    H = -np.eye(40)
-    say("chol_inv_upper not positive definite")
-    _, _, _, info = E.chol_inv_upper(cuda(H), raise_on_fail=False)
-    assert int(info.item()) > 0
+@pytest.mark.parametrize("n", [40, 130])
+def test_chol_inv_upper_reports_non_pd(E, n):
+    """H[0][0] < 0 is the last pivot of the reversed factorization (the last diagonal block when n > 64): info
+    names it, as LAPACK's info names the first non-positive leading minor, and U comes back zero."""
+    H = np.eye(n)
+    H[0, 0] = -5.0
+    say(f"chol_inv_upper not positive definite, n={n}")
+    _, U, _, info = E.chol_inv_upper(cuda(H), damp=0.0, raise_on_fail=False)
+    assert int(info.item()) == n
+    assert float(U.abs().max()) == 0.0
     with pytest.raises(E.LinAlgError):
-        E.chol_inv_upper(cuda(H))
+        E.chol_inv_upper(cuda(H), damp=0.0)
 
 
 @pytest.mark.parametrize("m,n,seed", [(48, 960, 201), (20, 2560, 1301), (8, 4096, 7), (4, 9728, 3301)])
