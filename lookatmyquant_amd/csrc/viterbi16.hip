@@ -47,6 +47,20 @@ __device__ __forceinline__ float cval(const uint32_t (&Ch)[SPT / 2], int i)
     return (i & 1) ? h2f_hi(Ch[i >> 1]) : h2f_lo(Ch[i >> 1]);
 }
 
+// x - C[i] as fma(C[i], -1, x) with C[i] read in place from its fp16 half of the register (v_fma_mix_f32):
+// one rounding of the exact difference, the value of the float32 subtraction x - float(C[i]). Written as asm
+// because the compiler turns fma(c, -1, x) back into a conversion and a subtraction.
+template <int SPT>
+__device__ __forceinline__ float xmc(float x, const uint32_t (&Ch)[SPT / 2], int i)
+{
+    float d;
+    if (i & 1)
+        asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(Ch[i >> 1]), "v"(x));
+    else
+        asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[0,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(Ch[i >> 1]), "v"(x));
+    return d;
+}
+
 // Search one path of TV steps; thread 0 writes path[0..TV). xs: TV float32 targets. start < 0: free first state.
 // xbuf: QS floats of LDS (indexed through swz). back: (TV-1)*1024 words (LDS or global). red: 32 words of LDS.
 template <int L, int K>
@@ -66,10 +80,12 @@ __device__ void viterbi_big(const float* xs, int TV, uint32_t (&Ch)[VBig<L, K>::
     }
     float xprev = xs[0];
     for (int t = 1; t < TV; ++t) {
+        // best[j]: minimum so far of group j = q*GQ + g; hw[j]: its winning h, already shifted to bits [j*K, j*K+K).
+        // With more than 16 groups a thread has no registers to spare for hw: the h go straight into bits.
+        constexpr bool SEP = V::G <= 16;
         float best[V::G];
-        uint32_t bits = 0;  // the winning h of group j = q*GQ + g in bits [j*K, j*K+K)
-#pragma unroll
-        for (int j = 0; j < V::G; ++j) best[j] = __builtin_inff();
+        uint32_t hw[SEP ? V::G : 1];
+        uint32_t bits = 0;  // the winning h of group j in bits [j*K, j*K+K)
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
 #pragma unroll
@@ -78,7 +94,7 @@ __device__ void viterbi_big(const float* xs, int TV, uint32_t (&Ch)[VBig<L, K>::
                 float c[V::SQ];
 #pragma unroll
                 for (int i = 0; i < V::SQ; ++i) {
-                    const float d = xprev - cval<V::SPT>(Ch, p * V::SQ + i);
+                    const float d = xmc<V::SPT>(xprev, Ch, p * V::SQ + i);
                     const float dd = d * d;
                     c[i] = bprev[p * V::GQ + i / V::NB] + dd;
                 }
@@ -95,12 +111,26 @@ __device__ void viterbi_big(const float* xs, int TV, uint32_t (&Ch)[VBig<L, K>::
 #pragma unroll
                     for (int g = 0; g < V::GQ; ++g) {
                         const int j = q * V::GQ + g;
-                        const uint32_t mk = (uint32_t)(V::NB - 1) << (j * K);
-                        const uint32_t with_h = (bits & ~mk) | ((uint32_t)h << (j * K));
-                        if (c[g] < best[j]) { best[j] = c[g]; bits = with_h; }
+                        if (h == 0) {  // the first predecessor of every group (phases visit h in increasing order)
+                            best[j] = c[g];
+                            if (SEP) hw[j] = 0;
+                        } else {
+                            const bool lt = c[g] < best[j];  // strict: the lowest h keeps a tie
+                            best[j] = lt ? c[g] : best[j];
+                            if (SEP) {
+                                hw[j] = lt ? (uint32_t)h << (j * K) : hw[j];
+                            } else {
+                                const uint32_t mk = (uint32_t)(V::NB - 1) << (j * K);
+                                bits = lt ? ((bits & ~mk) | ((uint32_t)h << (j * K))) : bits;
+                            }
+                        }
                     }
                 }
             __syncthreads();
+        }
+        if (SEP) {
+#pragma unroll
+            for (int j = 0; j < V::G; ++j) bits |= hw[j];
         }
 #pragma unroll
         for (int j = 0; j < V::G; ++j) bprev[j] = best[j];
@@ -116,7 +146,7 @@ __device__ void viterbi_big(const float* xs, int TV, uint32_t (&Ch)[VBig<L, K>::
     for (int q = 0; q < 4; ++q)
 #pragma unroll
         for (int i = 0; i < V::SQ; ++i) {
-            const float d = xprev - cval<V::SPT>(Ch, q * V::SQ + i);
+            const float d = xmc<V::SPT>(xprev, Ch, q * V::SQ + i);
             const float dd = d * d;
             const float c = bprev[q * V::GQ + i / V::NB] + dd;
             if ((q == 0 && i == 0) || c < bv) { bv = c; bi = q * V::QS + V::SQ * tid + i; }
