@@ -6,7 +6,7 @@ trellis (fused Viterbi + in-block refit kernel per 128-column block, fp64 MFMA t
 the packed codes. W and H are resident in HBM when the timed region starts (the calibration capture that produces
 H is not part of a step).
 
-    python bench.py [--steps K] [--warmup W] [--L 16|12] [--k 2] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--L 16|12] [--k 2] [--no-cpu] [--workload c2|c3|c4] [--copy-probe MiB]
 
 The default is the benchmark configuration (config 2: 16-bit states, the fp16 quantile table); --L 12 runs the
 reference's own production trellis (the fitted 12-bit tables).
@@ -14,6 +14,15 @@ reference's own production trellis (the fitted 12-bit tables).
 Prints one JSON line: weights quantized per second (metric value), Viterbi rows/s, the roofline of the dominant
 kernel (the fused trellis block kernel) measured with HIP events on its stream, and the CPU oracle timed on a
 bounded row sample of the same workload.
+
+The other workloads measure the remaining kernels at their configurations' shapes (one JSON line each, with a
+roofline per kernel from HIP events):
+  --workload c3  config 3, one Qwen3.5-4B-shaped MLP block: Hessians of the gate/up input [131072, 2560] and of the
+                 down input [131072, 9728] with digit token weights, one factor per stage, the row-plan sweeps of
+                 gate/up [9728, 2560] and down [2560, 9728] (bits 1-4, 2.3 bpw) and the packed codes per group
+  --workload c4  config 4, one KL evaluation over paired bf16 logits [8192, 151936] per step
+--copy-probe M ends the run with one device-to-device copy of M MiB, the known-size reference for the HBM byte
+counters of a profiler run.
 """
 
 from __future__ import annotations
@@ -85,6 +94,182 @@ def cpu_baseline(W, H, table, L, k, in_seed, budget_s=12.0):
             "seconds_total_extrapolated": round(total, 3)}
 
 
+MFMA_F64_PEAK_TFLOPS = 78.6
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+HBM_PEAK_GBS = 8000.0
+
+
+def kernel_line(ms_per_step: float, work: float, peak: float, unit: str, bound: str, scale: float) -> dict:
+    """Roofline entry of one kernel: `work` algorithmic units per step (flops, ops or bytes), `scale` units per
+    reported unit (1e12 for TFLOP/s and TOP/s, 1e9 for GB/s)."""
+    achieved = work / (ms_per_step * 1e-3) / scale if ms_per_step > 0 else 0.0
+    return {"bound": bound, "ms_per_step": round(ms_per_step, 4), "achieved": round(achieved, 3), "peak": peak,
+            "unit": unit, "frac": round(achieved / peak, 4)}
+
+
+def timed(events: dict, key: str):
+    """Context manager recording a torch.cuda.Event pair on the current stream under events[key]."""
+    import contextlib
+
+    import torch
+
+    @contextlib.contextmanager
+    def cm():
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        yield
+        b.record()
+        events.setdefault(key, []).append((a, b))
+
+    return cm()
+
+
+def copy_probe(mib: int):
+    """One device-to-device copy of `mib` MiB: reads and writes that many bytes once."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    a = torch.ones(n, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    print(f"copy probe: {mib} MiB device-to-device", file=sys.stderr)
+
+
+def trail_flops(m: int, n: int, lazy: int = 128) -> float:
+    """Algorithmic flops of the trailing updates of one sweep: sum over blocks of 2 m (b1 - b0) (n - b1)."""
+    return float(sum(2 * m * (min(b0 + lazy, n) - b0) * (n - min(b0 + lazy, n)) for b0 in range(0, n, lazy)))
+
+
+def run_c3(args):
+    """Config 3: one MLP block (gate/up stage on the hidden input, down stage on the intermediate)."""
+    import numpy as np
+    import torch
+
+    from lookatmyquant_amd import engine as E
+    from lookatmyquant_amd import synthetic
+    from lookatmyquant_amd.quantize import quantize_stage_row_groups
+    from lookatmyquant_amd.tables import load_table, quantile_table
+
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    L = args.L
+    hid, inter, N = 2560, 9728, 131072
+    t0 = time.perf_counter()
+    Wg = torch.from_numpy(synthetic.weight(inter, hid, 0.015, 301)).to(dev).bfloat16()
+    Wu = torch.from_numpy(synthetic.weight(inter, hid, 0.015, 302)).to(dev).bfloat16()
+    Wd = torch.from_numpy(synthetic.weight(hid, inter, 0.015, 303)).to(dev).bfloat16()
+    X1 = torch.from_numpy(synthetic.calibration(N, hid, 304, 305)).to(dev).bfloat16()
+    # the down input is the block's intermediate: silu(X1 Wg^T) * (X1 Wu^T) in bf16, computed in slices
+    X2 = torch.empty(N, inter, dtype=torch.bfloat16, device=dev)
+    for b in range(0, N, 16384):
+        x = X1[b : b + 16384]
+        X2[b : b + 16384] = torch.nn.functional.silu(x @ Wg.t().contiguous()) * (x @ Wu.t().contiguous())
+    w = torch.from_numpy(synthetic.digit_weights(N, 306)).to(dev)
+    plans = {"gate": synthetic.row_plan(inter, 307), "up": synthetic.row_plan(inter, 308),
+             "down": synthetic.row_plan(hid, 309)}
+    tables = {b: (quantile_table(16, 0) if L == 16 else load_table(12, b)) for b in (1, 2, 3, 4)}
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t0
+    stages = [({"gate": Wg, "up": Wu}, X1, 1301), ({"down": Wd}, X2, 3301)]  # in_seed of layer 0's stages
+
+    def step(events):
+        out = {}
+        for targets, X, in_seed in stages:
+            n = X.shape[1]
+            with timed(events, f"hessian_{n}"):
+                H = E.hessian(X, w)
+            sub = {nm: W.double() for nm, W in targets.items()}
+            res = quantize_stage_row_groups(sub, {nm: plans[nm] for nm in sub}, H, in_seed, L=L, tables=tables,
+                                            events=events, chol_events=(events, f"chol_{n}"))
+            for nm, (st, S) in res.items():
+                for g in plans[nm]:
+                    rows = torch.as_tensor(g["rows"], device=dev)
+                    out[(nm, g["group"])] = E.pack_trellis(st.index_select(0, rows).contiguous(), g["bits"], L,
+                                                           check_paths=False)
+        return out
+
+    for _ in range(args.warmup):
+        step({})
+    torch.cuda.synchronize()
+    events: dict = {}
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        out = step(events)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t1) * 1e3 / args.steps
+    bad = sum(int(b.item()) for _, b in out.values())
+    assert bad == 0
+    weights = 2 * inter * hid + hid * inter
+    per = lambda key: sum(E.event_ms(events, key)) / args.steps
+    kern = {}
+    for n in (hid, inter):
+        kern[f"hessian_n{n}"] = kernel_line(per(f"hessian_{n}"), float(N) * n * (n + 1), MFMA_BF16_PEAK_TFLOPS,
+                                            "TFLOP/s", "mfma", 1e12)
+        kern[f"chol_inv_upper_n{n}"] = kernel_line(per(f"chol_{n}"), 4.0 * n ** 3 / 3, MFMA_F64_PEAK_TFLOPS,
+                                                   "TFLOP/s", "mfma", 1e12)
+    # trellis block kernels and trailing updates: every sweep is one width's rows of a stage
+    row_steps_total, ops_total, trail_total = 0.0, 0.0, 0.0
+    for targets, X, _ in stages:
+        n = X.shape[1]
+        for bits in (1, 2, 3, 4):
+            m = sum(len(g["rows"]) for nm in targets for g in plans[nm] if g["bits"] == bits)
+            if m == 0:
+                continue
+            rs = m * sum(row_steps(n, 16, 8, 128))
+            row_steps_total += rs
+            ops_total += rs * viterbi_ops_per_row_step(L, bits)
+            trail_total += trail_flops(m, n)
+    kern["trellis_block"] = kernel_line(per("block"), ops_total, round(VALU_PEAK_TOPS, 1), "TOP/s", "valu", 1e12)
+    kern["trailing_update"] = kernel_line(per("trailing"), trail_total, MFMA_F64_PEAK_TFLOPS, "TFLOP/s", "mfma", 1e12)
+    print(json.dumps({
+        "metric": METRIC, "value": round(weights / (ms * 1e-3), 1), "unit": "weights/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16->f32 (Hessian), f64/f32 (sweep)", "data": "synthetic",
+        "config": {"workload": f"config 3: Qwen3.5-4B-shaped MLP block, gate/up [9728, 2560] and down [2560, 9728], "
+                               f"Hessians from {N} bf16 tokens (10% digit tokens weighted 10x), row plans 2.3 bpw "
+                               f"bits 1-4, row trellis L={L}, one factor per stage, packed codes per group",
+                   "L": L, "tokens": N, "weights": weights, "setup_s": round(setup_s, 1)},
+        "viterbi_row_steps_per_s": round(row_steps_total / (ms * 1e-3), 1),
+        "kernels": kern}))
+
+
+def run_c4(args):
+    """Config 4: KL(p_ref || p_q) over paired bf16 logits [8192, 151936], one evaluation per step."""
+    import torch
+
+    from lookatmyquant_amd import engine as E
+
+    torch.cuda.set_device(0)
+    T, V = 8192, 151936
+    g1 = torch.Generator(device="cuda").manual_seed(401)
+    g2 = torch.Generator(device="cuda").manual_seed(402)
+    ref = (torch.randn(T, V, generator=g1, device="cuda") * 3.0).bfloat16()
+    q = (ref.float() + 0.3 * torch.randn(T, V, generator=g2, device="cuda")).bfloat16()
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        E.kl_rows(ref, q)
+    torch.cuda.synchronize()
+    events: dict = {}
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        with timed(events, "kl"):
+            kl, sums = E.kl_rows(ref, q)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t1) * 1e3 / args.steps
+    per = sum(E.event_ms(events, "kl")) / args.steps
+    nbytes = 2.0 * T * V * 2 + 4 * T
+    print(json.dumps({
+        "metric": "KL evaluations/s (per-token KL over paired bf16 logits)", "value": round(1e3 / ms, 2),
+        "unit": "evals/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16->f32", "data":
+        "synthetic (torch CUDA generator, seeds 401/402; ref ~ N(0, 3^2), q = ref + N(0, 0.3^2))",
+        "config": {"workload": "config 4: one KL evaluation over [8192, 151936] bf16 logit pairs per step",
+                   "tokens": T, "vocab": V, "mean_kl": float(sums[0] / sums[1])},
+        "kernels": {"kl_rows": kernel_line(per, nbytes, HBM_PEAK_GBS, "GB/s", "hbm", 1e9)}}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -93,12 +278,24 @@ def main():
     ap.add_argument("--L", type=int, default=16)
     ap.add_argument("--k", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--workload", choices=("c2", "c3", "c4"), default="c2")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MiB")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the per-matrix hot path runs on one MI355X here (rows would shard across "
               "GPUs with no communication; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "c3":
+        run_c3(args)
+    elif args.workload == "c4":
+        run_c4(args)
+    else:
+        run_c2(args)
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
 
+
+def run_c2(args):
     import numpy as np
     import torch
 

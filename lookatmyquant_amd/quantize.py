@@ -207,16 +207,27 @@ def stage_statistics(Xq_chunks, w_chunks=None, Xr_chunks=None):
 
 
 def quantize_stage_row_groups(targets: dict, groups: dict, H: torch.Tensor, in_seed: int, L: int = 12,
-                              width: int = 16, look: int = 8, tables: dict | None = None, events: dict | None = None):
+                              width: int = 16, look: int = 8, tables: dict | None = None, events: dict | None = None,
+                              chol_events: tuple | None = None):
     """Every matrix of a stage, row group by row group, with the row trellis at the group's width: the same result
     as quantize_row_groups(target, groups, round_group) with round_group = the tr<bits> word of (target[rows], H,
     in_seed, out_rot=False), for each matrix. targets: {name: W [m, n]}; groups: {name: [{"rows", "bits"}]};
     tables: {bits: float64 table} (default: the cached L = 12 tables). Returns {name: (states int32 [m, n] on the
-    GPU, S float64 [m] on the GPU)}; the codes entries and reconstructions follow from them."""
+    GPU, S float64 [m] on the GPU)}; the codes entries and reconstructions follow from them. events / chol_events
+    ((dict, key)): torch.cuda.Event pairs around the sweep kernels / the factorization, for timing."""
     dev = E._abi.device()
     names = list(targets)
     Hr = E.rotate_hessian(torch.as_tensor(H).to(dev, torch.float64).contiguous(), in_seed)
-    _, U, dead, _ = E.chol_inv_upper(Hr)
+    ev = None
+    if chol_events is not None:
+        ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        ev[0].record()
+    _, U, dead, info = E.chol_inv_upper(Hr, raise_on_fail=chol_events is None)
+    if ev is not None:
+        ev[1].record()
+        chol_events[0].setdefault(chol_events[1], []).append(ev)
+        if int(info.item()):
+            raise E.LinAlgError(f"linalg.cholesky: the leading minor of order {int(info.item())} is not positive-definite")
     X_all, S_all = {}, {}
     for nm in names:
         W = torch.as_tensor(targets[nm]).to(dev, torch.float64).contiguous()
