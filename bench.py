@@ -94,6 +94,10 @@ def cpu_baseline(W, H, table, L, k, in_seed, budget_s=12.0):
             "seconds_total_extrapolated": round(total, 3)}
 
 
+# HBM bytes per launch of the dominant kernel, from two rocprofv3 counter runs (FETCH_SIZE, WRITE_SIZE) scaled by a
+# 1 GiB copy's readings (profiles/ldlq_trellis_block_big_config2_L16_k2.md); keyed by (kernel, L, k).
+MEASURED_TRAFFIC = {("ldlq_trellis_block_big_kernel", 16, 2): 16627978}
+
 MFMA_F64_PEAK_TFLOPS = 78.6
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 HBM_PEAK_GBS = 8000.0
@@ -347,6 +351,7 @@ def run_c2(args):
     achieved = ops_step / (blk_ms_step * 1e-3) / 1e12
     value = m * n / (ms * 1e-3)
     rows_per_s = m / (ms * 1e-3)
+    kname = "ldlq_trellis_block_big_kernel" if L >= E.BIG_L else "ldlq_trellis_block_kernel"
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "weights/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
@@ -357,9 +362,9 @@ def run_c2(args):
                    "table": "reference e-means L=12 table" if L == 12 else f"fp16 Gaussian quantiles, 2^{L} entries"},
         "viterbi_rows_per_s": round(rows_per_s, 1),
         "viterbi_row_steps_per_s": round(m * sum(per_block) / (ms * 1e-3), 1),
-        "roofline": {"kernel": "ldlq_trellis_block_big_kernel" if L >= E.BIG_L else "ldlq_trellis_block_kernel", "bound": "valu", "achieved": round(achieved, 3),
+        "roofline": {"kernel": kname, "bound": "valu", "achieved": round(achieved, 3),
                      "peak": round(VALU_PEAK_TOPS, 1), "unit": "TOP/s", "frac": round(achieved / VALU_PEAK_TOPS, 4),
-                     "traffic": None, "launches_per_step": len(per_block),
+                     "traffic": MEASURED_TRAFFIC.get((kname, L, k)), "launches_per_step": len(per_block),
                      "avg_launch_us": round(1e3 * sum(blk) / len(blk), 2),
                      "ops_per_row_step": viterbi_ops_per_row_step(L, k)},
         "phase_ms": {"block_kernels": round(blk_ms_step, 4), "trailing_updates": round(sum(trl) / args.steps, 4)},
