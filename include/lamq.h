@@ -163,9 +163,12 @@ int lamq_row_rms(const double* X, int64_t rows, int64_t n, int64_t ldx, double* 
  * opgraph/frame.py:498-505.
  *   X [N, n] bf16 (row stride ldx; n and ldx even, X 4-byte aligned);  w NULL (every w_t = 1) or
  *   [N] float32;  H [n, n] float32 (row stride ldH).
+ * Without w, and with n and ldx multiples of 8 and X 16-byte aligned, the 256x256-tile kernel runs.
  * With w the weighted operand is split into two bf16 parts (hi + lo) so the products keep float32
- * precision. Small n splits the tokens over workgroups; the partial sums then go through the
- * workspace (lamq_gram_workspace_size(N, n, 1) bytes, possibly 0) and are added in a fixed order.
+ * precision (twice the MFMA work; lamq_hessian_accum_rows below is exact and costs one product when
+ * the weights take few values). Small n splits the tokens over workgroups; the partial sums then go
+ * through the workspace (lamq_gram_workspace_size(N, n, 1) bytes, possibly 0) and are added in a
+ * fixed order.
  * lamq_hessian_finalize mirrors the lower triangle, divides by ntok (quantize.py:1470) and, if H64
  * is given, writes the float64 copy the sweep consumes.
  * ---------------------------------------------------------------------------------------------- */
@@ -179,6 +182,21 @@ int lamq_hessian_finalize(float* H, int64_t n, int64_t ldH, float ntok, double* 
  * Workspace: lamq_gram_workspace_size(N, n, 0) bytes. */
 int lamq_cross_gram(const uint16_t* Xr, const uint16_t* Xq, int64_t N, int64_t n, int64_t ldx, const float* w,
                     float scale, float* D, int64_t ldD, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The same sums over a list of token rows, unweighted, on the 256x256-tile kernel:
+ *   H[i, j] += scale * sum_{r in rows} X[r, i] X[r, j]   (lower triangle)
+ *   D[i, j] += scale * sum_{r in rows} Xr[r, i] Xq[r, j]
+ * A token weight shared by a set of rows is the scale of that set's call: quantize.py:1389-1391 weights
+ * tokens by their kind (token_weights with the digits specs, quantize.py:593-607, gives at most three
+ * distinct weights), so H = sum over the distinct weights c of w_c * X_c^T X_c, with exact bf16
+ * products and float32 sums. rows: nrows int32 indices into X (each < the rows of X);
+ * n and ldx multiples of 8, X 16-byte aligned (else LAMQ_EUNSUP). Workspace:
+ * lamq_gram_workspace_size(nrows, n, 1 or 0) bytes. */
+int lamq_hessian_accum_rows(const uint16_t* X, const int32_t* rows, int64_t nrows, int64_t n, int64_t ldx, float scale,
+                            float* H, int64_t ldH, void* workspace, size_t workspace_bytes, void* stream);
+int lamq_cross_gram_rows(const uint16_t* Xr, const uint16_t* Xq, const int32_t* rows, int64_t nrows, int64_t n,
+                         int64_t ldx, float scale, float* D, int64_t ldD, void* workspace, size_t workspace_bytes,
+                         void* stream);
 
 /* ------------------------------------------------------------------------------------------------
  * Per-token KL(p_ref || p_q) of two bf16 logit matrices in one streaming pass.

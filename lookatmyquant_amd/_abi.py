@@ -41,6 +41,8 @@ SIGNATURES = {
     "lamq_hessian_accum": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_flt, _p, _c_i64, _p, _c_size, _p]),
     "lamq_hessian_finalize": (_c_int, [_p, _c_i64, _c_i64, _c_flt, _p, _c_i64, _p]),
     "lamq_cross_gram": (_c_int, [_p, _p, _c_i64, _c_i64, _c_i64, _p, _c_flt, _p, _c_i64, _p, _c_size, _p]),
+    "lamq_hessian_accum_rows": (_c_int, [_p, _p, _c_i64, _c_i64, _c_i64, _c_flt, _p, _c_i64, _p, _c_size, _p]),
+    "lamq_cross_gram_rows": (_c_int, [_p, _p, _p, _c_i64, _c_i64, _c_i64, _c_flt, _p, _c_i64, _p, _c_size, _p]),
     "lamq_kl_workspace_size": (_c_size, [_c_i64]),
     "lamq_kl_rows": (_c_int, [_p, _p, _c_i64, _c_i64, _c_i64, _c_i64, _p, _p, _p, _p, _c_size, _p]),
     "lamq_pack_trellis": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _p, _c_i64, _p, _p]),

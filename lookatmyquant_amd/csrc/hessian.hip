@@ -5,6 +5,7 @@
 // split into bf16 hi + lo parts (hi = bf16(w*x), lo = bf16(w*x - hi), exact up to 2^-16 relative)
 // and both are multiplied, so the products keep the precision of the reference's fp32 w*x.
 #include "common.h"
+#include <type_traits>
 
 typedef __bf16 lamq_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float lamq_f32x16 __attribute__((ext_vector_type(16)));
@@ -156,6 +157,275 @@ __global__ __launch_bounds__(256) void gram_kernel(const uint16_t* __restrict__ 
             }
 }
 
+// ------------------------------------------------------------------------------------------------
+// The unweighted Gram on 256x256 output tiles (the weighted case reaches it class by class: a weight
+// shared by a set of tokens scales that set's product, see lamq_hessian_accum_rows).
+//
+// One workgroup of four waves per tile (features I x features J); wave (wi, wj) owns the 128x128
+// quarter of 4x4 MFMA tiles of 32x32 (v_mfma_f32_32x32x16_bf16), its 256 accumulators in AGPRs.
+// Tokens advance in stages of GK = 32 through GNS LDS stage buffers filled by direct global->LDS loads
+// (global_load_lds_dwordx4, 16 bytes per lane, no registers): GNS - 1 stages are in flight while one is
+// consumed, and one barrier per stage both publishes the landed stage and frees the buffer of the
+// previous one. The loads of the next stage are issued between the MFMAs, one per four. The LDS keeps
+// the activations as they lie in memory, [token][feature] with 512-byte rows (256 features) whose
+// 16-byte chunks are XOR-swizzled by 4 * (token & 3); the MFMA fragments (8 consecutive tokens of one
+// feature per lane) come from two ds_read_b64_tr_b16 each: within a 16-lane group, lane s points at
+// token k0 + s/4, features m0 + 4*(s%4), and lane i receives tokens k0..k0+3 of feature m0 + i. The LDS
+// serves 32 lanes (two groups: 4 tokens x 2 feature pairs) at once, and the swizzle puts their eight
+// 32-byte pieces in eight different bank windows. Tokens past the range and features past n load a zero
+// row (a stale token in LDS would reach every output).
+// ------------------------------------------------------------------------------------------------
+#define GT 256
+#define GK 32
+#define GNS 5                      // LDS stages (5 x 32 KB: all of a CU's LDS)
+#define GSTAGE (2 * GK * GT * 2)   // bytes per stage: operands A and B, GK rows of 512 bytes each
+
+typedef short lamq_i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) lamq_i16x4 lamq_lds_i16x4;
+
+__device__ uint4 lamq_zero_row[GT / 8];  // 512 zero bytes: the source of masked loads
+
+__device__ __forceinline__ uint32_t gsw(int token, int chunk)
+{
+    return (uint32_t)(token * (GT * 2) + ((chunk ^ (4 * (token & 3))) << 4));
+}
+
+// s_waitcnt vmcnt(n): at most n of this wave's vector-memory operations still outstanding
+template <int N>
+__device__ __forceinline__ void wait_vm()
+{
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// One direct global->LDS load (16 bytes per lane into m0 + 16 * lane). M0 is saved and restored around it.
+__device__ __forceinline__ void load_lds16(const void* g, uint32_t m)
+{
+    uint32_t keep;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(keep)
+                 : "v"(g), "s"(m)
+                 : "memory");
+}
+
+// Tile order: logical tiles run through panels of GP tile columns, row by row, so the workgroups resident
+// at one time work on a compact block of tiles and share feature blocks of the activations (a third fewer
+// bytes fetched past L2 than row-major order). Workgroup b takes split b / tiles, tile b % tiles.
+#define GP 8
+__device__ __forceinline__ void gram_tile(int64_t t, int64_t nt, bool sym, int64_t& I, int64_t& J)
+{
+    for (int64_t c0 = 0; c0 < nt; c0 += GP) {
+        const int64_t c1 = c0 + GP < nt ? c0 + GP : nt;
+        const int64_t r0 = sym ? c0 : 0;
+        int64_t count;
+        if (sym) {
+            const int64_t tri = c1 - c0;  // rows c0 .. c1-1 hold 1 .. tri tiles, the rows below tri each
+            count = tri * (tri + 1) / 2 + (nt - c1) * tri;
+        } else {
+            count = nt * (c1 - c0);
+        }
+        if (t >= count) {
+            t -= count;
+            continue;
+        }
+        for (int64_t r = r0; r < nt; ++r) {
+            const int64_t w = sym ? ((r < c1 ? r : c1 - 1) - c0 + 1) : (c1 - c0);
+            if (t < w) {
+                I = r;
+                J = c0 + t;
+                return;
+            }
+            t -= w;
+        }
+    }
+    I = J = 0;  // not reached for t < the tile count
+}
+
+// ROWS: the tokens are rows tok[kb..ke) of X (else rows kb..ke).
+template <bool SYM, bool ROWS>
+__global__ __launch_bounds__(256) void gram256_kernel(const uint16_t* __restrict__ Xa, const uint16_t* __restrict__ Xb,
+                                                      int64_t N, int64_t n, int64_t ldx, const int32_t* __restrict__ tok,
+                                                      float scale, float* __restrict__ out, int64_t ldo, int64_t slab,
+                                                      int partial, int64_t tokens_per_split, int64_t tiles)
+{
+    __shared__ __align__(16) uint8_t lds[GNS * GSTAGE];
+    const int64_t split = blockIdx.x / tiles;
+    int64_t I, J;
+    gram_tile(blockIdx.x - split * tiles, cdiv(n, GT), SYM, I, J);
+    const int64_t kb = split * tokens_per_split;
+    const int64_t ke = kb + tokens_per_split < N ? kb + tokens_per_split : N;
+    const int64_t span = ke - kb;
+    const int nst = (int)cdiv(span, GK);
+    const bool diag = SYM && I == J;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wi = wave >> 1, wj = wave & 1;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+
+    // Loads. Wave w, instruction q (0..3) covers rows 2*(4w + q) and +1 of a stage, for operand A and for
+    // operand B (a diagonal tile loads A twice: 8 loads per wave and stage keep the vmcnt bookkeeping fixed);
+    // lane l fills slot l%32 of row 2*(4w + q) + l/32 with the chunk slot ^ 4*(row & 3), and row & 3 =
+    // 2*(q & 1) + l/32. The loads are issued from asm, so the compiler's wait insertion leaves them to the
+    // explicit vmcnt waits and the barrier.
+    const int lrow = lane >> 5, slot = lane & 31;
+    const int64_t fA = I * GT, fB = diag ? I * GT : J * GT;
+    const uint16_t* XB = diag ? Xa : Xb;
+    const uint16_t* zrow = reinterpret_cast<const uint16_t*>(lamq_zero_row);
+    asm volatile("" : "+s"(zrow));  // computed once, not rebuilt at every load
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
+    int64_t loff[2];  // element offset of this lane's chunk from the pair's first row (contiguous tokens)
+    int coff[2];      // element offset of this lane's chunk within its row
+    bool fok[2][2];   // [operand][q parity]: the chunk lies within n
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+        const int c = slot ^ (4 * (2 * par + lrow));
+        coff[par] = 8 * c;
+        loff[par] = lrow * ldx + 8 * c;
+        fok[0][par] = fA + 8 * c < n;
+        fok[1][par] = fB + 8 * c < n;
+    }
+    // with a row list, the wave's 8 rows of a stage (tokens kb + st*GK + 8w + k) are read one stage early
+    auto load_idx = [&](int st, int32_t (&ix)[8]) {
+        if (!ROWS) return;
+        const int64_t tb = kb + (int64_t)st * GK + 8 * wv;
+        if (tb + 8 <= ke) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) ix[k] = tok[tb + k];
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) ix[k] = tb + k < ke ? tok[tb + k] : 0;
+        }
+    };
+    auto piece = [&](int st, int q, int op, const int32_t (&ix)[8]) {
+        const int rp = 2 * (4 * wv + q);  // first row of the pair (uniform)
+        const bool ok = ((int64_t)st * GK + rp + lrow < span) && fok[op][q & 1];
+        const uint16_t* X = op ? XB : Xa;
+        const int64_t f0 = op ? fB : fA;
+        const uint16_t* src;
+        if (ROWS) {
+            // both indices as scalars first: selecting between two array elements by lane would become an
+            // indexed (scratch) access
+            const int32_t ra = __builtin_amdgcn_readfirstlane(ix[2 * q]);
+            const int32_t rb = __builtin_amdgcn_readfirstlane(ix[2 * q + 1]);
+            src = X + (int64_t)(lrow ? rb : ra) * ldx + f0 + coff[q & 1];
+        } else {
+            src = X + (kb + (int64_t)st * GK + rp) * ldx + f0 + loff[q & 1];
+        }
+        const uint32_t m = lds_base + (uint32_t)((st % GNS) * GSTAGE + op * GK * 512 + rp * 512);
+        load_lds16(ok ? (const void*)src : (const void*)zrow, m);
+    };
+
+    // fragment read offsets within a stage: group g = lane/16, i = lane%16; token 8*(g/2) + i/4 (+4 for the
+    // second read, +16 per k-step), feature 16*(g%2) + 4*(i%4) + 32*t within the wave's 128 features
+    const int g = lane >> 4, li = lane & 15;
+    const int tk = 8 * (g >> 1) + (li >> 2);
+    uint32_t offA[4], offB[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int fa = wi * 128 + 32 * t + 16 * (g & 1) + 4 * (li & 3);
+        const int fb = wj * 128 + 32 * t + 16 * (g & 1) + 4 * (li & 3);
+        offA[t] = gsw(tk, fa >> 3) + ((fa >> 2) & 1) * 8;
+        offB[t] = GK * 512 + gsw(tk, fb >> 3) + ((fb >> 2) & 1) * 8;
+    }
+    // The fragment reads are issued from asm with immediate offsets (+2048 for the second read of a fragment,
+    // +8192 per k-step) off one address per fragment and stage; asm reads are invisible to the compiler's wait
+    // insertion, so frag_wait takes the fragments as operands: nothing that uses them can move above it.
+    using v2u = uint32_t __attribute__((ext_vector_type(2)));
+    auto tr_read = [&](uint32_t addr, v2u& lo, v2u& hi, auto ks_tag) {
+        constexpr int ks = decltype(ks_tag)::value;
+        asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"
+                     : "=v"(lo), "=v"(hi)
+                     : "v"(addr), "n"(ks * 16 * 512), "n"(ks * 16 * 512 + 4 * 512)
+                     : "memory");
+    };
+    auto as_frag = [](v2u lo, v2u hi) {
+        const uint32_t __attribute__((ext_vector_type(4))) v = {lo[0], lo[1], hi[0], hi[1]};
+        return __builtin_bit_cast(lamq_bf16x8, v);
+    };
+    auto frags = [&](uint32_t S, auto ks_tag, lamq_bf16x8 (&af)[4], lamq_bf16x8 (&bf)[4]) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            v2u a0, a1, b0, b1;
+            tr_read(S + offA[t], a0, a1, ks_tag);
+            tr_read(S + offB[t], b0, b1, ks_tag);
+            af[t] = as_frag(a0, a1);
+            bf[t] = as_frag(b0, b1);
+        }
+    };
+    // s_waitcnt lgkmcnt(N) tied to the fragments it guards
+    auto frag_wait = [](auto n_tag, lamq_bf16x8 (&af)[4], lamq_bf16x8 (&bf)[4]) {
+        constexpr int N = decltype(n_tag)::value;
+        asm volatile("s_waitcnt lgkmcnt(%8)"
+                     : "+v"(af[0]), "+v"(af[1]), "+v"(af[2]), "+v"(af[3]), "+v"(bf[0]), "+v"(bf[1]), "+v"(bf[2]), "+v"(bf[3])
+                     : "n"(N)
+                     : "memory");
+    };
+
+    lamq_f32x16 acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
+
+    int32_t ix[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int st = 0; st < GNS - 1; ++st) {
+        load_idx(st, ix);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            piece(st, q, 0, ix);
+            piece(st, q, 1, ix);
+        }
+    }
+    load_idx(GNS - 1, ix);
+    for (int st = 0; st < nst; ++st) {
+        wait_vm<8 * (GNS - 2)>();  // stage st has landed (this wave's part)
+        __syncthreads();           // every wave's part; the buffer of stage st - 1 is free
+        const uint32_t S = lds_base + (uint32_t)((st % GNS) * GSTAGE);
+        const int sn = st + GNS - 1;  // the stage loaded during this one, into the freed buffer
+        lamq_bf16x8 af[2][4], bf[2][4];
+        frags(S, std::integral_constant<int, 0>{}, af[0], bf[0]);
+        frags(S, std::integral_constant<int, 1>{}, af[1], bf[1]);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int ti = 0; ti < 4; ++ti) {
+                if (ti == 0) {  // 16 reads per k-step, issued in order: the first k-step's are done at 15 outstanding
+                    if (ks == 0)  // (the counter field holds at most 15)
+                        frag_wait(std::integral_constant<int, 15>{}, af[0], bf[0]);
+                    else
+                        frag_wait(std::integral_constant<int, 0>{}, af[1], bf[1]);
+                }
+#pragma unroll
+                for (int tj = 0; tj < 4; ++tj)
+                    acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks][ti], bf[ks][tj], acc[ti][tj], 0, 0, 0);
+                const int p = ks * 4 + ti;  // one load of the next stage in the shadow of every four MFMAs
+                piece(sn, p >> 1, p & 1, ix);
+            }
+        load_idx(sn + 1, ix);
+    }
+    wait_vm<0>();  // no load may still be writing this workgroup's LDS when it ends
+    // result layout (32x32): lane l, register v -> row 8*(v/4) + 4*(l/32) + v%4, column l%32
+    float* o = out + (partial ? split * slab : 0);
+    const int64_t fi = I * GT, fj = J * GT;
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int64_t i = fi + wi * 128 + ti * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                const int64_t j = fj + wj * 128 + tj * 32 + (lane & 31);
+                if (i < n && j < n && (!SYM || j <= i)) {
+                    float* p = o + i * ldo + j;
+                    if (partial)
+                        *p = acc[ti][tj][v];
+                    else
+                        *p = *p + scale * acc[ti][tj][v];
+                }
+            }
+}
+
 // out[i][j] += scale * sum_s slab_s[i][j], s ascending (lower triangle when SYM).
 __global__ void gram_reduce_kernel(const float* __restrict__ parts, int64_t splits, int64_t slab, int64_t n,
                                    float scale, float* __restrict__ out, int64_t ldo, int sym)
@@ -169,11 +439,19 @@ __global__ void gram_reduce_kernel(const float* __restrict__ parts, int64_t spli
     *p = *p + scale * s;
 }
 
-static int64_t gram_splits(int64_t N, int64_t n, bool sym)
+// The 256-tile kernel needs 16-byte rows: n and the row stride multiples of 8 bf16, a 16-byte aligned base.
+static bool gram256_ok(const uint16_t* X, int64_t n, int64_t ldx)
 {
-    const int64_t nt = cdiv(n, HT);
+    return (n % 8) == 0 && (ldx % 8) == 0 && ((uintptr_t)X % 16) == 0;
+}
+
+// Token splits: enough workgroups to fill the chip (about two per CU for the 128 tiles, one for the 256 tiles),
+// at least 1024 tokens per split.
+static int64_t gram_splits(int64_t N, int64_t n, bool sym, int64_t edge)
+{
+    const int64_t nt = cdiv(n, edge);
     const int64_t tiles = sym ? nt * (nt + 1) / 2 : nt * nt;
-    int64_t s = cdiv(1024, tiles);
+    int64_t s = cdiv(edge == GT ? 256 : 1024, tiles);
     const int64_t maxs = N / 1024 > 1 ? N / 1024 : 1;
     if (s > maxs) s = maxs;
     if (s < 1) s = 1;
@@ -183,16 +461,57 @@ static int64_t gram_splits(int64_t N, int64_t n, bool sym)
 extern "C" size_t lamq_gram_workspace_size(int64_t N, int64_t n, int sym)
 {
     if (N < 1 || n < 1) return 0;
-    const int64_t s = gram_splits(N, n, sym != 0);
+    int64_t s = gram_splits(N, n, sym != 0, HT);
+    const int64_t s2 = gram_splits(N, n, sym != 0, GT);
+    if (s2 > s) s = s2;
     return s > 1 ? (size_t)s * (size_t)n * (size_t)n * sizeof(float) : 0;
+}
+
+static int gram_reduce(float* parts, int64_t nsplit, int64_t n, float scale, float* out, int64_t ldo, bool sym,
+                       hipStream_t s)
+{
+    hipLaunchKernelGGL(gram_reduce_kernel, dim3((unsigned)cdiv(n, 64), (unsigned)cdiv(n, 4)), dim3(256), 0, s, parts,
+                       nsplit, n * n, n, scale, out, ldo, sym ? 1 : 0);
+    LAMQ_LAUNCH_CHECK();
+    return LAMQ_OK;
+}
+
+// The unweighted Gram of the tokens tok[0..N) (or 0..N) on the 256-tile kernel.
+static int gram256_launch(const uint16_t* Xa, const uint16_t* Xb, int64_t N, int64_t n, int64_t ldx, const int32_t* tok,
+                          float scale, float* out, int64_t ldo, bool sym, void* ws, size_t ws_bytes, hipStream_t s)
+{
+    const int64_t nt = cdiv(n, GT);
+    const int64_t tiles = sym ? nt * (nt + 1) / 2 : nt * nt;
+    const int64_t splits = gram_splits(N, n, sym, GT);
+    const int64_t per = cdiv(cdiv(N, splits), GK) * GK;
+    const int64_t nsplit = cdiv(N, per);
+    const bool partial = nsplit > 1;
+    const int64_t slab = n * n;
+    if (partial && (!ws || ws_bytes < (size_t)nsplit * (size_t)slab * sizeof(float))) return LAMQ_EINVAL;
+    float* dst = partial ? reinterpret_cast<float*>(ws) : out;
+    const int64_t ldd = partial ? n : ldo;
+    dim3 grid((unsigned)(tiles * nsplit));
+#define GRAM256(S, R)                                                                                               \
+    hipLaunchKernelGGL((gram256_kernel<S, R>), grid, dim3(256), 0, s, Xa, Xb, N, n, ldx, tok, scale, dst, ldd, slab, \
+                       partial ? 1 : 0, per, tiles)
+    if (sym) {
+        if (tok) GRAM256(true, true); else GRAM256(true, false);
+    } else {
+        if (tok) GRAM256(false, true); else GRAM256(false, false);
+    }
+#undef GRAM256
+    LAMQ_LAUNCH_CHECK();
+    return partial ? gram_reduce(dst, nsplit, n, scale, out, ldo, sym, s) : LAMQ_OK;
 }
 
 static int gram_launch(const uint16_t* Xa, const uint16_t* Xb, int64_t N, int64_t n, int64_t ldx, const float* w,
                        float scale, float* out, int64_t ldo, bool sym, void* ws, size_t ws_bytes, hipStream_t s)
 {
+    if (!w && gram256_ok(Xa, n, ldx) && gram256_ok(Xb, n, ldx))
+        return gram256_launch(Xa, Xb, N, n, ldx, nullptr, scale, out, ldo, sym, ws, ws_bytes, s);
     const int64_t nt = cdiv(n, HT);
     const int64_t tiles = sym ? nt * (nt + 1) / 2 : nt * nt;
-    const int64_t splits = gram_splits(N, n, sym);
+    const int64_t splits = gram_splits(N, n, sym, HT);
     const int64_t per = cdiv(cdiv(N, splits), KT) * KT;
     const int64_t nsplit = cdiv(N, per);
     const bool partial = nsplit > 1;
@@ -210,12 +529,7 @@ static int gram_launch(const uint16_t* Xa, const uint16_t* Xb, int64_t N, int64_
     }
 #undef GRAM_LAUNCH
     LAMQ_LAUNCH_CHECK();
-    if (partial) {
-        hipLaunchKernelGGL(gram_reduce_kernel, dim3((unsigned)cdiv(n, 64), (unsigned)cdiv(n, 4)), dim3(256), 0, s, dst,
-                           nsplit, slab, n, scale, out, ldo, sym ? 1 : 0);
-        LAMQ_LAUNCH_CHECK();
-    }
-    return LAMQ_OK;
+    return partial ? gram_reduce(dst, nsplit, n, scale, out, ldo, sym, s) : LAMQ_OK;
 }
 
 static bool gram_args_ok(const uint16_t* X, int64_t N, int64_t n, int64_t ldx)
@@ -264,4 +578,24 @@ extern "C" int lamq_hessian_finalize(float* H, int64_t n, int64_t ldH, float nto
                        as_stream(stream), H, n, ldH, ntok, H64, ldH64);
     LAMQ_LAUNCH_CHECK();
     return LAMQ_OK;
+}
+
+extern "C" int lamq_hessian_accum_rows(const uint16_t* X, const int32_t* rows, int64_t nrows, int64_t n, int64_t ldx,
+                                       float scale, float* H, int64_t ldH, void* workspace, size_t workspace_bytes,
+                                       void* stream)
+{
+    if (!gram_args_ok(X, nrows, n, ldx) || !rows || !H || ldH < n) return LAMQ_EINVAL;
+    if (!gram256_ok(X, n, ldx)) return LAMQ_EUNSUP;
+    if (nrows == 0) return LAMQ_OK;
+    return gram256_launch(X, X, nrows, n, ldx, rows, scale, H, ldH, true, workspace, workspace_bytes, as_stream(stream));
+}
+
+extern "C" int lamq_cross_gram_rows(const uint16_t* Xr, const uint16_t* Xq, const int32_t* rows, int64_t nrows, int64_t n,
+                                    int64_t ldx, float scale, float* D, int64_t ldD, void* workspace, size_t workspace_bytes,
+                                    void* stream)
+{
+    if (!gram_args_ok(Xr, nrows, n, ldx) || !gram_args_ok(Xq, nrows, n, ldx) || !rows || !D || ldD < n) return LAMQ_EINVAL;
+    if (!gram256_ok(Xr, n, ldx) || !gram256_ok(Xq, n, ldx)) return LAMQ_EUNSUP;
+    if (nrows == 0) return LAMQ_OK;
+    return gram256_launch(Xr, Xq, nrows, n, ldx, rows, scale, D, ldD, false, workspace, workspace_bytes, as_stream(stream));
 }

@@ -273,14 +273,45 @@ def trailing_update(T: torch.Tensor, Z: torch.Tensor, U: torch.Tensor, b0: int, 
 # ----------------------------------------------------------------------------- statistics
 
 
+MAX_WEIGHT_CLASSES = 8
+
+
+def _tiled(X: torch.Tensor) -> bool:
+    """X meets the 256-tile Gram kernel's layout: 16-byte rows and base."""
+    n = X.shape[1]
+    return n % 8 == 0 and ld(X) % 8 == 0 and X.data_ptr() % 16 == 0
+
+
+def weight_classes(w: torch.Tensor):
+    """[(weight, int32 row indices)] for the distinct nonzero values of w when there are at most
+    MAX_WEIGHT_CLASSES of them (one host synchronisation), else None."""
+    vals = torch.unique(w)
+    if vals.numel() > MAX_WEIGHT_CLASSES:
+        return None
+    out = []
+    for v in vals.cpu().tolist():
+        if v != 0.0:
+            out.append((v, (w == v).nonzero().flatten().to(torch.int32)))
+    return out
+
+
 def hessian_accum(H: torch.Tensor, X: torch.Tensor, w: torch.Tensor | None = None, scale: float = 1.0) -> torch.Tensor:
-    """H (float32 [n, n], lower triangle) += scale * X^T diag(w) X for bf16 X [N, n]."""
+    """H (float32 [n, n], lower triangle) += scale * X^T diag(w) X for bf16 X [N, n]. Weights with few distinct
+    values go class by class through the unweighted kernel (exact products); others use the hi/lo split."""
     need(H, torch.float32, "H", 2)
     need(X, torch.bfloat16, "X", 2)
     N, n = X.shape
     wv = None
     if w is not None:
         wv = w.to(device=X.device, dtype=torch.float32).contiguous()
+        classes = weight_classes(wv) if _tiled(X) else None
+        if classes is not None:
+            for v, rows in classes:
+                nbytes = lib().lamq_gram_workspace_size(rows.numel(), n, 1)
+                ws = workspace(nbytes, X.device)
+                check(lib().lamq_hessian_accum_rows(ptr(X), ptr(rows), rows.numel(), n, ld(X), float(scale * v), ptr(H),
+                                                    ld(H), ptr(ws), nbytes, stream(X.device)), "hessian_accum_rows")
+            return H
     nbytes = lib().lamq_gram_workspace_size(N, n, 1)
     ws = workspace(nbytes, X.device)
     check(lib().lamq_hessian_accum(ptr(X), N, n, ld(X), ptr(wv), float(scale), ptr(H), ld(H), ptr(ws), nbytes,
@@ -314,6 +345,15 @@ def cross_gram_accum(D: torch.Tensor, Xr: torch.Tensor, Xq: torch.Tensor, w: tor
         raise ValueError("Xr and Xq must have the same shape and row stride")
     N, n = Xr.shape
     wv = None if w is None else w.to(device=Xr.device, dtype=torch.float32).contiguous()
+    if wv is not None and _tiled(Xr) and _tiled(Xq):
+        classes = weight_classes(wv)
+        if classes is not None:
+            for v, rows in classes:
+                nbytes = lib().lamq_gram_workspace_size(rows.numel(), n, 0)
+                ws = workspace(nbytes, Xr.device)
+                check(lib().lamq_cross_gram_rows(ptr(Xr), ptr(Xq), ptr(rows), rows.numel(), n, ld(Xr), float(scale * v),
+                                                 ptr(D), ld(D), ptr(ws), nbytes, stream(Xr.device)), "cross_gram_rows")
+            return D
     nbytes = lib().lamq_gram_workspace_size(N, n, 0)
     ws = workspace(nbytes, Xr.device)
     check(lib().lamq_cross_gram(ptr(Xr), ptr(Xq), N, n, ld(Xr), ptr(wv), float(scale), ptr(D), ld(D), ptr(ws), nbytes,

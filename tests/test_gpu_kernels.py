@@ -288,13 +288,20 @@ def test_end_to_end_gpu_factor_config2(E, golden, tables, config12):
 # ----------------------------------------------------------------------------- statistics and KL
 
 
-@pytest.mark.parametrize("N,n,weighted", [(4096, 960, False), (3000, 256, True), (2048, 2560, True)])
+@pytest.mark.parametrize("N,n,weighted", [(4096, 960, None), (3000, 256, "digits"), (2048, 2560, "digits"),
+                                          (2000, 264, "uniform"), (1000, 250, None), (777, 200, "digits")])
 def test_hessian(E, N, n, weighted):
+    """Unweighted and few-valued weights (digit tokens) take the 256-tile kernel (class by class), continuous weights
+    the hi/lo kernel, n not a multiple of 8 the 128-tile kernel; ragged token counts and partial tiles included."""
     from lookatmyquant_amd import synthetic
 
     X = synthetic.calibration(N, n, 12, 13)
-    w = synthetic.digit_weights(N, 14) if weighted else None
-    say(f"hessian N={N} n={n} weighted={weighted}")
+    w = None
+    if weighted == "digits":
+        w = synthetic.digit_weights(N, 14)
+    elif weighted == "uniform":
+        w = np.random.default_rng(15).uniform(0.1, 3.0, N).astype(np.float32)
+    say(f"hessian N={N} n={n} weights={weighted}")
     Xb = torch.from_numpy(X).to(torch.bfloat16).cuda()
     Hg = E.hessian(Xb, None if w is None else torch.from_numpy(w).cuda()).cpu().numpy()
     ref = O.hessian(X, w)
@@ -304,17 +311,22 @@ def test_hessian(E, N, n, weighted):
     assert np.array_equal(Hg, Hg.T)
 
 
-def test_cross_gram(E):
+@pytest.mark.parametrize("N,n,weighted", [(2500, 192, "digits"), (1500, 320, "uniform"), (900, 264, None)])
+def test_cross_gram(E, N, n, weighted):
     from lookatmyquant_amd import synthetic
 
-    N, n = 2500, 192
     Xr = synthetic.calibration(N, n, 21, 22)
     Xq = synthetic.bf16_round(Xr + 0.05 * np.random.default_rng(23).standard_normal(Xr.shape).astype(np.float32))
-    w = synthetic.digit_weights(N, 24)
-    say("cross gram")
+    if weighted == "digits":
+        w = synthetic.digit_weights(N, 24)
+    elif weighted == "uniform":
+        w = np.random.default_rng(25).uniform(0.1, 3.0, N).astype(np.float32)
+    else:
+        w = np.ones(N, dtype=np.float32)
+    say(f"cross gram N={N} n={n} weights={weighted}")
     D = torch.zeros(n, n, dtype=torch.float32, device="cuda")
     E.cross_gram_accum(D, torch.from_numpy(Xr).to(torch.bfloat16).cuda(), torch.from_numpy(Xq).to(torch.bfloat16).cuda(),
-                       torch.from_numpy(w).cuda(), scale=1.0 / N)
+                       None if weighted is None else torch.from_numpy(w).cuda(), scale=1.0 / N)
     ref = O.cross_gram(Xr, Xq, w)
     err = np.abs(D.cpu().numpy() - ref).max() / np.abs(ref).max()
     assert err < 1e-4
