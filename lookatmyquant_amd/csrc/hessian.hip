@@ -282,30 +282,33 @@ __global__ __launch_bounds__(256) void gram256_kernel(const uint16_t* __restrict
         fok[0][par] = fA + 8 * c < n;
         fok[1][par] = fB + 8 * c < n;
     }
-    // with a row list, the wave's 8 rows of a stage (tokens kb + st*GK + 8w + k) are read one stage early
-    auto load_idx = [&](int st, int32_t (&ix)[8]) {
+    // with a row list, the wave's 8 rows of a stage (tokens kb + st*GK + 8w + k) are read one stage early and
+    // turned into element offsets row * ldx (uniform: scalar arithmetic)
+    auto load_idx = [&](int st, int64_t (&ix)[8]) {
         if (!ROWS) return;
         const int64_t tb = kb + (int64_t)st * GK + 8 * wv;
+        int32_t r[8];
         if (tb + 8 <= ke) {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) ix[k] = tok[tb + k];
+            for (int k = 0; k < 8; ++k) r[k] = tok[tb + k];
         } else {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) ix[k] = tb + k < ke ? tok[tb + k] : 0;
+            for (int k = 0; k < 8; ++k) r[k] = tb + k < ke ? tok[tb + k] : 0;
         }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) ix[k] = (int64_t)__builtin_amdgcn_readfirstlane(r[k]) * ldx;
     };
-    auto piece = [&](int st, int q, int op, const int32_t (&ix)[8]) {
+    auto piece = [&](int st, int q, int op, const int64_t (&ix)[8]) {
         const int rp = 2 * (4 * wv + q);  // first row of the pair (uniform)
         const bool ok = ((int64_t)st * GK + rp + lrow < span) && fok[op][q & 1];
         const uint16_t* X = op ? XB : Xa;
         const int64_t f0 = op ? fB : fA;
         const uint16_t* src;
         if (ROWS) {
-            // both indices as scalars first: selecting between two array elements by lane would become an
+            // both offsets as scalars first: selecting between two array elements by lane would become an
             // indexed (scratch) access
-            const int32_t ra = __builtin_amdgcn_readfirstlane(ix[2 * q]);
-            const int32_t rb = __builtin_amdgcn_readfirstlane(ix[2 * q + 1]);
-            src = X + (int64_t)(lrow ? rb : ra) * ldx + f0 + coff[q & 1];
+            const int64_t oa = ix[2 * q], ob = ix[2 * q + 1];
+            src = X + (lrow ? ob : oa) + f0 + coff[q & 1];
         } else {
             src = X + (kb + (int64_t)st * GK + rp) * ldx + f0 + loff[q & 1];
         }
@@ -367,7 +370,7 @@ __global__ __launch_bounds__(256) void gram256_kernel(const uint16_t* __restrict
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
 
-    int32_t ix[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int64_t ix[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int st = 0; st < GNS - 1; ++st) {
         load_idx(st, ix);
@@ -445,13 +448,14 @@ static bool gram256_ok(const uint16_t* X, int64_t n, int64_t ldx)
     return (n % 8) == 0 && (ldx % 8) == 0 && ((uintptr_t)X % 16) == 0;
 }
 
-// Token splits: enough workgroups to fill the chip (about two per CU for the 128 tiles, one for the 256 tiles),
-// at least 1024 tokens per split.
+// Token splits: enough workgroups to fill the chip, at least 1024 tokens per split. The 128 tiles aim at about
+// four workgroups per CU; the 256 tiles (one workgroup per CU) at one round of at most 256 workgroups, since a
+// short second round would cost as much as the first.
 static int64_t gram_splits(int64_t N, int64_t n, bool sym, int64_t edge)
 {
     const int64_t nt = cdiv(n, edge);
     const int64_t tiles = sym ? nt * (nt + 1) / 2 : nt * nt;
-    int64_t s = cdiv(edge == GT ? 256 : 1024, tiles);
+    int64_t s = edge == GT ? 256 / tiles : cdiv(1024, tiles);
     const int64_t maxs = N / 1024 > 1 ? N / 1024 : 1;
     if (s > maxs) s = maxs;
     if (s < 1) s = 1;

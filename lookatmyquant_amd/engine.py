@@ -306,11 +306,19 @@ def hessian_accum(H: torch.Tensor, X: torch.Tensor, w: torch.Tensor | None = Non
         wv = w.to(device=X.device, dtype=torch.float32).contiguous()
         classes = weight_classes(wv) if _tiled(X) else None
         if classes is not None:
+            # the tokens gathered class by class into one contiguous copy: the contiguous kernel then runs over each
+            # class's slice (faster than gathering rows inside the kernel, at the cost of a copy of X)
+            Xs = X.index_select(0, torch.cat([rows for _, rows in classes]).long()) if len(classes) > 1 or \
+                classes[0][1].numel() != N else X
+            r0 = 0
             for v, rows in classes:
-                nbytes = lib().lamq_gram_workspace_size(rows.numel(), n, 1)
+                m = rows.numel()
+                part = Xs[r0 : r0 + m]
+                r0 += m
+                nbytes = lib().lamq_gram_workspace_size(m, n, 1)
                 ws = workspace(nbytes, X.device)
-                check(lib().lamq_hessian_accum_rows(ptr(X), ptr(rows), rows.numel(), n, ld(X), float(scale * v), ptr(H),
-                                                    ld(H), ptr(ws), nbytes, stream(X.device)), "hessian_accum_rows")
+                check(lib().lamq_hessian_accum(ptr(part), m, n, ld(part), None, float(scale * v), ptr(H), ld(H), ptr(ws),
+                                               nbytes, stream(X.device)), "hessian_accum")
             return H
     nbytes = lib().lamq_gram_workspace_size(N, n, 1)
     ws = workspace(nbytes, X.device)
@@ -348,7 +356,7 @@ def cross_gram_accum(D: torch.Tensor, Xr: torch.Tensor, Xq: torch.Tensor, w: tor
     if wv is not None and _tiled(Xr) and _tiled(Xq):
         classes = weight_classes(wv)
         if classes is not None:
-            for v, rows in classes:
+            for v, rows in classes:  # the cross-Gram (QEP only) gathers its rows inside the kernel, no copies
                 nbytes = lib().lamq_gram_workspace_size(rows.numel(), n, 0)
                 ws = workspace(nbytes, Xr.device)
                 check(lib().lamq_cross_gram_rows(ptr(Xr), ptr(Xq), ptr(rows), rows.numel(), n, ld(Xr), float(scale * v),

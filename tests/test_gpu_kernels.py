@@ -311,6 +311,26 @@ def test_hessian(E, N, n, weighted):
     assert np.array_equal(Hg, Hg.T)
 
 
+def test_hessian_accum_rows(E):
+    """lamq_hessian_accum_rows over a row list (repeats allowed, ragged count): scale * sum over the listed rows."""
+    from lookatmyquant_amd import synthetic
+
+    N, n = 3000, 520
+    X = synthetic.calibration(N, n, 16, 17)
+    rows = np.random.default_rng(18).integers(0, N, 1111).astype(np.int32)
+    say("hessian_accum_rows")
+    Xb = torch.from_numpy(X).to(torch.bfloat16).cuda()
+    H = torch.zeros(n, n, dtype=torch.float32, device="cuda")
+    rg = torch.from_numpy(rows).cuda()
+    nbytes = E.lib().lamq_gram_workspace_size(len(rows), n, 1)
+    ws = E.workspace(nbytes, Xb.device)
+    E.check(E.lib().lamq_hessian_accum_rows(E.ptr(Xb), E.ptr(rg), len(rows), n, n, 0.5, E.ptr(H), n, E.ptr(ws), nbytes,
+                                            E.stream(Xb.device)), "hessian_accum_rows")
+    Hg = np.tril(H.cpu().numpy())
+    ref = np.tril(0.5 * O.hessian(X[rows]) * len(rows))
+    assert np.abs(Hg - ref).max() < 1e-5 * np.abs(ref).max()
+
+
 @pytest.mark.parametrize("N,n,weighted", [(2500, 192, "digits"), (1500, 320, "uniform"), (900, 264, None)])
 def test_cross_gram(E, N, n, weighted):
     from lookatmyquant_amd import synthetic
