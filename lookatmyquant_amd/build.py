@@ -24,6 +24,11 @@ FLAGS = ["-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}", "-ffp-contract=
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-function"]
 
 
+# Per-file additions. The fp64 GEMM keeps its 64 accumulators in VGPR-form MFMAs (-amdgpu-mfma-vgpr-form): left to
+# itself, the register allocator carries them around the k-loop in VGPRs and copies them into AGPRs every stage.
+FILE_FLAGS = {"ldlq.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"], "chol.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def hipcc() -> str:
     h = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(h).exists():
@@ -40,7 +45,7 @@ def build(verbose: bool = False) -> Path:
 
     def compile_one(src: Path) -> Path:
         obj = objdir / (src.stem + ".o")
-        cmd = [cc, *FLAGS, "-I", str(CSRC), "-c", str(src), "-o", str(obj)]
+        cmd = [cc, *FLAGS, *FILE_FLAGS.get(src.name, []), "-I", str(CSRC), "-c", str(src), "-o", str(obj)]
         r = subprocess.run(cmd, capture_output=True, text=True)
         noise = "is not a recognized feature for this target"
         err = "\n".join(l for l in (r.stderr or "").splitlines() if noise not in l)

@@ -217,6 +217,23 @@ __device__ void viterbi_wg(const float* xs, int TV, const float (&Cr)[Vit<L, K>:
     __syncthreads();
 }
 
+// s_waitcnt vmcnt(n): at most n of this wave's vector-memory operations still outstanding
+template <int N>
+__device__ __forceinline__ void wait_vm()
+{
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// One direct global->LDS load (16 bytes per lane into m0 + 16 * lane). M0 is saved and restored around it.
+__device__ __forceinline__ void load_lds16(const void* g, uint32_t m)
+{
+    uint32_t keep;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(keep)
+                 : "v"(g), "s"(m)
+                 : "memory");
+}
+
 // Dispatch a functor over the (L, K) pairs the kernels are instantiated for: 2 <= L <= 12 with
 // K = 1..min(4, L-1) (at L = 12 every thread then owns 16 states). Returns LAMQ_EUNSUP otherwise.
 template <template <int, int> class F, typename... Args>

@@ -73,6 +73,8 @@ __global__ __launch_bounds__(256) void gemm_sub_f64_kernel(double* C, int64_t ld
         }
     }
     if (OVERWRITE) __syncthreads();
+    // all reads of C before any write (see gemm128_f64_kernel)
+    double cv[2][2][4];
 #pragma unroll
     for (int ti = 0; ti < 2; ++ti)
 #pragma unroll
@@ -81,13 +83,152 @@ __global__ __launch_bounds__(256) void gemm_sub_f64_kernel(double* C, int64_t ld
             for (int v = 0; v < 4; ++v) {
                 const int64_t row = wr + ti * 16 + 4 * v + lk;
                 const int64_t col = wc + tj * 16 + li;
-                if (row < M && col < N && (!LOWER || col <= row)) {
-                    double* p = C + row * ldc + col;
-                    if (OVERWRITE)
-                        *p = acc[ti][tj][v];
-                    else
-                        *p = *p - acc[ti][tj][v];
+                cv[ti][tj][v] = (!OVERWRITE && row < M && col < N && (!LOWER || col <= row)) ? C[row * ldc + col] : 0.0;
+            }
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < 2; ++tj)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int64_t row = wr + ti * 16 + 4 * v + lk;
+                const int64_t col = wc + tj * 16 + li;
+                if (row < M && col < N && (!LOWER || col <= row))
+                    C[row * ldc + col] = OVERWRITE ? acc[ti][tj][v] : cv[ti][tj][v] - acc[ti][tj][v];
+            }
+}
+
+// The same C -= A op(B) (no OVERWRITE) for large products: workgroup tile 128x128, four waves of 64x64 = 4x4
+// MFMA tiles (64 accumulators per lane, AGPRs). Operands go straight from memory into LDS (global_load_lds,
+// 16 bytes = two doubles per lane, no registers), 32 deep in k, two stage buffers: one barrier per stage
+// publishes the stage and frees the other buffer for the next stage's loads, which are issued between the
+// MFMAs. LDS keeps the operands as they lie in memory, in 16-byte chunks XOR-swizzled so that the fragment
+// reads (one double per lane) are bank-conflict-free for the 32 lanes the LDS serves at once:
+//   [row][k] operands (A; B when TRANSB): 256-byte rows of 32 k, chunk c of row r at c ^ (r & 15): the 16 rows
+//     of a fragment read hit 16 different 16-byte bank windows;
+//   [k][col] operands (B): 1 KB rows of 128 columns, chunk c of row k at c ^ 8*(k & 1): the two k-rows read
+//     together sit 128 bytes apart in the banks.
+// Rows past M / N and k past K load zero chunks. Needs even leading dimensions, even K (and even N for a
+// [k][col] B) and 16-byte aligned operands (gemm_sub_f64 checks; other shapes take the kernel above).
+#define G8_BM 128
+#define G8_BK 32
+#define G8_ASZ (G8_BM * G8_BK * 8)   // bytes of one operand stage (32 KB)
+
+__device__ double lamq_zero_chunk[2];
+
+template <bool TRANSB, bool LOWER>
+__global__ __launch_bounds__(256) void gemm128_f64_kernel(double* __restrict__ C, int64_t ldc, const double* __restrict__ A,
+                                                          int64_t lda, const double* __restrict__ B, int64_t ldb, int64_t M,
+                                                          int64_t N, int64_t K, const int32_t* __restrict__ info)
+{
+    __shared__ __align__(16) uint8_t lds[2][2][G8_ASZ];  // [buffer][operand]
+    if (info && *info != 0) return;
+    const int64_t tr = (int64_t)blockIdx.y * G8_BM, tc = (int64_t)blockIdx.x * G8_BM;
+    if (LOWER && tc > tr + G8_BM - 1) return;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
+    const double* zc = lamq_zero_chunk;
+    asm volatile("" : "+s"(zc));
+
+    // loads: 32 instructions of 1 KB per operand and stage, 8 per wave (instruction q of wave w is number 8w + q)
+    //   [row][k]: instruction i covers rows 4i .. 4i+3, lane l row 4i + l/16, slot l%16, chunk (l%16) ^ (row & 15)
+    //   [k][col]: instruction i covers k-row i, lane l slot l, chunk l ^ 8*(i & 1)
+    auto load_rowk = [&](const double* X, int64_t ldx, int64_t r0, int64_t R, int64_t k0, int i, uint32_t m) {
+        const int r = 4 * i + (lane >> 4);
+        const int c = (lane & 15) ^ (r & 15);
+        const int64_t row = r0 + r, k = k0 + 2 * c;
+        const bool ok = row < R && k < K;
+        const double* g = ok ? X + row * ldx + k : zc;
+        load_lds16(g, m);
+    };
+    auto load_kcol = [&](const double* X, int64_t ldx, int64_t c0, int64_t k0, int i, uint32_t m) {
+        const int c = lane ^ (8 * (i & 1));
+        const int64_t k = k0 + i, col = c0 + 2 * c;
+        const bool ok = k < K && col < N;
+        const double* g = ok ? X + k * ldx + col : zc;
+        load_lds16(g, m);
+    };
+    auto piece = [&](int64_t k0, int buf, int q, int op) {
+        const int i = 8 * wv + q;
+        const uint32_t m = lds_base + (uint32_t)((buf * 2 + op) * G8_ASZ + i * 1024);
+        if (op == 0)
+            load_rowk(A, lda, tr, M, k0, i, m);
+        else if (TRANSB)
+            load_rowk(B, ldb, tc, N, k0, i, m);
+        else
+            load_kcol(B, ldb, tc, k0, i, m);
+    };
+
+    lamq_d4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = lamq_d4{0.0, 0.0, 0.0, 0.0};
+    const int li = lane & 15, lk = lane >> 4;
+    // fragment addresses (bytes within an operand stage) for k = k4 + lk
+    auto aaddr = [&](int row, int k) -> uint32_t { return (uint32_t)(row * 256 + (((k >> 1) ^ (row & 15)) << 4) + (k & 1) * 8); };
+    auto baddr = [&](int col, int k) -> uint32_t {
+        return TRANSB ? aaddr(col, k) : (uint32_t)(k * 1024 + (((col >> 1) ^ (8 * (k & 1))) << 4) + (col & 1) * 8);
+    };
+
+    const int nst = (int)cdiv(K, G8_BK);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        piece(0, 0, q, 0);
+        piece(0, 0, q, 1);
+    }
+    for (int st = 0; st < nst; ++st) {
+        wait_vm<0>();     // this wave's loads of stage st have landed
+        __syncthreads();  // everyone's; the other buffer (stage st - 1) is free
+        const int buf = st & 1;
+        const uint8_t* As = lds[buf][0];
+        const uint8_t* Bs = lds[buf][1];
+#pragma unroll
+        for (int k4 = 0; k4 < G8_BK; k4 += 4) {
+            double a[4], b[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                a[t] = *reinterpret_cast<const double*>(As + aaddr(wr + 16 * t + li, k4 + lk));
+                b[t] = *reinterpret_cast<const double*>(Bs + baddr(wc + 16 * t + li, k4 + lk));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i], b[j], acc[i][j], 0, 0, 0);
+                // the next stage's 16 loads, one per four MFMAs over the stage's first four k-steps (after the
+                // last stage they load zero chunks into the buffer no one reads: no branch in the loop)
+                if (k4 < 16) {
+                    const int p = (k4 / 4) * 4 + i;
+                    piece((int64_t)(st + 1) * G8_BK, buf ^ 1, p >> 1, p & 1);
                 }
+            }
+        }
+    }
+    wait_vm<0>();
+    // D layout (16x16): lane l, register v -> row 4*v + l/16, column l%16. All of C's values are read before any is
+    // written: interleaved, every read would wait for the write before it (the compiler cannot tell them apart).
+    double cv[4][4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int64_t row = tr + wr + 16 * i + 4 * v + lk;
+                const int64_t col = tc + wc + 16 * j + li;
+                cv[i][j][v] = (row < M && col < N && (!LOWER || col <= row)) ? C[row * ldc + col] : 0.0;
+            }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int64_t row = tr + wr + 16 * i + 4 * v + lk;
+                const int64_t col = tc + wc + 16 * j + li;
+                if (row < M && col < N && (!LOWER || col <= row)) C[row * ldc + col] = cv[i][j][v] - acc[i][j][v];
             }
 }
 
@@ -96,6 +237,17 @@ static int gemm_sub_f64(double* C, int64_t ldc, const double* A, int64_t lda, co
                         int64_t N, int64_t K, const int32_t* info, hipStream_t s)
 {
     if (M <= 0 || N <= 0 || K <= 0) return LAMQ_OK;
+    // the 128 tiles once there are enough of them to fill most of the chip, for operands it can load in 16-byte
+    // chunks
+    // (a [k][col] B chunk holds columns col, col + 1: N even keeps the pair inside the row)
+    const bool chunks = (lda % 2) == 0 && (ldb % 2) == 0 && (K % 2) == 0 && (TRANSB || (N % 2) == 0) &&
+                        ((uintptr_t)A % 16) == 0 && ((uintptr_t)B % 16) == 0;
+    if (!OVERWRITE && chunks && cdiv(M, G8_BM) * cdiv(N, G8_BM) >= 128) {
+        dim3 grid((unsigned)cdiv(N, G8_BM), (unsigned)cdiv(M, G8_BM));
+        hipLaunchKernelGGL((gemm128_f64_kernel<TRANSB, LOWER>), grid, dim3(256), 0, s, C, ldc, A, lda, B, ldb, M, N, K, info);
+        LAMQ_LAUNCH_CHECK();
+        return LAMQ_OK;
+    }
     dim3 grid((unsigned)cdiv(N, 64), (unsigned)cdiv(M, 64));
     hipLaunchKernelGGL((gemm_sub_f64_kernel<TRANSB, LOWER, OVERWRITE>), grid, dim3(256), 0, s, C, ldc, A, lda, B, ldb, M, N,
                        K, info);

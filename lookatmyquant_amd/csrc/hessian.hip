@@ -190,23 +190,6 @@ __device__ __forceinline__ uint32_t gsw(int token, int chunk)
     return (uint32_t)(token * (GT * 2) + ((chunk ^ (4 * (token & 3))) << 4));
 }
 
-// s_waitcnt vmcnt(n): at most n of this wave's vector-memory operations still outstanding
-template <int N>
-__device__ __forceinline__ void wait_vm()
-{
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// One direct global->LDS load (16 bytes per lane into m0 + 16 * lane). M0 is saved and restored around it.
-__device__ __forceinline__ void load_lds16(const void* g, uint32_t m)
-{
-    uint32_t keep;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
-                 : "=&s"(keep)
-                 : "v"(g), "s"(m)
-                 : "memory");
-}
-
 // Tile order: logical tiles run through panels of GP tile columns, row by row, so the workgroups resident
 // at one time work on a compact block of tiles and share feature blocks of the activations (a third fewer
 // bytes fetched past L2 than row-major order). Workgroup b takes split b / tiles, tile b % tiles.
@@ -408,25 +391,32 @@ __global__ __launch_bounds__(256) void gram256_kernel(const uint16_t* __restrict
         load_idx(sn + 1, ix);
     }
     wait_vm<0>();  // no load may still be writing this workgroup's LDS when it ends
-    // result layout (32x32): lane l, register v -> row 8*(v/4) + 4*(l/32) + v%4, column l%32
+    // result layout (32x32): lane l, register v -> row 8*(v/4) + 4*(l/32) + v%4, column l%32. Per row of MFMA
+    // tiles, the 64 outputs of this lane are read before any is written (interleaved, every read would wait for
+    // the write before it).
     float* o = out + (partial ? split * slab : 0);
     const int64_t fi = I * GT, fj = J * GT;
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti)
+    for (int ti = 0; ti < 4; ++ti) {
+        float hv[4][16];
 #pragma unroll
         for (int tj = 0; tj < 4; ++tj)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int64_t i = fi + wi * 128 + ti * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
                 const int64_t j = fj + wj * 128 + tj * 32 + (lane & 31);
-                if (i < n && j < n && (!SYM || j <= i)) {
-                    float* p = o + i * ldo + j;
-                    if (partial)
-                        *p = acc[ti][tj][v];
-                    else
-                        *p = *p + scale * acc[ti][tj][v];
-                }
+                hv[tj][v] = (!partial && i < n && j < n && (!SYM || j <= i)) ? o[i * ldo + j] : 0.0f;
             }
+#pragma unroll
+        for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int64_t i = fi + wi * 128 + ti * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                const int64_t j = fj + wj * 128 + tj * 32 + (lane & 31);
+                if (i < n && j < n && (!SYM || j <= i))
+                    o[i * ldo + j] = partial ? acc[ti][tj][v] : hv[tj][v] + scale * acc[ti][tj][v];
+            }
+    }
 }
 
 // out[i][j] += scale * sum_s slab_s[i][j], s ascending (lower triangle when SYM).

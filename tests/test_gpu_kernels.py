@@ -106,13 +106,15 @@ def test_viterbi_long_paths_use_workspace(E, tables):
 # ----------------------------------------------------------------------------- fp64 building blocks
 
 
-def test_trailing_update_matches_oracle_order(E):
+@pytest.mark.parametrize("m,n,b0,b1", [(200, 300, 64, 192), (2309, 2560, 128, 256), (1800, 1571, 0, 128)])
+def test_trailing_update_matches_oracle_order(E, m, n, b0, b1):
+    """Small shapes take the 64-tile kernel, large ones (>= 256 tiles of 128) the LDS-staged 128-tile kernel; ragged
+    rows included."""
     rng = np.random.default_rng(5)
-    m, n, b0, b1 = 200, 300, 64, 192
     T = rng.standard_normal((m, n))
     Z = rng.standard_normal((m, b1 - b0))
     U = np.triu(rng.standard_normal((n, n)))
-    say("trailing update")
+    say(f"trailing update m={m} n={n}")
     got = E.trailing_update(cuda(T), cuda(Z), cuda(U), b0, b1).cpu().numpy()
     ref = T.copy()
     acc = np.zeros((m, n - b1))
@@ -125,7 +127,7 @@ def test_trailing_update_matches_oracle_order(E):
     assert err < 1e-14
 
 
-@pytest.mark.parametrize("n", [64, 100, 200, 960])
+@pytest.mark.parametrize("n", [64, 100, 200, 960, 2500])
 def test_chol_inv_upper(E, n):
     rng = np.random.default_rng(n)
     X = rng.standard_normal((2 * n + 50, n))
