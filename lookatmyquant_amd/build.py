@@ -26,7 +26,11 @@ FLAGS = ["-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}", "-ffp-contract=
 
 # Per-file additions. The fp64 GEMM keeps its 64 accumulators in VGPR-form MFMAs (-amdgpu-mfma-vgpr-form): left to
 # itself, the register allocator carries them around the k-loop in VGPRs and copies them into AGPRs every stage.
-FILE_FLAGS = {"ldlq.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"], "chol.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+# The L <= 12 trellis search never produces a NaN (costs are finite or +inf, and inf - inf never forms), so it is
+# built with -fno-honor-nans: "c < best ? c : best" then becomes v_min_f32, which needs no compare mask and spares
+# the hazard waits of the compare-select pairs. (The 16-bit-state search measured no better with it.)
+FILE_FLAGS = {"ldlq.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"], "chol.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+              "viterbi.hip": ["-fno-honor-nans"]}
 
 
 def hipcc() -> str:

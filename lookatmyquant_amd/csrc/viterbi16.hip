@@ -80,9 +80,12 @@ __device__ void viterbi_big(const float* xs, int TV, uint32_t (&Ch)[VBig<L, K>::
     }
     float xprev = xs[0];
     for (int t = 1; t < TV; ++t) {
-        // best[j]: minimum so far of group j = q*GQ + g; hw[j]: its winning h, already shifted to bits [j*K, j*K+K).
-        // With more than 16 groups a thread has no registers to spare for hw: the h go straight into bits.
+        // best[j]: minimum so far of group j = q*GQ + g; hw[j]: its winning h, packed into bits [j*K, j*K+K) once per
+        // step. With 16 predecessors (K = 4) hw holds h itself, an inline constant of the selects (the compiler
+        // schedules this form better there); otherwise h already shifted into place. With more than 16 groups a
+        // thread has no registers to spare for hw: the h go straight into bits.
         constexpr bool SEP = V::G <= 16;
+        constexpr bool SMALL_H = K >= 4;
         float best[V::G];
         uint32_t hw[SEP ? V::G : 1];
         uint32_t bits = 0;  // the winning h of group j in bits [j*K, j*K+K)
@@ -118,7 +121,7 @@ __device__ void viterbi_big(const float* xs, int TV, uint32_t (&Ch)[VBig<L, K>::
                             const bool lt = c[g] < best[j];  // strict: the lowest h keeps a tie
                             best[j] = lt ? c[g] : best[j];
                             if (SEP) {
-                                hw[j] = lt ? (uint32_t)h << (j * K) : hw[j];
+                                hw[j] = lt ? (SMALL_H ? (uint32_t)h : (uint32_t)h << (j * K)) : hw[j];
                             } else {
                                 const uint32_t mk = (uint32_t)(V::NB - 1) << (j * K);
                                 bits = lt ? ((bits & ~mk) | ((uint32_t)h << (j * K))) : bits;
@@ -128,7 +131,13 @@ __device__ void viterbi_big(const float* xs, int TV, uint32_t (&Ch)[VBig<L, K>::
                 }
             __syncthreads();
         }
-        if (SEP) {
+        if (SEP && SMALL_H) {
+            // the empty asm keeps the compiler from folding the shift back into the selects
+#pragma unroll
+            for (int j = 0; j < V::G; ++j) asm volatile("" : "+v"(hw[j]));
+#pragma unroll
+            for (int j = 0; j < V::G; ++j) bits |= hw[j] << (j * K);
+        } else if (SEP) {
 #pragma unroll
             for (int j = 0; j < V::G; ++j) bits |= hw[j];
         }
