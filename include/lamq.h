@@ -134,6 +134,12 @@ int lamq_zero_columns(double* T, int64_t m, int64_t n, int64_t ldT, const uint8_
  *   workspace: lamq_chol_inv_upper_workspace_size(n) bytes
  * ---------------------------------------------------------------------------------------------- */
 size_t lamq_chol_inv_upper_workspace_size(int64_t n);
+/* flags of lamq_chol_inv_upper_ex: LAMQ_CHOL_KEEP_DEAD leaves a zero diagonal as it is (no unit diagonal at dead
+ * columns; the damping mean counts it as zero), as opgraph/ldlq_gpu.py:15-25 (ldlq_factor) damps. */
+#define LAMQ_CHOL_KEEP_DEAD 1
+int lamq_chol_inv_upper_ex(const double* H, int64_t n, int64_t ldH, double damp, int flags, double* Hd,
+                           int64_t ldHd, double* U, int64_t ldU, uint8_t* dead, int32_t* info, void* workspace,
+                           size_t workspace_bytes, void* stream);
 int lamq_chol_inv_upper(const double* H, int64_t n, int64_t ldH, double damp, double* Hd, int64_t ldHd,
                         double* U, int64_t ldU, uint8_t* dead, int32_t* info, void* workspace,
                         size_t workspace_bytes, void* stream);

@@ -4,6 +4,7 @@
     trellis_values(L, k, T=256, seed=0, refine=None, fit=None)             codes.py:187 (cached tables)
     is_trellis_path(states, L, k)                                          codes.py:246
     ScalarCode(domain), RowTrellisCode(L, k, T=256, width=16, look=8, seed=0, values=None)   codes.py:322,386
+    TrellisCode(L, k, T=320, width=16, seed=0, values=None)                codes.py:363
     ldlq_words(Ws, H, code, seeds, incoherent=True, in_seed=None, out_rot=True) -> list[Net] codes.py:413
     ldlq_word(W, H, code, seed, incoherent=True)                           codes.py:465
     hadamard, hadamard_factors, rht                                        codes.py:83-132
@@ -136,6 +137,34 @@ class RowTrellisCode:
         return self.values.to(X.device, X.dtype)[path]
 
 
+class TrellisCode:
+    """Sequences of T consecutive outputs (one column) onto trellis paths with a free first state (codes.py:363-383):
+    block LDLQ settles `width` columns at a time, each column of the block cut into m/T sequences searched
+    independently. The rows must come in whole sequences (m a multiple of T)."""
+
+    def __init__(self, L: int, k: int, T: int = 320, width: int = 16, seed: int = 0, values=None):
+        self.L, self.k, self.T, self.width = L, k, T, width
+        self.values = trellis_values(L, k, T, seed) if values is None else torch.as_tensor(values, dtype=torch.float64)
+        if len(self.values) != 1 << L:
+            raise ValueError("a table needs 2^L values")
+        self.domain = TRELLIS(self.values, L, k)
+
+    def _seqs(self, X: torch.Tensor) -> torch.Tensor:
+        o, w = X.shape
+        if o % self.T:
+            raise ValueError(f"{o} rows are not whole sequences of {self.T}")
+        return X.reshape(o // self.T, self.T, w).permute(0, 2, 1).reshape(-1, self.T)
+
+    def states(self, X: torch.Tensor) -> torch.Tensor:
+        """The states of every column's sequences, in X's layout (rows x columns)."""
+        o, w = X.shape
+        st = viterbi(self._seqs(X), self.values, self.L, self.k)
+        return st.reshape(o // self.T, w, self.T).permute(0, 2, 1).reshape(o, w)
+
+    def project(self, X: torch.Tensor) -> torch.Tensor:
+        return self.values.to(X.device, X.dtype)[self.states(X)]
+
+
 # ----------------------------------------------------------------------------- words
 
 
@@ -187,12 +216,42 @@ def ldlq_words(Ws: list, H: torch.Tensor | None, code, seeds: list[int], incoher
     """(incoherence ->) per-row RMS scale -> (block LDLQ under H ->) the code, for matrices that read the same input
     (codes.py:413-462). With H the columns are settled code.width at a time and the later ones re-solved under U;
     without H the code is applied directly. Row trellis and scalar codes run on the fused GPU sweep kernels."""
-    if not isinstance(code, (RowTrellisCode, ScalarCode)):
+    if not isinstance(code, (RowTrellisCode, ScalarCode, TrellisCode)):
         raise NotImplementedError(f"{type(code).__name__} is not one of the codes this path implements")
+    if isinstance(code, TrellisCode) and any(torch.as_tensor(W).shape[0] % code.T for W in Ws):
+        raise ValueError(f"the column trellis needs whole sequences of {code.T} rows in every matrix")
     dev, X, S, rin = _prepare(Ws, seeds, incoherent, in_seed, out_rot)
     rows_label = ("u" if out_rot else "o") if incoherent else "o"
     cols_label = "v" if incoherent else "i"
     m, n = X.shape
+    if isinstance(code, TrellisCode):
+        # the generic sweep, each block's columns projected by the column-sequence search (codes.py:441-458)
+        from .frame import Environment
+        from .syntax import sweep
+
+        if H is None:
+            codes = code.states(X / S[:, None]).to(torch.int32)
+        else:
+            Hr = E.rotate_hessian(torch.as_tensor(H).to(dev, torch.float64).contiguous(), rin) if incoherent else \
+                torch.as_tensor(H).to(dev, torch.float64).contiguous()
+            codes = torch.empty(m, n, dtype=torch.int32, device=dev)
+            table = code.values.to(dev, torch.float64)
+
+            def project(j, x, T):
+                st = code.states(x / S[:, None])
+                codes[:, j : j + x.shape[1]] = st.to(torch.int32)
+                return table[st] * S[:, None]
+
+            sweep(X, Environment(Hr), project, width=code.width)
+        codes = codes.cpu()
+        values = code.values.double()[codes.long()]
+        domain = Domain("trellis", float(code.k), levels=code.domain.levels, axis="t", state_bits=code.L)
+        nets = _nets(Ws, seeds, X, values, S.cpu(), domain, rows_label, rin, out_rot, incoherent, codes)
+        for net in nets:  # rows split into (sequence, position): the sequences' start bits are counted per column
+            c = net.cores["W"]
+            c.data = c.data.reshape(-1, code.T, c.data.shape[1])
+            c.labels = ("s", "t", c.labels[1])
+        return nets
     if isinstance(code, RowTrellisCode):
         table = code.values.to(dev, torch.float64).contiguous()
         if H is None:

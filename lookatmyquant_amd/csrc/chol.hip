@@ -12,10 +12,11 @@
 
 #define NBK 64
 
-// dead = diag(H) == 0; the damping delta = damp * mean(diag H') where H' has unit diagonal at dead.
+// dead = diag(H) == 0; the damping delta = damp * mean(diag H') where H' has unit diagonal at dead (with
+// keep_dead, H' = H: the dead diagonal stays zero and counts as zero).
 __global__ __launch_bounds__(256) void diag_stats_kernel(const double* __restrict__ H, int64_t n, int64_t ldH, double damp,
-                                                         uint8_t* __restrict__ dead, double* __restrict__ delta,
-                                                         int32_t* __restrict__ info)
+                                                         int keep_dead, uint8_t* __restrict__ dead,
+                                                         double* __restrict__ delta, int32_t* __restrict__ info)
 {
     __shared__ double part[256];
     double s = 0.0;
@@ -23,7 +24,7 @@ __global__ __launch_bounds__(256) void diag_stats_kernel(const double* __restric
         const double d = H[i * ldH + i];
         const bool z = d == 0.0;
         if (dead) dead[i] = z ? 1 : 0;
-        s += z ? 1.0 : d;
+        s += (z && !keep_dead) ? 1.0 : d;
     }
     part[threadIdx.x] = s;
     __syncthreads();
@@ -38,15 +39,16 @@ __global__ __launch_bounds__(256) void diag_stats_kernel(const double* __restric
     }
 }
 
-// A = J Hd J (lower triangle), Hd = H with unit diagonal at dead columns plus delta on the diagonal.
+// A = J Hd J (lower triangle), Hd = H with unit diagonal at dead columns (unless keep_dead) plus delta on the
+// diagonal.
 __global__ void prep_kernel(const double* __restrict__ H, int64_t n, int64_t ldH, const double* __restrict__ delta,
-                            double* __restrict__ A, double* __restrict__ Hd, int64_t ldHd)
+                            int keep_dead, double* __restrict__ A, double* __restrict__ Hd, int64_t ldHd)
 {
     const int64_t i = (int64_t)blockIdx.y * 16 + threadIdx.y;
     const int64_t j = (int64_t)blockIdx.x * 64 + threadIdx.x;
     if (i >= n || j >= n) return;
     double v = H[i * ldH + j];
-    if (i == j) v = (v == 0.0 ? 1.0 : v) + *delta;
+    if (i == j) v = ((v == 0.0 && !keep_dead) ? 1.0 : v) + *delta;
     // the factorization reads the lower triangle of H, as LAPACK's lower Cholesky does: H[i][j]
     // with i >= j lands on A[n-1-j][n-1-i], in the lower triangle of A
     if (i >= j) A[(n - 1 - j) * n + (n - 1 - i)] = v;
@@ -161,21 +163,23 @@ extern "C" size_t lamq_chol_inv_upper_workspace_size(int64_t n)
     return (size_t)n * (size_t)n * sizeof(double) + (size_t)cdiv(n, NBK) * NBK * NBK * sizeof(double) + 256;
 }
 
-extern "C" int lamq_chol_inv_upper(const double* H, int64_t n, int64_t ldH, double damp, double* Hd, int64_t ldHd,
-                                   double* U, int64_t ldU, uint8_t* dead, int32_t* info, void* workspace,
-                                   size_t workspace_bytes, void* stream)
+extern "C" int lamq_chol_inv_upper_ex(const double* H, int64_t n, int64_t ldH, double damp, int flags, double* Hd,
+                                      int64_t ldHd, double* U, int64_t ldU, uint8_t* dead, int32_t* info, void* workspace,
+                                      size_t workspace_bytes, void* stream)
 {
     if (!H || !U || !info || !workspace || n < 1 || ldH < n || ldU < n || (Hd && ldHd < n)) return LAMQ_EINVAL;
+    if (flags & ~LAMQ_CHOL_KEEP_DEAD) return LAMQ_EINVAL;
+    const int keep_dead = (flags & LAMQ_CHOL_KEEP_DEAD) ? 1 : 0;
     if (workspace_bytes < lamq_chol_inv_upper_workspace_size(n)) return LAMQ_EINVAL;
     if (n > (int64_t)1 << 20) return LAMQ_EUNSUP;
     hipStream_t s = as_stream(stream);
     double* A = reinterpret_cast<double*>(workspace);
     double* Linv = A + n * n;  // cdiv(n, NBK) blocks of NBK x NBK
     double* delta = Linv + cdiv(n, NBK) * NBK * NBK;
-    hipLaunchKernelGGL(diag_stats_kernel, dim3(1), dim3(256), 0, s, H, n, ldH, damp, dead, delta, info);
+    hipLaunchKernelGGL(diag_stats_kernel, dim3(1), dim3(256), 0, s, H, n, ldH, damp, keep_dead, dead, delta, info);
     LAMQ_LAUNCH_CHECK();
     const dim3 g2((unsigned)cdiv(n, 64), (unsigned)cdiv(n, 16)), b2(64, 16);
-    hipLaunchKernelGGL(prep_kernel, g2, b2, 0, s, H, n, ldH, delta, A, Hd, ldHd);
+    hipLaunchKernelGGL(prep_kernel, g2, b2, 0, s, H, n, ldH, delta, keep_dead, A, Hd, ldHd);
     LAMQ_LAUNCH_CHECK();
     // Cholesky of A = J Hd J, lower
     for (int64_t k0 = 0; k0 < n; k0 += NBK) {
@@ -211,4 +215,11 @@ extern "C" int lamq_chol_inv_upper(const double* H, int64_t n, int64_t ldH, doub
     hipLaunchKernelGGL(reverse_kernel, g2, b2, 0, s, U, n, ldU, info);
     LAMQ_LAUNCH_CHECK();
     return LAMQ_OK;
+}
+
+extern "C" int lamq_chol_inv_upper(const double* H, int64_t n, int64_t ldH, double damp, double* Hd, int64_t ldHd,
+                                   double* U, int64_t ldU, uint8_t* dead, int32_t* info, void* workspace,
+                                   size_t workspace_bytes, void* stream)
+{
+    return lamq_chol_inv_upper_ex(H, n, ldH, damp, 0, Hd, ldHd, U, ldU, dead, info, workspace, workspace_bytes, stream);
 }

@@ -124,9 +124,13 @@ def unrotate_columns(X: torch.Tensor, seed: int) -> torch.Tensor:
 # ----------------------------------------------------------------------------- environment (frame.py:515-522)
 
 
-def chol_inv_upper(H: torch.Tensor, damp: float = 0.01, raise_on_fail: bool = True):
+CHOL_KEEP_DEAD = 1
+
+
+def chol_inv_upper(H: torch.Tensor, damp: float = 0.01, raise_on_fail: bool = True, keep_dead: bool = False):
     """(Hd, U, dead, info): the damped H, the upper Cholesky factor of its inverse, the dead-column mask and the
-    failing pivot (0 when H is positive definite after damping; raises LinAlgError then unless told not to)."""
+    failing pivot (0 when H is positive definite after damping; raises LinAlgError then unless told not to).
+    keep_dead: zero diagonal entries stay zero (ldlq_factor's damping) instead of becoming 1 (Environment's)."""
     need(H, torch.float64, "H", 2)
     n = H.shape[0]
     if H.shape[1] != n:
@@ -137,8 +141,9 @@ def chol_inv_upper(H: torch.Tensor, damp: float = 0.01, raise_on_fail: bool = Tr
     info = torch.empty(1, dtype=torch.int32, device=H.device)
     nbytes = lib().lamq_chol_inv_upper_workspace_size(n)
     ws = workspace(nbytes, H.device)
-    check(lib().lamq_chol_inv_upper(ptr(H), n, ld(H), float(damp), ptr(Hd), n, ptr(U), n, ptr(dead), ptr(info), ptr(ws),
-                                    nbytes, stream(H.device)), "chol_inv_upper")
+    check(lib().lamq_chol_inv_upper_ex(ptr(H), n, ld(H), float(damp), CHOL_KEEP_DEAD if keep_dead else 0, ptr(Hd), n,
+                                       ptr(U), n, ptr(dead), ptr(info), ptr(ws), nbytes, stream(H.device)),
+          "chol_inv_upper")
     if raise_on_fail:
         bad = int(info.item())
         if bad:

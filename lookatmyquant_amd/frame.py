@@ -86,6 +86,7 @@ class Net:
         if self._matrix is None:
             dev = E._abi.device()
             Q = self.cores["W"].data.to(dev, torch.float64)
+            Q = Q.reshape(-1, Q.shape[-1])  # a column trellis keeps its rows split into (sequence, position)
             S = self.cores["W.S"].data.to(dev, torch.float64)
             X = Q * S[:, None]
             if self.rot_in is not None:

@@ -48,10 +48,10 @@ def parse(program: str):
 
 
 def trellis_code(k: int, T: int = 256, rows: tuple | None = (16, 8), L: int = 12, values=None):
-    """The code of a tr<k> program: the row trellis (width, look) = rows (quantize.py:588-590 with --trellis-rows);
-    the column trellis (rows=None) is not part of this path."""
+    """The code of a tr<k> program (quantize.py:588-590): the row trellis (width, look) = rows with --trellis-rows,
+    else the column trellis over sequences of T outputs."""
     if rows is None:
-        raise NotImplementedError("the column-wise TrellisCode layout is not part of this path")
+        return C.TrellisCode(L, k, T=T, values=values)
     return C.RowTrellisCode(L, k, T=256, width=rows[0], look=rows[1], values=values)
 
 

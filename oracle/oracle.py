@@ -11,6 +11,10 @@ Parity status of each function (what pins it is listed in the test named beside 
   ldlq_trellis       least-squares refit identity, H = c*I composition, reference vectors
   ldlq_scalar        least-squares refit identity, eager GPTQ identity, reference vectors
   environment        LAPACK closed form; U^T U = H_damped^-1
+  ldlq_factor        U^T U = (H + d mean(diag H) I)^-1 at the first d that factors; the retry path
+  ldlq_round         the eager GPTQ loop of ldlq_gpu.py (reference vectors of ldlq_scalar); lazy-block invariance
+  sweep              equals the C sweeps (ldlq_scalar, ldlq_trellis) under their projections
+  column_trellis_*   per-sequence viterbi (pinned above) on the reshaped columns; brute force for tiny L
   hadamard / rht     orthogonality, |H_ij| = 1/sqrt(n), Kronecker closed forms
   hessian            fp64 closed form X^T diag(w) X / N
   kl_rows            fp64 closed form; KL(p||p) = 0; Gaussian-logit closed form
@@ -135,6 +139,93 @@ def environment(H, damp: float = 0.01):
     Hinv = Li.T @ Li
     U = np.linalg.cholesky(Hinv).T
     return H, U, dead
+
+
+def ldlq_factor(Hr, damp: float = 0.01) -> np.ndarray:
+    """U of opgraph/ldlq_gpu.py:15-25: H = (Hr + Hr^T)/2 damped by d*mean(diag H) for d = damp, 10 damp, 100 damp until
+    it factors (a zero diagonal stays zero and counts in the mean); U = upper Cholesky factor of the damped H's inverse.
+    Raises AssertionError when no damping factors."""
+    H = np.asarray(Hr, dtype=np.float64)
+    H = 0.5 * (H + H.T)
+    for d in (damp, 10 * damp, 100 * damp):
+        try:
+            Lc = np.linalg.cholesky(H + d * np.mean(np.diag(H)) * np.eye(len(H)))
+        except np.linalg.LinAlgError:
+            continue
+        Li = np.linalg.inv(Lc)
+        return np.linalg.cholesky(Li.T @ Li).T
+    raise AssertionError("H is not positive definite even with damping")
+
+
+def ldlq_round(X, U, levels, block: int = 128) -> np.ndarray:
+    """The levels opgraph/ldlq_gpu.py:28-49 chooses: the width-1 sweep of ldlq_scalar with unit row scales (bucketize
+    on the midpoints, the rounding error carried through U, lazy blocks of `block`)."""
+    lv = np.asarray(levels, dtype=np.float64)
+    idx = ldlq_scalar(X, U, lv, 1, np.ones(np.shape(X)[0]), block)
+    return lv[idx]
+
+
+def sweep(W, U, project, width: int = 1, lazy: int = 128, dead=None) -> np.ndarray:
+    """The generic block sweep of opgraph/syntax.py:86-124 in numpy: columns settled `width` at a time, project(j, cols, T)
+    returns the settled block, E = cols - q, z = E U_BB^-1, the rest of the lazy run refit at once and the columns after
+    it by one product per run. Returns each column as it stood before it was settled."""
+    from scipy.linalg import solve_triangular
+
+    T = np.array(W, dtype=np.float64, copy=True)
+    U = np.asarray(U, dtype=np.float64)
+    if dead is not None:
+        T[:, np.asarray(dead, dtype=bool)] = 0.0
+    if lazy % width:
+        raise ValueError("lazy must be a multiple of width")
+    m, n = T.shape
+    before = np.empty_like(T)
+    for b0 in range(0, n, lazy):
+        b1 = min(b0 + lazy, n)
+        Z = np.empty((m, b1 - b0))
+        for j in range(b0, b1, width):
+            w = min(width, b1 - j)
+            before[:, j : j + w] = T[:, j : j + w]
+            q = np.asarray(project(j, T[:, j : j + w].copy(), T), dtype=np.float64).reshape(m, w)
+            E = T[:, j : j + w] - q
+            z = solve_triangular(U[j : j + w, j : j + w].T, E.T, lower=True).T  # z U_BB = E
+            T[:, j + w : b1] -= z @ U[j : j + w, j + w : b1]
+            Z[:, j - b0 : j - b0 + w] = z
+        if b1 < n:
+            T[:, b1:] -= Z @ U[b0:b1, b1:]
+    return before
+
+
+def column_trellis_states(X, table64, L: int, k: int, T: int) -> np.ndarray:
+    """TrellisCode's search (opgraph/codes.py:371-378): each column cut into sequences of T consecutive rows, each
+    sequence the nearest path from a free first state; the states in X's layout."""
+    X = np.asarray(X, dtype=np.float64)
+    o, w = X.shape
+    seqs = X.reshape(o // T, T, w).transpose(0, 2, 1).reshape(-1, T)
+    st = viterbi(seqs, table64, L, k)
+    return st.reshape(o // T, w, T).transpose(0, 2, 1).reshape(o, w)
+
+
+def ldlq_words_column_trellis(W, H, table64, L: int, k: int, T: int, seed: int, in_seed: int, width: int = 16):
+    """ldlq_words([W], H, TrellisCode(L, k, T), [seed], in_seed=in_seed) (codes.py:413-462): rows rotated by R_out,
+    columns by R_in, per-row RMS scale, the generic sweep with the column-sequence projection. The states and the row
+    scales (H None: the code applied directly)."""
+    W = np.asarray(W, dtype=np.float64)
+    X = rht(W.shape[0], seed) @ W @ rht(W.shape[1], in_seed).T
+    S = row_scale(X)
+    tb = np.asarray(table64, dtype=np.float64)
+    if H is None:
+        return column_trellis_states(X / S[:, None], tb, L, k, T), S
+    R = rht(W.shape[1], in_seed)
+    _, U, dead = environment(R @ np.asarray(H, dtype=np.float64) @ R.T)
+    states = np.empty(X.shape, dtype=np.int64)
+
+    def project(j, x, _T):
+        st = column_trellis_states(x / S[:, None], tb, L, k, T)
+        states[:, j : j + x.shape[1]] = st
+        return tb[st] * S[:, None]
+
+    sweep(X, U, project, width, 128, dead if dead.any() else None)
+    return states, S
 
 
 # ----------------------------------------------------------------------------- Hadamard and RHT (codes.py:83-132)

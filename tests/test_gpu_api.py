@@ -190,6 +190,105 @@ def test_cross_target_is_the_damped_solve():
     assert np.abs(M - ref).max() < 1e-9
 
 
+def test_ldlq_factor_and_round(golden, config12):
+    """ldlq_gpu.ldlq_factor / ldlq_round (ldlq_gpu.py:15-49): the factor of the symmetrised, damped H (retrying with
+    more damping, a zero diagonal kept zero) and the levels the reference's config-1 vectors hold."""
+    from lookatmyquant_amd import ldlq_gpu
+
+    n = 200
+    rng = np.random.default_rng(21)
+    A = rng.standard_normal((3 * n, n))
+    H = A.T @ A / (3 * n)
+    H[7, :] = 0
+    H[:, 7] = 0
+    Hr = H + 1e-4 * np.triu(rng.standard_normal((n, n)), 1)  # not symmetric: the factor symmetrises first
+    say("ldlq_factor n=200 with a zero diagonal")
+    U = ldlq_gpu.ldlq_factor(torch.from_numpy(Hr)).cpu().numpy()
+    ref = O.ldlq_factor(Hr)
+    assert np.abs(U - ref).max() < 1e-9 * np.abs(ref).max()
+    Q, _ = np.linalg.qr(rng.standard_normal((96, 96)))
+    lam = np.ones(96)
+    lam[0] = -0.05
+    Hn = Q @ np.diag(lam) @ Q.T
+    say("ldlq_factor retry")
+    Un = ldlq_gpu.ldlq_factor(torch.from_numpy(Hn)).cpu().numpy()
+    assert np.abs(Un - O.ldlq_factor(Hn)).max() < 1e-8 * np.abs(Un).max()
+    lam[0] = -5.0
+    with pytest.raises(AssertionError):
+        ldlq_gpu.ldlq_factor(torch.from_numpy(Q @ np.diag(lam) @ Q.T))
+
+    W, H1 = config12
+    g = golden("nested_lm3_c1")
+    R = O.rht(960, 201)
+    X = W.astype(np.float64) @ R.T
+    S = O.row_scale(X)
+    say("ldlq_round config 1")
+    U1 = ldlq_gpu.ldlq_factor(torch.from_numpy(R @ H1 @ R.T))
+    got = ldlq_gpu.ldlq_round(torch.from_numpy(X / S[:, None]), U1, torch.from_numpy(g["levels"]))
+    assert got.dtype == torch.float64 and got.shape == (960, 960)
+    assert np.array_equal(got.cpu().numpy(), g["levels"][g["idx"]])
+
+
+@pytest.mark.parametrize("with_h", [True, False])
+def test_column_trellis_words(tables, with_h):
+    """ldlq_words with the column TrellisCode (codes.py:363-383): the generic sweep, each block's columns cut into
+    sequences of T rows searched from a free first state -- the oracle's states, sequences on trellis paths, the
+    reconstruction the states' values times the row scales, rotated back."""
+    from lookatmyquant_amd import codes as C
+
+    m, n, T = 320, 96, 160
+    rng = np.random.default_rng(22)
+    W = rng.standard_normal((m, n)) * np.abs(rng.standard_t(5, n))
+    A = rng.standard_normal((400, n)) * np.abs(rng.standard_t(4, n))
+    H = A.T @ A / 400 if with_h else None
+    code = C.TrellisCode(12, 2, T=T, values=tables[2].copy())
+    say(f"column trellis ldlq_words H={with_h}")
+    net = C.ldlq_words([torch.from_numpy(W)], None if H is None else torch.from_numpy(H), code, [5], in_seed=6)[0]
+    st, S = O.ldlq_words_column_trellis(W, H, tables[2], 12, 2, T, 5, 6)
+    assert np.array_equal(net.codes.numpy(), st)
+    assert np.abs(net.cores["W.S"].data.numpy() / S - 1).max() < 1e-13
+    c = net.cores["W"]
+    assert c.labels[:2] == ("s", "t") and c.data.shape == (m // T, T, n)
+    seqs = st.reshape(m // T, T, n).transpose(0, 2, 1).reshape(-1, T)
+    assert C.is_trellis_path(torch.from_numpy(seqs), 12, 2)
+    What = net.matrix(dtype=torch.float64).numpy()
+    ref = O.rht(m, 5).T @ (S[:, None] * tables[2][st]) @ O.rht(n, 6)
+    assert np.abs(What - ref).max() < 1e-10 * np.abs(ref).max()
+    with pytest.raises(ValueError):
+        C.ldlq_words([torch.from_numpy(W[:100])], None, code, [5], in_seed=6)
+
+
+def test_chol_keep_dead_flag():
+    """lamq_chol_inv_upper_ex with LAMQ_CHOL_KEEP_DEAD: a zero diagonal is damped, not replaced by 1, and the mean
+    counts it as zero; without the flag it is the Environment factor; an unknown flag is EINVAL."""
+    from lookatmyquant_amd import engine as E
+
+    n = 130
+    rng = np.random.default_rng(23)
+    A = rng.standard_normal((3 * n, n))
+    H = A.T @ A / (3 * n)
+    H[0, :] = 0
+    H[:, 0] = 0
+    Ht = torch.from_numpy(H).cuda()
+    say("chol keep_dead n=130")
+    Hd, U, dead, info = E.chol_inv_upper(Ht, keep_dead=True)
+    assert int(info.item()) == 0 and bool(dead[0]) and int(dead.sum()) == 1
+    ref = O.ldlq_factor(H)
+    assert np.abs(U.cpu().numpy() - ref).max() < 1e-9 * np.abs(ref).max()
+    assert abs(Hd[0, 0].item() - 0.01 * np.mean(np.diag(H))) < 1e-15
+    Hd2, U2, _, _ = E.chol_inv_upper(Ht)
+    _, Ue, _ = O.environment(H)
+    assert np.abs(U2.cpu().numpy() - Ue).max() < 1e-9 * np.abs(Ue).max()
+    assert Hd2[0, 0].item() > 1.0
+    lib = E._abi.lib()
+    ws = torch.empty(lib.lamq_chol_inv_upper_workspace_size(n), dtype=torch.uint8, device="cuda")
+    out = torch.empty(n, n, dtype=torch.float64, device="cuda")
+    inf = torch.zeros(1, dtype=torch.int32, device="cuda")
+    rc = lib.lamq_chol_inv_upper_ex(Ht.data_ptr(), n, n, 0.01, 2, None, 0, out.data_ptr(), n, None, inf.data_ptr(),
+                                    ws.data_ptr(), ws.numel(), None)
+    assert rc == -1  # LAMQ_EINVAL
+
+
 def test_error_paths():
     from lookatmyquant_amd import codes as C
     from lookatmyquant_amd import engine as E

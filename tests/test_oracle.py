@@ -190,6 +190,108 @@ def test_sweep_lazy_equals_eager_for_scalar():
     assert (a == b).mean() > 0.99
 
 
+def test_numpy_sweep_equals_the_c_sweeps(tables):
+    """The generic numpy sweep (syntax.py:86-124), given the scalar projection of ldlq_words and the row-trellis step
+    of RowTrellisCode, settles what the two C sweeps settle (both pinned to the reference's vectors above), dead
+    columns included; its `before` columns agree to rounding."""
+    n, m = 72, 8
+    H = _spd(n, 11)
+    H[5, :] = 0
+    H[:, 5] = 0
+    _, U, dead = O.environment(H)
+    rng = np.random.default_rng(12)
+    W = rng.standard_normal((m, n))
+    S = O.row_scale(W)
+    lv = O.lloyd_max(2)
+    mids = (lv[1:] + lv[:-1]) / 2
+    got = np.empty((m, n), dtype=np.int64)
+
+    def scalar(j, x, T):
+        i = np.searchsorted(mids, x[:, 0] / S, side="left")  # torch.bucketize, right=False
+        got[:, j] = i
+        return lv[i] * S
+
+    before = O.sweep(W, U, scalar, 1, 32, dead)
+    idx, before_c = O.ldlq_scalar(W, U, lv, 1, S, 32, dead, want_before=True)
+    assert np.array_equal(got, idx)
+    assert np.abs(before - before_c).max() < 1e-11
+
+    width, look = 8, 4
+    state = np.zeros(m, dtype=np.int64)
+
+    def step(j, x, T):
+        nonlocal state
+        ahead = T[:, j + width : j + width + look]
+        p = O.viterbi(np.concatenate([x, ahead], 1) / S[:, None], tables[3], 12, 3, start=state)[:, : x.shape[1]]
+        got[:, j : j + x.shape[1]] = p
+        state = p[:, -1]
+        return tables[3][p] * S[:, None]
+
+    O.sweep(W, U, step, width, 32, dead)
+    st = O.ldlq_trellis(W, U, S, tables[3], 12, 3, width, look, 32, dead)
+    assert np.array_equal(got, st)
+
+
+def test_column_trellis_states_are_per_sequence_searches(tables):
+    """TrellisCode's reshape (codes.py:371-378): rows s*T .. s*T+T-1 of column c are one free-start sequence."""
+    T, o, w = 24, 72, 5
+    X = np.random.default_rng(13).standard_normal((o, w))
+    st = O.column_trellis_states(X, tables[2], 12, 2, T)
+    for s in range(o // T):
+        for c in range(w):
+            assert np.array_equal(st[s * T : (s + 1) * T, c], O.viterbi(X[s * T : (s + 1) * T, c][None], tables[2], 12, 2)[0])
+
+
+def test_column_trellis_words_without_H_is_round_to_nearest_path(tables):
+    """Without H, ldlq_words with the column trellis is the search on the rotated, scaled rows; the states of each
+    sequence lie on one trellis path."""
+    W = np.random.default_rng(14).standard_normal((48, 16))
+    st, S = O.ldlq_words_column_trellis(W, None, tables[2], 12, 2, 24, 3, 4)
+    X = O.rht(48, 3) @ W @ O.rht(16, 4).T
+    assert np.allclose(S, np.sqrt((X**2).mean(1)), rtol=1e-14)
+    seqs = st.reshape(2, 24, 16).transpose(0, 2, 1).reshape(-1, 24)
+    assert np.all((seqs[:, 1:] >> 2) == (seqs[:, :-1] & 1023))
+
+
+def test_ldlq_factor_damping_and_retries():
+    """ldlq_gpu.py:15-25: U^T U inverts H + d mean(diag H) I at the first d in (damp, 10 damp, 100 damp) that factors;
+    a zero diagonal stays zero and counts in the mean; none factoring raises AssertionError."""
+    n = 24
+    H = _spd(n, 15)
+    A = np.random.default_rng(16).standard_normal((n, n)) * 1e-3
+    U = O.ldlq_factor(H + (A - A.T))  # the antisymmetric part is dropped
+    assert np.allclose(U, np.triu(U)) and np.all(np.diag(U) > 0)
+    assert np.abs(U.T @ U @ (H + 0.01 * np.mean(np.diag(H)) * np.eye(n)) - np.eye(n)).max() < 1e-10
+    H0 = H.copy()
+    H0[3, :] = 0
+    H0[:, 3] = 0
+    U0 = O.ldlq_factor(H0)
+    assert np.abs(U0.T @ U0 @ (H0 + 0.01 * np.mean(np.diag(H0)) * np.eye(n)) - np.eye(n)).max() < 1e-10
+    Q, _ = np.linalg.qr(np.random.default_rng(17).standard_normal((n, n)))
+    lam = np.ones(n)
+    lam[0] = -0.05  # mean(diag) = mean(lam) ~ 0.96: fails at d = 0.01, factors at 0.1
+    Hn = Q @ np.diag(lam) @ Q.T
+    Un = O.ldlq_factor(Hn)
+    assert np.abs(Un.T @ Un @ (Hn + 0.1 * np.mean(lam) * np.eye(n)) - np.eye(n)).max() < 1e-9
+    lam[0] = -5.0
+    with pytest.raises(AssertionError):
+        O.ldlq_factor(Q @ np.diag(lam) @ Q.T)
+
+
+def test_ldlq_round_is_the_one_rate_nested_sweep(golden, config12):
+    """ldlq_gpu.py documents ldlq_round(X/S, ldlq_factor(Hr), levels) as nested.multirate_sweep with one rate: on
+    config 1 it chooses the reference's levels (nested_lm3 vectors), whatever the lazy block."""
+    W, H = config12
+    g = golden("nested_lm3_c1")
+    R = O.rht(960, 201)
+    X = W.astype(np.float64) @ R.T
+    S = O.row_scale(X)
+    U = O.ldlq_factor(R @ H @ R.T)
+    want = g["levels"][g["idx"]]
+    assert np.array_equal(O.ldlq_round(X[:64] / S[:64, None], U, g["levels"]), want[:64])
+    assert (O.ldlq_round(X[:16] / S[:16, None], U, g["levels"], block=64) == want[:16]).mean() > 0.99
+
+
 def test_environment_is_the_cholesky_factor_of_the_inverse():
     H = _spd(30, 7)
     H[4, :] = 0
