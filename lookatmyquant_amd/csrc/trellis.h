@@ -1,0 +1,396 @@
+// Bitshift-trellis search (opgraph/codes.py:151-181) shared by the standalone kernels and the fused
+// block-LDLQ kernels, and the in-block refit of the fused kernels (opgraph/syntax.py:109-121).
+//
+// Layout. The 2^L states fall into R = 2^(L-K) groups of NB = 2^K: group r collects the states h*R + r
+// (h < NB), which are the possible predecessors of the states r*NB + b. One step of the reference
+// (codes.py:170-172) is best(r) = min_h cost(h*R + r) with the lowest h on ties, then
+// cost'(r*NB + b) = best(r) + (x_t - C[r*NB + b])^2. Thread t of NT owns the G groups r = G*t + g and keeps
+// the values of their NB*G member states h*R + G*t + g in registers. Between steps only the group minima
+// B (R floats) travel through LDS: member h*R + r has the path cost B((h*R + r) >> K) + (x - C)^2, which
+// its group's owner forms itself with the reference's three rounded operations (difference, square, sum),
+// hence the same float32 value. Per step a thread reads the B entries of its members, forms the NB costs
+// of each of its groups, keeps the minimum and its h (strict comparison in increasing h: the lowest h wins
+// a tie, as torch's min does) and writes its G new minima: R floats written and R read per step, a
+// quarter of the full cost vector.
+#pragma once
+#include "common.h"
+
+#define LAMQ_WMAX 16  // widest block the fused kernels settle at once
+
+template <int L, int K, int NT>
+struct VX {
+    static constexpr int NS = 1 << L;
+    static constexpr int R = 1 << (L - K);
+    static constexpr int NB = 1 << K;
+    static constexpr int ACT = R >= NT ? NT : R;   // threads that own groups
+    static constexpr int G = R >= NT ? R / NT : 1;  // groups per thread
+    static constexpr int SPT = G * NB;              // member states per thread
+    // G >= NB: the B entries of a thread's members are NB runs of M consecutive entries, run h starting at
+    // h*(R >> K) + M*t. G < NB: one entry per h, (h*R + G*t) >> K, shared by NB/G neighbouring threads.
+    static constexpr bool RUN = G >= NB;
+    static constexpr int M = RUN ? G / NB : 1;
+};
+
+// s_waitcnt lgkmcnt(0) + s_barrier: orders this workgroup's LDS traffic without waiting for its
+// outstanding global loads (prefetches stay in flight across the search's barriers).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+__device__ __forceinline__ double readlane_f64(double v, int lane)
+{
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)b, lane);
+    const int hi = __builtin_amdgcn_readlane((int)(b >> 32), lane);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+__device__ __forceinline__ float h2f_lo(uint32_t u) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(u & 0xFFFFu)); }
+__device__ __forceinline__ float h2f_hi(uint32_t u) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(u >> 16)); }
+
+// x - C as fma(C, -1, x) with C read in place from its fp16 half of a register (v_fma_mix_f32): one rounding of
+// the exact difference, the value of the float32 subtraction x - float(C). Written as asm because the compiler
+// turns fma(c, -1, x) back into a conversion and a subtraction.
+__device__ __forceinline__ float xmc_lo(float x, uint32_t c)
+{
+    float d;
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[0,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(c), "v"(x));
+    return d;
+}
+__device__ __forceinline__ float xmc_hi(float x, uint32_t c)
+{
+    float d;
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(c), "v"(x));
+    return d;
+}
+
+// The member state values of thread t: member i = h*G + g is state h*R + G*t + g.
+template <class V>
+struct TabF32 {
+    float v[V::SPT];
+    __device__ __forceinline__ void load(const float* __restrict__ C, int t)
+    {
+#pragma unroll
+        for (int h = 0; h < V::NB; ++h)
+#pragma unroll
+            for (int g = 0; g < V::G; ++g) v[h * V::G + g] = C[h * V::R + V::G * t + g];
+    }
+    __device__ __forceinline__ void hold() {}
+    __device__ __forceinline__ float dsq(float x, int i) const
+    {
+        const float d = x - v[i];
+        return d * d;
+    }
+};
+
+// fp16 values packed two per register (tables whose values fp16 holds exactly).
+template <class V>
+struct TabF16 {
+    static_assert(V::G % 2 == 0, "members in pairs");
+    uint32_t v[V::SPT / 2];
+    __device__ __forceinline__ void load(const uint16_t* __restrict__ C16, int t)
+    {
+#pragma unroll
+        for (int h = 0; h < V::NB; ++h)
+#pragma unroll
+            for (int g = 0; g < V::G; g += 2)
+                v[(h * V::G + g) / 2] = *reinterpret_cast<const uint32_t*>(C16 + h * V::R + V::G * t + g);
+    }
+    // keeps the compiler from unpacking the table out of the step loop (twice the registers)
+    __device__ __forceinline__ void hold()
+    {
+#pragma unroll
+        for (int i = 0; i < V::SPT / 2; ++i) asm volatile("" : "+v"(v[i]));
+    }
+    __device__ __forceinline__ float dsq(float x, int i) const
+    {
+        const float d = (i & 1) ? xmc_hi(x, v[i >> 1]) : xmc_lo(x, v[i >> 1]);
+        return d * d;
+    }
+};
+
+// Search one path of TV steps; path[0..TV) is complete when this returns (it ends with a barrier).
+//   xs: TV float32 targets (LDS or global). start < 0 leaves the first state free, else only the states
+//   (start << K | b) & (2^L - 1) may begin (codes.py:164-167). buf: DBL ? 2R : R floats of LDS (with one
+//   buffer each step takes a second barrier, between the reads of the old minima and the writes of the new).
+//   back: (TV-1) * ACT entries (LDS or global), entry t*ACT + owner holding the winning h of each of the
+//   owner's groups for the step that produced B_{t+1}. red: 2*(NT/64) words of LDS.
+//   Final state: the lowest among the minimal costs (codes.py:173); traceback codes.py:176-179.
+struct NoHook {
+    __device__ __forceinline__ void operator()() const {}
+};
+
+// hook() runs once the forward pass is done (the caller's chance to issue loads that the final argmin and the
+// traceback then cover). BACK_GLOBAL: back-pointers in global memory, published to the tracing thread by a full
+// barrier (otherwise only LDS is ordered, and the caller's outstanding loads stay in flight).
+template <int L, int K, int NT, bool DBL, bool BACK_GLOBAL = false, typename BackT, class Tab, class Hook = NoHook>
+__device__ void viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* buf, BackT* back, int* path, float* red,
+                           Hook hook = Hook())
+{
+    using V = VX<L, K, NT>;
+    constexpr int G = V::G, NB = V::NB, M = V::M, R = V::R;
+    static_assert(G * K <= 8 * (int)sizeof(BackT), "one back-pointer entry per thread and step");
+    const int tid = threadIdx.x;
+    const bool act = tid < V::ACT;
+    int ent[NB];
+#pragma unroll
+    for (int h = 0; h < NB; ++h) ent[h] = V::RUN ? h * (R >> K) + M * tid : (h * R + G * tid) >> K;
+    float bv[NB][M];
+    {
+        const int rs = start >= 0 ? (start & (R - 1)) : -1;
+#pragma unroll
+        for (int h = 0; h < NB; ++h)
+#pragma unroll
+            for (int e = 0; e < M; ++e) bv[h][e] = (rs < 0 || ent[h] + e == rs) ? 0.0f : __builtin_inff();
+    }
+    int cur = 0;
+    float x = xs[0];
+    for (int t = 0; t < TV - 1; ++t) {
+        const float xn = xs[t + 1];
+        if (act) {
+            tab.hold();
+            uint32_t bits = 0;
+            float* dst = buf + (DBL ? (cur ^ 1) * R : 0);
+            // groups in chunks of CK sharing one B entry per h (RUN) or all of them; each chunk stored when done
+            constexpr int CK = V::RUN ? NB : G;
+#pragma unroll
+            for (int e = 0; e < G / CK; ++e) {
+                float best[CK];
+#pragma unroll
+                for (int gg = 0; gg < CK; ++gg) {
+                    const int g = e * CK + gg;
+                    float b = bv[0][e] + tab.dsq(x, g);
+                    uint32_t hs = 0;
+#pragma unroll
+                    for (int h = 1; h < NB; ++h) {
+                        const float c = bv[h][e] + tab.dsq(x, h * G + g);
+                        const bool lt = c < b;
+                        b = lt ? c : b;
+                        hs = lt ? (uint32_t)h : hs;
+                    }
+                    best[gg] = b;
+                    bits |= hs << (g * K);
+                }
+                lds_store_swz<CK>(dst, G * tid + e * CK, best);
+            }
+            back[t * V::ACT + tid] = (BackT)bits;
+        }
+        lds_barrier();
+        cur ^= 1;
+        x = xn;
+        if (act) {
+#pragma unroll
+            for (int h = 0; h < NB; ++h) lds_load_swz<M>(buf + (DBL ? cur * R : 0), ent[h], bv[h]);
+        }
+        if (!DBL) lds_barrier();
+    }
+    hook();
+    // final costs, the lowest state on ties (a thread's states increase with (h, g))
+    float bvv = __builtin_inff();
+    int bi = 0x7fffffff;
+    if (act) {
+        tab.hold();
+#pragma unroll
+        for (int h = 0; h < NB; ++h)
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float c = bv[h][V::RUN ? (g >> K) : 0] + tab.dsq(x, h * G + g);
+                if ((h == 0 && g == 0) || c < bvv) {
+                    bvv = c;
+                    bi = h * R + G * tid + g;
+                }
+            }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bvv, off);
+        const int oi = __shfl_xor(bi, off);
+        if (ov < bvv || (ov == bvv && oi < bi)) {
+            bvv = ov;
+            bi = oi;
+        }
+    }
+    int* redi = reinterpret_cast<int*>(red + NT / 64);
+    if ((tid & 63) == 0) {
+        red[tid >> 6] = bvv;
+        redi[tid >> 6] = bi;
+    }
+    if (BACK_GLOBAL)
+        __syncthreads();
+    else
+        lds_barrier();
+    if (tid == 0) {
+        float v = red[0];
+        int s = redi[0];
+        for (int wv = 1; wv < NT / 64; ++wv)
+            if (red[wv] < v || (red[wv] == v && redi[wv] < s)) {
+                v = red[wv];
+                s = redi[wv];
+            }
+        path[TV - 1] = s;
+        for (int t = TV - 1; t > 0; --t) {
+            const int r = s >> K;
+            const int owner = r / G;
+            const int g = r - owner * G;
+            const int h = (int)((back[(t - 1) * V::ACT + owner] >> (g * K)) & (uint32_t)(NB - 1));
+            s = r + h * R;
+            path[t - 1] = s;
+        }
+    }
+    lds_barrier();
+}
+
+// ------------------------------------------------------------------------------------------------ refit
+// One block step of the fused sweep settles w <= 16 columns j..j+w of a row (syntax.py:109-121):
+//   E = T[j+c] - table64[path[c]] * S
+//   z = E U_BB^-1: z[c] = (E[c] - sum_{l<c} z[l] U[j+l][j+c]) / U[j+c][j+c], an fma chain in l (one wave)
+//   T[col] = T[col] - sum_l z[l] U[j+l][col] for col in [j+w, b1), the sum an fma chain from l = 0
+// The U operands do not depend on the row's search, so they are fetched before it and arrive while it runs.
+
+// E (lanes c < w of wave 0, which also store the states) and the forward substitution by wave 0 given ucol[l] =
+// U[j+l][j+c] for lane c = tid % 16. Writes z to zs (LDS) and Zj.
+template <class UCol>
+__device__ __forceinline__ void refit_solve(UCol ucolf, double* trow, int jo, int w, const int* path,
+                                            const double* __restrict__ table64, double Sr, int32_t* states_j,
+                                            double* Zj, double* zs)
+{
+    const int tid = threadIdx.x;
+    double e = 0.0;
+    if (tid < w) {
+        const int p = path[tid];
+        states_j[tid] = p;
+        const double qs = table64[p] * Sr;
+        e = trow[jo + tid] - qs;
+    }
+    double acc = e, zme = 0.0;
+    // U_BB's column in two halves of eight rows (the second fetched only after the first is used)
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        double ucol[LAMQ_WMAX / 2];
+#pragma unroll
+        for (int i = 0; i < LAMQ_WMAX / 2; ++i) ucol[i] = ucolf(half * (LAMQ_WMAX / 2) + i);
+#pragma unroll
+        for (int i = 0; i < LAMQ_WMAX / 2; ++i) {
+            const int l = half * (LAMQ_WMAX / 2) + i;
+            if (l < w) {
+                const double zl = readlane_f64(acc / ucol[i], l);
+                if (tid == l) zme = zl;
+                if (tid > l && tid < w) acc = fma(-zl, ucol[i], acc);
+            }
+        }
+        asm volatile("" ::: "memory");
+    }
+    if (tid < w) {
+        zs[tid] = zme;
+        Zj[tid] = zme;
+    }
+}
+
+// U staged in LDS (the fused kernels with room for it): rows j..j+w of U from column j to b1, fetched by direct
+// global->LDS loads before the search (wave v of NT/64 takes rows v, v + NT/64, ...; four 64-dword pieces per
+// row), urows[l][c] = U[j+l][j+c]. No registers are held across the search.
+template <int NT, int LAZY>
+__device__ __forceinline__ void refit_fetch_lds(double (*urows)[LAZY], const double* __restrict__ U, int64_t ldU,
+                                                int64_t j, int w, int64_t b1)
+{
+    static_assert(LAZY * 2 == 4 * 64, "four 64-dword pieces per row");
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int len = 2 * (int)(b1 - j);  // dwords from column j to b1 (<= 2 * LAZY)
+    for (int l = wv; l < w; l += NT / 64) {
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(U + (j + l) * ldU + j);
+        const uint32_t dst = lds_addr(&urows[l][0]);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            if (p * 64 < len) {
+                const int d = p * 64 + lane;
+                load_lds4(src + (d < len ? d : 0), dst + p * 256);  // lanes past b1 fill the row's padding
+            }
+        }
+    }
+}
+
+template <int NT, int LAZY>
+__device__ void refit_apply_lds(double (*urows)[LAZY], double* trow, int jo, int w, int nc, const int* path,
+                                const double* __restrict__ table64, double Sr, int32_t* states_j, double* Zj,
+                                double* zs)
+{
+    const int tid = threadIdx.x;
+    wait_vm<0>();
+    lds_barrier();
+    if (tid < 64) {
+        const int c = tid & (LAMQ_WMAX - 1);
+        refit_solve([&](int l) { return urows[l][c]; }, trow, jo, w, path, table64, Sr, states_j, Zj, zs);
+    }
+    lds_barrier();
+    if (tid < nc) {
+        double acc = 0.0;
+#pragma unroll
+        for (int l = 0; l < LAMQ_WMAX; ++l)
+            if (l < w) acc = fma(zs[l], urows[l][w + tid], acc);
+        trow[jo + w + tid] = trow[jo + w + tid] - acc;
+    }
+    lds_barrier();
+}
+
+// U held in registers (the kernels whose LDS is full): ub, entry (tid/16, tid%16) of the upper triangle of U_BB
+// (first 256 threads), staged into LDS (ubb) after the search; uc, CH consecutive terms of one column of the update
+// (16/CH threads per column, the chain passed along them in order).
+template <int CH>
+struct RefitRegs {
+    double ub;
+    double uc[CH];
+};
+
+template <int NT, int CH>
+__device__ __forceinline__ void refit_fetch_regs(RefitRegs<CH>& o, const double* __restrict__ U, int64_t ldU, int64_t j,
+                                                 int w, int nc)
+{
+    constexpr int TPC = LAMQ_WMAX / CH;
+    static_assert(NT >= LAMQ_WMAX * LAMQ_WMAX, "one U_BB entry per thread");
+    const int tid = threadIdx.x;
+    o.ub = 0.0;
+    if (tid < LAMQ_WMAX * LAMQ_WMAX) {
+        const int l = tid / LAMQ_WMAX, c = tid % LAMQ_WMAX;
+        if (l <= c && c < w) o.ub = U[(j + l) * ldU + j + c];
+    }
+    const int col = tid / TPC, q = tid % TPC;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) o.uc[i] = 0.0;
+    if (col < nc) {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int l = q * CH + i;
+            if (l < w) o.uc[i] = U[(j + l) * ldU + j + w + col];
+        }
+    }
+}
+
+template <int NT, int CH>
+__device__ void refit_apply_regs(const RefitRegs<CH>& o, double* trow, int jo, int w, int nc, const int* path,
+                                 const double* __restrict__ table64, double Sr, int32_t* states_j, double* Zj,
+                                 double* ubb, double* zs)
+{
+    constexpr int TPC = LAMQ_WMAX / CH;
+    const int tid = threadIdx.x;
+    if (tid < LAMQ_WMAX * LAMQ_WMAX) ubb[tid] = o.ub;
+    lds_barrier();
+    if (tid < 64) {
+        const int c = tid & (LAMQ_WMAX - 1);
+        refit_solve([&](int l) { return ubb[l * LAMQ_WMAX + c]; }, trow, jo, w, path, table64, Sr, states_j, Zj, zs);
+    }
+    lds_barrier();
+    const int col = tid / TPC, q = tid % TPC;
+    double acc = 0.0;
+#pragma unroll
+    for (int p = 0; p < TPC; ++p) {
+        if (q == p && col < nc) {
+#pragma unroll
+            for (int i = 0; i < CH; ++i) {
+                const int l = p * CH + i;
+                if (l < w) acc = fma(zs[l], o.uc[i], acc);
+            }
+        }
+        if (p + 1 < TPC) acc = __shfl_up(acc, 1, TPC);
+    }
+    if (q == TPC - 1 && col < nc) trow[jo + w + col] = trow[jo + w + col] - acc;
+    lds_barrier();
+}

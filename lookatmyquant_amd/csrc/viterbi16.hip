@@ -1,24 +1,28 @@
 // Trellis search with 2^13 .. 2^16 states (the 16-bit-state configurations), standalone and fused into the
-// row-trellis LDLQ block.
+// row-trellis LDLQ block. One 1024-thread workgroup per row; the state values are packed fp16 in VGPRs (the
+// kernels take tables whose values fp16 holds exactly, as the 16-bit configurations' Gaussian-quantile table;
+// x - C is then exact in float32). Back-pointers are one 32-bit word per thread and step (G*k <= 32 bits), in LDS.
 //
-// One 1024-thread workgroup per row. The states are cut into four quarters of QS = 2^(L-2); thread t owns the
-// SQ = 2^L/4096 consecutive states [q*QS + SQ*t, q*QS + SQ*t + SQ) of every quarter q. Those are exactly the
-// successors of its predecessor groups r = q*QS/2^k + SQ*t/2^k + g (g < SQ/2^k), so a thread needs, per step,
-// the path costs of the states h*2^(L-k) + r of its groups, which other threads own. They are exchanged
-// through an LDS window of one quarter: in phase p every thread writes its own states of quarter p and then
-// folds those of its predecessors that lie in quarter p, so all 16 waves work in every phase. Predecessors
-// reach a group in increasing h (a quarter index never decreases with h, and within a phase h is visited in
-// increasing order), so the strict comparison keeps the lowest h on ties, as torch's min does.
-// A thread keeps its state values as packed fp16 in VGPRs (the kernels take tables whose values fp16 holds
-// exactly, as the 16-bit configurations' Gaussian-quantile table; x - C is then exact in float32) and, between
-// steps, only the minimum of each of its groups: the path cost of its state (g, b) is bprev[g] +
-// (x_prev - C)^2, formed again when written to the window with the same three rounded operations, hence the
-// same float32 value. Back-pointers are one 32-bit word per thread and step (G*k <= 32 bits), in LDS.
-#include "common.h"
+// Up to 2^14 groups (every configuration but L = 16, k = 1) the search is trellis.h's: only the group minima
+// (at most 64 KB) pass through LDS each step.
+//
+// L = 16, k = 1 (2^15 groups, 128 KB of minima) keeps the quarter-window search below. The states are cut into
+// four quarters of QS = 2^(L-2); thread t owns the SQ = 2^L/4096 consecutive states [q*QS + SQ*t, q*QS + SQ*t + SQ)
+// of every quarter q. Those are exactly the successors of its predecessor groups r = q*QS/2^k + SQ*t/2^k + g
+// (g < SQ/2^k), so a thread needs, per step, the path costs of the states h*2^(L-k) + r of its groups, which
+// other threads own. They are exchanged through an LDS window of one quarter: in phase p every thread writes its
+// own states of quarter p and then folds those of its predecessors that lie in quarter p, so all 16 waves work in
+// every phase. Predecessors reach a group in increasing h (a quarter index never decreases with h, and within a
+// phase h is visited in increasing order), so the strict comparison keeps the lowest h on ties, as torch's min
+// does. Between steps a thread keeps only the minimum of each of its groups: the path cost of its state (g, b) is
+// bprev[g] + (x_prev - C)^2, formed again when written to the window with the same three rounded operations,
+// hence the same float32 value.
+#include "trellis.h"
 
 #define BIG_NT 1024
 #define BIG_TV 24       // longest fused search: width + look
-#define BIG_LAZY 256
+#define BIG_LAZY 128
+#define BIG_GX_MAX_R 16384  // most groups of the minima-exchange search (64 KB of LDS)
 
 template <int L, int K>
 struct VBig {
@@ -37,28 +41,10 @@ struct VBig {
     static constexpr int offset(int h, int q) { return (h * R + q * RQ) % QS; }
 };
 
-__device__ __forceinline__ float h2f_lo(uint32_t u) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(u & 0xFFFFu)); }
-__device__ __forceinline__ float h2f_hi(uint32_t u) { return (float)__builtin_bit_cast(_Float16, (unsigned short)(u >> 16)); }
-
-// state value i of this thread from the packed registers
-template <int SPT>
-__device__ __forceinline__ float cval(const uint32_t (&Ch)[SPT / 2], int i)
-{
-    return (i & 1) ? h2f_hi(Ch[i >> 1]) : h2f_lo(Ch[i >> 1]);
-}
-
-// x - C[i] as fma(C[i], -1, x) with C[i] read in place from its fp16 half of the register (v_fma_mix_f32):
-// one rounding of the exact difference, the value of the float32 subtraction x - float(C[i]). Written as asm
-// because the compiler turns fma(c, -1, x) back into a conversion and a subtraction.
 template <int SPT>
 __device__ __forceinline__ float xmc(float x, const uint32_t (&Ch)[SPT / 2], int i)
 {
-    float d;
-    if (i & 1)
-        asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(Ch[i >> 1]), "v"(x));
-    else
-        asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[0,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(Ch[i >> 1]), "v"(x));
-    return d;
+    return (i & 1) ? xmc_hi(x, Ch[i >> 1]) : xmc_lo(x, Ch[i >> 1]);
 }
 
 // Search one path of TV steps; thread 0 writes path[0..TV). xs: TV float32 targets. start < 0: free first state.
@@ -220,19 +206,49 @@ __global__ __launch_bounds__(BIG_NT) void viterbi_rows_big_kernel(const float* _
     viterbi_big<L, K>(x + row * ldx, T, Ch, start ? start[row] : -1, xbuf, back, states + row * lds, red);
 }
 
+// minima-exchange search (trellis.h), for up to BIG_GX_MAX_R groups
+template <int L, int K, bool BACK_GLOBAL>
+__global__ __launch_bounds__(BIG_NT) void viterbi_rows_gx_kernel(const float* __restrict__ x, int T, int64_t ldx,
+                                                                 const uint16_t* __restrict__ table16,
+                                                                 const int32_t* __restrict__ start,
+                                                                 int32_t* __restrict__ states, int64_t lds,
+                                                                 uint32_t* __restrict__ back_ws)
+{
+    using V = VX<L, K, BIG_NT>;
+    constexpr bool DBL = V::R <= 4096;
+    __shared__ __align__(16) float buf[(DBL ? 2 : 1) * V::R];
+    __shared__ uint32_t back_lds[BACK_GLOBAL ? 1 : (BIG_TV - 1) * V::ACT];
+    __shared__ float red[2 * (BIG_NT / 64)];
+    const int64_t row = blockIdx.x;
+    TabF16<V> tab;
+    tab.load(table16, threadIdx.x);
+    uint32_t* back = BACK_GLOBAL ? back_ws + row * (int64_t)(T - 1) * BIG_NT : back_lds;
+    viterbi_gx<L, K, BIG_NT, DBL, BACK_GLOBAL>(x + row * ldx, T, tab, start ? start[row] : -1, buf, back,
+                                             states + row * lds, red);
+}
+
 template <int L, int K>
 struct ViterbiRowsBig {
     static int run(const float* x, int64_t B, int T, int64_t ldx, const uint16_t* table16, const int32_t* start,
                    int32_t* states, int64_t lds, void* ws, size_t ws_bytes, hipStream_t s)
     {
+        constexpr bool GX = VX<L, K, BIG_NT>::R <= BIG_GX_MAX_R;
         if (T <= BIG_TV) {
-            hipLaunchKernelGGL((viterbi_rows_big_kernel<L, K, false>), dim3((unsigned)B), dim3(BIG_NT), 0, s, x, T, ldx,
-                               table16, start, states, lds, (uint32_t*)nullptr);
+            if constexpr (GX)
+                hipLaunchKernelGGL((viterbi_rows_gx_kernel<L, K, false>), dim3((unsigned)B), dim3(BIG_NT), 0, s, x, T, ldx,
+                                   table16, start, states, lds, (uint32_t*)nullptr);
+            else
+                hipLaunchKernelGGL((viterbi_rows_big_kernel<L, K, false>), dim3((unsigned)B), dim3(BIG_NT), 0, s, x, T, ldx,
+                                   table16, start, states, lds, (uint32_t*)nullptr);
         } else {
             const size_t need = (size_t)B * (size_t)(T - 1) * BIG_NT * sizeof(uint32_t);
             if (!ws || ws_bytes < need) return LAMQ_EINVAL;
-            hipLaunchKernelGGL((viterbi_rows_big_kernel<L, K, true>), dim3((unsigned)B), dim3(BIG_NT), 0, s, x, T, ldx,
-                               table16, start, states, lds, (uint32_t*)ws);
+            if constexpr (GX)
+                hipLaunchKernelGGL((viterbi_rows_gx_kernel<L, K, true>), dim3((unsigned)B), dim3(BIG_NT), 0, s, x, T, ldx,
+                                   table16, start, states, lds, (uint32_t*)ws);
+            else
+                hipLaunchKernelGGL((viterbi_rows_big_kernel<L, K, true>), dim3((unsigned)B), dim3(BIG_NT), 0, s, x, T, ldx,
+                                   table16, start, states, lds, (uint32_t*)ws);
         }
         LAMQ_LAUNCH_CHECK();
         return LAMQ_OK;
@@ -341,14 +357,81 @@ __global__ __launch_bounds__(BIG_NT) void ldlq_trellis_block_big_kernel(
     if (tid == 0) state[row] = st;
 }
 
+// The same with the minima-exchange search and the prefetched refit of trellis.h (four threads per column of the
+// in-block update).
+template <int L, int K>
+__global__ __launch_bounds__(BIG_NT) void ldlq_trellis_block_gx_kernel(
+    const double* __restrict__ T, int64_t n, int64_t ldT, const double* __restrict__ U, int64_t ldU,
+    const double* __restrict__ S, const double* __restrict__ table64, const uint16_t* __restrict__ table16,
+    int64_t b0, int64_t b1, int width, int look, int32_t* __restrict__ state, int32_t* __restrict__ states,
+    int64_t lds, double* __restrict__ Z, int64_t ldZ)
+{
+    using V = VX<L, K, BIG_NT>;
+    constexpr bool DBL = V::R <= 4096;
+    // one record, small arrays first: their addresses stay within the 16-bit offset of LDS instructions
+    struct alignas(16) Smem {
+        double trow[BIG_LAZY + BIG_TV];
+        double ubb[LAMQ_WMAX * LAMQ_WMAX];
+        double zs[LAMQ_WMAX];
+        float xs[BIG_TV];
+        int path[BIG_TV];
+        float red[2 * (BIG_NT / 64)];
+        float buf[(DBL ? 2 : 1) * V::R];
+        uint32_t back[(BIG_TV - 1) * V::ACT];
+    };
+    __shared__ Smem sm;
+    double* trow = sm.trow;
+    double* ubb = sm.ubb;
+    double* zs = sm.zs;
+    float* xs = sm.xs;
+    int* path = sm.path;
+    float* red = sm.red;
+    float* buf = sm.buf;
+    uint32_t* back = sm.back;
+
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x;
+    TabF16<V> tab;
+    tab.load(table16, tid);
+    const int64_t cend = (b1 + look < n) ? b1 + look : n;
+    const double* Tr = T + row * ldT;
+    for (int64_t c = tid; c < cend - b0; c += BIG_NT) trow[c] = Tr[b0 + c];
+    const double Sr = S[row];
+    int st = state[row];
+    lds_barrier();
+
+    for (int64_t j = b0; j < b1; j += width) {
+        const int w = (int)((j + width <= b1) ? width : (b1 - j));
+        const int64_t ahead = n - (j + w);
+        const int a = (int)(ahead < look ? ahead : look);
+        const int TV = w + a;
+        const int jo = (int)(j - b0);
+        const int nc = (int)(b1 - j - w);
+        if (tid < TV) xs[tid] = (float)(trow[jo + tid] / Sr);
+        lds_barrier();
+        // the refit's U operands are fetched when the forward pass ends, under the final argmin and the traceback
+        RefitRegs<4> ops;
+        viterbi_gx<L, K, BIG_NT, DBL>(xs, TV, tab, st, buf, back, path, red,
+                                      [&]() { refit_fetch_regs<BIG_NT, 4>(ops, U, ldU, j, w, nc); });
+        refit_apply_regs<BIG_NT, 4>(ops, trow, jo, w, nc, path, table64, Sr, states + row * lds + j, Z + row * ldZ + jo, ubb,
+                               zs);
+        st = path[w - 1];
+    }
+    if (tid == 0) state[row] = st;
+}
+
 template <int L, int K>
 struct TrellisBlockBig {
     static int run(const double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU, const double* S,
                    const double* table64, const uint16_t* table16, int64_t b0, int64_t b1, int width, int look,
                    int32_t* state, int32_t* states, int64_t lds, double* Z, int64_t ldZ, hipStream_t s)
     {
-        hipLaunchKernelGGL((ldlq_trellis_block_big_kernel<L, K>), dim3((unsigned)m), dim3(BIG_NT), 0, s, T, n, ldT, U, ldU,
-                           S, table64, table16, b0, b1, width, look, state, states, lds, Z, ldZ);
+        if constexpr (VX<L, K, BIG_NT>::R <= BIG_GX_MAX_R)
+            hipLaunchKernelGGL((ldlq_trellis_block_gx_kernel<L, K>), dim3((unsigned)m), dim3(BIG_NT), 0, s, T, n, ldT, U,
+                               ldU, S, table64, table16, b0, b1, width, look, state, states, lds, Z, ldZ);
+        else
+            hipLaunchKernelGGL((ldlq_trellis_block_big_kernel<L, K>), dim3((unsigned)m), dim3(BIG_NT), 0, s, T, n, ldT, U,
+                               ldU, S, table64, table16, b0, b1, width, look, state, states, lds, Z, ldZ);
         LAMQ_LAUNCH_CHECK();
         return LAMQ_OK;
     }
@@ -364,7 +447,7 @@ extern "C" int lamq_ldlq_trellis16_block(double* T, int64_t m, int64_t n, int64_
     if (m < 0 || n < 1 || ldT < n || ldU < n || lds < n || b0 < 0 || b1 <= b0 || b1 > n || width < 1 || look < 0)
         return LAMQ_EINVAL;
     if (ldZ < b1 - b0) return LAMQ_EINVAL;
-    if (width + look > BIG_TV || b1 - b0 > BIG_LAZY || m > 0x7fffffff) return LAMQ_EUNSUP;
+    if (width > LAMQ_WMAX || width + look > BIG_TV || b1 - b0 > BIG_LAZY || m > 0x7fffffff) return LAMQ_EUNSUP;
     if (m == 0) return LAMQ_OK;
     return dispatch_big<TrellisBlockBig>(L, k, T, m, n, ldT, U, ldU, S, table64, table16, b0, b1, width, look, state,
                                          states, lds, Z, ldZ, as_stream(stream));
