@@ -121,9 +121,45 @@ struct NoHook {
 // hook() runs once the forward pass is done (the caller's chance to issue loads that the final argmin and the
 // traceback then cover). BACK_GLOBAL: back-pointers in global memory, published to the tracing thread by a full
 // barrier (otherwise only LDS is ordered, and the caller's outstanding loads stay in flight).
-template <int L, int K, int NT, bool DBL, bool BACK_GLOBAL = false, typename BackT, class Tab, class Hook = NoHook>
-__device__ void viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* buf, BackT* back, int* path, float* red,
-                           Hook hook = Hook())
+// lexicographic (v, i) minimum of the wave through DPP moves (no LDS): quad swaps, half-row and row mirrors, then the
+// row broadcasts; lane 63 ends up with the minimum of all 64 lanes.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ void argmin_dpp(float& v, int& i)
+{
+    const float ov = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROWS, 0xF, false));
+    const int oi = __builtin_amdgcn_update_dpp(i, i, CTRL, ROWS, 0xF, false);
+    if (ov < v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
+    }
+}
+
+__device__ __forceinline__ void wave_argmin(float& v, int& i)
+{
+    argmin_dpp<0xB1, 0xF>(v, i);   // quad_perm [1,0,3,2]
+    argmin_dpp<0x4E, 0xF>(v, i);   // quad_perm [2,3,0,1]
+    argmin_dpp<0x141, 0xF>(v, i);  // row_half_mirror
+    argmin_dpp<0x140, 0xF>(v, i);  // row_mirror
+    argmin_dpp<0x142, 0xA>(v, i);  // row_bcast15 into rows 1 and 3
+    argmin_dpp<0x143, 0xC>(v, i);  // row_bcast31 into rows 2 and 3
+}
+
+// Search one path of TV steps. With PATHREG (TV <= 64) the path comes back in a register of wave 0, lane c holding
+// path[c] (the return value), and is also stored to path[0..TV) (LDS or global); otherwise lane 0 of wave 0 stores
+// path[] as the traceback goes and the return value is 0. Ends with a barrier after which path[] is complete.
+//   xs: TV float32 targets (LDS or global). start < 0 leaves the first state free, else only the states
+//   (start << K | b) & (2^L - 1) may begin (codes.py:164-167). buf: DBL ? 2R : R floats of LDS (with one
+//   buffer each step takes a second barrier, between the reads of the old minima and the writes of the new).
+//   back: (TV-1) * ACT entries (LDS or global), entry t*ACT + owner holding the winning h of each of the
+//   owner's groups for the step that produced B_{t+1}. red: 2*(NT/64) words of LDS.
+//   Final state: the lowest among the minimal costs (codes.py:173); traceback codes.py:176-179.
+// hook() runs once the forward pass is done (the caller's chance to issue loads that the final argmin and the
+// traceback then cover). BACK_GLOBAL: back-pointers in global memory, published to the tracing wave by a full
+// barrier (otherwise only LDS is ordered, and the caller's outstanding loads stay in flight).
+template <int L, int K, int NT, bool DBL, bool BACK_GLOBAL = false, bool PATHREG = false, typename BackT, class Tab,
+          class Hook = NoHook>
+__device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* buf, BackT* back, int* path, float* red,
+                          Hook hook = Hook())
 {
     using V = VX<L, K, NT>;
     constexpr int G = V::G, NB = V::NB, M = V::M, R = V::R;
@@ -199,17 +235,9 @@ __device__ void viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* 
                 }
             }
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(bvv, off);
-        const int oi = __shfl_xor(bi, off);
-        if (ov < bvv || (ov == bvv && oi < bi)) {
-            bvv = ov;
-            bi = oi;
-        }
-    }
+    wave_argmin(bvv, bi);
     int* redi = reinterpret_cast<int*>(red + NT / 64);
-    if ((tid & 63) == 0) {
+    if ((tid & 63) == 63) {
         red[tid >> 6] = bvv;
         redi[tid >> 6] = bi;
     }
@@ -217,25 +245,67 @@ __device__ void viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* 
         __syncthreads();
     else
         lds_barrier();
-    if (tid == 0) {
+    int pathv = 0;
+    if (tid < 64) {
+        // wave 0 traces back; every lane combines the waves' minima, so s is uniform
         float v = red[0];
         int s = redi[0];
+#pragma unroll
         for (int wv = 1; wv < NT / 64; ++wv)
             if (red[wv] < v || (red[wv] == v && redi[wv] < s)) {
                 v = red[wv];
                 s = redi[wv];
             }
-        path[TV - 1] = s;
-        for (int t = TV - 1; t > 0; --t) {
-            const int r = s >> K;
-            const int owner = r / G;
-            const int g = r - owner * G;
-            const int h = (int)((back[(t - 1) * V::ACT + owner] >> (g * K)) & (uint32_t)(NB - 1));
-            s = r + h * R;
-            path[t - 1] = s;
+        s = __builtin_amdgcn_readfirstlane(s);
+        const auto emit = [&](int c, int sc) {
+            if (PATHREG)
+                pathv = tid == c ? sc : pathv;
+            else if (tid == 0)
+                path[c] = sc;
+        };
+        emit(TV - 1, s);
+        // D steps per round trip to the back-pointers: lane 0 reads the word of s's group for step t; lanes 1..NB
+        // the words of the groups step t-1 continues from (one per h that step t may pick); with D = 3, lanes
+        // NB+1 .. NB+NB^2 those of step t-2 (one per pair of picks). Then the picks resolve through readlane.
+        constexpr int D = (1 + NB + NB * NB <= 64) ? 3 : 2;
+        constexpr int LG = __builtin_ctz(G);
+        const int lane = tid;
+        const int level = lane == 0 ? 0 : (lane <= NB ? 1 : ((D == 3 && lane <= NB + NB * NB) ? 2 : 0));
+        const uint32_t sp1 = (uint32_t)(level == 1 ? lane - 1 : (level == 2 ? (lane - 1 - NB) / NB : 0)) * R;
+        const uint32_t sp2 = (uint32_t)(level == 2 ? (lane - 1 - NB) % NB : 0) * R;
+        const auto pick = [&](uint32_t word, uint32_t r) {  // the state before r's group at that step
+            return r + ((word >> ((r & (G - 1)) * K)) & (uint32_t)(NB - 1)) * (uint32_t)R;
+        };
+        int t = TV - 1;
+        for (; t >= D; t -= D) {
+            const uint32_t r = (uint32_t)s >> K;
+            uint32_t grp = r;
+            if (level >= 1) grp = (grp + sp1) >> K;
+            if (level >= 2) grp = (grp + sp2) >> K;
+            const uint32_t wd = (uint32_t)back[(t - 1 - level) * V::ACT + (grp >> LG)];
+            const uint32_t s1 = pick((uint32_t)__builtin_amdgcn_readfirstlane((int)wd), r);
+            const uint32_t h1 = s1 >> (L - K);
+            const uint32_t s2 = pick((uint32_t)__builtin_amdgcn_readlane((int)wd, 1 + h1), s1 >> K);
+            emit(t - 1, (int)s1);
+            emit(t - 2, (int)s2);
+            if (D == 3) {
+                const uint32_t h2 = s2 >> (L - K);
+                const uint32_t s3 = pick((uint32_t)__builtin_amdgcn_readlane((int)wd, 1 + NB + h1 * NB + h2), s2 >> K);
+                emit(t - 3, (int)s3);
+                s = (int)s3;
+            } else {
+                s = (int)s2;
+            }
         }
+        for (; t >= 1; --t) {
+            const uint32_t r = (uint32_t)s >> K;
+            s = (int)pick((uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)back[(t - 1) * V::ACT + (r >> LG)]), r);
+            emit(t - 1, s);
+        }
+        if (PATHREG && tid < TV) path[tid] = pathv;
     }
     lds_barrier();
+    return pathv;
 }
 
 // ------------------------------------------------------------------------------------------------ refit
@@ -247,17 +317,19 @@ __device__ void viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* 
 
 // E (lanes c < w of wave 0, which also store the states) and the forward substitution by wave 0 given ucol[l] =
 // U[j+l][j+c] for lane c = tid % 16. Writes z to zs (LDS) and Zj.
+// E (lanes c < w of wave 0, which also store the states) and the forward substitution by wave 0 given ucolf(l) =
+// U[j+l][j+c] for lane c = tid % 16 and q = table64[path[c]] (lanes c < w). The diagonal enters through its
+// reciprocal, as BLAS trsm kernels apply it: z[c] = acc * (1 / U[j+c][j+c]). Writes z to zs (LDS) and Zj.
 template <class UCol>
-__device__ __forceinline__ void refit_solve(UCol ucolf, double* trow, int jo, int w, const int* path,
-                                            const double* __restrict__ table64, double Sr, int32_t* states_j,
-                                            double* Zj, double* zs)
+__device__ __forceinline__ void refit_solve(UCol ucolf, double* trow, int jo, int w, double q, double Sr, double* Zj,
+                                            double* zs)
 {
     const int tid = threadIdx.x;
+    const int c = tid & (LAMQ_WMAX - 1);
+    const double rinv = 1.0 / ucolf(c);
     double e = 0.0;
     if (tid < w) {
-        const int p = path[tid];
-        states_j[tid] = p;
-        const double qs = table64[p] * Sr;
+        const double qs = q * Sr;
         e = trow[jo + tid] - qs;
     }
     double acc = e, zme = 0.0;
@@ -271,7 +343,7 @@ __device__ __forceinline__ void refit_solve(UCol ucolf, double* trow, int jo, in
         for (int i = 0; i < LAMQ_WMAX / 2; ++i) {
             const int l = half * (LAMQ_WMAX / 2) + i;
             if (l < w) {
-                const double zl = readlane_f64(acc / ucol[i], l);
+                const double zl = readlane_f64(acc * rinv, l);
                 if (tid == l) zme = zl;
                 if (tid > l && tid < w) acc = fma(-zl, ucol[i], acc);
             }
@@ -308,17 +380,23 @@ __device__ __forceinline__ void refit_fetch_lds(double (*urows)[LAZY], const dou
     }
 }
 
+// pv: the path register of the search (wave 0, lane c = path[c]).
 template <int NT, int LAZY>
-__device__ void refit_apply_lds(double (*urows)[LAZY], double* trow, int jo, int w, int nc, const int* path,
+__device__ void refit_apply_lds(double (*urows)[LAZY], double* trow, int jo, int w, int nc, int pv,
                                 const double* __restrict__ table64, double Sr, int32_t* states_j, double* Zj,
                                 double* zs)
 {
     const int tid = threadIdx.x;
     wait_vm<0>();
+    double qset = 0.0;
+    if (tid < w) {
+        qset = table64[pv];
+        states_j[tid] = pv;
+    }
     lds_barrier();
     if (tid < 64) {
         const int c = tid & (LAMQ_WMAX - 1);
-        refit_solve([&](int l) { return urows[l][c]; }, trow, jo, w, path, table64, Sr, states_j, Zj, zs);
+        refit_solve([&](int l) { return urows[l][c]; }, trow, jo, w, qset, Sr, Zj, zs);
     }
     lds_barrier();
     if (tid < nc) {
@@ -365,17 +443,22 @@ __device__ __forceinline__ void refit_fetch_regs(RefitRegs<CH>& o, const double*
 }
 
 template <int NT, int CH>
-__device__ void refit_apply_regs(const RefitRegs<CH>& o, double* trow, int jo, int w, int nc, const int* path,
+__device__ void refit_apply_regs(const RefitRegs<CH>& o, double* trow, int jo, int w, int nc, int pv,
                                  const double* __restrict__ table64, double Sr, int32_t* states_j, double* Zj,
                                  double* ubb, double* zs)
 {
     constexpr int TPC = LAMQ_WMAX / CH;
     const int tid = threadIdx.x;
+    double qset = 0.0;
+    if (tid < w) {
+        qset = table64[pv];
+        states_j[tid] = pv;
+    }
     if (tid < LAMQ_WMAX * LAMQ_WMAX) ubb[tid] = o.ub;
     lds_barrier();
     if (tid < 64) {
         const int c = tid & (LAMQ_WMAX - 1);
-        refit_solve([&](int l) { return ubb[l * LAMQ_WMAX + c]; }, trow, jo, w, path, table64, Sr, states_j, Zj, zs);
+        refit_solve([&](int l) { return ubb[l * LAMQ_WMAX + c]; }, trow, jo, w, qset, Sr, Zj, zs);
     }
     lds_barrier();
     const int col = tid / TPC, q = tid % TPC;

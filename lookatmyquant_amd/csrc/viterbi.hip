@@ -121,8 +121,8 @@ __global__ __launch_bounds__(LAMQ_NT) void ldlq_trellis_block_kernel(
         refit_fetch_lds<LAMQ_NT, LAMQ_LAZY_MAX>(urows, U, ldU, j, w, b1);
         if (tid < TV) xs[tid] = (float)(trow[jo + tid] / Sr);
         lds_barrier();
-        viterbi_gx<L, K, LAMQ_NT, true>(xs, TV, tab, st, buf, back, path, red);
-        refit_apply_lds<LAMQ_NT, LAMQ_LAZY_MAX>(urows, trow, jo, w, nc, path, table64, Sr, states + row * lds + j,
+        const int pv = viterbi_gx<L, K, LAMQ_NT, true, false, true>(xs, TV, tab, st, buf, back, path, red);
+        refit_apply_lds<LAMQ_NT, LAMQ_LAZY_MAX>(urows, trow, jo, w, nc, pv, table64, Sr, states + row * lds + j,
                                                 Z + row * ldZ + jo, zs);
         st = path[w - 1];
     }

@@ -411,9 +411,9 @@ __global__ __launch_bounds__(BIG_NT) void ldlq_trellis_block_gx_kernel(
         lds_barrier();
         // the refit's U operands are fetched when the forward pass ends, under the final argmin and the traceback
         RefitRegs<4> ops;
-        viterbi_gx<L, K, BIG_NT, DBL>(xs, TV, tab, st, buf, back, path, red,
-                                      [&]() { refit_fetch_regs<BIG_NT, 4>(ops, U, ldU, j, w, nc); });
-        refit_apply_regs<BIG_NT, 4>(ops, trow, jo, w, nc, path, table64, Sr, states + row * lds + j, Z + row * ldZ + jo, ubb,
+        const int pv = viterbi_gx<L, K, BIG_NT, DBL, false, true>(
+            xs, TV, tab, st, buf, back, path, red, [&]() { refit_fetch_regs<BIG_NT, 4>(ops, U, ldU, j, w, nc); });
+        refit_apply_regs<BIG_NT, 4>(ops, trow, jo, w, nc, pv, table64, Sr, states + row * lds + j, Z + row * ldZ + jo, ubb,
                                zs);
         st = path[w - 1];
     }

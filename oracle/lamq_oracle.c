@@ -98,7 +98,8 @@ int orc_viterbi(const float* x, int64_t B, int T, int64_t ldx, const float* C, i
  *   T[j+w : b1] -= z @ U[cols, j+w : b1]                                         (syntax.py:120)
  *   after the run: T[b1 :] -= Z @ U[b0:b1, b1:]                                   (syntax.py:123)
  * Order of floating-point operations used here (and by the HIP kernels):
- *   z[c]  = (E[c] fma-minus sum_{l<c} z[l]*U[j+l][j+c], l ascending) / U[j+c][j+c]
+ *   z[c]  = (E[c] fma-minus sum_{l<c} z[l]*U[j+l][j+c], l ascending) * (1 / U[j+c][j+c])
+ *           (the diagonal through its reciprocal, as BLAS trsm kernels apply it)
  *   acc   = sum_l z[l]*U[j+l][col] as an fma chain from 0, l ascending;  T[col] = T[col] - acc
  *   trail = sum_c Z[c]*U[b0+c][col] as an fma chain from 0, c ascending; T[col] = T[col] - trail
  * ------------------------------------------------------------------------------------- */
@@ -107,7 +108,7 @@ static void solve_block(const double* E, int w, const double* U, int64_t ldU, in
     for (int c = 0; c < w; ++c) {
         double acc = E[c];
         for (int l = 0; l < c; ++l) acc = fma(-z[l], U[(j + l) * ldU + j + c], acc);
-        z[c] = acc / U[(j + c) * ldU + j + c];
+        z[c] = acc * (1.0 / U[(j + c) * ldU + j + c]);
     }
 }
 
