@@ -26,11 +26,11 @@ FLAGS = ["-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}", "-ffp-contract=
 
 # Per-file additions. The fp64 GEMM keeps its 64 accumulators in VGPR-form MFMAs (-amdgpu-mfma-vgpr-form): left to
 # itself, the register allocator carries them around the k-loop in VGPRs and copies them into AGPRs every stage.
-# The L <= 12 trellis search never produces a NaN (costs are finite or +inf, and inf - inf never forms), so it is
-# built with -fno-honor-nans: "c < best ? c : best" then becomes v_min_f32, which needs no compare mask and spares
-# the hazard waits of the compare-select pairs. (The 16-bit-state search measured no better with it.)
+# The trellis searches never produce a NaN (costs are finite or +inf, and inf - inf never forms), so they are
+# built with -fno-honor-nans: a group's minimum is then a v_min/v_min3 tree, which needs no compare masks and spares
+# the hazard waits of compare-select pairs.
 FILE_FLAGS = {"ldlq.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"], "chol.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
-              "viterbi.hip": ["-fno-honor-nans"]}
+              "viterbi.hip": ["-fno-honor-nans"], "viterbi16.hip": ["-fno-honor-nans"]}
 
 
 def hipcc() -> str:

@@ -193,16 +193,18 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
 #pragma unroll
                 for (int gg = 0; gg < CK; ++gg) {
                     const int g = e * CK + gg;
-                    float b = bv[0][e] + tab.dsq(x, g);
-                    uint32_t hs = 0;
+                    float c[NB];
 #pragma unroll
-                    for (int h = 1; h < NB; ++h) {
-                        const float c = bv[h][e] + tab.dsq(x, h * G + g);
-                        const bool lt = c < b;
-                        b = lt ? c : b;
-                        hs = lt ? (uint32_t)h : hs;
-                    }
+                    for (int h = 0; h < NB; ++h) c[h] = bv[h][e] + tab.dsq(x, h * G + g);
+                    // the minimum, then the lowest h attaining it (costs are never NaN: finite or +inf)
+                    float b = c[0];
+#pragma unroll
+                    for (int h = 1; h < NB; ++h) b = fminf(b, c[h]);
+                    uint32_t hs = NB - 1;
+#pragma unroll
+                    for (int h = NB - 2; h >= 0; --h) hs = c[h] == b ? (uint32_t)h : hs;
                     best[gg] = b;
+                    asm volatile("" : "+v"(hs));  // keeps h a small integer: one shift-or per group, no wide constants
                     bits |= hs << (g * K);
                 }
                 lds_store_swz<CK>(dst, G * tid + e * CK, best);
