@@ -11,6 +11,7 @@
 #include "gemm_f64.h"
 
 #define NBK 64
+#define NB2 256  // panel width of the two-level blocking (a multiple of NBK)
 
 // dead = diag(H) == 0; the damping delta = damp * mean(diag H') where H' has unit diagonal at dead (with
 // keep_dead, H' = H: the dead diagonal stays zero and counts as zero).
@@ -181,34 +182,60 @@ extern "C" int lamq_chol_inv_upper_ex(const double* H, int64_t n, int64_t ldH, d
     const dim3 g2((unsigned)cdiv(n, 64), (unsigned)cdiv(n, 16)), b2(64, 16);
     hipLaunchKernelGGL(prep_kernel, g2, b2, 0, s, H, n, ldH, delta, keep_dead, A, Hd, ldHd);
     LAMQ_LAUNCH_CHECK();
-    // Cholesky of A = J Hd J, lower
-    for (int64_t k0 = 0; k0 < n; k0 += NBK) {
-        const int nb = (int)(n - k0 < NBK ? n - k0 : NBK);
-        double* Lk = Linv + (k0 / NBK) * NBK * NBK;
-        hipLaunchKernelGGL(diag_block_kernel, dim3(1), dim3(64), 0, s, A, n, k0, nb, Lk, info);
-        LAMQ_LAUNCH_CHECK();
-        const int64_t rest = n - k0 - nb;
+    // Cholesky of A = J Hd J, lower, in panels of NB2 columns: inside a panel, 64-wide steps update only the panel's
+    // own columns; the columns after it get one product of depth NB2 per panel (a quarter of the traffic of 64-deep
+    // updates of the whole trailing matrix)
+    for (int64_t K0 = 0; K0 < n; K0 += NB2) {
+        const int64_t pe = (K0 + NB2 < n) ? K0 + NB2 : n;
+        for (int64_t k0 = K0; k0 < pe; k0 += NBK) {
+            const int nb = (int)(n - k0 < NBK ? n - k0 : NBK);
+            double* Lk = Linv + (k0 / NBK) * NBK * NBK;
+            hipLaunchKernelGGL(diag_block_kernel, dim3(1), dim3(64), 0, s, A, n, k0, nb, Lk, info);
+            LAMQ_LAUNCH_CHECK();
+            const int64_t rest = n - k0 - nb;
+            if (rest > 0) {
+                double* P = A + (k0 + nb) * n + k0;
+                // P = P Lkk^-T (the row-wise triangular solve as one product, in place: one tile column)
+                int rc = gemm_sub_f64<true, false, true>(P, n, P, n, Lk, NBK, rest, nb, nb, info, s);
+                if (rc) return rc;
+                const int64_t pc = pe - (k0 + nb);
+                if (pc > 0) {
+                    rc = gemm_sub_f64<true, true>(A + (k0 + nb) * n + k0 + nb, n, P, n, P, n, rest, pc, nb, info, s);
+                    if (rc) return rc;
+                }
+            }
+        }
+        const int64_t rest = n - pe;
         if (rest > 0) {
-            double* P = A + (k0 + nb) * n + k0;
-            // P = P Lkk^-T (the row-wise triangular solve as one product, in place: one tile column)
-            int rc = gemm_sub_f64<true, false, true>(P, n, P, n, Lk, NBK, rest, nb, nb, info, s);
-            if (rc) return rc;
-            rc = gemm_sub_f64<true, true>(A + (k0 + nb) * n + k0 + nb, n, P, n, P, n, rest, rest, nb, info, s);
+            const double* P = A + pe * n + K0;
+            int rc = gemm_sub_f64<true, true>(A + pe * n + pe, n, P, n, P, n, rest, rest, pe - K0, info, s);
             if (rc) return rc;
         }
     }
-    // X = L^-1 into U (right-looking solve of L X = I): X_k = Lkk^-1 B_k, then B_i -= L_ik X_k below
+    // X = L^-1 into U (right-looking solve of L X = I): X_k = Lkk^-1 B_k, then B_i -= L_ik X_k below, inside the
+    // panel at once and below it once per panel (X is lower triangular, so the panel's rows are zero right of
+    // their diagonal and one product of depth NB2 carries the panel's steps)
     hipLaunchKernelGGL(identity_kernel, g2, b2, 0, s, U, n, ldU);
     LAMQ_LAUNCH_CHECK();
-    for (int64_t k0 = 0; k0 < n; k0 += NBK) {
-        const int nb = (int)(n - k0 < NBK ? n - k0 : NBK);
-        const double* Lk = Linv + (k0 / NBK) * NBK * NBK;
-        int rc = gemm_sub_f64<false, false, true>(U + k0 * ldU, ldU, Lk, NBK, U + k0 * ldU, ldU, nb, k0 + nb, nb, info, s);
-        if (rc) return rc;
-        const int64_t rest = n - k0 - nb;
+    for (int64_t K0 = 0; K0 < n; K0 += NB2) {
+        const int64_t pe = (K0 + NB2 < n) ? K0 + NB2 : n;
+        for (int64_t k0 = K0; k0 < pe; k0 += NBK) {
+            const int nb = (int)(n - k0 < NBK ? n - k0 : NBK);
+            const double* Lk = Linv + (k0 / NBK) * NBK * NBK;
+            int rc = gemm_sub_f64<false, false, true>(U + k0 * ldU, ldU, Lk, NBK, U + k0 * ldU, ldU, nb, k0 + nb, nb, info,
+                                                      s);
+            if (rc) return rc;
+            const int64_t rin = pe - (k0 + nb);
+            if (rin > 0) {
+                rc = gemm_sub_f64<false, false>(U + (k0 + nb) * ldU, ldU, A + (k0 + nb) * n + k0, n, U + k0 * ldU, ldU, rin,
+                                                k0 + nb, nb, info, s);
+                if (rc) return rc;
+            }
+        }
+        const int64_t rest = n - pe;
         if (rest > 0) {
-            rc = gemm_sub_f64<false, false>(U + (k0 + nb) * ldU, ldU, A + (k0 + nb) * n + k0, n, U + k0 * ldU, ldU, rest,
-                                            k0 + nb, nb, info, s);
+            int rc = gemm_sub_f64<false, false>(U + pe * ldU, ldU, A + pe * n + K0, n, U + K0 * ldU, ldU, rest, pe, pe - K0,
+                                                info, s);
             if (rc) return rc;
         }
     }
