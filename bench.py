@@ -95,8 +95,8 @@ def cpu_baseline(W, H, table, L, k, in_seed, budget_s=12.0):
 
 
 # HBM bytes per launch of the dominant kernel, from two rocprofv3 counter runs (FETCH_SIZE, WRITE_SIZE) scaled by a
-# 1 GiB copy's readings (profiles/ldlq_trellis_block_big_config2_L16_k2.md); keyed by (kernel, L, k).
-MEASURED_TRAFFIC = {("ldlq_trellis_block_big_kernel", 16, 2): 16627978}
+# 1 GiB copy's readings (profiles/ldlq_trellis_block_gx_config2_L16_k2.md); keyed by (kernel, L, k).
+MEASURED_TRAFFIC = {("ldlq_trellis_block_gx_kernel", 16, 2): 10838044}
 
 MFMA_F64_PEAK_TFLOPS = 78.6
 MFMA_BF16_PEAK_TFLOPS = 2500.0
@@ -351,7 +351,10 @@ def run_c2(args):
     achieved = ops_step / (blk_ms_step * 1e-3) / 1e12
     value = m * n / (ms * 1e-3)
     rows_per_s = m / (ms * 1e-3)
-    kname = "ldlq_trellis_block_big_kernel" if L >= E.BIG_L else "ldlq_trellis_block_kernel"
+    if L < E.BIG_L:
+        kname = "ldlq_trellis_block_kernel"
+    else:  # the minima-exchange kernel up to 2^14 groups, the quarter-window one beyond (L = 16, k = 1)
+        kname = "ldlq_trellis_block_gx_kernel" if L - k <= 14 else "ldlq_trellis_block_big_kernel"
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "weights/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",

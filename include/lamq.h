@@ -64,8 +64,8 @@ int lamq_viterbi_rows(const float* x, int64_t B, int T, int64_t ldx, const float
  *   states   [m, n] int32 output for columns [b0, b1) (row stride lds)
  *   Z        [m, b1-b0] float64 output: the block's refit coefficients z = E U_BB^-1 (row stride ldZ),
  *            the left operand of the trailing update
- * width divides lazy = b1-b0 except in the last block; width + look <= 24; b1 - b0 <= 128.
- * Supported: 2 <= L <= 12 with 1 <= k <= min(4, L-1).
+ * width divides lazy = b1-b0 except in the last block; width <= 16, width + look <= 24; b1 - b0 <= 128
+ * (the reference runs 16, 8 and 128). Supported: 2 <= L <= 12 with 1 <= k <= min(4, L-1).
  * ---------------------------------------------------------------------------------------------- */
 int lamq_ldlq_trellis_block(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU,
                             const double* S, const double* table64, const float* table32, int L, int k,
@@ -89,7 +89,8 @@ int lamq_ldlq_scalar_block(double* T, int64_t m, int64_t n, int64_t ldT, const d
  * lamq_viterbi_rows and lamq_ldlq_trellis_block (the same references, the same arithmetic and tie rules)
  * for tables whose values are exactly representable in fp16, passed as their fp16 bit patterns
  * (table16, 4-byte aligned; table64 holds the same values in float64 for the settled values).
- * One 1024-thread workgroup per row. The fused block needs width + look <= 24 and b1 - b0 <= 256; the
+ * One 1024-thread workgroup per row. The fused block needs width <= 16, width + look <= 24 and
+ * b1 - b0 <= 128; the
  * standalone search keeps back-pointers of paths longer than 24 steps in the workspace:
  * lamq_viterbi16_workspace_size(B, T, L, k) bytes.
  * ---------------------------------------------------------------------------------------------- */
