@@ -106,7 +106,7 @@ int lamq_ldlq_trellis16_block(double* T, int64_t m, int64_t n, int64_t ldT, cons
 /* ------------------------------------------------------------------------------------------------
  * The lazy trailing update T[:, b1:n] -= Z @ U[b0:b1, b1:n] on fp64 MFMA.
  * Replaces opgraph/syntax.py:122-123 (and opgraph/ldlq_gpu.py:48).
- *   Z [m, b1-b0] (row stride ldZ), b1 - b0 <= 256.
+ *   Z [m, b1-b0] (row stride ldZ), b1 - b0 <= 1024.
  * ---------------------------------------------------------------------------------------------- */
 int lamq_trailing_update_f64(double* T, int64_t m, int64_t n, int64_t ldT, const double* Z, int64_t ldZ,
                              const double* U, int64_t ldU, int64_t b0, int64_t b1, void* stream);

@@ -89,7 +89,7 @@ extern "C" int lamq_trailing_update_f64(double* T, int64_t m, int64_t n, int64_t
 {
     if (!T || !Z || !U || m < 0 || n < 1 || ldT < n || ldU < n || b0 < 0 || b1 <= b0 || b1 > n || ldZ < b1 - b0)
         return LAMQ_EINVAL;
-    if (b1 - b0 > 256) return LAMQ_EUNSUP;
+    if (b1 - b0 > 1024) return LAMQ_EUNSUP;
     if (m == 0 || b1 == n) return LAMQ_OK;
     return gemm_sub_f64<false, false>(T + b1, ldT, Z, ldZ, U + b0 * ldU + b1, ldU, m, n - b1, b1 - b0, nullptr,
                                       as_stream(stream));

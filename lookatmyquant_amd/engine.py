@@ -181,18 +181,53 @@ def ldlq_trellis(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, table64: tor
         block = lib().lamq_ldlq_trellis_block
     state = torch.zeros(m, dtype=torch.int32, device=dev)
     states = torch.empty(m, n, dtype=torch.int32, device=dev)
-    Z = torch.empty(m, lazy, dtype=torch.float64, device=dev)
-    for b0 in range(0, n, lazy):
-        b1 = min(b0 + lazy, n)
-        ev = _event_pair(events, "block")
-        check(block(ptr(T), m, n, n, ptr(U), ld(U), ptr(S), ptr(table64), ptr(t32), L, k, b0, b1, width, look, ptr(state),
-                    ptr(states), n, ptr(Z), lazy, s), "ldlq_trellis_block")
-        _event_end(ev)
-        if b1 < n:
-            ev = _event_pair(events, "trailing")
-            check(lib().lamq_trailing_update_f64(ptr(T), m, n, n, ptr(Z), lazy, ptr(U), ld(U), b0, b1, s), "trailing_update")
+    outer = _outer_run(lazy)
+    Z = torch.empty(m, outer, dtype=torch.float64, device=dev)
+    for B0 in range(0, n, outer):
+        B1 = min(B0 + outer, n)
+        for b0 in range(B0, B1, lazy):
+            b1 = min(b0 + lazy, n)
+            ev = _event_pair(events, "block")
+            zb = Z[:, b0 - B0 :]
+            check(block(ptr(T), m, n, n, ptr(U), ld(U), ptr(S), ptr(table64), ptr(t32), L, k, b0, b1, width, look,
+                        ptr(state), ptr(states), n, ptr(zb), outer, s), "ldlq_trellis_block")
             _event_end(ev)
+            _refit_run(T, U, zb, b0, b1, B1, look, events)
+        _refit_rest(T, U, Z, B0, B1, look, events)
     return states
+
+
+def _outer_run(lazy: int) -> int:
+    """Columns whose trailing updates are gathered into one product: a multiple of lazy, 512 at lazy = 128."""
+    return lazy * max(1, 512 // lazy)
+
+
+def _refit_run(T, U, zb, b0, b1, B1, look, events):
+    """The trailing update of lazy block [b0, b1) restricted to the columns its outer run still reads: [b1, B1 + look)
+    (the run's later blocks and the look-ahead of its last one)."""
+    m, n = T.shape
+    e1 = min(B1 + look, n)
+    if b1 >= e1:
+        return
+    ev = _event_pair(events, "trailing")
+    # T[:, b1:e1] -= Z U[b0:b1, b1:e1]: the entry point on the first e1 columns
+    check(lib().lamq_trailing_update_f64(ptr(T), m, e1, ld(T), ptr(zb), ld(zb), ptr(U), ld(U), b0, b1, stream(T.device)),
+          "trailing_update")
+    _event_end(ev)
+
+
+def _refit_rest(T, U, Z, B0, B1, look, events):
+    """The columns past the outer run [B0, B1) and its look-ahead get the run's blocks at once:
+    T[:, c0:] -= Z[:, :B1-B0] U[B0:B1, c0:] with c0 = B1 + look (syntax.py:123 summed over the run's blocks)."""
+    m, n = T.shape
+    c0 = B1 + look
+    if c0 >= n:
+        return
+    sh = c0 - B1  # shift the column origin so that the entry point's b1 lands on c0
+    ev = _event_pair(events, "trailing")
+    check(lib().lamq_trailing_update_f64(T.data_ptr() + 8 * sh, m, n - sh, ld(T), ptr(Z), ld(Z), U.data_ptr() + 8 * sh,
+                                         ld(U), B0, B1, stream(T.device)), "trailing_update")
+    _event_end(ev)
 
 
 def _event_pair(events: dict | None, key: str):
@@ -233,13 +268,17 @@ def ldlq_scalar(T0: torch.Tensor, U: torch.Tensor, levels: torch.Tensor, mode: i
         dd = dead.to(device=dev, dtype=torch.uint8).contiguous()
         check(lib().lamq_zero_columns(ptr(T), m, n, n, ptr(dd), s), "zero_columns")
     idx = torch.empty(m, n, dtype=torch.int32, device=dev)
-    Z = torch.empty(m, lazy, dtype=torch.float64, device=dev)
-    for b0 in range(0, n, lazy):
-        b1 = min(b0 + lazy, n)
-        check(lib().lamq_ldlq_scalar_block(ptr(T), m, n, n, ptr(U), ld(U), ptr(S), ptr(levels), levels.numel(), mode, b0,
-                                           b1, ptr(idx), n, ptr(Z), lazy, s), "ldlq_scalar_block")
-        if b1 < n:
-            check(lib().lamq_trailing_update_f64(ptr(T), m, n, n, ptr(Z), lazy, ptr(U), ld(U), b0, b1, s), "trailing_update")
+    outer = _outer_run(lazy)
+    Z = torch.empty(m, outer, dtype=torch.float64, device=dev)
+    for B0 in range(0, n, outer):
+        B1 = min(B0 + outer, n)
+        for b0 in range(B0, B1, lazy):
+            b1 = min(b0 + lazy, n)
+            zb = Z[:, b0 - B0 :]
+            check(lib().lamq_ldlq_scalar_block(ptr(T), m, n, n, ptr(U), ld(U), ptr(S), ptr(levels), levels.numel(), mode,
+                                               b0, b1, ptr(idx), n, ptr(zb), outer, s), "ldlq_scalar_block")
+            _refit_run(T, U, zb, b0, b1, B1, 0, None)
+        _refit_rest(T, U, Z, B0, B1, 0, None)
     return idx
 
 
