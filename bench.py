@@ -6,10 +6,10 @@ trellis (fused Viterbi + in-block refit kernel per 128-column block, fp64 MFMA t
 the packed codes. W and H are resident in HBM when the timed region starts (the calibration capture that produces
 H is not part of a step).
 
-    python bench.py [--steps K] [--warmup W] [--L 16|12] [--k 2] [--no-cpu] [--workload c2|c3|c4] [--copy-probe MiB]
+    python bench.py [--steps K] [--warmup W] [--L 16|12] [--k 2] [--no-cpu] [--workload c2|c3|c4|c5] [--copy-probe MiB]
 
 The default is the benchmark configuration (config 2: 16-bit states, the fp16 quantile table); --L 12 runs the
-reference's own production trellis (the fitted 12-bit tables).
+reference's own production trellis (the fitted 12-bit tables), the default of the c3 and c5 workloads.
 
 Prints one JSON line: weights quantized per second (metric value), Viterbi rows/s, the roofline of the dominant
 kernel (the fused trellis block kernel) measured with HIP events on its stream, and the CPU oracle timed on a
@@ -21,6 +21,11 @@ roofline per kernel from HIP events):
                  down input [131072, 9728] with digit token weights, one factor per stage, the row-plan sweeps of
                  gate/up [9728, 2560] and down [2560, 9728] (bits 1-4, 2.3 bpw) and the packed codes per group
   --workload c4  config 4, one KL evaluation over paired bf16 logits [8192, 151936] per step
+  --workload c5  config 5, the end-to-end build of a random-initialised Qwen3.5-4B-shaped stack (36 layers x 7
+                 linears, hidden 2560, GQA 32/8 x 128, MLP 9728): calibration forwards of 32 x 2048 token ids through
+                 the reference and the quantized stream, per-stage Hessians and QEP cross terms (alpha 0.5), the
+                 row-plan trellis codes (bits 1-4, 2.3 bpw) and the packed codes; one step is the whole build
+                 (--layers N builds the first N layers)
 --copy-probe M ends the run with one device-to-device copy of M MiB, the known-size reference for the HBM byte
 counters of a profiler run.
 """
@@ -274,17 +279,58 @@ def run_c4(args):
         "kernels": {"kl_rows": kernel_line(per, nbytes, HBM_PEAK_GBS, "GB/s", "hbm", 1e9)}}))
 
 
+def run_c5(args):
+    """Config 5: the whole build of a random-initialised Qwen3.5-4B-shaped stack, one build per step."""
+    import torch
+
+    from lookatmyquant_amd import stack
+
+    torch.cuda.set_device(0)
+    sh = stack.Shape()
+    tokens, w = stack.calibration_tokens()
+    # warmup: one layer (kernel and GEMM selection, table uploads)
+    for _ in range(args.warmup):
+        stack.build(tokens, sh, w, L=args.L, layers=1)
+    torch.cuda.synchronize()
+    timer = stack.Timer()
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        out = stack.build(tokens, sh, w, L=args.L, layers=args.layers, timer=timer)
+    torch.cuda.synchronize()
+    secs = (time.perf_counter() - t1) / args.steps
+    bad = sum(int(p[1].item()) for ent in out["codes"].values() for (_, _, _, p) in ent)
+    assert bad == 0
+    weights = out["weights"]
+    print(json.dumps({
+        "metric": METRIC, "value": round(weights / secs, 1), "unit": "weights/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(secs * 1e3, 1), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16 (forwards, statistics) / f64 (factor, sweep) / f32 (search)",
+        "data": "synthetic (random-initialised stack, token ids uniform over the vocabulary, seed 501)",
+        "config": {"workload": f"config 5: end-to-end build of a Qwen3.5-4B-shaped stack, {args.layers} of 36 layers x 7 "
+                               "linears, 32 x 2048 calibration tokens through both streams, QEP alpha 0.5, row-plan "
+                               f"trellis L={args.L} bits 1-4 at 2.3 bpw, packed codes",
+                   "layers": args.layers, "weights": weights, "bits_per_weight": round(out["bits"] / weights, 4),
+                   "seconds_per_build": round(secs, 2), "target_seconds": 180,
+                   "stages_damped_more": out["redamped"],
+                   "seconds_by_phase": {k: round(v / args.steps, 2) for k, v in timer.t.items()}}}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--L", type=int, default=16)
+    ap.add_argument("--L", type=int, default=None,
+                    help="trellis state bits: default 16 for c2 (the benchmark table), 12 for c3 and c5 (the reference's "
+                         "production trellis)")
     ap.add_argument("--k", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", choices=("c2", "c3", "c4"), default="c2")
+    ap.add_argument("--workload", choices=("c2", "c3", "c4", "c5"), default="c2")
+    ap.add_argument("--layers", type=int, default=36)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MiB")
     args = ap.parse_args()
+    if args.L is None:
+        args.L = 16 if args.workload == "c2" else 12
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the per-matrix hot path runs on one MI355X here (rows would shard across "
               "GPUs with no communication; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
@@ -293,6 +339,8 @@ def main():
         run_c3(args)
     elif args.workload == "c4":
         run_c4(args)
+    elif args.workload == "c5":
+        run_c5(args)
     else:
         run_c2(args)
     if args.copy_probe:

@@ -172,6 +172,11 @@ def cross_target(H: torch.Tensor, D: torch.Tensor, alpha: float, lam: float = LA
     """M = I + alpha ((H + lam mean(diag H) I)^-1 D^T)^T (quantize.py:1330-1335), D = X_ref^T X_q / N - H. The
     damped H is symmetric positive definite, so the solve is the Cholesky solve of lamq_chol_inv_upper's factor:
     (H + d I)^-1 = U^T U. Returned on the CPU in float64."""
+    return cross_map(H, D, alpha, lam).cpu()
+
+
+def cross_map(H: torch.Tensor, D: torch.Tensor, alpha: float, lam: float = LAM) -> torch.Tensor:
+    """cross_target's M, float64 on the GPU."""
     dev = E._abi.device()
     Hg = torch.as_tensor(H).to(dev, torch.float64).contiguous()
     Dg = torch.as_tensor(D).to(dev, torch.float64).contiguous()
@@ -179,7 +184,7 @@ def cross_target(H: torch.Tensor, D: torch.Tensor, alpha: float, lam: float = LA
     _, U, _, _ = E.chol_inv_upper(Hg, damp=lam)
     # (H + d I)^-1 D^T = U^T (U D^T); then M = I + alpha (.)^T
     Y = U.T @ (U @ Dg.T)
-    return (torch.eye(n, dtype=torch.float64, device=dev) + alpha * Y.T).cpu()
+    return torch.eye(n, dtype=torch.float64, device=dev) + alpha * Y.T
 
 
 def stage_statistics(Xq_chunks, w_chunks=None, Xr_chunks=None):
@@ -208,13 +213,14 @@ def stage_statistics(Xq_chunks, w_chunks=None, Xr_chunks=None):
 
 def quantize_stage_row_groups(targets: dict, groups: dict, H: torch.Tensor, in_seed: int, L: int = 12,
                               width: int = 16, look: int = 8, tables: dict | None = None, events: dict | None = None,
-                              chol_events: tuple | None = None):
+                              chol_events: tuple | None = None, damp: float = 0.01):
     """Every matrix of a stage, row group by row group, with the row trellis at the group's width: the same result
     as quantize_row_groups(target, groups, round_group) with round_group = the tr<bits> word of (target[rows], H,
     in_seed, out_rot=False), for each matrix. targets: {name: W [m, n]}; groups: {name: [{"rows", "bits"}]};
     tables: {bits: float64 table} (default: the cached L = 12 tables). Returns {name: (states int32 [m, n] on the
     GPU, S float64 [m] on the GPU)}; the codes entries and reconstructions follow from them. events / chol_events
-    ((dict, key)): torch.cuda.Event pairs around the sweep kernels / the factorization, for timing."""
+    ((dict, key)): torch.cuda.Event pairs around the sweep kernels / the factorization, for timing. damp: the
+    Environment's damping fraction (frame.py:521)."""
     dev = E._abi.device()
     names = list(targets)
     Hr = E.rotate_hessian(torch.as_tensor(H).to(dev, torch.float64).contiguous(), in_seed)
@@ -222,7 +228,7 @@ def quantize_stage_row_groups(targets: dict, groups: dict, H: torch.Tensor, in_s
     if chol_events is not None:
         ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
         ev[0].record()
-    _, U, dead, info = E.chol_inv_upper(Hr, raise_on_fail=chol_events is None)
+    _, U, dead, info = E.chol_inv_upper(Hr, damp=damp, raise_on_fail=chol_events is None)
     if ev is not None:
         ev[1].record()
         chol_events[0].setdefault(chol_events[1], []).append(ev)

@@ -1,0 +1,65 @@
+"""The layer loop (lookatmyquant_amd.stack, the caller of quantize.py:1280-1314, 1416-1560, 1626-1690) on a small
+stack: the statistics it forms are the closed forms of the activations it captured, and every row group's codes are
+the oracle's row-trellis words of the stage's QEP target under those statistics, bit for bit."""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def test_small_stack_build():
+    from lookatmyquant_amd import stack
+    from lookatmyquant_amd.tables import load_table
+
+    assert torch.cuda.is_available()
+    sh = stack.Shape(hidden=512, heads=8, kv_heads=4, head_dim=128, inter=1024, layers=2, vocab=1000)
+    tok, w = stack.calibration_tokens(sequences=4, T=256, vocab=1000, seed=11)
+    say("stack build: 2 layers, hidden 512, 1024 calibration tokens")
+    out = stack.build(tok, sh, w, alpha=0.5, chunk=2, keep=2)
+    shapes = stack.matrix_shapes(sh)
+    assert out["weights"] == 2 * sum(m * n for m, n in shapes.values())
+    assert 1.0 < out["bits"] / out["weights"] < 4.1
+    for key, ent in out["codes"].items():
+        assert sum(len(g["rows"]) for g, _, _, _ in ent) == shapes[key.split(".", 1)[1]][0]
+        assert all(int(p[1].item()) == 0 for _, _, _, p in ent)  # every row a trellis path from state 0
+    tables = {b: np.array(load_table(12, b)) for b in (1, 2, 3, 4)}
+    wn = np.asarray(w, dtype=np.float64).reshape(-1)
+    for (i, s), (Xq, Xr, H, D, M, in_seed, plans) in out["stages"].items():
+        xq = Xq.float().numpy().astype(np.float64)
+        xr = Xr.float().numpy().astype(np.float64)
+        Hn = (xq * wn[:, None]).T @ xq / len(xq)
+        Dn = (xr * wn[:, None]).T @ xq / len(xq)
+        assert np.abs(H.numpy() - Hn).max() < 1e-4 * np.abs(Hn).max()
+        assert np.abs(D.numpy() - Dn).max() < 1e-4 * np.abs(Dn).max()
+        # the QEP map of quantize.py:1330-1335 from the statistics the build used (float32 sums, so the map is
+        # compared on those, not on the closed forms)
+        Hg, Dg = H.numpy(), D.numpy()
+        Mn = np.eye(len(Hg)) + 0.5 * np.linalg.solve(Hg + 0.1 * np.mean(np.diag(Hg)) * np.eye(len(Hg)), (Dg - Hg).T).T
+        assert np.abs(M.numpy() - Mn).max() < 1e-9 * np.abs(Mn).max()
+        if (i, s) == (0, 0):  # both streams enter the first layer equal: no cross term yet
+            assert np.abs(M.numpy() - np.eye(len(Mn))).max() < 1e-3
+        elif s == 1:  # the o_proj input already sees the quantized q/k/v
+            assert np.abs(M.numpy() - np.eye(len(Mn))).max() > 1e-3
+        Wl = stack.layer_weights(i, sh, torch.device("cuda"))
+        for nm, groups in plans.items():
+            target = Wl[nm].double().cpu().numpy() @ M.numpy()
+            states = torch.cat([st for g, st, _, _ in out["codes"][f"{i}.{nm}"]]).cpu().numpy()
+            rows_all = np.concatenate([np.asarray(g["rows"]) for g in groups])
+            by_row = dict(zip(rows_all.tolist(), range(len(rows_all))))
+            for g in groups[:2]:
+                rows = np.asarray(g["rows"])[:32]
+                ref, _, _ = O.ldlq_words_trellis(target[rows], H.numpy(), tables[g["bits"]], 12, g["bits"], in_seed)
+                got = states[[by_row[r] for r in rows.tolist()]]
+                say(f"layer {i} stage {s} {nm} group {g['group']} bits {g['bits']}")
+                assert np.array_equal(got, ref)
