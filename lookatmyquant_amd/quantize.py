@@ -187,6 +187,27 @@ def cross_map(H: torch.Tensor, D: torch.Tensor, alpha: float, lam: float = LAM) 
     return torch.eye(n, dtype=torch.float64, device=dev) + alpha * Y.T
 
 
+def qep_targets(H: torch.Tensor, D: torch.Tensor, alpha: float, Ws: dict, lam: float = LAM) -> dict:
+    """W* = W M for every matrix of a stage (quantize.py:1505), M = cross_target(H, D, alpha, lam), float64 on the
+    GPU. When the stage has fewer rows than inputs M is not formed: W M = W + alpha ((W D) (H + d I)^-1) =
+    W + alpha (U^T (U (W D)^T))^T, 6 m n^2 flops against 4 n^3 + 2 m n^2."""
+    dev = E._abi.device()
+    n = H.shape[0]
+    Wg = {nm: torch.as_tensor(W).to(dev, torch.float64) for nm, W in Ws.items()}
+    m = sum(W.shape[0] for W in Wg.values())
+    if m >= n:
+        M = cross_map(H, D, alpha, lam)
+        return {nm: W @ M for nm, W in Wg.items()}
+    Hg = torch.as_tensor(H).to(dev, torch.float64).contiguous()
+    Dg = torch.as_tensor(D).to(dev, torch.float64).contiguous()
+    _, U, _, _ = E.chol_inv_upper(Hg, damp=lam)
+    out = {}
+    for nm, W in Wg.items():
+        Y = U.T @ (U @ (W @ Dg).T)  # (H + d I)^-1 (W D)^T
+        out[nm] = W + alpha * Y.T
+    return out
+
+
 def stage_statistics(Xq_chunks, w_chunks=None, Xr_chunks=None):
     """H = (1/N) sum_t w_t x_t x_t^T and, for a cross-term stage, D = (1/N) sum_t w_t x_ref,t x_q,t^T, from bf16
     activation chunks [tokens, n] on the GPU (quantize.py:1416-1470). Returns float64 (H, D or None)."""

@@ -5,7 +5,7 @@ Per layer, two streams of calibration activations go through the layer: the refe
 full-precision weights and the quantized stream through the weights quantized so far. Each stage (q/k/v, o,
 gate/up, down: the matrices reading one input) takes its input from both streams, forms H = X_q^T W X_q / N with
 the token weights and the QEP cross term D = X_ref^T W X_q / N, moves the target to W* = W M with
-M = I + alpha ((H + lam mean(diag H) I)^-1 (D - H)^T)^T (quantize.py:1330-1335, 1505), quantizes every matrix of
+M = I + alpha ((H + lam mean(diag H) I)^-1 (D - H)^T)^T (quantize.py:1330-1335, 1505; qep_targets), quantizes every matrix of
 the stage by its row groups (quantize_stage_row_groups: one factor, one sweep per width), and writes the
 reconstruction back, so the next stage's input already sees it. Then both streams advance through the layer.
 
@@ -24,7 +24,7 @@ import torch
 
 from . import engine as E
 from . import synthetic
-from .quantize import cross_map, matrix_seeds, quantize_stage_row_groups
+from .quantize import matrix_seeds, qep_targets, quantize_stage_row_groups
 from .tables import load_table, quantile_table
 
 
@@ -137,8 +137,8 @@ def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | Non
     statistics, the QEP target, the row-group trellis codes (a 2.3 bpw row plan per matrix, bits 1-4) and the
     quantized weights written back. Returns {"codes": {"i.name": [(group, states, scales, packed)]}, "weights": n,
     "bits": total rate bits, "redamped": {"i.first matrix": damping} for stages that needed more than 0.01}. token_w: per-token weights [S, T] (mean 1), or None. keep: the first `keep` layers
-    also return their stages' inputs and statistics under "stages" (for tests: {(i, s): (X_q, X_ref, H, D, M,
-    in_seed, plans)}, on the CPU)."""
+    also return their stages' inputs and statistics under "stages" (for tests: {(i, s): (X_q, X_ref, H, D,
+    {name: W*}, in_seed, plans)}, on the CPU)."""
     dev = E._abi.device()
     S_, T = tokens.shape
     nl = sh.layers if layers is None else layers
@@ -194,12 +194,11 @@ def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | Non
             t2 = time.perf_counter()
             timer.add("forward", t2 - t1)
             H, D = _stage_statistics(xqf, wt, xr[s])
-            M = cross_map(H, D - H, alpha)
+            targets = qep_targets(H, D - H, alpha, {nm: wr[nm] for nm in names})
             torch.cuda.synchronize()
             t3 = time.perf_counter()
             timer.add("statistics", t3 - t2)
             _, in_seed = matrix_seeds(i, names[0], 0, names[0])
-            targets = {nm: wr[nm].double() @ M for nm in names}
             plans = {nm: synthetic.row_plan(shapes[nm][0], plan_seed + 10 * i + STAGE_INDEX[nm]) for nm in names}
             # a stage whose statistics the damping of the reference's Environment cannot make positive definite (float32
             # sums of a nearly singular H, as the o_proj input of a random-initialised stack with near-uniform
@@ -213,7 +212,8 @@ def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | Non
                         raise
                     redamped[f"{i}.{names[0]}"] = 10 * d
             if i < keep:
-                kept[(i, s)] = (torch.cat(xqf).cpu(), torch.cat(xr[s]).cpu(), H.cpu(), D.cpu(), M.cpu(), in_seed, plans)
+                kept[(i, s)] = (torch.cat(xqf).cpu(), torch.cat(xr[s]).cpu(), H.cpu(), D.cpu(),
+                                {nm: t.cpu() for nm, t in targets.items()}, in_seed, plans)
             for nm, (st, Srow) in res.items():
                 wq[nm] = _reconstruct(st, Srow, plans[nm], tables, in_seed).to(torch.bfloat16)
                 ent = []
@@ -226,7 +226,7 @@ def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | Non
                 n_w += shapes[nm][0] * shapes[nm][1]
             torch.cuda.synchronize()
             timer.add("quantize", time.perf_counter() - t3)
-            del xq, xqf, targets, M, H, D
+            del xq, xqf, targets, H, D
         # both streams through the layer (the quantized one with its last matrix now quantized)
         t4 = time.perf_counter()
         hq = [h1 + _lin(torch.nn.functional.silu(_lin(x, wq["mlp.gate_proj"])) * _lin(x, wq["mlp.up_proj"]),

@@ -35,7 +35,7 @@ def test_small_stack_build():
         assert all(int(p[1].item()) == 0 for _, _, _, p in ent)  # every row a trellis path from state 0
     tables = {b: np.array(load_table(12, b)) for b in (1, 2, 3, 4)}
     wn = np.asarray(w, dtype=np.float64).reshape(-1)
-    for (i, s), (Xq, Xr, H, D, M, in_seed, plans) in out["stages"].items():
+    for (i, s), (Xq, Xr, H, D, targets, in_seed, plans) in out["stages"].items():
         xq = Xq.float().numpy().astype(np.float64)
         xr = Xr.float().numpy().astype(np.float64)
         Hn = (xq * wn[:, None]).T @ xq / len(xq)
@@ -46,14 +46,15 @@ def test_small_stack_build():
         # compared on those, not on the closed forms)
         Hg, Dg = H.numpy(), D.numpy()
         Mn = np.eye(len(Hg)) + 0.5 * np.linalg.solve(Hg + 0.1 * np.mean(np.diag(Hg)) * np.eye(len(Hg)), (Dg - Hg).T).T
-        assert np.abs(M.numpy() - Mn).max() < 1e-9 * np.abs(Mn).max()
-        if (i, s) == (0, 0):  # both streams enter the first layer equal: no cross term yet
-            assert np.abs(M.numpy() - np.eye(len(Mn))).max() < 1e-3
-        elif s == 1:  # the o_proj input already sees the quantized q/k/v
-            assert np.abs(M.numpy() - np.eye(len(Mn))).max() > 1e-3
         Wl = stack.layer_weights(i, sh, torch.device("cuda"))
         for nm, groups in plans.items():
-            target = Wl[nm].double().cpu().numpy() @ M.numpy()
+            Wn = Wl[nm].double().cpu().numpy()
+            target = targets[nm].numpy()
+            assert np.abs(target - Wn @ Mn).max() < 1e-9 * np.abs(Wn).max()  # both forms of qep_targets
+            if (i, s) == (0, 0):  # both streams enter the first layer equal: no cross term yet
+                assert np.abs(target - Wn).max() < 1e-3 * np.abs(Wn).max()
+            elif s == 1:  # the o_proj input already sees the quantized q/k/v
+                assert np.abs(target - Wn).max() > 1e-3 * np.abs(Wn).max()
             states = torch.cat([st for g, st, _, _ in out["codes"][f"{i}.{nm}"]]).cpu().numpy()
             rows_all = np.concatenate([np.asarray(g["rows"]) for g in groups])
             by_row = dict(zip(rows_all.tolist(), range(len(rows_all))))
