@@ -99,29 +99,37 @@ __global__ __launch_bounds__(256) void gemm_sub_f64_kernel(double* C, int64_t ld
 }
 
 // The same C -= A op(B) (no OVERWRITE) for large products: workgroup tile 128x128, four waves of 64x64 = 4x4
-// MFMA tiles (64 accumulators per lane, AGPRs). Operands go straight from memory into LDS (global_load_lds,
-// 16 bytes = two doubles per lane, no registers), 32 deep in k, two stage buffers: one barrier per stage
+// MFMA tiles (64 accumulators per lane, VGPR-form). Operands go straight from memory into LDS (global_load_lds,
+// 16 bytes = two doubles per lane, no registers), BK deep in k, two stage buffers: one barrier per stage
 // publishes the stage and frees the other buffer for the next stage's loads, which are issued between the
-// MFMAs. LDS keeps the operands as they lie in memory, in 16-byte chunks XOR-swizzled so that the fragment
-// reads (one double per lane) are bank-conflict-free for the 32 lanes the LDS serves at once:
-//   [row][k] operands (A; B when TRANSB): 256-byte rows of 32 k, chunk c of row r at c ^ (r & 15): the 16 rows
-//     of a fragment read hit 16 different 16-byte bank windows;
+// MFMAs. With BK = 16 a workgroup holds 64 KB of LDS and at most 256 VGPRs per lane, so two workgroups share a
+// CU and each SIMD runs two waves that cover each other's stage barriers and epilogue (measured: 53-57 TF/s at
+// K = 512 against 45-47 for BK = 32 with one workgroup per CU). LDS keeps the operands as they lie in memory, in
+// 16-byte chunks XOR-swizzled so that the fragment reads (one double per lane) are bank-conflict-free:
+//   [row][k] operands (A; B when TRANSB): rows of BK doubles, chunk c of row r at c ^ (r & 15) for 16 chunks a
+//     row (BK = 32), c ^ ((r >> 1) & 7) for 8 (BK = 16: rows 2m and 2m + 1 sit 128 bytes apart in the banks):
+//     the 16 rows of a fragment read hit 16 different 16-byte bank windows;
 //   [k][col] operands (B): 1 KB rows of 128 columns, chunk c of row k at c ^ 8*(k & 1): the two k-rows read
 //     together sit 128 bytes apart in the banks.
 // Rows past M / N and k past K load zero chunks. Needs even leading dimensions, even K (and even N for a
 // [k][col] B) and 16-byte aligned operands (gemm_sub_f64 checks; other shapes take the kernel above).
 #define G8_BM 128
-#define G8_BK 32
-#define G8_ASZ (G8_BM * G8_BK * 8)   // bytes of one operand stage (32 KB)
+#define G8_BK 16
 
 __device__ double lamq_zero_chunk[2];
 
-template <bool TRANSB, bool LOWER>
-__global__ __launch_bounds__(256) void gemm128_f64_kernel(double* __restrict__ C, int64_t ldc, const double* __restrict__ A,
-                                                          int64_t lda, const double* __restrict__ B, int64_t ldb, int64_t M,
-                                                          int64_t N, int64_t K, const int32_t* __restrict__ info)
+template <bool TRANSB, bool LOWER, int BK>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BK == 16 ? 2 : 1, BK == 16 ? 2 : 1))) void
+gemm128_f64_kernel(double* __restrict__ C, int64_t ldc, const double* __restrict__ A, int64_t lda,
+                   const double* __restrict__ B, int64_t ldb, int64_t M, int64_t N, int64_t K,
+                   const int32_t* __restrict__ info)
 {
-    __shared__ __align__(16) uint8_t lds[2][2][G8_ASZ];  // [buffer][operand]
+    constexpr int ASZ = G8_BM * BK * 8;  // bytes of one operand stage
+    constexpr int RB = BK * 8;           // bytes of a [row][k] row
+    constexpr int CPR = RB / 16;         // 16-byte chunks per [row][k] row
+    constexpr int RPI = 64 / CPR;        // [row][k] rows per 1 KB load instruction
+    constexpr int IPW = BK / 4;          // load instructions per wave, operand and stage
+    __shared__ __align__(16) uint8_t lds[2][2][ASZ];  // [buffer][operand]
     if (info && *info != 0) return;
     const int64_t tr = (int64_t)blockIdx.y * G8_BM, tc = (int64_t)blockIdx.x * G8_BM;
     if (LOWER && tc > tr + G8_BM - 1) return;
@@ -131,13 +139,16 @@ __global__ __launch_bounds__(256) void gemm128_f64_kernel(double* __restrict__ C
     const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
     const double* zc = lamq_zero_chunk;
     asm volatile("" : "+s"(zc));
+    // chunk swizzle of [row][k] rows: the 16 rows of a fragment land in 16 different 16-byte windows of the 64 banks
+    auto rsw = [](int r) { return CPR == 16 ? (r & 15) : ((r >> 1) & 7); };
 
-    // loads: 32 instructions of 1 KB per operand and stage, 8 per wave (instruction q of wave w is number 8w + q)
-    //   [row][k]: instruction i covers rows 4i .. 4i+3, lane l row 4i + l/16, slot l%16, chunk (l%16) ^ (row & 15)
+    // loads: BK instructions of 1 KB per operand and stage, IPW per wave (instruction q of wave w is IPW*w + q)
+    //   [row][k]: instruction i covers rows RPI*i .. RPI*i + RPI-1, lane l row RPI*i + l/CPR, slot l%CPR,
+    //             chunk (l%CPR) ^ rsw(row)
     //   [k][col]: instruction i covers k-row i, lane l slot l, chunk l ^ 8*(i & 1)
     auto load_rowk = [&](const double* X, int64_t ldx, int64_t r0, int64_t R, int64_t k0, int i, uint32_t m) {
-        const int r = 4 * i + (lane >> 4);
-        const int c = (lane & 15) ^ (r & 15);
+        const int r = RPI * i + lane / CPR;
+        const int c = (lane % CPR) ^ rsw(r);
         const int64_t row = r0 + r, k = k0 + 2 * c;
         const bool ok = row < R && k < K;
         const double* g = ok ? X + row * ldx + k : zc;
@@ -151,8 +162,8 @@ __global__ __launch_bounds__(256) void gemm128_f64_kernel(double* __restrict__ C
         load_lds16(g, m);
     };
     auto piece = [&](int64_t k0, int buf, int q, int op) {
-        const int i = 8 * wv + q;
-        const uint32_t m = lds_base + (uint32_t)((buf * 2 + op) * G8_ASZ + i * 1024);
+        const int i = IPW * wv + q;
+        const uint32_t m = lds_base + (uint32_t)((buf * 2 + op) * ASZ + i * 1024);
         if (op == 0)
             load_rowk(A, lda, tr, M, k0, i, m);
         else if (TRANSB)
@@ -168,14 +179,14 @@ __global__ __launch_bounds__(256) void gemm128_f64_kernel(double* __restrict__ C
         for (int j = 0; j < 4; ++j) acc[i][j] = lamq_d4{0.0, 0.0, 0.0, 0.0};
     const int li = lane & 15, lk = lane >> 4;
     // fragment addresses (bytes within an operand stage) for k = k4 + lk
-    auto aaddr = [&](int row, int k) -> uint32_t { return (uint32_t)(row * 256 + (((k >> 1) ^ (row & 15)) << 4) + (k & 1) * 8); };
+    auto aaddr = [&](int row, int k) -> uint32_t { return (uint32_t)(row * RB + (((k >> 1) ^ rsw(row)) << 4) + (k & 1) * 8); };
     auto baddr = [&](int col, int k) -> uint32_t {
         return TRANSB ? aaddr(col, k) : (uint32_t)(k * 1024 + (((col >> 1) ^ (8 * (k & 1))) << 4) + (col & 1) * 8);
     };
 
-    const int nst = (int)cdiv(K, G8_BK);
+    const int nst = (int)cdiv(K, BK);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < IPW; ++q) {
         piece(0, 0, q, 0);
         piece(0, 0, q, 1);
     }
@@ -186,7 +197,7 @@ __global__ __launch_bounds__(256) void gemm128_f64_kernel(double* __restrict__ C
         const uint8_t* As = lds[buf][0];
         const uint8_t* Bs = lds[buf][1];
 #pragma unroll
-        for (int k4 = 0; k4 < G8_BK; k4 += 4) {
+        for (int k4 = 0; k4 < BK; k4 += 4) {
             double a[4], b[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
@@ -197,39 +208,47 @@ __global__ __launch_bounds__(256) void gemm128_f64_kernel(double* __restrict__ C
             for (int i = 0; i < 4; ++i) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i], b[j], acc[i][j], 0, 0, 0);
-                // the next stage's 16 loads, one per four MFMAs over the stage's first four k-steps (after the
+                // the next stage's 2*IPW loads, one per four MFMAs over the stage's first k-steps (after the
                 // last stage they load zero chunks into the buffer no one reads: no branch in the loop)
-                if (k4 < 16) {
+                {
                     const int p = (k4 / 4) * 4 + i;
-                    piece((int64_t)(st + 1) * G8_BK, buf ^ 1, p >> 1, p & 1);
+                    if (p < 2 * IPW) piece((int64_t)(st + 1) * BK, buf ^ 1, p >> 1, p & 1);
                 }
             }
         }
     }
     wait_vm<0>();
-    // D layout (16x16): lane l, register v -> row 4*v + l/16, column l%16. All of C's values are read before any is
-    // written: interleaved, every read would wait for the write before it (the compiler cannot tell them apart).
-    double cv[4][4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
+    // D layout (16x16): lane l, register v -> row 4*v + l/16, column l%16. C is read two row-groups of 16 ahead of
+    // its writes: one wait counter covers loads and stores alike, so a read issued after a write would wait for it.
+    auto cload = [&](int i, double(&g)[4][4]) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int64_t row = tr + wr + 16 * i + 4 * v + lk;
                 const int64_t col = tc + wc + 16 * j + li;
-                cv[i][j][v] = (row < M && col < N && (!LOWER || col <= row)) ? C[row * ldc + col] : 0.0;
+                g[j][v] = (row < M && col < N && (!LOWER || col <= row)) ? C[row * ldc + col] : 0.0;
             }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
+    };
+    auto cstore = [&](int i, const double(&g)[4][4]) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int64_t row = tr + wr + 16 * i + 4 * v + lk;
                 const int64_t col = tc + wc + 16 * j + li;
-                if (row < M && col < N && (!LOWER || col <= row)) C[row * ldc + col] = cv[i][j][v] - acc[i][j][v];
+                if (row < M && col < N && (!LOWER || col <= row)) C[row * ldc + col] = g[j][v] - acc[i][j][v];
             }
+    };
+    double g0[4][4], g1[4][4];
+    cload(0, g0);
+    cload(1, g1);
+    cstore(0, g0);
+    cload(2, g0);
+    cstore(1, g1);
+    cload(3, g1);
+    cstore(2, g0);
+    cstore(3, g1);
 }
 
 template <bool TRANSB, bool LOWER, bool OVERWRITE = false>
@@ -244,7 +263,8 @@ static int gemm_sub_f64(double* C, int64_t ldc, const double* A, int64_t lda, co
                         ((uintptr_t)A % 16) == 0 && ((uintptr_t)B % 16) == 0;
     if (!OVERWRITE && chunks && cdiv(M, G8_BM) * cdiv(N, G8_BM) >= 128) {
         dim3 grid((unsigned)cdiv(N, G8_BM), (unsigned)cdiv(M, G8_BM));
-        hipLaunchKernelGGL((gemm128_f64_kernel<TRANSB, LOWER>), grid, dim3(256), 0, s, C, ldc, A, lda, B, ldb, M, N, K, info);
+        hipLaunchKernelGGL((gemm128_f64_kernel<TRANSB, LOWER, G8_BK>), grid, dim3(256), 0, s, C, ldc, A, lda, B, ldb, M, N,
+                           K, info);
         LAMQ_LAUNCH_CHECK();
         return LAMQ_OK;
     }
