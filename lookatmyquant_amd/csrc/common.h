@@ -19,6 +19,19 @@ static inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream
 
 __host__ __device__ static inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// MI355X dispatches the workgroups of a grid to its 8 XCDs round-robin (workgroup b to XCD b % 8), and each XCD
+// has its own L2. xcd_remap(b, G) renumbers the grid so that XCD x runs one contiguous range of logical
+// workgroups, in order: workgroups resident on one XCD at one time are neighbours in the logical order and
+// share the data they read through that XCD's L2. A bijection on [0, G): XCD x receives G / 8 workgroups, one
+// more for the first G % 8 XCDs.
+#define LAMQ_XCDS 8
+__device__ __forceinline__ int64_t xcd_remap(int64_t b, int64_t G)
+{
+    const int64_t x = b % LAMQ_XCDS, r = b / LAMQ_XCDS;
+    const int64_t q = G / LAMQ_XCDS, extra = G % LAMQ_XCDS;
+    return x < extra ? x * (q + 1) + r : extra * (q + 1) + (x - extra) * q + r;
+}
+
 // LDS float index -> bank-spread index: the 16-byte chunk index (x >> 2) has its low two bits xor'ed with bits
 // 4-5 of itself, a bijection within every 64 floats. Writes of consecutive threads at a stride of 16 floats then
 // fall on 16 different 16-byte bank groups, and reads of consecutive 16-byte chunks stay conflict-free.

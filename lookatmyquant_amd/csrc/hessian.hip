@@ -191,8 +191,9 @@ __device__ __forceinline__ uint32_t gsw(int token, int chunk)
 }
 
 // Tile order: logical tiles run through panels of GP tile columns, row by row, so the workgroups resident
-// at one time work on a compact block of tiles and share feature blocks of the activations (a third fewer
-// bytes fetched past L2 than row-major order). Workgroup b takes split b / tiles, tile b % tiles.
+// at one time work on a compact block of tiles and share feature blocks of the activations. Logical
+// workgroup b (xcd_remap of the grid index: the 32 workgroups one XCD holds at a time are neighbours) takes
+// split b / tiles, tile b % tiles.
 #define GP 8
 __device__ __forceinline__ void gram_tile(int64_t t, int64_t nt, bool sym, int64_t& I, int64_t& J)
 {
@@ -231,9 +232,10 @@ __global__ __launch_bounds__(256) void gram256_kernel(const uint16_t* __restrict
                                                       int partial, int64_t tokens_per_split, int64_t tiles)
 {
     __shared__ __align__(16) uint8_t lds[GNS * GSTAGE];
-    const int64_t split = blockIdx.x / tiles;
+    const int64_t b = xcd_remap(blockIdx.x, gridDim.x);
+    const int64_t split = b / tiles;
     int64_t I, J;
-    gram_tile(blockIdx.x - split * tiles, cdiv(n, GT), SYM, I, J);
+    gram_tile(b - split * tiles, cdiv(n, GT), SYM, I, J);
     const int64_t kb = split * tokens_per_split;
     const int64_t ke = kb + tokens_per_split < N ? kb + tokens_per_split : N;
     const int64_t span = ke - kb;
