@@ -4,6 +4,7 @@ are what the reference-compatible modules (codes, frame, nested, quantize, compi
 
 from __future__ import annotations
 
+import ctypes
 from functools import lru_cache
 
 import torch
@@ -160,11 +161,22 @@ def ldlq_trellis(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, table64: tor
     """States [m, n] int32 of the row-trellis block LDLQ of X (rotated rows, not divided by S) under U.
     events: optional dict; each launch of the block kernel and of the trailing update is bracketed by a pair of
     torch.cuda.Event on this stream, appended to events["block"] and events["trailing"]."""
+    return ldlq_trellis_groups(X, S, U, [(X.shape[0], k, table64, table32)], L, width, look, lazy, dead, events)
+
+
+def ldlq_trellis_groups(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, groups: list, L: int, width: int = 16,
+                        look: int = 8, lazy: int = 128, dead: torch.Tensor | None = None,
+                        events: dict | None = None) -> torch.Tensor:
+    """ldlq_trellis over consecutive row groups that share U but not the code: groups = [(rows, k, table64,
+    table32 or None)] in row order, summing to X's rows. Each lazy block runs the block kernel group by group and
+    then one trailing update over all rows (the update is row by row, so this is the same as sweeping each group
+    on its own, with fewer and larger products)."""
     need(X, torch.float64, "X", 2)
     need(U, torch.float64, "U", 2)
     need(S, torch.float64, "S", 1)
-    need(table64, torch.float64, "table64", 1)
     m, n = X.shape
+    if sum(int(g[0]) for g in groups) != m:
+        raise ValueError("the row groups must cover X's rows")
     if lazy % width:
         raise ValueError("lazy must be a multiple of width and of block")
     T = X.clone(memory_format=torch.contiguous_format)
@@ -173,25 +185,35 @@ def ldlq_trellis(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, table64: tor
     if dead is not None:
         dd = dead.to(device=dev, dtype=torch.uint8).contiguous()
         check(lib().lamq_zero_columns(ptr(T), m, n, n, ptr(dd), s), "zero_columns")
-    if L >= BIG_L:
-        t32 = half_bits(table64) if table32 is None or table32.dtype != torch.int16 else table32
-        block = lib().lamq_ldlq_trellis16_block
-    else:
-        t32 = table64.to(torch.float32) if table32 is None else table32
-        block = lib().lamq_ldlq_trellis_block
+    block = lib().lamq_ldlq_trellis16_block if L >= BIG_L else lib().lamq_ldlq_trellis_block
+    parts = []
+    r0 = 0
+    for rows, k, table64, table32 in groups:
+        need(table64, torch.float64, "table64", 1)
+        if L >= BIG_L:
+            t32 = half_bits(table64) if table32 is None or table32.dtype != torch.int16 else table32
+        else:
+            t32 = table64.to(torch.float32) if table32 is None else table32
+        if rows:
+            parts.append((r0, int(rows), int(k), table64, t32))
+        r0 += int(rows)
     state = torch.zeros(m, dtype=torch.int32, device=dev)
     states = torch.empty(m, n, dtype=torch.int32, device=dev)
     outer = _outer_run(lazy)
     Z = torch.empty(m, outer, dtype=torch.float64, device=dev)
+    vp = ctypes.c_void_p
     for B0 in range(0, n, outer):
         B1 = min(B0 + outer, n)
         for b0 in range(B0, B1, lazy):
             b1 = min(b0 + lazy, n)
-            ev = _event_pair(events, "block")
             zb = Z[:, b0 - B0 :]
-            check(block(ptr(T), m, n, n, ptr(U), ld(U), ptr(S), ptr(table64), ptr(t32), L, k, b0, b1, width, look,
-                        ptr(state), ptr(states), n, ptr(zb), outer, s), "ldlq_trellis_block")
-            _event_end(ev)
+            for r0, rows, k, table64, t32 in parts:
+                ev = _event_pair(events, "block")
+                check(block(vp(T.data_ptr() + 8 * r0 * n), rows, n, n, ptr(U), ld(U), vp(S.data_ptr() + 8 * r0),
+                            ptr(table64), ptr(t32), L, k, b0, b1, width, look, vp(state.data_ptr() + 4 * r0),
+                            vp(states.data_ptr() + 4 * r0 * n), n, vp(zb.data_ptr() + 8 * r0 * outer), outer, s),
+                      "ldlq_trellis_block")
+                _event_end(ev)
             _refit_run(T, U, zb, b0, b1, B1, look, events)
         _refit_rest(T, U, Z, B0, B1, look, events)
     return states

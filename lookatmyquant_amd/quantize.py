@@ -264,16 +264,23 @@ def quantize_stage_row_groups(targets: dict, groups: dict, H: torch.Tensor, in_s
     for nm in names:
         for g in groups[nm]:
             by_bits.setdefault(int(g["bits"]), []).append((nm, torch.as_tensor(g["rows"], dtype=torch.long)))
+    # all of the stage's rows go through one sweep: the block kernel runs width by width on consecutive row
+    # groups, and each trailing update covers every row at once
     out = {nm: torch.empty(X_all[nm].shape, dtype=torch.int32, device=dev) for nm in names}
+    idx, sweep_groups = [], []
     for bits, parts in sorted(by_bits.items()):
         table = (tables or {}).get(bits)
         table = torch.from_numpy(C.load_table(12, bits).copy()) if table is None else torch.as_tensor(table, dtype=torch.float64)
-        idx = [(nm, rows.to(dev)) for nm, rows in parts]
-        X = torch.cat([X_all[nm].index_select(0, r) for nm, r in idx])
-        S = torch.cat([S_all[nm].index_select(0, r) for nm, r in idx])
-        st = E.ldlq_trellis(X, S, U, table.to(dev), L, bits, width, look, 128, dead=dead, events=events)
-        r0 = 0
-        for nm, r in idx:
-            out[nm].index_copy_(0, r, st[r0 : r0 + len(r)])
-            r0 += len(r)
+        rows = 0
+        for nm, r in parts:
+            idx.append((nm, r.to(dev)))
+            rows += len(r)
+        sweep_groups.append((rows, bits, table.to(dev), None))
+    X = torch.cat([X_all[nm].index_select(0, r) for nm, r in idx])
+    S = torch.cat([S_all[nm].index_select(0, r) for nm, r in idx])
+    st = E.ldlq_trellis_groups(X, S, U, sweep_groups, L, width, look, 128, dead=dead, events=events)
+    r0 = 0
+    for nm, r in idx:
+        out[nm].index_copy_(0, r, st[r0 : r0 + len(r)])
+        r0 += len(r)
     return {nm: (out[nm], S_all[nm]) for nm in names}
