@@ -4,7 +4,7 @@
 // Hd^-1 = V^-T V^-1 and U = V^-1 = J L^-1 J is upper with a positive diagonal: the factor
 // torch.linalg.cholesky(torch.cholesky_inverse(torch.linalg.cholesky(Hd)), upper=True) returns.
 // One Cholesky (n^3/3 flops) and one triangular inverse (n^3/3) replace the reference's three
-// factorizations (4n^3/3). Both are blocked right-looking with 64-wide panels. One wave factors each
+// factorizations (4n^3/3). Both are blocked right-looking with 64-wide panels. One workgroup factors each
 // diagonal block in LDS and inverts it (Lkk^-1 kept in the workspace); the panel below, the block rows
 // of the inverse and all trailing updates are then fp64 MFMA products: panel = A_panel Lkk^-T,
 // X_k = Lkk^-1 B_k.
@@ -57,69 +57,153 @@ __global__ void prep_kernel(const double* __restrict__ H, int64_t n, int64_t ldH
 }
 
 // The nb x nb diagonal block at (k0, k0) of A (lower): its Cholesky factor Lkk, written back into A, and
-// Lkk^-1 (lower), written to Linv (ld NBK). One wave, everything in registers and fully unrolled (register
-// arrays need compile-time indices); a block shorter than NBK is padded with the identity.
-// Factorization: lane i holds row i, r[j] = a[i][j]. Column c: d = a[c][c]; l[i][c] = a[i][c] / sqrt(d)
-// (l[c][c] = sqrt(d)); a[i][j] -= l[i][c] l[j][c] for j > c. Column c of L is published through LDS
-// (lt[c][i] = l[i][c]) and read back as broadcasts.
-// Inverse: lane c holds column c of X = L^-1, x = e_c initially; for l = 0..: x[l] /= l[l][l];
-// x[i] -= l[i][l] x[l] for i > l (the l[i][l] broadcast from lt).
-__global__ __launch_bounds__(64) void diag_block_kernel(double* __restrict__ A, int64_t n, int64_t k0, int nb,
+// Lkk^-1 (lower, ld NBK) into Linv. One workgroup of four waves with the block in LDS, in four steps of 16
+// columns p:
+//   (1) wave 0 factors the 16 x 16 diagonal block D_p in registers (lane i holds row i; column values move
+//       between lanes by readlane): column c, d = a[c][c], l[c][c] = sqrt(d), l[i][c] = a[i][c] * (1/l[c][c])
+//       as LAPACK's unblocked potf2 scales, a[i][j] -= l[i][c] l[j][c]; then inverts the factor (lane c holds
+//       column c of D_p^-1, forward substitution with the same reciprocals);
+//   (2) the tiles below it become L_Ip = A_Ip D_p^-T (one MFMA tile per wave);
+//   (3) the lower trailing tiles take A_IJ -= L_Ip L_Jp^T (MFMA).
+// Then Lkk^-1 by block rows: Linv_pp = D_p^-1, Linv_pq = -D_p^-1 sum_{q<=r<p} L_pr Linv_rq, one level per p.
+// A block shorter than NBK is padded with the identity. The loops over p run at run time, so the code stays a few
+// KB (a fully unrolled 64-step kernel spends most of its time fetching instructions).
+#define DB_LD 65  // LDS row stride of the block, in doubles
+
+__global__ __launch_bounds__(256) void diag_block_kernel(double* __restrict__ A, int64_t n, int64_t k0, int nb,
                                                         double* __restrict__ Linv, int32_t* __restrict__ info)
 {
-    __shared__ __align__(16) double lt[NBK][NBK];  // lt[c][i] = L[i][c]
+    __shared__ double blk[NBK * DB_LD];  // the block, then L
+    __shared__ double inv[NBK * DB_LD];  // Lkk^-1
+    __shared__ double dinv[4][16 * 17];  // D_p^-1, [row * 17 + col]
+    __shared__ int sfail;
     if (*info != 0) return;
-    const int lane = threadIdx.x;
-    const bool live = lane < nb;
-    double r[NBK];
-    // branch-free loads: rows and columns clamped into the block, padding selected afterwards
-    const double* Ar = A + (k0 + (live ? lane : 0)) * n + k0;
-#pragma unroll
-    for (int j = 0; j < NBK; ++j) {
-        const double v = Ar[j < nb ? j : nb - 1];
-        r[j] = (live && j < nb) ? (j <= lane ? v : 0.0) : (j == lane ? 1.0 : 0.0);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int li = lane & 15, lk = lane >> 4;
+    for (int e = tid; e < NBK * NBK; e += 256) {
+        const int i = e >> 6, j = e & 63;
+        double v;
+        if (i < nb && j < nb)
+            v = j <= i ? A[(k0 + i) * n + k0 + j] : 0.0;
+        else
+            v = i == j ? 1.0 : 0.0;
+        blk[i * DB_LD + j] = v;
+        inv[i * DB_LD + j] = 0.0;
     }
-    int fail = 0;  // the first non-positive pivot; the loop runs on without branching, its output unused
+    if (tid == 0) sfail = 0;
+    __syncthreads();
+    auto B = [&](int i, int j) -> double& { return blk[i * DB_LD + j]; };
+    for (int p = 0; p < 4; ++p) {
+        const int c0 = 16 * p;
+        if (wave == 0) {  // (1); lanes 16..63 repeat lanes 0..15
+            double r[16];
 #pragma unroll
-    for (int c = 0; c < NBK; ++c) {
-        lt[c][lane] = r[c];
-        const double d = lt[c][c];
-        fail = (fail == 0 && !(d > 0.0)) ? (int)(k0 + c + 1) : fail;
-        const double sd = sqrt(d);
-        const double lic = lane > c ? r[c] / sd : (lane == c ? sd : 0.0);
-        r[c] = lic;
-        lt[c][lane] = lic;
+            for (int j = 0; j < 16; ++j) r[j] = j <= li ? B(c0 + li, c0 + j) : 0.0;
+            double rc[16];  // 1 / l[c][c], the same in every lane
+            int fail = 0;   // the first non-positive pivot (the same in every lane)
 #pragma unroll
-        for (int j = c + 1; j < NBK; ++j) r[j] = fma(-lic, lt[c][j], r[j]);
-        // the empty asm pins this step's updates here: without it the compiler sinks them into per-column dot
-        // products (a left-looking order) that keep every broadcast value live. One group per step, after all of
-        // the step's loads, so the loads still issue back to back.
+            for (int c = 0; c < 16; ++c) {
+                const double d = readlane_f64(r[c], c);
+                fail = (fail == 0 && !(d > 0.0)) ? (int)(k0 + c0 + c + 1) : fail;
+                const double sd = sqrt(d);
+                const double rs = 1.0 / sd;
+                rc[c] = rs;
+                const double lic = li > c ? r[c] * rs : (li == c ? sd : 0.0);
+                r[c] = lic;
 #pragma unroll
-        for (int j = c + 1; j < NBK; ++j) asm volatile("" : "+v"(r[j]));
+                for (int j = c + 1; j < 16; ++j) r[j] = fma(-lic, readlane_f64(lic, j), r[j]);
+            }
+            if (lane < 16) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) B(c0 + li, c0 + j) = j <= li ? r[j] : 0.0;
+            }
+            // the inverse reads the factor back from LDS (the same value in every lane)
+            double x[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) x[i] = i == li ? 1.0 : 0.0;
+#pragma unroll
+            for (int l = 0; l < 16; ++l) {
+                x[l] = x[l] * rc[l];
+#pragma unroll
+                for (int i = l + 1; i < 16; ++i) x[i] = fma(-B(c0 + i, c0 + l), x[l], x[i]);
+            }
+            if (lane < 16) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    dinv[p][i * 17 + li] = x[i];
+                    inv[(c0 + i) * DB_LD + c0 + li] = x[i];
+                }
+            }
+            if (lane == 0 && fail != 0) sfail = fail;
+        }
+        __syncthreads();
+        if (sfail != 0) {  // uniform: every thread leaves
+            if (tid == 0) *info = sfail;
+            return;
+        }
+        // (2) wave w: tile I = p + 1 + w. MFMA 16x16x4 operands: lane l gives A[l % 16][k4 + l / 16] and
+        // B[k4 + l / 16][l % 16]; result register v of lane l is row 4v + l / 16, column l % 16.
+        {
+            const int I = p + 1 + wave;
+            if (I < 4) {
+                lamq_d4 acc = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk)
+                    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(B(16 * I + li, c0 + 4 * kk + lk),
+                                                               dinv[p][li * 17 + 4 * kk + lk], acc, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) B(16 * I + 4 * v + lk, c0 + li) = acc[v];
+            }
+        }
+        __syncthreads();
+        // (3) tiles (I, J), p < J <= I < 4, round-robin over the waves
+        {
+            const int m = 3 - p;
+            const int T = m * (m + 1) / 2;
+            for (int t = wave; t < T; t += 4) {
+                int ii = 0, jj = t;
+                while (jj > ii) {
+                    jj -= ii + 1;
+                    ++ii;
+                }
+                const int I = p + 1 + ii, J = p + 1 + jj;
+                lamq_d4 acc = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk)
+                    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(B(16 * I + li, c0 + 4 * kk + lk),
+                                                               B(16 * J + li, c0 + 4 * kk + lk), acc, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) B(16 * I + 4 * v + lk, 16 * J + li) -= acc[v];
+            }
+        }
+        __syncthreads();
     }
-    if (fail != 0) {  // uniform
-        if (lane == 0) *info = fail;
-        return;
+    // Lkk^-1 below the diagonal blocks: level p, wave q < p
+    for (int p = 1; p < 4; ++p) {
+        const int q = wave;
+        if (q < p) {
+            lamq_d4 t = {0.0, 0.0, 0.0, 0.0};
+            for (int r = q; r < p; ++r) {
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk)
+                    t = __builtin_amdgcn_mfma_f64_16x16x4f64(B(16 * p + li, 16 * r + 4 * kk + lk),
+                                                             inv[(16 * r + 4 * kk + lk) * DB_LD + 16 * q + li], t, 0, 0, 0);
+            }
+            // the result layout of t is the B-operand layout of its k-steps: register kk holds rows 4kk + l / 16
+            lamq_d4 o = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+                o = __builtin_amdgcn_mfma_f64_16x16x4f64(dinv[p][li * 17 + 4 * kk + lk], t[kk], o, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) inv[(16 * p + 4 * v + lk) * DB_LD + 16 * q + li] = -o[v];
+        }
+        __syncthreads();
     }
-    if (live) {
-        double* Aw = A + (k0 + lane) * n + k0;
-#pragma unroll
-        for (int j = 0; j < NBK; ++j)
-            if (j < nb && j <= lane) Aw[j] = r[j];
+    for (int e = tid; e < NBK * NBK; e += 256) {
+        const int i = e >> 6, j = e & 63;
+        if (i < nb && j <= i) A[(k0 + i) * n + k0 + j] = blk[i * DB_LD + j];
+        Linv[i * NBK + j] = j <= i ? inv[i * DB_LD + j] : 0.0;
     }
-    double x[NBK];
-#pragma unroll
-    for (int i = 0; i < NBK; ++i) x[i] = i == lane ? 1.0 : 0.0;
-#pragma unroll
-    for (int l = 0; l < NBK; ++l) {
-        x[l] = x[l] / lt[l][l];
-#pragma unroll
-        for (int i = l + 1; i < NBK; ++i) x[i] = fma(-lt[l][i], x[l], x[i]);
-#pragma unroll
-        for (int i = l + 1; i < NBK; ++i) asm volatile("" : "+v"(x[i]));
-    }
-#pragma unroll
-    for (int i = 0; i < NBK; ++i) Linv[i * NBK + lane] = x[i];
 }
 
 __global__ void identity_kernel(double* __restrict__ X, int64_t n, int64_t ldX)
@@ -190,7 +274,7 @@ extern "C" int lamq_chol_inv_upper_ex(const double* H, int64_t n, int64_t ldH, d
         for (int64_t k0 = K0; k0 < pe; k0 += NBK) {
             const int nb = (int)(n - k0 < NBK ? n - k0 : NBK);
             double* Lk = Linv + (k0 / NBK) * NBK * NBK;
-            hipLaunchKernelGGL(diag_block_kernel, dim3(1), dim3(64), 0, s, A, n, k0, nb, Lk, info);
+            hipLaunchKernelGGL(diag_block_kernel, dim3(1), dim3(256), 0, s, A, n, k0, nb, Lk, info);
             LAMQ_LAUNCH_CHECK();
             const int64_t rest = n - k0 - nb;
             if (rest > 0) {

@@ -24,6 +24,15 @@ __host__ __device__ static inline int64_t cdiv(int64_t a, int64_t b) { return (a
 // workgroups, in order: workgroups resident on one XCD at one time are neighbours in the logical order and
 // share the data they read through that XCD's L2. A bijection on [0, G): XCD x receives G / 8 workgroups, one
 // more for the first G % 8 XCDs.
+// v of lane `lane` (a wave-uniform index) in every lane
+__device__ __forceinline__ double readlane_f64(double v, int lane)
+{
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)b, lane);
+    const int hi = __builtin_amdgcn_readlane((int)(b >> 32), lane);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
 #define LAMQ_XCDS 8
 __device__ __forceinline__ int64_t xcd_remap(int64_t b, int64_t G)
 {

@@ -127,7 +127,7 @@ def test_trailing_update_matches_oracle_order(E, m, n, b0, b1):
     assert err < 1e-14
 
 
-@pytest.mark.parametrize("n", [64, 100, 200, 960, 2500])
+@pytest.mark.parametrize("n", [16, 64, 100, 200, 960, 2500])
 def test_chol_inv_upper(E, n):
     rng = np.random.default_rng(n)
     X = rng.standard_normal((2 * n + 50, n))
@@ -149,6 +149,18 @@ def test_chol_inv_upper(E, n):
     assert err < 1e-10
     # U^T U = Hd^-1
     assert np.abs(Ug.T @ Ug @ Hd_o - np.eye(n)).max() < 1e-9
+
+
+@pytest.mark.parametrize("n,k", [(300, 3), (300, 37), (300, 250)])
+def test_chol_inv_upper_reports_a_pivot_inside_a_block(E, n, k):
+    """A negative diagonal entry at H[k][k] of an otherwise diagonal H is pivot n - k of the reversed
+    factorization: inside a diagonal block, at a 16-column step boundary or not, and in a padded last block."""
+    H = np.diag(np.linspace(1.0, 2.0, n))
+    H[k, k] = -1.0
+    say(f"chol_inv_upper pivot n={n} k={k}")
+    _, U, _, info = E.chol_inv_upper(cuda(H), damp=0.0, raise_on_fail=False)
+    assert int(info.item()) == n - k
+    assert float(U.abs().max()) == 0.0
 
 
 @pytest.mark.parametrize("n", [40, 130])
