@@ -10,8 +10,13 @@
 // X_k = Lkk^-1 B_k.
 #include "gemm_f64.h"
 
+#include <mutex>
+
 #define NBK 64
-#define NB2 256  // panel width of the two-level blocking (a multiple of NBK)
+#ifndef LAMQ_NB2
+#define LAMQ_NB2 512
+#endif
+#define NB2 LAMQ_NB2  // panel width of the two-level blocking (a multiple of NBK)
 
 // dead = diag(H) == 0; the damping delta = damp * mean(diag H') where H' has unit diagonal at dead (with
 // keep_dead, H' = H: the dead diagonal stays zero and counts as zero).
@@ -241,6 +246,92 @@ __global__ void reverse_kernel(double* __restrict__ U, int64_t n, int64_t ldU, c
     U[i * ldU + j] = 0.0;
 }
 
+// One internal stream per device (default priority) with the events that order it against the caller's stream.
+// The enqueue of one factorization holds the device's mutex, so calls from several host threads do not interleave
+// their use of the events.
+struct SideStream {
+    std::mutex mu;
+    hipStream_t s = nullptr;
+    hipEvent_t fork = nullptr, step = nullptr, join = nullptr;
+};
+#define LAMQ_MAX_DEVICES 64
+static SideStream g_side[LAMQ_MAX_DEVICES];
+static std::mutex g_side_init;
+
+static int side_stream(SideStream** out)
+{
+    int dev = 0;
+    LAMQ_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= LAMQ_MAX_DEVICES) return LAMQ_EUNSUP;
+    std::lock_guard<std::mutex> lock(g_side_init);
+    SideStream& ss = g_side[dev];
+    if (!ss.s) {
+        hipStream_t st = nullptr;
+        hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+        LAMQ_HIP_CHECK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+        for (int i = 0; i < 3; ++i) LAMQ_HIP_CHECK(hipEventCreateWithFlags(&ev[i], hipEventDisableTiming));
+        ss.fork = ev[0];
+        ss.step = ev[1];
+        ss.join = ev[2];
+        ss.s = st;
+    }
+    *out = &ss;
+    return LAMQ_OK;
+}
+
+// The blocked steps of the factorization (stream s) and of the inverse (stream si).
+static int chol_steps(double* A, int64_t n, double* Linv, double* U, int64_t ldU, int32_t* info, hipStream_t s,
+                      hipStream_t si, hipEvent_t step)
+{
+    // Cholesky of A = J Hd J, lower, in panels of NB2 columns: inside a panel, 64-wide steps update only the panel's
+    // own columns; the columns after it get one product of depth NB2 per panel.
+    // X = L^-1 into U (right-looking solve of L X = I): X_k = Lkk^-1 B_k, then B_i -= L_ik X_k below, inside the
+    // panel at once and below it once per panel (X is lower triangular, so the panel's rows are zero right of
+    // their diagonal and one product of depth NB2 carries the panel's steps).
+    for (int64_t K0 = 0; K0 < n; K0 += NB2) {
+        const int64_t pe = (K0 + NB2 < n) ? K0 + NB2 : n;
+        for (int64_t k0 = K0; k0 < pe; k0 += NBK) {
+            const int nb = (int)(n - k0 < NBK ? n - k0 : NBK);
+            double* Lk = Linv + (k0 / NBK) * NBK * NBK;
+            hipLaunchKernelGGL(diag_block_kernel, dim3(1), dim3(256), 0, s, A, n, k0, nb, Lk, info);
+            LAMQ_LAUNCH_CHECK();
+            const int64_t rest = n - k0 - nb;
+            double* P = A + (k0 + nb) * n + k0;
+            int rc;
+            if (rest > 0) {
+                // P = P Lkk^-T (the row-wise triangular solve as one product, in place: one tile column)
+                rc = gemm_sub_f64<true, false, true>(P, n, P, n, Lk, NBK, rest, nb, nb, info, s);
+                if (rc) return rc;
+            }
+            LAMQ_HIP_CHECK(hipEventRecord(step, s));
+            LAMQ_HIP_CHECK(hipStreamWaitEvent(si, step, 0));
+            const int64_t pc = pe - (k0 + nb);
+            if (rest > 0 && pc > 0) {
+                rc = gemm_sub_f64<true, true>(A + (k0 + nb) * n + k0 + nb, n, P, n, P, n, rest, pc, nb, info, s);
+                if (rc) return rc;
+            }
+            // the inverse's step k
+            rc = gemm_sub_f64<false, false, true>(U + k0 * ldU, ldU, Lk, NBK, U + k0 * ldU, ldU, nb, k0 + nb, nb, info,
+                                                  si);
+            if (rc) return rc;
+            if (pc > 0) {
+                rc = gemm_sub_f64<false, false>(U + (k0 + nb) * ldU, ldU, P, n, U + k0 * ldU, ldU, pc, k0 + nb, nb, info,
+                                                si);
+                if (rc) return rc;
+            }
+        }
+        const int64_t rest = n - pe;
+        if (rest > 0) {
+            const double* P = A + pe * n + K0;
+            int rc = gemm_sub_f64<true, true>(A + pe * n + pe, n, P, n, P, n, rest, rest, pe - K0, info, s);
+            if (rc) return rc;
+            rc = gemm_sub_f64<false, false>(U + pe * ldU, ldU, P, n, U + K0 * ldU, ldU, rest, pe, pe - K0, info, si);
+            if (rc) return rc;
+        }
+    }
+    return LAMQ_OK;
+}
+
 extern "C" size_t lamq_chol_inv_upper_workspace_size(int64_t n)
 {
     if (n < 1) return 0;
@@ -258,6 +349,11 @@ extern "C" int lamq_chol_inv_upper_ex(const double* H, int64_t n, int64_t ldH, d
     if (workspace_bytes < lamq_chol_inv_upper_workspace_size(n)) return LAMQ_EINVAL;
     if (n > (int64_t)1 << 20) return LAMQ_EUNSUP;
     hipStream_t s = as_stream(stream);
+    SideStream* side = nullptr;
+    int rc = side_stream(&side);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lock(side->mu);
+    hipStream_t si = side->s;
     double* A = reinterpret_cast<double*>(workspace);
     double* Linv = A + n * n;  // cdiv(n, NBK) blocks of NBK x NBK
     double* delta = Linv + cdiv(n, NBK) * NBK * NBK;
@@ -266,63 +362,19 @@ extern "C" int lamq_chol_inv_upper_ex(const double* H, int64_t n, int64_t ldH, d
     const dim3 g2((unsigned)cdiv(n, 64), (unsigned)cdiv(n, 16)), b2(64, 16);
     hipLaunchKernelGGL(prep_kernel, g2, b2, 0, s, H, n, ldH, delta, keep_dead, A, Hd, ldHd);
     LAMQ_LAUNCH_CHECK();
-    // Cholesky of A = J Hd J, lower, in panels of NB2 columns: inside a panel, 64-wide steps update only the panel's
-    // own columns; the columns after it get one product of depth NB2 per panel (a quarter of the traffic of 64-deep
-    // updates of the whole trailing matrix)
-    for (int64_t K0 = 0; K0 < n; K0 += NB2) {
-        const int64_t pe = (K0 + NB2 < n) ? K0 + NB2 : n;
-        for (int64_t k0 = K0; k0 < pe; k0 += NBK) {
-            const int nb = (int)(n - k0 < NBK ? n - k0 : NBK);
-            double* Lk = Linv + (k0 / NBK) * NBK * NBK;
-            hipLaunchKernelGGL(diag_block_kernel, dim3(1), dim3(256), 0, s, A, n, k0, nb, Lk, info);
-            LAMQ_LAUNCH_CHECK();
-            const int64_t rest = n - k0 - nb;
-            if (rest > 0) {
-                double* P = A + (k0 + nb) * n + k0;
-                // P = P Lkk^-T (the row-wise triangular solve as one product, in place: one tile column)
-                int rc = gemm_sub_f64<true, false, true>(P, n, P, n, Lk, NBK, rest, nb, nb, info, s);
-                if (rc) return rc;
-                const int64_t pc = pe - (k0 + nb);
-                if (pc > 0) {
-                    rc = gemm_sub_f64<true, true>(A + (k0 + nb) * n + k0 + nb, n, P, n, P, n, rest, pc, nb, info, s);
-                    if (rc) return rc;
-                }
-            }
-        }
-        const int64_t rest = n - pe;
-        if (rest > 0) {
-            const double* P = A + pe * n + K0;
-            int rc = gemm_sub_f64<true, true>(A + pe * n + pe, n, P, n, P, n, rest, rest, pe - K0, info, s);
-            if (rc) return rc;
-        }
-    }
-    // X = L^-1 into U (right-looking solve of L X = I): X_k = Lkk^-1 B_k, then B_i -= L_ik X_k below, inside the
-    // panel at once and below it once per panel (X is lower triangular, so the panel's rows are zero right of
-    // their diagonal and one product of depth NB2 carries the panel's steps)
-    hipLaunchKernelGGL(identity_kernel, g2, b2, 0, s, U, n, ldU);
+    // The inverse X = L^-1 runs on the side stream, one 64-column step behind the factorization: its step k needs
+    // Lkk^-1 and the panel L_ik of the factor's step k (an event after that step's panel solve), nothing the
+    // factor writes later. The factor's in-panel and trailing updates and the inverse's products then overlap.
+    LAMQ_HIP_CHECK(hipEventRecord(side->fork, s));
+    LAMQ_HIP_CHECK(hipStreamWaitEvent(si, side->fork, 0));
+    hipLaunchKernelGGL(identity_kernel, g2, b2, 0, si, U, n, ldU);
     LAMQ_LAUNCH_CHECK();
-    for (int64_t K0 = 0; K0 < n; K0 += NB2) {
-        const int64_t pe = (K0 + NB2 < n) ? K0 + NB2 : n;
-        for (int64_t k0 = K0; k0 < pe; k0 += NBK) {
-            const int nb = (int)(n - k0 < NBK ? n - k0 : NBK);
-            const double* Lk = Linv + (k0 / NBK) * NBK * NBK;
-            int rc = gemm_sub_f64<false, false, true>(U + k0 * ldU, ldU, Lk, NBK, U + k0 * ldU, ldU, nb, k0 + nb, nb, info,
-                                                      s);
-            if (rc) return rc;
-            const int64_t rin = pe - (k0 + nb);
-            if (rin > 0) {
-                rc = gemm_sub_f64<false, false>(U + (k0 + nb) * ldU, ldU, A + (k0 + nb) * n + k0, n, U + k0 * ldU, ldU, rin,
-                                                k0 + nb, nb, info, s);
-                if (rc) return rc;
-            }
-        }
-        const int64_t rest = n - pe;
-        if (rest > 0) {
-            int rc = gemm_sub_f64<false, false>(U + pe * ldU, ldU, A + pe * n + K0, n, U + K0 * ldU, ldU, rest, pe, pe - K0,
-                                                info, s);
-            if (rc) return rc;
-        }
-    }
+    rc = chol_steps(A, n, Linv, U, ldU, info, s, si, side->step);
+    // the caller's stream waits for the side stream, also after a failed launch
+    const hipError_t e1 = hipEventRecord(side->join, si);
+    const hipError_t e2 = e1 == hipSuccess ? hipStreamWaitEvent(s, side->join, 0) : e1;
+    if (rc) return rc;
+    if (e2 != hipSuccess) return (int)e2;
     hipLaunchKernelGGL(reverse_kernel, g2, b2, 0, s, U, n, ldU, info);
     LAMQ_LAUNCH_CHECK();
     return LAMQ_OK;

@@ -15,6 +15,13 @@
         if (e_ != hipSuccess) return (int)e_;                 \
     } while (0)
 
+// a HIP runtime call's error, returned as the entry point's status
+#define LAMQ_HIP_CHECK(call)                                  \
+    do {                                                      \
+        hipError_t e_ = (call);                               \
+        if (e_ != hipSuccess) return (int)e_;                 \
+    } while (0)
+
 static inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 __host__ __device__ static inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
