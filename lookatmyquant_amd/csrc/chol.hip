@@ -65,35 +65,61 @@ __global__ void prep_kernel(const double* __restrict__ H, int64_t n, int64_t ldH
 // Lkk^-1 (lower, ld NBK) into Linv. One workgroup of four waves with the block in LDS, in four steps of 16
 // columns p:
 //   (1) wave 0 factors the 16 x 16 diagonal block D_p in registers (lane i holds row i; column values move
-//       between lanes by readlane): column c, d = a[c][c], l[c][c] = sqrt(d), l[i][c] = a[i][c] * (1/l[c][c])
-//       as LAPACK's unblocked potf2 scales, a[i][j] -= l[i][c] l[j][c]; then inverts the factor (lane c holds
-//       column c of D_p^-1, forward substitution with the same reciprocals);
+//       between lanes by readlane): column c, d = a[c][c], r = 1/sqrt(d), l[c][c] = d r, l[i][c] = a[i][c] r
+//       (a reciprocal scaling, as LAPACK's unblocked potf2 scales by 1/l[c][c]), a[i][j] -= l[i][c] l[j][c];
+//       then inverts the factor (lane c holds column c of D_p^-1, forward substitution with the same r);
 //   (2) the tiles below it become L_Ip = A_Ip D_p^-T (one MFMA tile per wave);
 //   (3) the lower trailing tiles take A_IJ -= L_Ip L_Jp^T (MFMA).
 // Then Lkk^-1 by block rows: Linv_pp = D_p^-1, Linv_pq = -D_p^-1 sum_{q<=r<p} L_pr Linv_rq, one level per p.
-// A block shorter than NBK is padded with the identity. The loops over p run at run time, so the code stays a few
+// Every workgroup of the launch factors the block for itself (the same arithmetic, the same result) and then solves
+// its 64 rows of the panel below the block, L_ik = A_ik Lkk^-T (MFMA); workgroup 0 writes Lkk and Lkk^-1. The panel
+// solve thus needs no launch of its own after the factor. A block shorter than NBK is padded with the identity. The loops over p run at run time, so the code stays a few
 // KB (a fully unrolled 64-step kernel spends most of its time fetching instructions).
 #define DB_LD 65  // LDS row stride of the block, in doubles
 
+// 1/sqrt(d) for a positive normal d: the hardware estimate and two Newton steps y <- y + y/2 (1 - d y^2), within a
+// few units in the last place
+__device__ __forceinline__ double rsqrt_f64(double d)
+{
+    double y = __builtin_amdgcn_rsq(d);
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+        const double e = fma(-(d * y), y, 1.0);
+        y = fma(0.5 * y, e, y);
+    }
+    return y;
+}
+
 __global__ __launch_bounds__(256) void diag_block_kernel(double* __restrict__ A, int64_t n, int64_t k0, int nb,
-                                                        double* __restrict__ Linv, int32_t* __restrict__ info)
+                                                        int64_t rest, double* __restrict__ Linv,
+                                                        int32_t* __restrict__ info)
 {
     __shared__ double blk[NBK * DB_LD];  // the block, then L
     __shared__ double inv[NBK * DB_LD];  // Lkk^-1
+    __shared__ double prow[NBK * DB_LD]; // this workgroup's 64 rows of the panel below the block
     __shared__ double dinv[4][16 * 17];  // D_p^-1, [row * 17 + col]
     __shared__ int sfail;
     if (*info != 0) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int li = lane & 15, lk = lane >> 4;
-    for (int e = tid; e < NBK * NBK; e += 256) {
-        const int i = e >> 6, j = e & 63;
-        double v;
-        if (i < nb && j < nb)
-            v = j <= i ? A[(k0 + i) * n + k0 + j] : 0.0;
-        else
-            v = i == j ? 1.0 : 0.0;
-        blk[i * DB_LD + j] = v;
-        inv[i * DB_LD + j] = 0.0;
+    const int64_t pr0 = k0 + nb + (int64_t)blockIdx.x * NBK;  // first panel row of this workgroup
+    const int prows = (int)(rest - (int64_t)blockIdx.x * NBK < NBK ? rest - (int64_t)blockIdx.x * NBK : NBK);
+    {  // all loads of a thread in flight at once, then the LDS writes
+        double v[NBK * NBK / 256], w[NBK * NBK / 256];
+#pragma unroll
+        for (int q = 0; q < NBK * NBK / 256; ++q) {
+            const int e = tid + 256 * q, i = e >> 6, j = e & 63;
+            const bool ld = i < nb && j <= i;  // j <= i < nb
+            v[q] = ld ? A[(k0 + i) * n + k0 + j] : 0.0;
+            w[q] = (i < prows && j < nb) ? A[(pr0 + i) * n + k0 + j] : 0.0;
+        }
+#pragma unroll
+        for (int q = 0; q < NBK * NBK / 256; ++q) {
+            const int e = tid + 256 * q, i = e >> 6, j = e & 63;
+            blk[i * DB_LD + j] = (i < nb && j < nb) ? v[q] : (i == j ? 1.0 : 0.0);
+            inv[i * DB_LD + j] = 0.0;
+            prow[i * DB_LD + j] = w[q];
+        }
     }
     if (tid == 0) sfail = 0;
     __syncthreads();
@@ -106,17 +132,25 @@ __global__ __launch_bounds__(256) void diag_block_kernel(double* __restrict__ A,
             for (int j = 0; j < 16; ++j) r[j] = j <= li ? B(c0 + li, c0 + j) : 0.0;
             double rc[16];  // 1 / l[c][c], the same in every lane
             int fail = 0;   // the first non-positive pivot (the same in every lane)
+            // the pivots form the serial chain; each is formed from lane-uniform values with exactly the operations
+            // lane c + 1 applies to its own entry, so the chain never waits on a lane-to-lane move
+            double d = readlane_f64(r[0], 0);
 #pragma unroll
             for (int c = 0; c < 16; ++c) {
-                const double d = readlane_f64(r[c], c);
                 fail = (fail == 0 && !(d > 0.0)) ? (int)(k0 + c0 + c + 1) : fail;
-                const double sd = sqrt(d);
-                const double rs = 1.0 / sd;
+                const double rs = rsqrt_f64(d);
+                const double sd = d * rs;
                 rc[c] = rs;
+                double dn = 0.0;
+                if (c < 15) {  // the next pivot: a[c+1][c+1] - l[c+1][c]^2
+                    const double l1 = readlane_f64(r[c], c + 1) * rs;
+                    dn = fma(-l1, l1, readlane_f64(r[c + 1], c + 1));
+                }
                 const double lic = li > c ? r[c] * rs : (li == c ? sd : 0.0);
                 r[c] = lic;
 #pragma unroll
                 for (int j = c + 1; j < 16; ++j) r[j] = fma(-lic, readlane_f64(lic, j), r[j]);
+                d = dn;
             }
             if (lane < 16) {
 #pragma unroll
@@ -204,6 +238,28 @@ __global__ __launch_bounds__(256) void diag_block_kernel(double* __restrict__ A,
         }
         __syncthreads();
     }
+    // the panel rows: P = A_rows Lkk^-T, wave w rows 16w..16w+15, four column tiles (B[k][j] = Lkk^-1[j][k]; past nb
+    // the rows hold zeros and Lkk^-1 the identity)
+    if (prows > 0) {
+        lamq_d4 acc[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = lamq_d4{0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) {
+            const double a = prow[(16 * wave + li) * DB_LD + 4 * kk + lk];
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                acc[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, inv[(16 * t + li) * DB_LD + 4 * kk + lk], acc[t], 0, 0, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int r = 16 * wave + 4 * v + lk, c = 16 * t + li;
+                if (r < prows && c < nb) A[(pr0 + r) * n + k0 + c] = acc[t][v];
+            }
+    }
+    if (blockIdx.x != 0) return;
     for (int e = tid; e < NBK * NBK; e += 256) {
         const int i = e >> 6, j = e & 63;
         if (i < nb && j <= i) A[(k0 + i) * n + k0 + j] = blk[i * DB_LD + j];
@@ -293,16 +349,14 @@ static int chol_steps(double* A, int64_t n, double* Linv, double* U, int64_t ldU
         for (int64_t k0 = K0; k0 < pe; k0 += NBK) {
             const int nb = (int)(n - k0 < NBK ? n - k0 : NBK);
             double* Lk = Linv + (k0 / NBK) * NBK * NBK;
-            hipLaunchKernelGGL(diag_block_kernel, dim3(1), dim3(256), 0, s, A, n, k0, nb, Lk, info);
-            LAMQ_LAUNCH_CHECK();
             const int64_t rest = n - k0 - nb;
             double* P = A + (k0 + nb) * n + k0;
+            // the factor of the diagonal block and the panel below it (P = P Lkk^-T): every workgroup factors the
+            // block for itself and solves 64 rows of the panel
+            const unsigned pg = rest > 0 ? (unsigned)cdiv(rest, NBK) : 1u;
+            hipLaunchKernelGGL(diag_block_kernel, dim3(pg), dim3(256), 0, s, A, n, k0, nb, rest, Lk, info);
+            LAMQ_LAUNCH_CHECK();
             int rc;
-            if (rest > 0) {
-                // P = P Lkk^-T (the row-wise triangular solve as one product, in place: one tile column)
-                rc = gemm_sub_f64<true, false, true>(P, n, P, n, Lk, NBK, rest, nb, nb, info, s);
-                if (rc) return rc;
-            }
             LAMQ_HIP_CHECK(hipEventRecord(step, s));
             LAMQ_HIP_CHECK(hipStreamWaitEvent(si, step, 0));
             const int64_t pc = pe - (k0 + nb);
