@@ -177,7 +177,10 @@ def test_chol_inv_upper_reports_non_pd(E, n):
         E.chol_inv_upper(cuda(H), damp=0.0)
 
 
-@pytest.mark.parametrize("m,n,seed", [(48, 960, 201), (20, 2560, 1301), (8, 4096, 7), (4, 9728, 3301)])
+# shapes: the MFMA kernel's specialised layouts (960: a = 16, b = 60; 2560: 128 x 20; 4096: 64 x 64; 9728: 64 x 152;
+# 3072: 256 x 12; 5120: 256 x 20), its generic layout (7680: 128 x 60) and more rows than workgroups (1030 x 960)
+@pytest.mark.parametrize("m,n,seed", [(48, 960, 201), (20, 2560, 1301), (8, 4096, 7), (4, 9728, 3301), (5, 3072, 5),
+                                      (3, 5120, 9), (6, 7680, 11), (1030, 960, 17)])
 def test_rht_rows(E, m, n, seed):
     rng = np.random.default_rng(n)
     W = rng.standard_normal((m, n))
