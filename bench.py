@@ -333,7 +333,7 @@ def main():
         args.L = 16 if args.workload == "c2" else 12
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the per-matrix hot path runs on one MI355X here (rows would shard across "
-              "GPUs with no communication; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "GPUs with no communication). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if args.workload == "c3":
         run_c3(args)

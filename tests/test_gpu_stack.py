@@ -64,3 +64,26 @@ def test_small_stack_build():
                 got = states[[by_row[r] for r in rows.tolist()]]
                 say(f"layer {i} stage {s} {nm} group {g['group']} bits {g['bits']}")
                 assert np.array_equal(got, ref)
+
+
+@pytest.mark.gpu
+def test_flash_attention_matches_the_unfused_path():
+    """The stack's causal grouped-query attention: the fused flash kernel against the one-sequence-at-a-time float32
+    softmax path, on bf16 inputs (both round the output to bf16; the tolerance is a few bf16 units of |v| ~ 1)."""
+    import torch
+
+    from lookatmyquant_amd import stack
+
+    sh = stack.Shape(hidden=512, heads=8, kv_heads=4, head_dim=128, inter=1024, layers=1, vocab=1000)
+    g = torch.Generator(device="cuda").manual_seed(11)
+    q = torch.randn(2, 8, 256, 128, generator=g, device="cuda").bfloat16()
+    k = torch.randn(2, 4, 256, 128, generator=g, device="cuda").bfloat16()
+    v = torch.randn(2, 4, 256, 128, generator=g, device="cuda").bfloat16()
+    try:
+        got = stack._attention_flash(q, k, v)
+    except RuntimeError as e:
+        pytest.skip(f"no fused flash attention in this build: {e}")
+    ref = stack._attention_unfused(q, k, v, sh)
+    err = (got.float() - ref.float()).abs().max().item()
+    print(f"flash vs unfused attention: max |diff| {err:.3e}", flush=True)
+    assert err < 3e-2
