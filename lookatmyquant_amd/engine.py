@@ -348,43 +348,48 @@ def _tiled(X: torch.Tensor) -> bool:
     return n % 8 == 0 and ld(X) % 8 == 0 and X.data_ptr() % 16 == 0
 
 
-def weight_classes(w: torch.Tensor):
-    """[(weight, int32 row indices)] for the distinct nonzero values of w when there are at most
-    MAX_WEIGHT_CLASSES of them (one host synchronisation), else None."""
+def weight_classes(w: torch.Tensor, include_zero: bool = False):
+    """[(weight, int32 row indices)] for the distinct values of w (the zero class only with include_zero) when there
+    are at most MAX_WEIGHT_CLASSES of them (one host synchronisation), else None."""
     vals = torch.unique(w)
     if vals.numel() > MAX_WEIGHT_CLASSES:
         return None
     out = []
     for v in vals.cpu().tolist():
-        if v != 0.0:
+        if v != 0.0 or include_zero:
             out.append((v, (w == v).nonzero().flatten().to(torch.int32)))
     return out
 
 
-def hessian_accum(H: torch.Tensor, X: torch.Tensor, w: torch.Tensor | None = None, scale: float = 1.0) -> torch.Tensor:
+def hessian_accum(H: torch.Tensor, X: torch.Tensor, w: torch.Tensor | None = None, scale: float = 1.0,
+                  classes: list | None = None) -> torch.Tensor:
     """H (float32 [n, n], lower triangle) += scale * X^T diag(w) X for bf16 X [N, n]. Weights with few distinct
-    values go class by class through the unweighted kernel (exact products); others use the hi/lo split."""
+    values are taken class by class through the unweighted kernel (exact products): the most frequent weight w0
+    over all tokens (contiguous), then (v - w0) over each other class's rows (gathered in the kernel). Other
+    weights use the hi/lo split. classes: weight_classes(w, include_zero=True), if the caller has it already."""
     need(H, torch.float32, "H", 2)
     need(X, torch.bfloat16, "X", 2)
     N, n = X.shape
     wv = None
     if w is not None:
         wv = w.to(device=X.device, dtype=torch.float32).contiguous()
-        classes = weight_classes(wv) if _tiled(X) else None
-        if classes is not None:
-            # the tokens gathered class by class into one contiguous copy: the contiguous kernel then runs over each
-            # class's slice (faster than gathering rows inside the kernel, at the cost of a copy of X)
-            Xs = X.index_select(0, torch.cat([rows for _, rows in classes]).long()) if len(classes) > 1 or \
-                classes[0][1].numel() != N else X
-            r0 = 0
+        if classes is None and _tiled(X):
+            classes = weight_classes(wv, include_zero=True)
+        if classes is not None and _tiled(X):
+            base, _ = max(classes, key=lambda c: c[1].numel())
+            if base != 0.0:
+                nbytes = lib().lamq_gram_workspace_size(N, n, 1)
+                ws = workspace(nbytes, X.device)
+                check(lib().lamq_hessian_accum(ptr(X), N, n, ld(X), None, float(scale * base), ptr(H), ld(H), ptr(ws),
+                                               nbytes, stream(X.device)), "hessian_accum")
             for v, rows in classes:
+                if v == base or rows.numel() == 0:
+                    continue
                 m = rows.numel()
-                part = Xs[r0 : r0 + m]
-                r0 += m
                 nbytes = lib().lamq_gram_workspace_size(m, n, 1)
                 ws = workspace(nbytes, X.device)
-                check(lib().lamq_hessian_accum(ptr(part), m, n, ld(part), None, float(scale * v), ptr(H), ld(H), ptr(ws),
-                                               nbytes, stream(X.device)), "hessian_accum")
+                check(lib().lamq_hessian_accum_rows(ptr(X), ptr(rows), m, n, ld(X), float(scale * (v - base)), ptr(H),
+                                                    ld(H), ptr(ws), nbytes, stream(X.device)), "hessian_accum_rows")
             return H
     nbytes = lib().lamq_gram_workspace_size(N, n, 1)
     ws = workspace(nbytes, X.device)
@@ -410,8 +415,9 @@ def hessian(X: torch.Tensor, w: torch.Tensor | None = None) -> torch.Tensor:
 
 
 def cross_gram_accum(D: torch.Tensor, Xr: torch.Tensor, Xq: torch.Tensor, w: torch.Tensor | None = None,
-                     scale: float = 1.0) -> torch.Tensor:
-    """D (float32 [n, n]) += scale * Xr^T diag(w) Xq (quantize.py:1457)."""
+                     scale: float = 1.0, classes: list | None = None) -> torch.Tensor:
+    """D (float32 [n, n]) += scale * Xr^T diag(w) Xq (quantize.py:1457). classes: weight_classes(w), if the caller
+    has it already (zero classes are skipped)."""
     need(D, torch.float32, "D", 2)
     need(Xr, torch.bfloat16, "Xr", 2)
     need(Xq, torch.bfloat16, "Xq", 2)
@@ -420,9 +426,12 @@ def cross_gram_accum(D: torch.Tensor, Xr: torch.Tensor, Xq: torch.Tensor, w: tor
     N, n = Xr.shape
     wv = None if w is None else w.to(device=Xr.device, dtype=torch.float32).contiguous()
     if wv is not None and _tiled(Xr) and _tiled(Xq):
-        classes = weight_classes(wv)
+        if classes is None:
+            classes = weight_classes(wv)
         if classes is not None:
             for v, rows in classes:  # the cross-Gram (QEP only) gathers its rows inside the kernel, no copies
+                if v == 0.0 or rows.numel() == 0:
+                    continue
                 nbytes = lib().lamq_gram_workspace_size(rows.numel(), n, 0)
                 ws = workspace(nbytes, Xr.device)
                 check(lib().lamq_cross_gram_rows(ptr(Xr), ptr(Xq), ptr(rows), rows.numel(), n, ld(Xr), float(scale * v),

@@ -175,6 +175,7 @@ def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | Non
     rope = tuple(t.to(dev) for t in rope_tables(T, sh, dev))
     chunks = [slice(c, min(c + chunk, S_)) for c in range(0, S_, chunk)]
     wt = None if token_w is None else [token_w[cs].reshape(-1).to(dev, torch.float32) for cs in chunks]
+    wcls = None if wt is None else [E.weight_classes(wc, include_zero=True) for wc in wt]
     # the embedding (shared by both streams: it is not quantized here)
     g = torch.Generator(device=dev).manual_seed(weight_seed * 1000 + 999)
     emb = (torch.randn(sh.vocab, sh.hidden, generator=g, device=dev, dtype=torch.float32) * sh.std).to(torch.bfloat16)
@@ -221,7 +222,7 @@ def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | Non
             torch.cuda.synchronize()
             t2 = time.perf_counter()
             timer.add("forward", t2 - t1)
-            H, D = _stage_statistics(xqf, wt, xr[s])
+            H, D = _stage_statistics(xqf, wt, xr[s], wcls)
             targets = qep_targets(H, D - H, alpha, {nm: wr[nm] for nm in names})
             torch.cuda.synchronize()
             t3 = time.perf_counter()
@@ -269,8 +270,9 @@ def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | Non
 STAGE_INDEX = {nm: j for j, nm in enumerate(n for st in STAGES for n in st)}
 
 
-def _stage_statistics(xq: list, w: list | None, xr: list):
-    """H = X_q^T W X_q / N and D = X_ref^T W X_q / N over the chunks (quantize.py:1416-1470), float64 on the GPU."""
+def _stage_statistics(xq: list, w: list | None, xr: list, classes: list | None = None):
+    """H = X_q^T W X_q / N and D = X_ref^T W X_q / N over the chunks (quantize.py:1416-1470), float64 on the GPU.
+    classes: per chunk, engine.weight_classes(w[c], include_zero=True) (computed once per build)."""
     dev = xq[0].device
     n = xq[0].shape[1]
     H = torch.zeros(n, n, dtype=torch.float32, device=dev)
@@ -280,8 +282,9 @@ def _stage_statistics(xq: list, w: list | None, xr: list):
         a = a.contiguous()
         b = b.contiguous()
         wc = None if w is None else w[c]
-        E.hessian_accum(H, a, wc)
-        E.cross_gram_accum(D, b, a, wc)
+        cc = None if classes is None else classes[c]
+        E.hessian_accum(H, a, wc, classes=cc)
+        E.cross_gram_accum(D, b, a, wc, classes=cc)
         ntok += a.shape[0]
     return E.hessian_finalize(H, float(ntok)), (D / ntok).double()
 
