@@ -61,8 +61,8 @@ __global__ void prep_kernel(const double* __restrict__ H, int64_t n, int64_t ldH
     if (Hd) Hd[i * ldHd + j] = v;
 }
 
-// The nb x nb diagonal block at (k0, k0) of A (lower): its Cholesky factor Lkk, written back into A, and
-// Lkk^-1 (lower, ld NBK) into Linv. One workgroup of four waves with the block in LDS, in four steps of 16
+// The nb x nb diagonal block at (k0, k0) of A (lower): its Cholesky factor Lkk and Lkk^-1 (lower, ld NBK, written
+// into Linv). One workgroup of four waves with the block in LDS, in four steps of 16
 // columns p:
 //   (1) wave 0 factors the 16 x 16 diagonal block D_p in registers (lane i holds row i; column values move
 //       between lanes by readlane): column c, d = a[c][c], r = 1/sqrt(d), l[c][c] = d r, l[i][c] = a[i][c] r
@@ -72,7 +72,7 @@ __global__ void prep_kernel(const double* __restrict__ H, int64_t n, int64_t ldH
 //   (3) the lower trailing tiles take A_IJ -= L_Ip L_Jp^T (MFMA).
 // Then Lkk^-1 by block rows: Linv_pp = D_p^-1, Linv_pq = -D_p^-1 sum_{q<=r<p} L_pr Linv_rq, one level per p.
 // Every workgroup of the launch factors the block for itself (the same arithmetic, the same result) and then solves
-// its 64 rows of the panel below the block, L_ik = A_ik Lkk^-T (MFMA); workgroup 0 writes Lkk and Lkk^-1. The panel
+// its 64 rows of the panel below the block, L_ik = A_ik Lkk^-T (MFMA); workgroup 0 writes Lkk^-1. The panel
 // solve thus needs no launch of its own after the factor. A block shorter than NBK is padded with the identity. The loops over p run at run time, so the code stays a few
 // KB (a fully unrolled 64-step kernel spends most of its time fetching instructions).
 #define DB_LD 65  // LDS row stride of the block, in doubles
@@ -259,10 +259,12 @@ __global__ __launch_bounds__(256) void diag_block_kernel(double* __restrict__ A,
                 if (r < prows && c < nb) A[(pr0 + r) * n + k0 + c] = acc[t][v];
             }
     }
+    // Lkk itself is not written back: nothing after this launch reads it (the panel, the updates and the inverse use
+    // the panel rows and Lkk^-1), and the other workgroups of this launch read the block as it was, so writing it in
+    // place would race with them
     if (blockIdx.x != 0) return;
     for (int e = tid; e < NBK * NBK; e += 256) {
         const int i = e >> 6, j = e & 63;
-        if (i < nb && j <= i) A[(k0 + i) * n + k0 + j] = blk[i * DB_LD + j];
         Linv[i * NBK + j] = j <= i ? inv[i * DB_LD + j] : 0.0;
     }
 }

@@ -151,6 +151,29 @@ def test_chol_inv_upper(E, n):
     assert np.abs(Ug.T @ Ug @ Hd_o - np.eye(n)).max() < 1e-9
 
 
+@pytest.mark.parametrize("n", [6000, 9728])
+def test_chol_inv_upper_large_inverse_identity(E, n):
+    """At the stage widths of the benchmark (many workgroups per 64-column step, the side stream busy with the
+    inverse) U^T U must invert Hd, on two calls in a row (the result may not depend on workgroup timing)."""
+    g = torch.Generator(device="cuda").manual_seed(n)
+    X = torch.randn(2 * n, n, generator=g, device="cuda", dtype=torch.float64)
+    H = X.T @ X / (2 * n)
+    eye = torch.eye(n, device="cuda", dtype=torch.float64)
+    say(f"chol_inv_upper U^T U Hd = I, n={n}")
+    first = None
+    for rep in range(2):
+        Hd, U, _, info = E.chol_inv_upper(H, damp=0.1)
+        assert int(info.item()) == 0
+        err = (U.T @ (U @ Hd) - eye).abs().max().item()
+        say(f"  call {rep}: |U^T U Hd - I| = {err:.3e}")
+        assert err < 1e-10
+        assert float(torch.tril(U, -1).abs().max()) == 0.0
+        if first is None:
+            first = U
+        else:
+            assert torch.equal(first, U)
+
+
 @pytest.mark.parametrize("n,k", [(300, 3), (300, 37), (300, 250)])
 def test_chol_inv_upper_reports_a_pivot_inside_a_block(E, n, k):
     """A negative diagonal entry at H[k][k] of an otherwise diagonal H is pivot n - k of the reversed
