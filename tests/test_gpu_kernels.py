@@ -106,7 +106,8 @@ def test_viterbi_long_paths_use_workspace(E, tables):
 # ----------------------------------------------------------------------------- fp64 building blocks
 
 
-@pytest.mark.parametrize("m,n,b0,b1", [(200, 300, 64, 192), (2309, 2560, 128, 256), (1800, 1571, 0, 128)])
+@pytest.mark.parametrize("m,n,b0,b1", [(200, 300, 64, 192), (2309, 2560, 128, 256), (1800, 1571, 0, 128),
+                                       (2600, 3100, 0, 384)])
 def test_trailing_update_matches_oracle_order(E, m, n, b0, b1):
     """Small shapes take the 64-tile kernel, large ones (>= 256 tiles of 128) the LDS-staged 128-tile kernel; ragged
     rows included."""
