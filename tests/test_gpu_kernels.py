@@ -289,6 +289,27 @@ def test_ldlq_trellis_ragged_matches_oracle(E, tables):
     assert np.array_equal(st, ref)
 
 
+def test_ldlq_trellis_full_width_matches_oracle(E, tables):
+    """The down stage's width (n = 9,728: 76 lazy blocks, 19 runs of trailing updates on the 128-tile kernel, the
+    factor's large-n path): 64 rows swept on the GPU, two of them against the C oracle with the same U."""
+    n, m = 9728, 64
+    g = torch.Generator(device="cuda").manual_seed(97)
+    Xa = torch.randn(2 * n, n, generator=g, device="cuda", dtype=torch.float64)
+    H = Xa.T @ Xa / (2 * n)
+    del Xa
+    _, U, _, _ = E.chol_inv_upper(H)
+    X = torch.randn(m, n, generator=g, device="cuda", dtype=torch.float64)
+    Xh = X.cpu().numpy()
+    S = O.row_scale(Xh)
+    say("ldlq trellis 64 x 9728, L = 12, k = 2")
+    st = E.ldlq_trellis(X, cuda(S), U, cuda(tables[2]), 12, 2).cpu().numpy()
+    rows = [0, 37]
+    ref = O.ldlq_trellis(Xh[rows], U.cpu().numpy(), S[rows], tables[2], 12, 2)
+    same = (st[rows] == ref).mean()
+    say(f"  states equal to the oracle's: {same:.6f}")
+    assert np.array_equal(st[rows], ref)
+
+
 def test_ldlq_scalar_matches_reference_config1(E, golden, config12):
     """Config 1 (960 x 960, 3-bit Lloyd-Max, nested_words path): indices equal the reference's."""
     W, H = config12
