@@ -32,14 +32,17 @@ __device__ __forceinline__ void kl_chunk(KLPart& p, const float (&r)[8], const f
         p.sq *= (double)__expf(p.mq - cq);
         p.mq = cq;
     }
+    // e^(v - m) = 2^(v log2(e) - m log2(e)): one fma and the hardware 2^x per term
+    const float l2e = 1.4426950408889634f;
+    const float mr2 = p.mr * l2e, mq2 = p.mq * l2e;
     float sr = 0.0f, ar = 0.0f, sq = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e)
         if (e < cnt) {
-            const float er = __expf(r[e] - p.mr);
+            const float er = __builtin_amdgcn_exp2f(fmaf(r[e], l2e, -mr2));
             sr += er;
             ar = fmaf(er, r[e] - q[e], ar);
-            sq += __expf(q[e] - p.mq);
+            sq += __builtin_amdgcn_exp2f(fmaf(q[e], l2e, -mq2));
         }
     p.sr += (double)sr;
     p.ar += (double)ar;
