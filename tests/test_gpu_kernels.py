@@ -373,6 +373,44 @@ def test_hessian(E, N, n, weighted):
     assert np.array_equal(Hg, Hg.T)
 
 
+def test_hessian_zero_weight_class(E):
+    """Token weights with a zero class: the most frequent weight runs over all tokens and the zero-weight tokens are
+    taken back out by a correction of -w0 over their rows."""
+    from lookatmyquant_amd import synthetic
+
+    N, n = 3000, 264
+    X = synthetic.calibration(N, n, 31, 32)
+    rng = np.random.default_rng(33)
+    w = np.ones(N, np.float32)
+    w[rng.random(N) < 0.2] = 0.0
+    w[rng.random(N) < 0.1] = 10.0
+    say("hessian with zero-weight tokens")
+    Hg = E.hessian(torch.from_numpy(X).to(torch.bfloat16).cuda(), torch.from_numpy(w).cuda()).cpu().numpy()
+    ref = O.hessian(X, w)
+    err = np.abs(Hg - ref).max() / np.abs(ref).max()
+    say(f"  max |H - H64| / max |H64| = {err:.3e}")
+    assert err < 1e-4
+
+
+@pytest.mark.parametrize("N,n,weighted", [(16384, 6000, True), (4096, 9728, False)])
+def test_hessian_large_against_float32(E, N, n, weighted):
+    """The 256-tile kernel at the widths of the benchmark (hundreds of tiles, workgroups renumbered XCD by XCD):
+    against a float32 product of the same bf16 activations on the GPU."""
+    g = torch.Generator(device="cuda").manual_seed(n)
+    X = torch.randn(N, n, generator=g, device="cuda").bfloat16()
+    w = None
+    if weighted:
+        w = torch.ones(N, device="cuda")
+        w[torch.rand(N, generator=g, device="cuda") < 0.1] = 10.0
+    say(f"hessian N={N} n={n} against float32")
+    H = E.hessian(X, w)
+    Xf = X.float()
+    ref = (Xf.T @ (Xf * (w[:, None] if w is not None else 1.0))) / N
+    err = ((H.float() - ref).abs().max() / ref.abs().max()).item()
+    say(f"  max |H - ref| / max |ref| = {err:.3e}")
+    assert err < 1e-4
+
+
 def test_hessian_accum_rows(E):
     """lamq_hessian_accum_rows over a row list (repeats allowed, ragged count): scale * sum over the listed rows."""
     from lookatmyquant_amd import synthetic
