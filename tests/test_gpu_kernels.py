@@ -274,6 +274,25 @@ def test_ldlq_trellis_L16_matches_reference(E, golden, config12):
     assert np.array_equal(st, g["states"])
 
 
+@pytest.mark.parametrize("k", [1, 3, 4])
+def test_ldlq_trellis_L16_other_widths_match_oracle(E, k):
+    """The 16-bit-state sweep at the widths a row plan also assigns (k = 1: the quarter-window kernel; k = 3, 4: the
+    minima-exchange kernel), 3 rows x 272 columns (two lazy blocks, the second ragged), against the C oracle."""
+    from lookatmyquant_amd.tables import quantile_table
+
+    rng = np.random.default_rng(40 + k)
+    m, n = 3, 272
+    Xa = rng.standard_normal((600, n))
+    _, U, _ = O.environment(Xa.T @ Xa / 600)
+    X = rng.standard_normal((m, n))
+    S = O.row_scale(X)
+    tab = np.asarray(quantile_table(16, 0), dtype=np.float64)
+    say(f"ldlq trellis L=16 k={k}, 3 x 272")
+    st = E.ldlq_trellis(cuda(X), cuda(S), cuda(U), cuda(tab), 16, k).cpu().numpy()
+    ref = O.ldlq_trellis(X, U, S, tab, 16, k)
+    assert np.array_equal(st, ref)
+
+
 def test_ldlq_trellis_ragged_matches_oracle(E, tables):
     """n not a multiple of the lazy block or of the width, m not a multiple of anything."""
     rng = np.random.default_rng(11)
