@@ -111,6 +111,13 @@ int lamq_ldlq_trellis16_block(double* T, int64_t m, int64_t n, int64_t ldT, cons
 int lamq_trailing_update_f64(double* T, int64_t m, int64_t n, int64_t ldT, const double* Z, int64_t ldZ,
                              const double* U, int64_t ldU, int64_t b0, int64_t b1, void* stream);
 
+/* C [M, N] -= A [M, K] @ op(B) in fp64 (op(B) = B [K, N], or B^T for B [N, K] when transb), with op(B) optionally
+ * triangular: tri = 1 when op(B)[k][j] = 0 for k < j, tri = 2 when op(B)[k][j] = 0 for k > j (the zero part is then
+ * skipped, not read). The products of the QEP targets with the inverse factor, (H + lambda I)^-1 = U^T U
+ * (quantize.py:1330-1335, 1503): W D U^T U as two triangular products. */
+int lamq_gemm_sub_f64(double* C, int64_t ldc, const double* A, int64_t lda, const double* B, int64_t ldb, int64_t M,
+                      int64_t N, int64_t K, int transb, int tri, void* stream);
+
 /* One step of the generic sweep for a projection Q [m, w] computed by the caller (opgraph/syntax.py:117-121):
  * E = T[:, j:j+w] - Q, z = E U_BB^-1, T[:, j+w:b1] -= z @ U[j:j+w, j+w:b1], Z[:, j-b0 : j-b0+w] = z.
  * The same arithmetic as the fused block kernels; w <= 64. */

@@ -29,6 +29,7 @@ SIGNATURES = {
     "lamq_ldlq_trellis16_block": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _p, _p, _c_int, _c_int, _c_i64,
                                            _c_i64, _c_int, _c_int, _p, _p, _c_i64, _p, _c_i64, _p]),
     "lamq_trailing_update_f64": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _c_i64, _c_i64, _c_i64, _p]),
+    "lamq_gemm_sub_f64": (_c_int, [_p, _c_i64, _p, _c_i64, _p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _p]),
     "lamq_refit_step": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _c_i64, _c_i64, _c_int, _c_i64, _c_i64, _p,
                                  _c_i64, _p]),
     "lamq_zero_columns": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _p]),

@@ -115,10 +115,15 @@ __global__ __launch_bounds__(256) void gemm_sub_f64_kernel(double* C, int64_t ld
 // [k][col] B) and 16-byte aligned operands (gemm_sub_f64 checks; other shapes take the kernel above).
 #define G8_BM 128
 #define G8_BK 16
+#define LAMQ_TRI_KGE 1
+#define LAMQ_TRI_KLE 2
 
 __device__ double lamq_zero_chunk[2];
 
-template <bool TRANSB, bool LOWER, int BK>
+// TRI: the k-range of a tile column when op(B) is triangular, stages wholly in its zero part skipped:
+// LAMQ_TRI_KGE (op(B)[k][j] = 0 for k < j, a lower op(B)): k from the tile's first column on;
+// LAMQ_TRI_KLE (op(B)[k][j] = 0 for k > j, an upper op(B)): k up to the tile's last column.
+template <bool TRANSB, bool LOWER, int BK, int TRI = 0>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BK == 16 ? 2 : 1, BK == 16 ? 2 : 1))) void
 gemm128_f64_kernel(double* __restrict__ C, int64_t ldc, const double* __restrict__ A, int64_t lda,
                    const double* __restrict__ B, int64_t ldb, int64_t M, int64_t N, int64_t K,
@@ -184,13 +189,16 @@ gemm128_f64_kernel(double* __restrict__ C, int64_t ldc, const double* __restrict
         return TRANSB ? aaddr(col, k) : (uint32_t)(k * 1024 + (((col >> 1) ^ (8 * (k & 1))) << 4) + (col & 1) * 8);
     };
 
-    const int nst = (int)cdiv(K, BK);
+    int st0 = 0, nst = (int)cdiv(K, BK);
+    if (TRI == LAMQ_TRI_KGE) st0 = (int)(tc / BK);
+    if (TRI == LAMQ_TRI_KLE && tc + G8_BM < K) nst = (int)cdiv(tc + G8_BM, BK);
+    if (st0 >= nst) st0 = nst;  // an empty range: no loads, C - 0 written back
 #pragma unroll
     for (int q = 0; q < IPW; ++q) {
-        piece(0, 0, q, 0);
-        piece(0, 0, q, 1);
+        piece((int64_t)st0 * BK, st0 & 1, q, 0);
+        piece((int64_t)st0 * BK, st0 & 1, q, 1);
     }
-    for (int st = 0; st < nst; ++st) {
+    for (int st = st0; st < nst; ++st) {
         wait_vm<0>();     // this wave's loads of stage st have landed
         __syncthreads();  // everyone's; the other buffer (stage st - 1) is free
         const int buf = st & 1;
@@ -251,7 +259,9 @@ gemm128_f64_kernel(double* __restrict__ C, int64_t ldc, const double* __restrict
     cstore(3, g1);
 }
 
-template <bool TRANSB, bool LOWER, bool OVERWRITE = false>
+// TRI (LAMQ_TRI_KGE, LAMQ_TRI_KLE): op(B) is triangular and the 128-tile kernel skips the stages of its zero part (the
+// other kernel reads the zeros).
+template <bool TRANSB, bool LOWER, bool OVERWRITE = false, int TRI = 0>
 static int gemm_sub_f64(double* C, int64_t ldc, const double* A, int64_t lda, const double* B, int64_t ldb, int64_t M,
                         int64_t N, int64_t K, const int32_t* info, hipStream_t s)
 {
@@ -263,8 +273,8 @@ static int gemm_sub_f64(double* C, int64_t ldc, const double* A, int64_t lda, co
                         ((uintptr_t)A % 16) == 0 && ((uintptr_t)B % 16) == 0;
     if (!OVERWRITE && chunks && cdiv(M, G8_BM) * cdiv(N, G8_BM) >= 128) {
         dim3 grid((unsigned)cdiv(N, G8_BM), (unsigned)cdiv(M, G8_BM));
-        hipLaunchKernelGGL((gemm128_f64_kernel<TRANSB, LOWER, G8_BK>), grid, dim3(256), 0, s, C, ldc, A, lda, B, ldb, M, N,
-                           K, info);
+        hipLaunchKernelGGL((gemm128_f64_kernel<TRANSB, LOWER, G8_BK, TRI>), grid, dim3(256), 0, s, C, ldc, A, lda, B, ldb,
+                           M, N, K, info);
         LAMQ_LAUNCH_CHECK();
         return LAMQ_OK;
     }

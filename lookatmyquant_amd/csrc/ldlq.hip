@@ -95,6 +95,25 @@ extern "C" int lamq_trailing_update_f64(double* T, int64_t m, int64_t n, int64_t
                                       as_stream(stream));
 }
 
+// C -= A op(B), fp64, with op(B) optionally triangular (tri 1: op(B)[k][j] = 0 for k < j; tri 2: for k > j): the
+// products of the QEP targets with the inverse factor U (quantize.py:1330-1335: (H + lambda I)^-1 = U^T U).
+extern "C" int lamq_gemm_sub_f64(double* C, int64_t ldc, const double* A, int64_t lda, const double* B, int64_t ldb,
+                                 int64_t M, int64_t N, int64_t K, int transb, int tri, void* stream)
+{
+    if (!C || !A || !B || M < 0 || N < 0 || K < 0 || ldc < N || lda < K || ldb < (transb ? K : N)) return LAMQ_EINVAL;
+    if (tri < 0 || tri > 2 || (transb != 0 && transb != 1)) return LAMQ_EINVAL;
+    if (M == 0 || N == 0 || K == 0) return LAMQ_OK;
+    hipStream_t s = as_stream(stream);
+    if (transb) {
+        if (tri == 1) return gemm_sub_f64<true, false, false, LAMQ_TRI_KGE>(C, ldc, A, lda, B, ldb, M, N, K, nullptr, s);
+        if (tri == 2) return gemm_sub_f64<true, false, false, LAMQ_TRI_KLE>(C, ldc, A, lda, B, ldb, M, N, K, nullptr, s);
+        return gemm_sub_f64<true, false>(C, ldc, A, lda, B, ldb, M, N, K, nullptr, s);
+    }
+    if (tri == 1) return gemm_sub_f64<false, false, false, LAMQ_TRI_KGE>(C, ldc, A, lda, B, ldb, M, N, K, nullptr, s);
+    if (tri == 2) return gemm_sub_f64<false, false, false, LAMQ_TRI_KLE>(C, ldc, A, lda, B, ldb, M, N, K, nullptr, s);
+    return gemm_sub_f64<false, false>(C, ldc, A, lda, B, ldb, M, N, K, nullptr, s);
+}
+
 // T[:, dead] = 0 at the start of a sweep (opgraph/syntax.py:101).
 __global__ void zero_columns_kernel(double* __restrict__ T, int64_t m, int64_t n, int64_t ldT, const uint8_t* __restrict__ dead)
 {

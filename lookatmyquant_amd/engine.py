@@ -336,6 +336,21 @@ def trailing_update(T: torch.Tensor, Z: torch.Tensor, U: torch.Tensor, b0: int, 
     return T
 
 
+def gemm_sub(C: torch.Tensor, A: torch.Tensor, B: torch.Tensor, transb: bool = False, tri: int = 0) -> torch.Tensor:
+    """C -= A @ op(B) in place (op(B) = B.T when transb), fp64 on MFMA; tri = 1 / 2 when op(B) is lower / upper
+    triangular (its zero part is skipped)."""
+    need(C, torch.float64, "C", 2)
+    need(A, torch.float64, "A", 2)
+    need(B, torch.float64, "B", 2)
+    M, N = C.shape
+    K = A.shape[1]
+    if A.shape[0] != M or (B.shape != (N, K) if transb else B.shape != (K, N)):
+        raise ValueError("gemm_sub: shapes do not agree")
+    check(lib().lamq_gemm_sub_f64(ptr(C), ld(C), ptr(A), ld(A), ptr(B), ld(B), M, N, K, 1 if transb else 0, int(tri),
+                                  stream(C.device)), "gemm_sub")
+    return C
+
+
 # ----------------------------------------------------------------------------- statistics
 
 

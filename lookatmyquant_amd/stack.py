@@ -223,10 +223,13 @@ def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | Non
             t2 = time.perf_counter()
             timer.add("forward", t2 - t1)
             H, D = _stage_statistics(xqf, wt, xr[s], wcls)
+            torch.cuda.synchronize()
+            t25 = time.perf_counter()
+            timer.add("statistics", t25 - t2)
             targets = qep_targets(H, D - H, alpha, {nm: wr[nm] for nm in names})
             torch.cuda.synchronize()
             t3 = time.perf_counter()
-            timer.add("statistics", t3 - t2)
+            timer.add("qep_targets", t3 - t25)
             _, in_seed = matrix_seeds(i, names[0], 0, names[0])
             plans = {nm: synthetic.row_plan(shapes[nm][0], plan_seed + 10 * i + STAGE_INDEX[nm]) for nm in names}
             # a stage whose statistics the damping of the reference's Environment cannot make positive definite (float32

@@ -128,6 +128,31 @@ def test_trailing_update_matches_oracle_order(E, m, n, b0, b1):
     assert err < 1e-14
 
 
+@pytest.mark.parametrize("M,N,K,transb,tri", [(1500, 1700, 1700, True, 1), (1500, 1700, 1700, False, 2),
+                                               (1300, 2000, 900, False, 0), (200, 300, 300, True, 1),
+                                               (200, 300, 300, False, 2)])
+def test_gemm_sub_triangular(E, M, N, K, transb, tri):
+    """C -= A op(B) with op(B) triangular (tri 1: lower, the QEP's Z U^T; tri 2: upper, the QEP's P U): the 128-tile
+    kernel skips the zero stages, the 64-tile kernel reads them; against a float64 product on the GPU."""
+    g = torch.Generator(device="cuda").manual_seed(M + N + K + tri)
+    C = torch.randn(M, N, generator=g, device="cuda", dtype=torch.float64)
+    A = torch.randn(M, K, generator=g, device="cuda", dtype=torch.float64)
+    Bm = torch.randn(N, K, generator=g, device="cuda", dtype=torch.float64) if transb else \
+        torch.randn(K, N, generator=g, device="cuda", dtype=torch.float64)
+    opB = Bm.T if transb else Bm
+    if tri == 1:
+        opB = torch.tril(opB)
+    elif tri == 2:
+        opB = torch.triu(opB)
+    Bm = (opB.T if transb else opB).contiguous()
+    ref = C - A @ opB
+    say(f"gemm_sub M={M} N={N} K={K} transb={transb} tri={tri}")
+    got = E.gemm_sub(C.clone(), A, Bm, transb=transb, tri=tri)
+    err = ((got - ref).abs().max() / ref.abs().max()).item()
+    say(f"  max relative difference {err:.3e}")
+    assert err < 1e-13
+
+
 @pytest.mark.parametrize("n", [16, 64, 100, 200, 960, 2500])
 def test_chol_inv_upper(E, n):
     rng = np.random.default_rng(n)
