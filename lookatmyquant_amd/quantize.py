@@ -236,29 +236,45 @@ def stage_statistics(Xq_chunks, w_chunks=None, Xr_chunks=None):
 # ----------------------------------------------------------------------------- the batched stage path
 
 
+def stage_factor(H: torch.Tensor, in_seed: int, damp: float = 0.01):
+    """The stage's factor as quantize_stage_row_groups makes it: (U, dead, info) of the rotated, damped H (no host
+    synchronisation: info is a device value, 0 when positive definite)."""
+    dev = E._abi.device()
+    Hr = E.rotate_hessian(torch.as_tensor(H).to(dev, torch.float64).contiguous(), in_seed)
+    _, U, dead, info = E.chol_inv_upper(Hr, damp=damp, raise_on_fail=False)
+    return U, dead, info
+
+
 def quantize_stage_row_groups(targets: dict, groups: dict, H: torch.Tensor, in_seed: int, L: int = 12,
                               width: int = 16, look: int = 8, tables: dict | None = None, events: dict | None = None,
-                              chol_events: tuple | None = None, damp: float = 0.01):
+                              chol_events: tuple | None = None, damp: float = 0.01, factor: tuple | None = None):
     """Every matrix of a stage, row group by row group, with the row trellis at the group's width: the same result
     as quantize_row_groups(target, groups, round_group) with round_group = the tr<bits> word of (target[rows], H,
     in_seed, out_rot=False), for each matrix. targets: {name: W [m, n]}; groups: {name: [{"rows", "bits"}]};
     tables: {bits: float64 table} (default: the cached L = 12 tables). Returns {name: (states int32 [m, n] on the
     GPU, S float64 [m] on the GPU)}; the codes entries and reconstructions follow from them. events / chol_events
     ((dict, key)): torch.cuda.Event pairs around the sweep kernels / the factorization, for timing. damp: the
-    Environment's damping fraction (frame.py:521)."""
+    Environment's damping fraction (frame.py:521). factor: stage_factor(H, in_seed, damp), if the caller has made it
+    already (for instance on another stream, next to other work); a non-positive-definite factor raises."""
     dev = E._abi.device()
     names = list(targets)
-    Hr = E.rotate_hessian(torch.as_tensor(H).to(dev, torch.float64).contiguous(), in_seed)
-    ev = None
-    if chol_events is not None:
-        ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-        ev[0].record()
-    _, U, dead, info = E.chol_inv_upper(Hr, damp=damp, raise_on_fail=chol_events is None)
-    if ev is not None:
-        ev[1].record()
-        chol_events[0].setdefault(chol_events[1], []).append(ev)
+    if factor is not None:
+        U, dead, info = factor
         if int(info.item()):
             raise E.LinAlgError(f"linalg.cholesky: the leading minor of order {int(info.item())} is not positive-definite")
+    else:
+        Hr = E.rotate_hessian(torch.as_tensor(H).to(dev, torch.float64).contiguous(), in_seed)
+        ev = None
+        if chol_events is not None:
+            ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            ev[0].record()
+        _, U, dead, info = E.chol_inv_upper(Hr, damp=damp, raise_on_fail=chol_events is None)
+        if ev is not None:
+            ev[1].record()
+            chol_events[0].setdefault(chol_events[1], []).append(ev)
+            if int(info.item()):
+                raise E.LinAlgError(f"linalg.cholesky: the leading minor of order {int(info.item())} is not "
+                                    "positive-definite")
     X_all, S_all = {}, {}
     for nm in names:
         W = torch.as_tensor(targets[nm]).to(dev, torch.float64).contiguous()

@@ -24,7 +24,7 @@ import torch
 
 from . import engine as E
 from . import synthetic
-from .quantize import matrix_seeds, qep_targets, quantize_stage_row_groups
+from .quantize import matrix_seeds, qep_targets, quantize_stage_row_groups, stage_factor
 from .tables import load_table, quantile_table
 
 
@@ -168,6 +168,8 @@ def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | Non
     also return their stages' inputs and statistics under "stages" (for tests: {(i, s): (X_q, X_ref, H, D,
     {name: W*}, in_seed, plans)}, on the CPU)."""
     dev = E._abi.device()
+    main = torch.cuda.current_stream(dev)
+    side = torch.cuda.Stream(dev)  # default priority
     S_, T = tokens.shape
     nl = sh.layers if layers is None else layers
     timer = timer or Timer()
@@ -226,18 +228,27 @@ def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | Non
             torch.cuda.synchronize()
             t25 = time.perf_counter()
             timer.add("statistics", t25 - t2)
+            _, in_seed = matrix_seeds(i, names[0], 0, names[0])
+            # the stage's factor (rotation of H, damped inverse factor) on a second stream, next to the QEP targets
+            # (their own factor of H + lambda I and products) on this one: the two are independent
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                factor = stage_factor(H, in_seed, 0.01)
             targets = qep_targets(H, D - H, alpha, {nm: wr[nm] for nm in names})
+            main.wait_stream(side)
+            for t in factor:
+                t.record_stream(main)
             torch.cuda.synchronize()
             t3 = time.perf_counter()
             timer.add("qep_targets", t3 - t25)
-            _, in_seed = matrix_seeds(i, names[0], 0, names[0])
             plans = {nm: synthetic.row_plan(shapes[nm][0], plan_seed + 10 * i + STAGE_INDEX[nm]) for nm in names}
             # a stage whose statistics the damping of the reference's Environment cannot make positive definite (float32
             # sums of a nearly singular H, as the o_proj input of a random-initialised stack with near-uniform
             # attention gives) is damped more, as ldlq_gpu.ldlq_factor does (ldlq_gpu.py:19-23), and counted
             for d in (0.01, 0.1, 1.0):
                 try:
-                    res = quantize_stage_row_groups(targets, plans, H, in_seed, L=L, tables=tables, damp=d)
+                    res = quantize_stage_row_groups(targets, plans, H, in_seed, L=L, tables=tables, damp=d,
+                                                    factor=factor if d == 0.01 else None)
                     break
                 except E.LinAlgError:
                     if d == 1.0:
