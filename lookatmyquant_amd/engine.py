@@ -363,16 +363,29 @@ def _tiled(X: torch.Tensor) -> bool:
     return n % 8 == 0 and ld(X) % 8 == 0 and X.data_ptr() % 16 == 0
 
 
+_CLASS_CACHE: dict = {}
+
+
 def weight_classes(w: torch.Tensor, include_zero: bool = False):
     """[(weight, int32 row indices)] for the distinct values of w (the zero class only with include_zero) when there
-    are at most MAX_WEIGHT_CLASSES of them (one host synchronisation), else None."""
+    are at most MAX_WEIGHT_CLASSES of them, else None. Finding them synchronises with the host, so the last few
+    results are kept, keyed by the tensor's storage, shape and version counter (an in-place change of w bumps the
+    version)."""
+    key = (w.data_ptr(), tuple(w.shape), w.dtype, str(w.device), w._version, include_zero)
+    hit = _CLASS_CACHE.get(key)
+    if hit is not None and hit[0] is w:
+        return hit[1]
     vals = torch.unique(w)
     if vals.numel() > MAX_WEIGHT_CLASSES:
-        return None
-    out = []
-    for v in vals.cpu().tolist():
-        if v != 0.0 or include_zero:
-            out.append((v, (w == v).nonzero().flatten().to(torch.int32)))
+        out = None
+    else:
+        out = []
+        for v in vals.cpu().tolist():
+            if v != 0.0 or include_zero:
+                out.append((v, (w == v).nonzero().flatten().to(torch.int32)))
+    if len(_CLASS_CACHE) >= 16:
+        _CLASS_CACHE.pop(next(iter(_CLASS_CACHE)))
+    _CLASS_CACHE[key] = (w, out)
     return out
 
 
