@@ -235,10 +235,30 @@ int lamq_kl_rows(const uint16_t* ref, const uint16_t* q, int64_t T, int64_t V, i
  *   packed little-endian, k uint32 words per 32 symbols.
  *   states [m, n] int32 (row stride lds);  codes [m, ceil(n/32)*k] uint32 (row stride ldc)
  *   bad    [1] int32 device output, set to 1 if any row is not a trellis path from state 0
- *          (the reference raises ValueError); must be zero on entry. 1 <= k <= 4, k < L <= 16.
+ *          (the reference raises ValueError); must be zero on entry. 1 <= k <= 8, k < L <= 16.
  * ---------------------------------------------------------------------------------------------- */
 int lamq_pack_trellis(const int32_t* states, int64_t m, int64_t n, int64_t lds, int k, int L, uint32_t* codes,
                       int64_t ldc, int32_t* bad, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Pack one row group of a matrix's code array into the opgraph-packed-1 bitstream, reading the group's rows in
+ * place. Replaces compiler_artifact.py:225-240 (pack_symbols), :261-284 (valid_path, pack_trellis) and the
+ * per-group slicing and checks of encode_entry (:328-353: encoded[rows] - table_index * 4096, "a row crosses
+ * table identities", "scalar index outside table").
+ *   src    [src_rows, n] int32 (row stride ld >= n): the matrix's codes (trellis states or scalar symbols)
+ *   rows   [m] int64 indices into src (NULL: rows 0..m-1); a row outside [0, src_rows) sets bad bit 2 and
+ *          its code words to zero, nothing is read for it
+ *   base   subtracted from every entry (the group's table offset, table_index * 2^L)
+ *   trellis = 1: entries are row-trellis states; symbols state & (2^k - 1), each row padded forward to a
+ *          multiple of 32 and reversed; bad bit 1 if a row, after base, is not a path from state 0 in
+ *          [0, 2^L). 1 <= k < L <= 16.
+ *   trellis = 0: entries are scalar symbols packed in column order; bad bit 1 if one is outside [0, 2^k).
+ *   codes  [m, ceil(n/32)*k] uint32 (row stride ldc);  1 <= k <= 8
+ *   bad    [1] int32 device flags (must be zero on entry; the reference raises ValueError)
+ * lamq_pack_trellis(states, m, n, lds, k, L, ...) is lamq_pack_codes(states, lds, m, NULL, m, n, 0, k, L, 1, ...).
+ * ---------------------------------------------------------------------------------------------- */
+int lamq_pack_codes(const int32_t* src, int64_t ld, int64_t src_rows, const int64_t* rows, int64_t m, int64_t n,
+                    int32_t base, int k, int L, int trellis, uint32_t* codes, int64_t ldc, int32_t* bad, void* stream);
 
 #ifdef __cplusplus
 }

@@ -511,3 +511,28 @@ def pack_trellis(states: torch.Tensor, k: int, L: int = 12, check_paths: bool = 
     if int(bad.item()):
         raise ValueError("states are not a row trellis from zero")
     return codes
+
+
+def pack_codes(src: torch.Tensor, k: int, rows: torch.Tensor | None = None, base: int = 0, L: int = 12,
+               trellis: bool = True, out: torch.Tensor | None = None, bad: torch.Tensor | None = None):
+    """The code words [m, ceil(n/32)*k] (an int32 tensor holding uint32 bits) of rows `rows` (int64 on the device,
+    None for all rows) of the int32 code array src, minus `base`: row-trellis states (trellis) or scalar symbols.
+    Returns (codes, bad): bad an int32 device flag, nonzero if a row was not a path from state 0 (or a symbol was
+    outside [0, 2^k)). Several calls may share one `bad` flag; nothing synchronises."""
+    need(src, torch.int32, "src", 2)
+    nsrc, n = src.shape
+    if rows is not None:
+        if rows.dtype != torch.int64 or rows.device != src.device or rows.dim() != 1:
+            raise ValueError("rows must be a 1-d int64 tensor on the device of src")
+        rows = rows.contiguous()
+    m = nsrc if rows is None else rows.shape[0]
+    words = (n + 31) // 32 * k
+    if out is None:
+        out = torch.empty(m, words, dtype=torch.int32, device=src.device)
+    elif out.shape != (m, words) or out.dtype != torch.int32 or out.stride(1) != 1:
+        raise ValueError("out must be an int32 [m, ceil(n/32)*k] tensor with unit column stride")
+    if bad is None:
+        bad = torch.zeros(1, dtype=torch.int32, device=src.device)
+    check(lib().lamq_pack_codes(ptr(src), ld(src), nsrc, ptr(rows), m, n, int(base), k, L, 1 if trellis else 0, ptr(out),
+                                out.stride(0), ptr(bad), stream(src.device)), "pack_codes")
+    return out, bad

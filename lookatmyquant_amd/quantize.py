@@ -23,6 +23,7 @@ from __future__ import annotations
 import re
 import zlib
 
+import numpy as np
 import torch
 
 from . import codes as C
@@ -290,7 +291,10 @@ def quantize_stage_row_groups(targets: dict, groups: dict, H: torch.Tensor, in_s
     idx, sweep_groups = [], []
     for bits, parts in sorted(by_bits.items()):
         table = (tables or {}).get(bits)
-        table = torch.from_numpy(C.load_table(12, bits).copy()) if table is None else torch.as_tensor(table, dtype=torch.float64)
+        if table is None:
+            table = C.load_table(12, bits)
+        table = table if isinstance(table, torch.Tensor) else torch.from_numpy(np.array(table, dtype=np.float64))
+        table = table.to(torch.float64)
         rows = 0
         for nm, r in parts:
             idx.append((nm, r.to(dev)))

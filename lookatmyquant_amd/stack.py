@@ -22,6 +22,7 @@ from dataclasses import dataclass
 import numpy as np
 import torch
 
+from . import artifact
 from . import engine as E
 from . import synthetic
 from .quantize import matrix_seeds, qep_targets, quantize_stage_row_groups, stage_factor
@@ -163,8 +164,11 @@ def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | Non
           timer: Timer | None = None, keep: int = 0) -> dict:
     """The build of a random-initialised stack on calibration token ids [S, T]: per layer and stage, the two streams'
     statistics, the QEP target, the row-group trellis codes (a 2.3 bpw row plan per matrix, bits 1-4) and the
-    quantized weights written back. Returns {"codes": {"i.name": [(group, states, scales, packed)]}, "weights": n,
-    "bits": total rate bits, "redamped": {"i.first matrix": damping} for stages that needed more than 0.01}. token_w: per-token weights [S, T] (mean 1), or None. keep: the first `keep` layers
+    quantized weights written back. Returns {"codes": {"i.name": {"states": int32 [m, n], "scales": float64 [m],
+    "in_seed", "groups": the row plan, "packed": per group the code words (engine.pack_codes, read in place)}},
+    "weights": n, "bits": total rate bits, "redamped": {"i.first matrix": damping} for stages that needed more than
+    0.01, "bad": a device flag set if any packed row was not a trellis path, "L", "tables"}; export_codes writes the
+    codes as an opgraph-packed-1 artifact. token_w: per-token weights [S, T] (mean 1), or None. keep: the first `keep` layers
     also return their stages' inputs and statistics under "stages" (for tests: {(i, s): (X_q, X_ref, H, D,
     {name: W*}, in_seed, plans)}, on the CPU)."""
     dev = E._abi.device()
@@ -185,6 +189,7 @@ def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | Non
     hr = [h.clone() for h in hq]
     del emb
     codes, n_w, bits, kept, redamped = {}, 0, 0.0, {}, {}
+    bad = torch.zeros(1, dtype=torch.int32, device=dev)  # set if any packed row is not a trellis path from state 0
     shapes = matrix_shapes(sh)
     for i in range(nl):
         t0 = time.perf_counter()
@@ -259,13 +264,13 @@ def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | Non
                                 {nm: t.cpu() for nm, t in targets.items()}, in_seed, plans)
             for nm, (st, Srow) in res.items():
                 wq[nm] = _reconstruct(st, Srow, plans[nm], tables, in_seed).to(torch.bfloat16)
-                ent = []
+                packed = []
                 for gp in plans[nm]:
-                    rows = torch.as_tensor(gp["rows"], device=dev)
-                    packed = E.pack_trellis(st.index_select(0, rows).contiguous(), gp["bits"], L, check_paths=False)
-                    ent.append((gp, st.index_select(0, rows), Srow.index_select(0, rows).float(), packed))
+                    rows = torch.as_tensor(gp["rows"], dtype=torch.int64, device=dev)
+                    packed.append(E.pack_codes(st, gp["bits"], rows=rows, L=L, bad=bad)[0])
                     bits += len(gp["rows"]) * shapes[nm][1] * gp["bits"] + 16 * len(gp["rows"])
-                codes[f"{i}.{nm}"] = ent
+                codes[f"{i}.{nm}"] = {"states": st, "scales": Srow, "in_seed": in_seed, "groups": plans[nm],
+                                      "packed": packed}
                 n_w += shapes[nm][0] * shapes[nm][1]
             torch.cuda.synchronize()
             timer.add("quantize", time.perf_counter() - t3)
@@ -278,10 +283,34 @@ def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | Non
         del xr, wr, wq, h1q, x2q
         torch.cuda.synchronize()
         timer.add("forward", time.perf_counter() - t4)
-    return {"codes": codes, "weights": n_w, "bits": bits, "stages": kept, "redamped": redamped}
+    return {"codes": codes, "weights": n_w, "bits": bits, "stages": kept, "redamped": redamped, "bad": bad, "L": L,
+            "tables": tables}
 
 
 STAGE_INDEX = {nm: j for j, nm in enumerate(n for st in STAGES for n in st)}
+
+
+def export_codes(out: dict, path) -> dict:
+    """The build's codes as an opgraph-packed-1 artifact at `path` (compiler_artifact.py:307-371, 491-531): per
+    matrix model.layers.{i}.{name}.weight, its row groups in plan order with the words packed during the build, fp32
+    row scales, the stage rotation's signs and each group's fp32 table; semantic metadata {"matrices": ...} only
+    (the random-initialised stack has no dense state to store). Returns write_artifact's receipt."""
+    if out["L"] != artifact.STATE_BITS:
+        raise ValueError("opgraph-packed-1 stores 12-bit trellis states")
+    if int(out["bad"].item()):
+        raise ValueError("states are not a row trellis from zero")
+    tables = {b: np.asarray(t, dtype=np.float64).astype(np.float32) for b, t in out["tables"].items()}
+    tensors, matrices = {}, {}
+    for key, rec in out["codes"].items():
+        i, nm = key.split(".", 1)
+        name = f"model.layers.{i}.{nm}.weight"
+        m, n = rec["states"].shape
+        groups = [(np.asarray(gp["rows"], dtype=np.int64), int(gp["bits"]), "trellis", tables[int(gp["bits"])], words)
+                  for gp, words in zip(rec["groups"], rec["packed"])]
+        t, matrices[name] = artifact.encode_groups(name, (m, n), groups, rec["scales"].float().cpu().numpy(),
+                                                   artifact._input_signs(n, rec["in_seed"]))
+        tensors.update(t)
+    return artifact.write_artifact(path, tensors, {"matrices": matrices})
 
 
 def _stage_statistics(xq: list, w: list | None, xr: list, classes: list | None = None):

@@ -164,6 +164,144 @@ def test_artifact_packing(golden):
         assert np.array_equal(artifact.unpack_trellis(codes, bits, st.shape[1]), st)
 
 
+def _golden_artifact_inputs():
+    """The saved codes and state dict the reference's golden artifacts were exported from (the golden script's own
+    construction, over its committed arrays)."""
+    import importlib.util
+
+    from conftest import GOLDEN
+
+    spec = importlib.util.spec_from_file_location("make_artifact_golden", GOLDEN / "make_artifact_golden.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    a = dict(np.load(GOLDEN / "artifact_inputs.npz"))
+    return mod.saved_and_state(a, torch)
+
+
+def _same_files(a, b):
+    names = sorted(p.name for p in a.iterdir())
+    assert names == sorted(p.name for p in b.iterdir())
+    for n in names:
+        assert (a / n).read_bytes() == (b / n).read_bytes(), n
+
+
+def test_export_saved_codes_matches_the_reference_artifact(tmp_path):
+    """export_saved_codes over the golden saved codes (explicit row groups, inferred widths, scalar codes, embedding
+    buckets, a tied head, bf16/f16/i64/empty state, model assets): artifact.json and weights.bin equal the files the
+    reference wrote, byte for byte, and so does the receipt."""
+    import json
+
+    from conftest import GOLDEN
+    from lookatmyquant_amd import artifact
+
+    saved, state, alias = _golden_artifact_inputs()
+    receipts = json.loads((GOLDEN / "artifact_receipts.json").read_text())
+    say("export_saved_codes of the golden saved codes")
+    r = artifact.export_saved_codes(saved, tmp_path / "x", dense_tensors=state, model_dir=GOLDEN / "artifact_model")
+    _same_files(tmp_path / "x", GOLDEN / "artifact_export")
+    assert {k: v for k, v in r.items() if k != "path"} == receipts["export"]
+    say("encode_entry + write_artifact with shared tables")
+    tensors, meta = artifact.encode_entry("m.weight", alias)
+    semantic = {"matrices": {"m.weight": meta}}
+    r = artifact.write_artifact(tmp_path / "y", tensors, semantic,
+                                tensor_aliases=artifact.find_table_aliases(tensors, semantic))
+    _same_files(tmp_path / "y", GOLDEN / "artifact_alias")
+    assert {k: v for k, v in r.items() if k != "path"} == receipts["alias"]
+
+
+def test_encode_entry_rejects_what_the_reference_rejects():
+    from lookatmyquant_amd import artifact
+
+    saved, _, alias = _golden_artifact_inputs()
+    up = saved["matrices"]["model.layers.0.mlp.up_proj.weight"]
+
+    def variant(**kw):
+        e = dict(up)
+        e.update(kw)
+        return e
+
+    cases = []
+    st = up["states"].clone()
+    st[5, 9] = (int(st[5, 9]) & ~0xFFF) | ((int(st[5, 9]) + 1) & 0xFFF)  # a broken transition inside a row
+    cases.append((variant(states=st), "states are not a row trellis from zero"))
+    st = up["states"].clone()
+    r0 = int(up["row_groups"][0]["rows"][0])
+    st[r0, 3] += 4096  # one state in another table
+    cases.append((variant(states=st), "a row crosses table identities"))
+    st = up["states"].clone()
+    st[0, 0] = 3 * 4096  # beyond the concatenated tables
+    cases.append((variant(states=st), "invalid saved trellis table or states"))
+    groups = [dict(g) for g in up["row_groups"]]
+    groups[0] = dict(groups[0], table_index=1)
+    cases.append((variant(row_groups=groups), "invalid row group"))
+    groups = [dict(g) for g in up["row_groups"]][:2]
+    cases.append((variant(row_groups=groups), "row groups must cover every row exactly once"))
+    cases.append((variant(scales=up["scales"].double()), "saved row scales must be fp32"))
+    cases.append((variant(table=up["table"][:-1]), "invalid saved trellis table or states"))
+    cases.append((variant(log_g=0), "unsupported trained transforms"))
+    cases.append((variant(states=up["states"].float()), "saved entry must be a matrix"))
+    o = saved["matrices"]["model.layers.0.self_attn.o_proj.weight"]
+    codes = o["codes"].clone()
+    codes[3, 4] = 8
+    cases.append((dict(o, codes=codes), "scalar index outside table"))
+    for i, (entry, msg) in enumerate(cases):
+        say(f"encode_entry error case {i}: {msg}")
+        with pytest.raises(ValueError, match=msg):
+            artifact.encode_entry("x", entry)
+    with pytest.raises(ValueError, match="invalid input signs"):
+        artifact.encode_entry("x", up, signs=np.zeros(70, dtype=np.int8))
+
+
+@pytest.mark.parametrize("n", [1, 31, 32, 33, 70, 129])
+def test_pack_widths_and_layouts_match_the_oracle(n):
+    """pack_symbols and pack_trellis at every width 1..8 against the oracle's bit-by-bit restatement; pack_codes
+    reading a row group in place (rows gathered, a table offset subtracted) against the same rows packed alone."""
+    from lookatmyquant_amd import artifact
+    from lookatmyquant_amd import engine as E
+
+    rng = np.random.default_rng(100 + n)
+    m = 37
+    for bits in range(1, 9):
+        say(f"pack n={n} bits={bits}")
+        q = rng.integers(0, 1 << bits, (m, n))
+        assert np.array_equal(artifact.pack_symbols(q, bits), O.pack_symbols(q, bits))
+        st = np.zeros((m, n), dtype=np.int64)
+        s = np.zeros(m, dtype=np.int64)
+        for c in range(n):
+            s = ((s << bits) | rng.integers(0, 1 << bits, m)) & 4095
+            st[:, c] = s
+        words = artifact.pack_trellis(st, bits)
+        assert np.array_equal(words, O.pack_trellis(st, bits))
+        if n >= 32:  # long random paths are paths at one width only
+            assert artifact.infer_path_bits(st) == bits
+        # in place: every other row of a matrix whose states carry the offset 4096 * 2
+        big = np.zeros((2 * m, n), dtype=np.int64)
+        big[1::2] = st + 8192
+        rows = torch.arange(1, 2 * m, 2, device="cuda")
+        codes, bad = E.pack_codes(torch.from_numpy(big).int().cuda(), bits, rows=rows, base=8192, L=12)
+        assert int(bad.item()) == 0
+        assert np.array_equal(codes.cpu().numpy().view(np.uint32), words)
+        if n > 1:
+            bad_st = st.copy()
+            bad_st[m // 2, n // 2] ^= 1 << 11  # a high bit that no shift produced
+            if not artifact.valid_path(bad_st, bits):
+                with pytest.raises(ValueError, match="not a row trellis"):
+                    artifact.pack_trellis(bad_st, bits)
+        with pytest.raises(ValueError, match="invalid symbols or width"):
+            artifact.pack_symbols(np.full((2, n), 1 << bits), bits)
+
+
+def test_pack_codes_flags_rows_outside_the_source():
+    """A row index outside the code array is caught by the kernel's own bounds check: flagged, words zero, no read."""
+    from lookatmyquant_amd import engine as E
+
+    src = torch.zeros(4, 40, dtype=torch.int32, device="cuda")
+    rows = torch.tensor([0, 4, -1, 3], dtype=torch.int64, device="cuda")
+    codes, bad = E.pack_codes(src, 2, rows=rows)
+    assert int(bad.item()) == 2
+    assert int(codes.abs().sum().item()) == 0
+
+
 def test_environment_and_covariance(config12):
     from lookatmyquant_amd import synthetic
     from lookatmyquant_amd.frame import Environment, covariance

@@ -18,7 +18,7 @@ def say(*a):
     sys.stdout.flush()
 
 
-def test_small_stack_build():
+def test_small_stack_build(tmp_path):
     from lookatmyquant_amd import stack
     from lookatmyquant_amd.tables import load_table
 
@@ -30,9 +30,9 @@ def test_small_stack_build():
     shapes = stack.matrix_shapes(sh)
     assert out["weights"] == 2 * sum(m * n for m, n in shapes.values())
     assert 1.0 < out["bits"] / out["weights"] < 4.1
-    for key, ent in out["codes"].items():
-        assert sum(len(g["rows"]) for g, _, _, _ in ent) == shapes[key.split(".", 1)[1]][0]
-        assert all(int(p[1].item()) == 0 for _, _, _, p in ent)  # every row a trellis path from state 0
+    assert int(out["bad"].item()) == 0  # every packed row a trellis path from state 0
+    for key, rec in out["codes"].items():
+        assert sorted(r for g in rec["groups"] for r in g["rows"]) == list(range(shapes[key.split(".", 1)[1]][0]))
     tables = {b: np.array(load_table(12, b)) for b in (1, 2, 3, 4)}
     wn = np.asarray(w, dtype=np.float64).reshape(-1)
     for (i, s), (Xq, Xr, H, D, targets, in_seed, plans) in out["stages"].items():
@@ -55,15 +55,35 @@ def test_small_stack_build():
                 assert np.abs(target - Wn).max() < 1e-3 * np.abs(Wn).max()
             elif s == 1:  # the o_proj input already sees the quantized q/k/v
                 assert np.abs(target - Wn).max() > 1e-3 * np.abs(Wn).max()
-            states = torch.cat([st for g, st, _, _ in out["codes"][f"{i}.{nm}"]]).cpu().numpy()
-            rows_all = np.concatenate([np.asarray(g["rows"]) for g in groups])
-            by_row = dict(zip(rows_all.tolist(), range(len(rows_all))))
+            states = out["codes"][f"{i}.{nm}"]["states"].cpu().numpy()
             for g in groups[:2]:
                 rows = np.asarray(g["rows"])[:32]
                 ref, _, _ = O.ldlq_words_trellis(target[rows], H.numpy(), tables[g["bits"]], 12, g["bits"], in_seed)
-                got = states[[by_row[r] for r in rows.tolist()]]
                 say(f"layer {i} stage {s} {nm} group {g['group']} bits {g['bits']}")
-                assert np.array_equal(got, ref)
+                assert np.array_equal(states[rows], ref)
+    # the packed codes out: an opgraph-packed-1 artifact whose groups unpack to the build's states, row for row, and
+    # whose words are the oracle's packing of those states
+    from lookatmyquant_amd import artifact
+
+    say("export_codes")
+    receipt = stack.export_codes(out, tmp_path / "artifact")
+    assert receipt["all_tensor_bytes_verified"]
+    stored, meta = artifact.read_artifact(tmp_path / "artifact")
+    assert len(meta["matrices"]) == len(out["codes"])
+    for key, rec in out["codes"].items():
+        i, nm = key.split(".", 1)
+        name = f"model.layers.{i}.{nm}.weight"
+        states = rec["states"].cpu().numpy()
+        n = states.shape[1]
+        assert np.array_equal(stored[name + ".signs"], O.rht_signs(n, rec["in_seed"]).astype(np.int8))
+        for j, g in enumerate(rec["groups"]):
+            k = f"{name}.g{j}"
+            rows = stored[k + ".rows"].astype(np.int64)
+            assert np.array_equal(rows, np.asarray(g["rows"]))
+            assert np.array_equal(O.unpack_trellis(stored[k + ".codes"], g["bits"], n), states[rows])
+            if j == 0:
+                assert np.array_equal(stored[k + ".codes"][:8], O.pack_trellis(states[rows[:8]], g["bits"]))
+            assert np.array_equal(stored[k + ".scales"], rec["scales"].float().cpu().numpy()[rows])
 
 
 @pytest.mark.gpu

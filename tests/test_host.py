@@ -55,6 +55,12 @@ def test_argument_errors_are_reported_without_a_gpu():
                                      8, ptr(p), 8, None) == -2
     # a trellis width the kernels are not built for
     assert L.lamq_viterbi_rows(ptr(p), 1, 4, 4, ptr(p), 12, 7, None, ptr(q), 4, None, 0, None) == -2
+    # packing: widths beyond 8, a trellis no wider than its symbols, too few code words, more rows than the source
+    assert L.lamq_pack_codes(ptr(q), 8, 8, None, 8, 8, 0, 9, 12, 1, ptr(q), 8, ptr(q), None) == -1
+    assert L.lamq_pack_codes(ptr(q), 8, 8, None, 8, 8, 0, 4, 4, 1, ptr(q), 8, ptr(q), None) == -1
+    assert L.lamq_pack_codes(ptr(q), 8, 8, None, 8, 8, 0, 4, 12, 0, ptr(q), 3, ptr(q), None) == -1
+    assert L.lamq_pack_codes(ptr(q), 8, 4, None, 8, 8, 0, 2, 12, 1, ptr(q), 8, ptr(q), None) == -1
+    assert L.lamq_pack_codes(None, 8, 8, None, 8, 8, 0, 2, 12, 1, ptr(q), 8, ptr(q), None) == -1
     assert L.lamq_chol_inv_upper_workspace_size(10) >= 800
     assert L.lamq_viterbi_workspace_size(3, 100, 12, 2) == 3 * 100 * 256
 
