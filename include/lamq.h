@@ -114,7 +114,8 @@ int lamq_trailing_update_f64(double* T, int64_t m, int64_t n, int64_t ldT, const
 /* C [M, N] -= A [M, K] @ op(B) in fp64 (op(B) = B [K, N], or B^T for B [N, K] when transb), with op(B) optionally
  * triangular: tri = 1 when op(B)[k][j] = 0 for k < j, tri = 2 when op(B)[k][j] = 0 for k > j (the zero part is then
  * skipped, not read). The products of the QEP targets with the inverse factor, (H + lambda I)^-1 = U^T U
- * (quantize.py:1330-1335, 1503): W D U^T U as two triangular products. */
+ * (quantize.py:1330-1335, 1503): W D U^T U as two triangular products. Also the noise of compiler.py:124
+ * (ldlq_noise's triangular solve E A = eta diag(A), as the product (eta diag(A)) U with U = A^-1). */
 int lamq_gemm_sub_f64(double* C, int64_t ldc, const double* A, int64_t lda, const double* B, int64_t ldb, int64_t M,
                       int64_t N, int64_t K, int transb, int tri, void* stream);
 

@@ -20,6 +20,8 @@ Parity status of each function (what pins it is listed in the test named beside 
   kl_rows            fp64 closed form; KL(p||p) = 0; Gaussian-logit closed form
   lloyd_max          Max (1960) MSE table; GAUSS2 levels; reference vectors
   pack_symbols etc.  round trip and the reference's byte layout spelled out bit by bit
+  ldlq_noise         A A^T = Hr with A upper; tr(E_r Hr E_r^T) = sum diag(A)^2 eta^2 (QuIP Theorem 1's identity);
+                     E_r A = eta diag(A) exactly; zero noise gives W
 """
 
 from __future__ import annotations
@@ -440,6 +442,31 @@ def unpack_trellis(codes, bits: int, columns: int, state_bits: int = 12) -> np.n
         state = ((state << bits) | sym[:, i]) & ((1 << state_bits) - 1)
         out[:, i] = state
     return out
+
+
+# ----------------------------------------------------------------------------- LDLQ-shaped noise (compiler.py:110-129)
+
+
+def ldlq_noise(W, H, d: float, seed: int, eta_unit, row_rotation: bool = True):
+    """(W + E, E_r, A) of compiler.ldlq_noise: Wr = Ro W Ri^T (Ri = rht(n, seed+1), Ro = rht(m, seed)),
+    Hr = Ri H Ri^T + 0.01 mean(diag) I = A A^T with A upper triangular (the flipped lower Cholesky factor of the
+    flipped Hr), eta = eta_unit * RMS(Wr rows) * sqrt(d) (eta_unit: the standard normal draw), E_r A = eta diag(A) by
+    a triangular solve, E = Ro^T E_r Ri. LAPACK (numpy cholesky, scipy solve_triangular) in float64."""
+    from scipy.linalg import solve_triangular
+
+    W = np.asarray(W, dtype=np.float64)
+    m, n = W.shape
+    Ri = rht(n, seed + 1)
+    Ro = rht(m, seed) if row_rotation else None
+    Wr = Ro @ W @ Ri.T if row_rotation else W @ Ri.T
+    Hr = Ri @ np.asarray(H, dtype=np.float64) @ Ri.T
+    Hr = Hr + 0.01 * np.mean(np.diag(Hr)) * np.eye(n)
+    A = np.linalg.cholesky(Hr[::-1, ::-1])[::-1, ::-1]
+    S = np.sqrt(np.mean(Wr ** 2, axis=1, keepdims=True))
+    eta = np.asarray(eta_unit, dtype=np.float64) * S * d ** 0.5
+    Er = solve_triangular(A.T, (eta * np.diag(A)[None, :]).T, lower=True).T  # E_r A = eta diag(A)
+    E = Ro.T @ Er @ Ri if row_rotation else Er @ Ri
+    return W + E, Er, A
 
 
 # ----------------------------------------------------------------------------- end-to-end words

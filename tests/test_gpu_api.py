@@ -441,3 +441,120 @@ def test_error_paths():
                      C.RowTrellisCode(12, 2, width=16, look=20), [1], in_seed=2, out_rot=False)
     with pytest.raises(NotImplementedError):  # a 16-bit table that fp16 cannot hold
         C.viterbi(torch.zeros(2, 4), torch.randn(1 << 16, dtype=torch.float64), 16, 2)
+
+
+def test_ldlq_noise_matches_the_oracle():
+    """compiler.ldlq_noise against oracle.ldlq_noise on the same CPU-generator draw: rotations, damped factor and the
+    triangular product agree to float64 rounding; with and without the output rotation."""
+    from lookatmyquant_amd import compiler
+
+    rng = np.random.default_rng(43)
+    m, n = 96, 320
+    W = rng.standard_normal((m, n))
+    X = rng.standard_normal((2000, n)) * np.linspace(0.5, 2.0, n)
+    H = X.T @ X / 2000
+    for row_rotation in (True, False):
+        say(f"ldlq_noise row_rotation={row_rotation}")
+        out = compiler.ldlq_noise(torch.from_numpy(W), torch.from_numpy(H), 0.015, 11,
+                                  torch.Generator().manual_seed(3), row_rotation=row_rotation)
+        eta = torch.randn(m, n, generator=torch.Generator().manual_seed(3), dtype=torch.float64).numpy()
+        ref, _, _ = O.ldlq_noise(W, H, 0.015, 11, eta, row_rotation=row_rotation)
+        assert out.dtype == torch.float64 and out.device.type == "cpu"
+        err = np.abs(out.numpy() - ref).max() / np.abs(ref - W).max()
+        say(f"  max |diff| / max |E| = {err:.2e}")
+        assert err < 1e-10
+
+
+def test_fast_rht_and_rotated_moment():
+    from lookatmyquant_amd.finetune_lib import FastRHT, rotated_moment
+
+    rng = np.random.default_rng(44)
+    n = 2560
+    R = FastRHT(n, 17)
+    Rn = O.rht(n, 17)
+    X = rng.standard_normal((3, 5, n)).astype(np.float32)
+    say("FastRHT back/forward")
+    Xt = torch.from_numpy(X)
+    back = R.back(Xt)
+    assert back.dtype == torch.float32 and back.shape == Xt.shape and back.device.type == "cpu"
+    ref = X.astype(np.float64) @ Rn.T
+    assert np.abs(back.numpy() - ref).max() < 1e-6 * np.abs(ref).max()
+    fwd = R.forward(back)
+    assert np.abs(fwd.numpy() - X).max() < 1e-6 * np.abs(X).max()
+    A = rng.standard_normal((n, 64))
+    H = A @ A.T / 64
+    Hr = rotated_moment(torch.from_numpy(H), R)
+    assert Hr.dtype == torch.float64 and torch.equal(Hr, Hr.T)
+    ref = Rn @ H @ Rn.T
+    assert np.abs(Hr.cpu().numpy() - ref).max() < 1e-5 * np.abs(ref).max()
+
+
+def test_rounded_matches_the_oracle(config12, tables):
+    """finetune_lib.rounded over a row plan: each group's states are the oracle's row-trellis LDLQ of the rotated rows
+    at the given scales; the refitted scale satisfies its normal equation under env.H; W_hat is the rotated-back
+    scale * table[states]; a subset of rows gives those rows' result; the generic sweep (a non-RowPath code) and the
+    fused pass agree."""
+    from lookatmyquant_amd import synthetic
+    from lookatmyquant_amd.finetune_lib import FastRHT, RowPath, rotated_moment, rounded
+    from lookatmyquant_amd.frame import Environment
+
+    W, H = config12
+    W = W[:192].astype(np.float32)
+    n = W.shape[1]
+    R = FastRHT(n, 301)
+    Hr = rotated_moment(torch.from_numpy(H), R)
+    env = Environment(Hr)
+    plan = synthetic.row_plan(192, 5, groups=3)
+    groups = [(torch.tensor(g["rows"]), g["bits"], RowPath(torch.from_numpy(tables[g["bits"]].copy()), g["bits"]))
+              for g in plan]
+    Xr = R.back(torch.from_numpy(W)).double().numpy()
+    scale0 = torch.from_numpy(np.sqrt((Xr ** 2).mean(1)).astype(np.float32))
+    scale = scale0.clone()
+    say("rounded, fused")
+    W_hat, states = rounded(torch.from_numpy(W), R, groups, scale, env)
+    assert states.dtype == torch.int16 and states.shape == W.shape
+    Hd = env.H.cpu().numpy()
+    Ud = env.U.cpu().numpy()
+    st = states.numpy().astype(np.int64)
+    for g in plan[:4]:
+        rows = np.asarray(g["rows"])
+        ref = O.ldlq_trellis(Xr[rows], Ud, scale0.numpy()[rows].astype(np.float64), tables[g["bits"]], 12, g["bits"],
+                             dead=env.dead.cpu().numpy())
+        say(f"  group bits {g['bits']} rows {len(rows)}")
+        assert np.array_equal(st[rows], ref)
+        got = tables[g["bits"]][st[rows]]
+        s = scale.numpy()[rows].astype(np.float64)
+        resid = ((Xr[rows] - s[:, None] * got) @ Hd * got).sum(1)
+        assert np.abs(resid).max() < 1e-5 * np.abs((Xr[rows] @ Hd * got).sum(1)).max()
+    Q = np.empty(W.shape)
+    for g in plan:
+        rows = np.asarray(g["rows"])
+        Q[rows] = tables[g["bits"]][st[rows]]
+    ref = (scale.numpy()[:, None] * Q.astype(np.float32)).astype(np.float64) @ O.rht(n, 301)
+    assert np.abs(W_hat.numpy() - ref).max() < 1e-5 * np.abs(ref).max()
+    say("rounded, a subset of rows")
+    sub = np.arange(0, 192, 3)
+    scale_s = scale0.clone()
+    groups_s = [(g, k, RowPath(c.values, k)) for g, k, c in groups]
+    W_s, states_s = rounded(torch.from_numpy(W), R, groups_s, scale_s, env, rows=torch.from_numpy(sub))
+    assert torch.equal(states_s, states[sub])
+    assert torch.equal(scale_s[sub], scale[sub])
+    rest = np.setdiff1d(np.arange(192), sub)
+    assert torch.equal(scale_s[rest], scale0[rest])
+    say("rounded, generic sweep")
+
+    class Generic:
+        def __init__(self, code):
+            self.code, self.width, self.look, self.paths = code, code.width, code.look, []
+
+        def step(self, j, X, ahead):
+            q = self.code.step(j, X, ahead)
+            self.paths = self.code.paths
+            return q
+
+    scale_g = scale0.clone()
+    groups_g = [(g, k, Generic(RowPath(c.values, k))) for g, k, c in groups[:2]]
+    rows_g = torch.cat([g for g, _, _ in groups[:2]])
+    _, states_g = rounded(torch.from_numpy(W), R, groups_g, scale_g, env, rows=rows_g)
+    assert torch.equal(states_g, states[rows_g])
+    assert torch.allclose(scale_g[rows_g], scale[rows_g], rtol=1e-6, atol=0)

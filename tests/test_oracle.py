@@ -362,3 +362,42 @@ def test_pack_trellis_matches_reference_bytes(golden, bits):
     bad[1, 5] ^= 1 << 11
     with pytest.raises(ValueError):
         O.pack_trellis(bad, bits)
+
+
+def test_ldlq_noise_oracle_invariants():
+    """oracle.ldlq_noise (compiler.py:110-129): A is the upper factor of the damped rotated H; the rotated error has
+    LDLQ's energy, tr(E_r H E_r^T) = sum_j A_jj^2 eta_j^2 row by row (QuIP, Theorem 1); it is causal in column order
+    (column j of E_r depends only on noise columns <= j, which fixes the triangle); the rotations are orthogonal and
+    undone exactly; zero noise gives W."""
+    import torch
+
+    rng = np.random.default_rng(41)
+    m, n = 24, 40
+    W = rng.standard_normal((m, n))
+    X = rng.standard_normal((300, n)) * np.linspace(0.5, 2.0, n)
+    H = X.T @ X / 300
+    eta = torch.randn(m, n, generator=torch.Generator().manual_seed(5), dtype=torch.float64).numpy()
+    out, Er, A = O.ldlq_noise(W, H, 0.015, 7, eta)
+    Ri, Ro = O.rht(n, 8), O.rht(m, 7)
+    Hr = Ri @ H @ Ri.T
+    Hr = Hr + 0.01 * np.mean(np.diag(Hr)) * np.eye(n)
+    assert np.allclose(np.tril(A, -1), 0) and np.all(np.diag(A) > 0)
+    assert np.abs(A @ A.T - Hr).max() < 1e-12 * np.abs(Hr).max()
+    Wr = Ro @ W @ Ri.T
+    e = eta * np.sqrt(np.mean(Wr ** 2, axis=1, keepdims=True)) * 0.015 ** 0.5
+    energy = np.einsum("ij,jk,ik->i", Er, Hr, Er)
+    assert np.abs(energy - (e ** 2 * np.diag(A) ** 2).sum(1)).max() < 1e-10 * energy.max()
+    eta2 = eta.copy()
+    eta2[:, -1] += 1.0
+    _, Er2, _ = O.ldlq_noise(W, H, 0.015, 7, eta2)
+    assert np.abs(Er2[:, :-1] - Er[:, :-1]).max() < 1e-14 and np.abs(Er2[:, -1] - Er[:, -1]).min() > 0
+    eta3 = eta.copy()
+    eta3[:, 0] += 1.0
+    _, Er3, _ = O.ldlq_noise(W, H, 0.015, 7, eta3)
+    assert np.abs(Er3[:, 1:] - Er[:, 1:]).max() > 1e-6  # the first column's noise is carried into the later ones
+    E = out - W
+    assert np.abs(Ro @ E @ Ri.T - Er).max() < 1e-12 * np.abs(Er).max()
+    back, _, _ = O.ldlq_noise(W, H, 0.0, 7, eta)
+    assert np.array_equal(back, W)
+    out_in, Er_in, _ = O.ldlq_noise(W, H, 0.015, 7, eta, row_rotation=False)
+    assert np.abs((out_in - W) @ Ri.T - Er_in).max() < 1e-12 * np.abs(Er_in).max()
