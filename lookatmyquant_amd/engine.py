@@ -166,11 +166,13 @@ def ldlq_trellis(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, table64: tor
 
 def ldlq_trellis_groups(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, groups: list, L: int, width: int = 16,
                         look: int = 8, lazy: int = 128, dead: torch.Tensor | None = None,
-                        events: dict | None = None) -> torch.Tensor:
+                        events: dict | None = None, concurrent: bool | None = None) -> torch.Tensor:
     """ldlq_trellis over consecutive row groups that share U but not the code: groups = [(rows, k, table64,
-    table32 or None)] in row order, summing to X's rows. Each lazy block runs the block kernel group by group and
-    then one trailing update over all rows (the update is row by row, so this is the same as sweeping each group
-    on its own, with fewer and larger products)."""
+    table32 or None)] in row order, summing to X's rows. Rows do not interact (the block kernel and the trailing
+    update work row by row), so each group's sweep is independent of the others: with `concurrent` (the default
+    without events) every group runs its whole sweep, block kernels and its own trailing updates, on a stream of
+    its own, and the groups' VALU-bound searches and fp64 MFMA products overlap on the chip; the results are those
+    of sweeping the groups one after the other. With events every launch is timed on the caller's stream in turn."""
     need(X, torch.float64, "X", 2)
     need(U, torch.float64, "U", 2)
     need(S, torch.float64, "S", 1)
@@ -181,10 +183,9 @@ def ldlq_trellis_groups(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, group
         raise ValueError("lazy must be a multiple of width and of block")
     T = X.clone(memory_format=torch.contiguous_format)
     dev = X.device
-    s = stream(dev)
     if dead is not None:
         dd = dead.to(device=dev, dtype=torch.uint8).contiguous()
-        check(lib().lamq_zero_columns(ptr(T), m, n, n, ptr(dd), s), "zero_columns")
+        check(lib().lamq_zero_columns(ptr(T), m, n, n, ptr(dd), stream(dev)), "zero_columns")
     block = lib().lamq_ldlq_trellis16_block if L >= BIG_L else lib().lamq_ldlq_trellis_block
     parts = []
     r0 = 0
@@ -201,22 +202,55 @@ def ldlq_trellis_groups(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, group
     states = torch.empty(m, n, dtype=torch.int32, device=dev)
     outer = _outer_run(lazy)
     Z = torch.empty(m, outer, dtype=torch.float64, device=dev)
+    if concurrent is None:
+        concurrent = events is None
+    main = torch.cuda.current_stream(dev)
+    lanes = _group_streams(dev) if concurrent and len(parts) > 1 else [main]
+    for ln in lanes:
+        if ln is not main:
+            ln.wait_stream(main)
     vp = ctypes.c_void_p
+    # each group's rows as views: T, Z and the outputs of rows [r0, r0 + rows)
+    views = [(T.narrow(0, r0, rows), Z.narrow(0, r0, rows)) for r0, rows, _, _, _ in parts]
     for B0 in range(0, n, outer):
         B1 = min(B0 + outer, n)
         for b0 in range(B0, B1, lazy):
             b1 = min(b0 + lazy, n)
-            zb = Z[:, b0 - B0 :]
-            for r0, rows, k, table64, t32 in parts:
-                ev = _event_pair(events, "block")
-                check(block(vp(T.data_ptr() + 8 * r0 * n), rows, n, n, ptr(U), ld(U), vp(S.data_ptr() + 8 * r0),
-                            ptr(table64), ptr(t32), L, k, b0, b1, width, look, vp(state.data_ptr() + 4 * r0),
-                            vp(states.data_ptr() + 4 * r0 * n), n, vp(zb.data_ptr() + 8 * r0 * outer), outer, s),
-                      "ldlq_trellis_block")
-                _event_end(ev)
-            _refit_run(T, U, zb, b0, b1, B1, look, events)
-        _refit_rest(T, U, Z, B0, B1, look, events)
+            for p, (r0, rows, k, table64, t32) in enumerate(parts):
+                Tp, Zp = views[p]
+                with torch.cuda.stream(lanes[p % len(lanes)]):
+                    zb = Zp[:, b0 - B0 :]
+                    ev = _event_pair(events, "block")
+                    check(block(ptr(Tp), rows, n, n, ptr(U), ld(U), vp(S.data_ptr() + 8 * r0), ptr(table64), ptr(t32), L,
+                                k, b0, b1, width, look, vp(state.data_ptr() + 4 * r0), vp(states.data_ptr() + 4 * r0 * n),
+                                n, ptr(zb), outer, stream(dev)), "ldlq_trellis_block")
+                    _event_end(ev)
+                    if len(lanes) > 1:
+                        _refit_run(Tp, U, zb, b0, b1, B1, look, events)
+            if len(lanes) == 1:  # one product over every group's rows
+                _refit_run(T, U, Z[:, b0 - B0 :], b0, b1, B1, look, events)
+        if len(lanes) == 1:
+            _refit_rest(T, U, Z, B0, B1, look, events)
+        else:
+            for p, (Tp, Zp) in enumerate(views):
+                with torch.cuda.stream(lanes[p % len(lanes)]):
+                    _refit_rest(Tp, U, Zp, B0, B1, look, events)
+    for ln in lanes:
+        if ln is not main:
+            main.wait_stream(ln)
     return states
+
+
+_GROUP_STREAMS: dict = {}
+GROUP_STREAMS = 4  # streams per device for concurrent row groups (the box's hardware queues per process)
+
+
+def _group_streams(dev: torch.device) -> list:
+    """The device's streams for concurrent row groups (default priority), made once per process."""
+    key = torch.device(dev).index if torch.device(dev).index is not None else torch.cuda.current_device()
+    if key not in _GROUP_STREAMS:
+        _GROUP_STREAMS[key] = [torch.cuda.Stream(device=torch.device("cuda", key)) for _ in range(GROUP_STREAMS)]
+    return _GROUP_STREAMS[key]
 
 
 def _outer_run(lazy: int) -> int:

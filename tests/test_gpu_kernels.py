@@ -354,6 +354,42 @@ def test_ldlq_trellis_full_width_matches_oracle(E, tables):
     assert np.array_equal(st[rows], ref)
 
 
+@pytest.mark.parametrize("L", [12, 16])
+def test_ldlq_trellis_groups_concurrent_equals_serial_and_oracle(E, tables, L):
+    """Four row groups of different widths (and a fifth, empty one), each swept on its own stream, give the states of
+    the same sweep run group after group on one stream, bit for bit, and each group's states are the oracle's for its
+    rows alone (n = 1,100: three outer runs, a ragged last lazy block)."""
+    rng = np.random.default_rng(12 + L)
+    n = 1100
+    sizes, widths = [70, 0, 301, 129, 64], [1, 2, 2, 3, 4]
+    m = sum(sizes)
+    Xa = rng.standard_normal((2 * n, n))
+    H = Xa.T @ Xa / (2 * n)
+    _, U, _ = O.environment(H)
+    X = rng.standard_normal((m, n))
+    S = O.row_scale(X)
+    if L == 12:
+        tabs = {k: tables[k] for k in (1, 2, 3, 4)}
+    else:
+        from lookatmyquant_amd.tables import quantile_table
+
+        tabs = {k: np.array(quantile_table(16, 0)) for k in (1, 2, 3, 4)}
+    groups = [(r, k, cuda(tabs[k]), None) for r, k in zip(sizes, widths)]
+    say(f"ldlq_trellis_groups L={L}: {m} rows in 4 groups, concurrent and serial")
+    a = E.ldlq_trellis_groups(cuda(X), cuda(S), cuda(U), groups, L, concurrent=True)
+    b = E.ldlq_trellis_groups(cuda(X), cuda(S), cuda(U), groups, L, concurrent=False)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    st = a.cpu().numpy()
+    r0 = 0
+    for r, k in zip(sizes, widths):
+        if r:
+            pick = [r0 + r - 1] if L == 16 else list(range(r0, r0 + min(r, 8)))
+            ref = O.ldlq_trellis(X[pick], U, S[pick], tabs[k], L, k)
+            assert np.array_equal(st[pick], ref), (r0, k)
+        r0 += r
+
+
 def test_ldlq_scalar_matches_reference_config1(E, golden, config12):
     """Config 1 (960 x 960, 3-bit Lloyd-Max, nested_words path): indices equal the reference's."""
     W, H = config12
