@@ -141,10 +141,11 @@ int lamq_zero_columns(double* T, int64_t m, int64_t n, int64_t ldT, const uint8_
  *   info  [1] int32 device output: 0, or j+1 when the leading minor of order j+1 of J H J is not
  *         positive definite (torch.linalg.LinAlgError in the reference)
  *   workspace: lamq_chol_inv_upper_workspace_size(n) bytes
- * Part of the work runs on an internal stream of the current device (created on the first call, default priority),
- * ordered after the work already on `stream` and joined back into `stream` before the call returns, so the
- * results are ordered on `stream` like any other entry point's. Calls from several host threads on one device
- * serialise their enqueue on a lock.
+ * Part of the work runs on an internal stream (one per calling stream and device, up to eight, created on first use,
+ * default priority), ordered after the work already on `stream` and joined back into `stream` before the call
+ * returns, so the results are ordered on `stream` like any other entry point's; factorizations enqueued on
+ * different streams run side by side. Calls from several host threads on one stream serialise their enqueue on a
+ * lock.
  * ---------------------------------------------------------------------------------------------- */
 size_t lamq_chol_inv_upper_workspace_size(int64_t n);
 /* flags of lamq_chol_inv_upper_ex: LAMQ_CHOL_KEEP_DEAD leaves a zero diagonal as it is (no unit diagonal at dead

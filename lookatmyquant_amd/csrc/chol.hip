@@ -309,31 +309,49 @@ __global__ void reverse_kernel(double* __restrict__ U, int64_t n, int64_t ldU, c
 // their use of the events.
 struct SideStream {
     std::mutex mu;
+    bool used = false;
+    hipStream_t owner = nullptr;  // the caller's stream this side stream serves
     hipStream_t s = nullptr;
     hipEvent_t fork = nullptr, step = nullptr, join = nullptr;
 };
 #define LAMQ_MAX_DEVICES 64
-static SideStream g_side[LAMQ_MAX_DEVICES];
+#define LAMQ_SIDE_PER_DEVICE 8
+static SideStream g_side[LAMQ_MAX_DEVICES][LAMQ_SIDE_PER_DEVICE];
 static std::mutex g_side_init;
 
-static int side_stream(SideStream** out)
+// The side stream of the caller's stream on the current device, made on first use: factorizations enqueued on
+// different streams (for instance two of them run side by side) get different side streams, so that neither's
+// inverse waits behind the other's. Beyond LAMQ_SIDE_PER_DEVICE caller streams, callers share side streams (their
+// inverses then run one after the other; the results are the same).
+static int side_stream(hipStream_t caller, SideStream** out)
 {
     int dev = 0;
     LAMQ_HIP_CHECK(hipGetDevice(&dev));
     if (dev < 0 || dev >= LAMQ_MAX_DEVICES) return LAMQ_EUNSUP;
     std::lock_guard<std::mutex> lock(g_side_init);
-    SideStream& ss = g_side[dev];
-    if (!ss.s) {
+    SideStream* row = g_side[dev];
+    for (int i = 0; i < LAMQ_SIDE_PER_DEVICE; ++i)
+        if (row[i].used && row[i].owner == caller) {
+            *out = &row[i];
+            return LAMQ_OK;
+        }
+    for (int i = 0; i < LAMQ_SIDE_PER_DEVICE; ++i) {
+        SideStream& ss = row[i];
+        if (ss.used) continue;
         hipStream_t st = nullptr;
         hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
         LAMQ_HIP_CHECK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
-        for (int i = 0; i < 3; ++i) LAMQ_HIP_CHECK(hipEventCreateWithFlags(&ev[i], hipEventDisableTiming));
+        for (int j = 0; j < 3; ++j) LAMQ_HIP_CHECK(hipEventCreateWithFlags(&ev[j], hipEventDisableTiming));
         ss.fork = ev[0];
         ss.step = ev[1];
         ss.join = ev[2];
         ss.s = st;
+        ss.owner = caller;
+        ss.used = true;
+        *out = &ss;
+        return LAMQ_OK;
     }
-    *out = &ss;
+    *out = &row[(uintptr_t)caller % LAMQ_SIDE_PER_DEVICE];
     return LAMQ_OK;
 }
 
@@ -406,7 +424,7 @@ extern "C" int lamq_chol_inv_upper_ex(const double* H, int64_t n, int64_t ldH, d
     if (n > (int64_t)1 << 20) return LAMQ_EUNSUP;
     hipStream_t s = as_stream(stream);
     SideStream* side = nullptr;
-    int rc = side_stream(&side);
+    int rc = side_stream(s, &side);
     if (rc) return rc;
     std::lock_guard<std::mutex> lock(side->mu);
     hipStream_t si = side->s;

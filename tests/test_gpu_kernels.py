@@ -200,6 +200,33 @@ def test_chol_inv_upper_large_inverse_identity(E, n):
             assert torch.equal(first, U)
 
 
+def test_chol_inv_upper_on_two_streams(E):
+    """Two factorizations enqueued on two streams (each with its own internal inverse stream) run side by side and
+    give the factors they give one after the other, bit for bit."""
+    g = torch.Generator(device="cuda").manual_seed(23)
+    Hs = []
+    for n in (2560, 1100):
+        A = torch.randn(2 * n, n, generator=g, device="cuda", dtype=torch.float64)
+        Hs.append((A.T @ A / (2 * n)).contiguous())
+    say("chol_inv_upper: n = 2560 and 1100, one after the other, then on two streams")
+    ref = [E.chol_inv_upper(H)[1] for H in Hs]
+    torch.cuda.synchronize()
+    main = torch.cuda.current_stream()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for _ in range(2):
+        out = []
+        for H, st in zip(Hs, streams):
+            st.wait_stream(main)
+            with torch.cuda.stream(st):
+                out.append(E.chol_inv_upper(H, raise_on_fail=False))
+        for st in streams:
+            main.wait_stream(st)
+        torch.cuda.synchronize()
+        for (Hd, U, dead, info), r in zip(out, ref):
+            assert int(info.item()) == 0
+            assert torch.equal(U, r)
+
+
 @pytest.mark.parametrize("n,k", [(300, 3), (300, 37), (300, 250)])
 def test_chol_inv_upper_reports_a_pivot_inside_a_block(E, n, k):
     """A negative diagonal entry at H[k][k] of an otherwise diagonal H is pivot n - k of the reversed
