@@ -157,7 +157,9 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
     constexpr int G = V::G, NB = V::NB, M = V::M, R = V::R;
     static_assert(G * K <= 8 * (int)sizeof(BackT), "one back-pointer entry per thread and step");
     const int tid = threadIdx.x;
-    const bool act = tid < V::ACT;
+    // every thread owns groups when there are at least NT of them (the kernels launch exactly NT threads): a
+    // compile-time true then, and the step loop carries no exec-mask branches
+    const bool act = V::ACT >= NT || tid < V::ACT;
     int ent[NB];
 #pragma unroll
     for (int h = 0; h < NB; ++h) ent[h] = V::RUN ? h * (R >> K) + M * tid : (h * R + G * tid) >> K;
