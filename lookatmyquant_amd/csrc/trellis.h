@@ -54,6 +54,15 @@ __device__ __forceinline__ float xmc_hi(float x, uint32_t c)
     return d;
 }
 
+// 2 v + (this lane's bit of mask): one v_addc_co_u32 with the mask as its carry-in
+__device__ __forceinline__ uint32_t shift_in(uint32_t v, uint64_t mask)
+{
+    uint32_t r;
+    uint64_t carry;
+    asm("v_addc_co_u32_e64 %0, %1, %2, %2, %3" : "=v"(r), "=s"(carry) : "v"(v), "s"(mask));
+    return r;
+}
+
 // The member state values of thread t: member i = h*G + g is state h*R + G*t + g.
 template <class V>
 struct TabF32 {
@@ -181,25 +190,44 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
             float* dst = buf + (DBL ? (cur ^ 1) * R : 0);
             // groups in chunks of CK sharing one B entry per h (RUN) or all of them; each chunk stored when done
             constexpr int CK = V::RUN ? NB : G;
+            // with the tournament below (K = 2 in the 16-bit-state kernels) the groups are visited from the last to the
+            // first, so that the winning h can be shifted in bit by bit
+            constexpr bool TOUR = NB == 4 && L > 12;
 #pragma unroll
-            for (int e = 0; e < G / CK; ++e) {
+            for (int ei = 0; ei < G / CK; ++ei) {
+                const int e = TOUR ? G / CK - 1 - ei : ei;
                 float best[CK];
 #pragma unroll
-                for (int gg = 0; gg < CK; ++gg) {
+                for (int gi = 0; gi < CK; ++gi) {
+                    const int gg = TOUR ? CK - 1 - gi : gi;
                     const int g = e * CK + gg;
                     float c[NB];
 #pragma unroll
                     for (int h = 0; h < NB; ++h) c[h] = bv[h][e] + tab.dsq(x, h * G + g);
                     // the minimum, then the lowest h attaining it (costs are never NaN: finite or +inf)
-                    float b = c[0];
+                    if constexpr (TOUR) {
+                        // (at L <= 12 the extra register it takes would cost the kernel a wave of occupancy)
+                        // a two-level tournament with strict comparisons (a tie keeps the left, lower, side): the
+                        // winning pair hi = (min(c2,c3) < min(c0,c1)), then within it lo; h = 2 hi + lo enters bits
+                        // [2g, 2g+2) as two carry-ins (bits = 2 bits + bit), the comparisons staying lane masks
+                        const float m01 = fminf(c[0], c[1]), m23 = fminf(c[2], c[3]);
+                        const uint64_t hi = __builtin_amdgcn_ballot_w64(m23 < m01);
+                        const uint64_t lo = (hi & __builtin_amdgcn_ballot_w64(c[3] < c[2])) |
+                                            (~hi & __builtin_amdgcn_ballot_w64(c[1] < c[0]));
+                        best[gg] = fminf(m01, m23);
+                        bits = shift_in(bits, hi);
+                        bits = shift_in(bits, lo);
+                    } else {
+                        float b = c[0];
 #pragma unroll
-                    for (int h = 1; h < NB; ++h) b = fminf(b, c[h]);
-                    uint32_t hs = NB - 1;
+                        for (int h = 1; h < NB; ++h) b = fminf(b, c[h]);
+                        uint32_t hs = NB - 1;
 #pragma unroll
-                    for (int h = NB - 2; h >= 0; --h) hs = c[h] == b ? (uint32_t)h : hs;
-                    best[gg] = b;
-                    asm volatile("" : "+v"(hs));  // keeps h a small integer: one shift-or per group, no wide constants
-                    bits |= hs << (g * K);
+                        for (int h = NB - 2; h >= 0; --h) hs = c[h] == b ? (uint32_t)h : hs;
+                        best[gg] = b;
+                        asm volatile("" : "+v"(hs));  // keeps h a small integer: one shift-or per group, no wide constants
+                        bits |= hs << (g * K);
+                    }
                 }
                 lds_store_swz<CK>(dst, G * tid + e * CK, best);
             }
