@@ -101,7 +101,7 @@ def cpu_baseline(W, H, table, L, k, in_seed, budget_s=12.0):
 
 # HBM bytes per launch of the dominant kernel, from two rocprofv3 counter runs (FETCH_SIZE, WRITE_SIZE) scaled by a
 # 1 GiB copy's readings (profiles/ldlq_trellis_block_gx_config2_L16_k2.md); keyed by (kernel, L, k).
-MEASURED_TRAFFIC = {("ldlq_trellis_block_gx_kernel", 16, 2): 10838044}
+MEASURED_TRAFFIC = {("ldlq_trellis_block_gx_kernel", 16, 2): 10749602}
 
 MFMA_F64_PEAK_TFLOPS = 78.6
 MFMA_BF16_PEAK_TFLOPS = 2500.0
