@@ -192,7 +192,7 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
             constexpr int CK = V::RUN ? NB : G;
             // with the tournament below (K = 2 in the 16-bit-state kernels) the groups are visited from the last to the
             // first, so that the winning h can be shifted in bit by bit
-            constexpr bool TOUR = NB == 4 && L > 12;
+            constexpr bool TOUR = NB == 2 || (NB == 4 && L > 12);
 #pragma unroll
             for (int ei = 0; ei < G / CK; ++ei) {
                 const int e = TOUR ? G / CK - 1 - ei : ei;
@@ -205,7 +205,12 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
 #pragma unroll
                     for (int h = 0; h < NB; ++h) c[h] = bv[h][e] + tab.dsq(x, h * G + g);
                     // the minimum, then the lowest h attaining it (costs are never NaN: finite or +inf)
-                    if constexpr (TOUR) {
+                    if constexpr (NB == 2) {
+                        // the second state wins only if strictly lower; its bit enters as a carry-in
+                        const uint64_t lo = __builtin_amdgcn_ballot_w64(c[1] < c[0]);
+                        best[gg] = fminf(c[0], c[1]);
+                        bits = shift_in(bits, lo);
+                    } else if constexpr (TOUR) {
                         // (at L <= 12 the extra register it takes would cost the kernel a wave of occupancy)
                         // a two-level tournament with strict comparisons (a tie keeps the left, lower, side): the
                         // winning pair hi = (min(c2,c3) < min(c0,c1)), then within it lo; h = 2 hi + lo enters bits
