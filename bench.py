@@ -332,8 +332,10 @@ def run_c5(args):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default 10; c3 5; c5 1, a whole 36-layer build)")
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed steps first (default 3; c3 and c5 1, for c5 a one-layer build)")
     ap.add_argument("--L", type=int, default=None,
                     help="trellis state bits: default 16 for c2 (the benchmark table), 12 for c3 and c5 (the reference's "
                          "production trellis)")
@@ -347,6 +349,10 @@ def main():
                          "under DIR (a new directory) and report its size and the seconds it took, outside the "
                          "timed region")
     args = ap.parse_args()
+    if args.steps is None:
+        args.steps = {"c3": 5, "c5": 1}.get(args.workload, 10)
+    if args.warmup is None:
+        args.warmup = {"c3": 1, "c5": 1}.get(args.workload, 3)
     if args.L is None:
         args.L = 16 if args.workload == "c2" else 12
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
