@@ -478,8 +478,11 @@ def hessian(X: torch.Tensor, w: torch.Tensor | None = None) -> torch.Tensor:
 
 def cross_gram_accum(D: torch.Tensor, Xr: torch.Tensor, Xq: torch.Tensor, w: torch.Tensor | None = None,
                      scale: float = 1.0, classes: list | None = None) -> torch.Tensor:
-    """D (float32 [n, n]) += scale * Xr^T diag(w) Xq (quantize.py:1457). classes: weight_classes(w), if the caller
-    has it already (zero classes are skipped)."""
+    """D (float32 [n, n]) += scale * Xr^T diag(w) Xq (quantize.py:1457). Weights with few distinct values go class by
+    class through the unweighted kernel, as in hessian_accum: the most frequent weight w0 over all tokens
+    (contiguous), then (v - w0) over each other class's rows (gathered in the kernel). classes:
+    weight_classes(w, include_zero=True), if the caller has it already (classes that leave rows out are taken one by
+    one, each over its own rows)."""
     need(D, torch.float32, "D", 2)
     need(Xr, torch.bfloat16, "Xr", 2)
     need(Xq, torch.bfloat16, "Xq", 2)
@@ -489,15 +492,24 @@ def cross_gram_accum(D: torch.Tensor, Xr: torch.Tensor, Xq: torch.Tensor, w: tor
     wv = None if w is None else w.to(device=Xr.device, dtype=torch.float32).contiguous()
     if wv is not None and _tiled(Xr) and _tiled(Xq):
         if classes is None:
-            classes = weight_classes(wv)
+            classes = weight_classes(wv, include_zero=True)
         if classes is not None:
-            for v, rows in classes:  # the cross-Gram (QEP only) gathers its rows inside the kernel, no copies
-                if v == 0.0 or rows.numel() == 0:
+            base = 0.0
+            if sum(rows.numel() for _, rows in classes) == N:  # every token in a class: a contiguous base pass
+                base, _ = max(classes, key=lambda c: c[1].numel())
+            if base != 0.0:
+                nbytes = lib().lamq_gram_workspace_size(N, n, 0)
+                ws = workspace(nbytes, Xr.device)
+                check(lib().lamq_cross_gram(ptr(Xr), ptr(Xq), N, n, ld(Xr), None, float(scale * base), ptr(D), ld(D),
+                                            ptr(ws), nbytes, stream(Xr.device)), "cross_gram")
+            for v, rows in classes:  # the other classes' rows are gathered inside the kernel, no copies
+                if v == base or rows.numel() == 0:
                     continue
                 nbytes = lib().lamq_gram_workspace_size(rows.numel(), n, 0)
                 ws = workspace(nbytes, Xr.device)
-                check(lib().lamq_cross_gram_rows(ptr(Xr), ptr(Xq), ptr(rows), rows.numel(), n, ld(Xr), float(scale * v),
-                                                 ptr(D), ld(D), ptr(ws), nbytes, stream(Xr.device)), "cross_gram_rows")
+                check(lib().lamq_cross_gram_rows(ptr(Xr), ptr(Xq), ptr(rows), rows.numel(), n, ld(Xr),
+                                                 float(scale * (v - base)), ptr(D), ld(D), ptr(ws), nbytes,
+                                                 stream(Xr.device)), "cross_gram_rows")
             return D
     nbytes = lib().lamq_gram_workspace_size(N, n, 0)
     ws = workspace(nbytes, Xr.device)
