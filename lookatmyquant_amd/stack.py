@@ -160,7 +160,7 @@ class Timer:
 
 @torch.no_grad()
 def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | None = None, alpha: float = 0.5,
-          L: int = 12, plan_seed: int = 7000, chunk: int = 8, layers: int | None = None, weight_seed: int = 5000,
+          L: int = 12, plan_seed: int = 7000, chunk: int = 32, layers: int | None = None, weight_seed: int = 5000,
           timer: Timer | None = None, keep: int = 0) -> dict:
     """The build of a random-initialised stack on calibration token ids [S, T]: per layer and stage, the two streams'
     statistics, the QEP target, the row-group trellis codes (a 2.3 bpw row plan per matrix, bits 1-4) and the
@@ -168,7 +168,8 @@ def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | Non
     "in_seed", "groups": the row plan, "packed": per group the code words (engine.pack_codes, read in place)}},
     "weights": n, "bits": total rate bits, "redamped": {"i.first matrix": damping} for stages that needed more than
     0.01, "bad": a device flag set if any packed row was not a trellis path, "L", "tables"}; export_codes writes the
-    codes as an opgraph-packed-1 artifact. token_w: per-token weights [S, T] (mean 1), or None. keep: the first `keep` layers
+    codes as an opgraph-packed-1 artifact. chunk: calibration sequences per forward pass (the default takes config
+    5's 32 x 2048 tokens in one, about 17 GB of activations at its peak: fewer, larger products). token_w: per-token weights [S, T] (mean 1), or None. keep: the first `keep` layers
     also return their stages' inputs and statistics under "stages" (for tests: {(i, s): (X_q, X_ref, H, D,
     {name: W*}, in_seed, plans)}, on the CPU)."""
     dev = E._abi.device()
