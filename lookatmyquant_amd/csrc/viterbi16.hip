@@ -38,6 +38,13 @@ struct VBig {
     static_assert(SQ >= NB && SQ >= 2 && G * K <= 32, "layout");
     // quarter of the predecessors h*R + r of the groups of quarter q (independent of the thread, see above)
     static constexpr int quarter(int h, int q) { return (h * R + q * RQ) / QS; }
+    // with K = 1 the second predecessors of the quarters' groups are visited in increasing quarter (phases in order)
+    static constexpr bool second_in_order()
+    {
+        for (int q = 1; q < 4; ++q)
+            if (quarter(1, q) < quarter(1, q - 1)) return false;
+        return true;
+    }
     static constexpr int offset(int h, int q) { return (h * R + q * RQ) % QS; }
 };
 
@@ -54,6 +61,7 @@ __device__ void viterbi_big(const float* xs, int TV, uint32_t (&Ch)[VBig<L, K>::
                             uint32_t* back, int* path, float* red)
 {
     using V = VBig<L, K>;
+    static_assert(K != 1 || V::second_in_order(), "K = 1 shifts the groups' bits in increasing group order");
     const int tid = threadIdx.x;
     float bprev[V::G];  // index q*GQ + g
     {
@@ -103,6 +111,12 @@ __device__ void viterbi_big(const float* xs, int TV, uint32_t (&Ch)[VBig<L, K>::
                         if (h == 0) {  // the first predecessor of every group (phases visit h in increasing order)
                             best[j] = c[g];
                             if (SEP) hw[j] = 0;
+                        } else if constexpr (K == 1) {
+                            // the second predecessor wins only if strictly lower; its bit enters `bits` as a carry-in,
+                            // groups in increasing j (static_assert below), so group j's bit lands at G - 1 - j
+                            const uint64_t lt = __builtin_amdgcn_ballot_w64(c[g] < best[j]);
+                            best[j] = fminf(best[j], c[g]);
+                            bits = shift_in(bits, lt);
                         } else {
                             const bool lt = c[g] < best[j];  // strict: the lowest h keeps a tie
                             best[j] = lt ? c[g] : best[j];
@@ -166,7 +180,8 @@ __device__ void viterbi_big(const float* xs, int TV, uint32_t (&Ch)[VBig<L, K>::
             const int q = r / V::RQ, rem = r - q * V::RQ;
             const int owner = rem / V::GQ, g = rem - owner * V::GQ;
             const int j = q * V::GQ + g;
-            const int h = (int)((back[(t - 1) * BIG_NT + owner] >> (j * K)) & (uint32_t)(V::NB - 1));
+            const int pos = K == 1 ? V::G - 1 - j : j * K;  // K = 1: the bits were shifted in, group 0 first
+            const int h = (int)((back[(t - 1) * BIG_NT + owner] >> pos) & (uint32_t)(V::NB - 1));
             s = r + h * V::R;
             path[t - 1] = s;
         }
