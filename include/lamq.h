@@ -103,6 +103,18 @@ int lamq_ldlq_trellis16_block(double* T, int64_t m, int64_t n, int64_t ldT, cons
                               int64_t b0, int64_t b1, int width, int look, int32_t* state, int32_t* states,
                               int64_t lds, double* Z, int64_t ldZ, void* stream);
 
+/* The same fused block with the back-pointers in a caller's workspace: lamq_ldlq_trellis16_block's results, bit for
+ * bit. With 2^15 groups (L = 16, k = 1) the minima-exchange search's 128 KB of group minima leave no LDS for the
+ * back-pointers; given this workspace, that case runs the minima-exchange kernel (two barriers per step) instead of
+ * the quarter-window one (eight). Other (L, k) need none and ignore it.
+ * workspace: lamq_ldlq_trellis16_block_workspace_size(m, L, k) bytes (0: not needed), 4-byte aligned. */
+size_t lamq_ldlq_trellis16_block_workspace_size(int64_t m, int L, int k);
+int lamq_ldlq_trellis16_block_ws(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU,
+                                 const double* S, const double* table64, const uint16_t* table16, int L, int k,
+                                 int64_t b0, int64_t b1, int width, int look, int32_t* state, int32_t* states,
+                                 int64_t lds, double* Z, int64_t ldZ, void* workspace, size_t workspace_bytes,
+                                 void* stream);
+
 /* ------------------------------------------------------------------------------------------------
  * The lazy trailing update T[:, b1:n] -= Z @ U[b0:b1, b1:n] on fp64 MFMA.
  * Replaces opgraph/syntax.py:122-123 (and opgraph/ldlq_gpu.py:48).

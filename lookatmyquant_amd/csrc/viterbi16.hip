@@ -374,12 +374,14 @@ __global__ __launch_bounds__(BIG_NT) void ldlq_trellis_block_big_kernel(
 
 // The same with the minima-exchange search and the prefetched refit of trellis.h (four threads per column of the
 // in-block update).
-template <int L, int K>
+// BG: the back-pointers in back_ws, (BIG_TV - 1) * BIG_NT words per row, instead of LDS (the 2^15-group search,
+// whose 128 KB of group minima leave no LDS for them)
+template <int L, int K, bool BG>
 __global__ __launch_bounds__(BIG_NT) void ldlq_trellis_block_gx_kernel(
     const double* __restrict__ T, int64_t n, int64_t ldT, const double* __restrict__ U, int64_t ldU,
     const double* __restrict__ S, const double* __restrict__ table64, const uint16_t* __restrict__ table16,
     int64_t b0, int64_t b1, int width, int look, int32_t* __restrict__ state, int32_t* __restrict__ states,
-    int64_t lds, double* __restrict__ Z, int64_t ldZ)
+    int64_t lds, double* __restrict__ Z, int64_t ldZ, uint32_t* __restrict__ back_ws)
 {
     using V = VX<L, K, BIG_NT>;
     constexpr bool DBL = V::R <= 4096;
@@ -392,7 +394,7 @@ __global__ __launch_bounds__(BIG_NT) void ldlq_trellis_block_gx_kernel(
         int path[BIG_TV];
         float red[2 * (BIG_NT / 64)];
         float buf[(DBL ? 2 : 1) * V::R];
-        uint32_t back[(BIG_TV - 1) * V::ACT];
+        uint32_t back[BG ? 1 : (BIG_TV - 1) * V::ACT];
     };
     __shared__ Smem sm;
     double* trow = sm.trow;
@@ -402,9 +404,8 @@ __global__ __launch_bounds__(BIG_NT) void ldlq_trellis_block_gx_kernel(
     int* path = sm.path;
     float* red = sm.red;
     float* buf = sm.buf;
-    uint32_t* back = sm.back;
-
     const int64_t row = blockIdx.x;
+    uint32_t* back = BG ? back_ws + row * (int64_t)((BIG_TV - 1) * V::ACT) : sm.back;
     const int tid = threadIdx.x;
     TabF16<V> tab;
     tab.load(table16, tid);
@@ -426,7 +427,7 @@ __global__ __launch_bounds__(BIG_NT) void ldlq_trellis_block_gx_kernel(
         lds_barrier();
         // the refit's U operands are fetched when the forward pass ends, under the final argmin and the traceback
         RefitRegs<4> ops;
-        const int pv = viterbi_gx<L, K, BIG_NT, DBL, false, true>(
+        const int pv = viterbi_gx<L, K, BIG_NT, DBL, BG, true>(
             xs, TV, tab, st, buf, back, path, red, [&]() { refit_fetch_regs<BIG_NT, 4>(ops, U, ldU, j, w, nc); });
         refit_apply_regs<BIG_NT, 4>(ops, trow, jo, w, nc, pv, table64, Sr, states + row * lds + j, Z + row * ldZ + jo, ubb,
                                zs);
@@ -439,11 +440,14 @@ template <int L, int K>
 struct TrellisBlockBig {
     static int run(const double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU, const double* S,
                    const double* table64, const uint16_t* table16, int64_t b0, int64_t b1, int width, int look,
-                   int32_t* state, int32_t* states, int64_t lds, double* Z, int64_t ldZ, hipStream_t s)
+                   int32_t* state, int32_t* states, int64_t lds, double* Z, int64_t ldZ, uint32_t* back_ws, hipStream_t s)
     {
         if constexpr (VX<L, K, BIG_NT>::R <= BIG_GX_MAX_R)
-            hipLaunchKernelGGL((ldlq_trellis_block_gx_kernel<L, K>), dim3((unsigned)m), dim3(BIG_NT), 0, s, T, n, ldT, U,
-                               ldU, S, table64, table16, b0, b1, width, look, state, states, lds, Z, ldZ);
+            hipLaunchKernelGGL((ldlq_trellis_block_gx_kernel<L, K, false>), dim3((unsigned)m), dim3(BIG_NT), 0, s, T, n,
+                               ldT, U, ldU, S, table64, table16, b0, b1, width, look, state, states, lds, Z, ldZ, nullptr);
+        else if (back_ws)
+            hipLaunchKernelGGL((ldlq_trellis_block_gx_kernel<L, K, true>), dim3((unsigned)m), dim3(BIG_NT), 0, s, T, n,
+                               ldT, U, ldU, S, table64, table16, b0, b1, width, look, state, states, lds, Z, ldZ, back_ws);
         else
             hipLaunchKernelGGL((ldlq_trellis_block_big_kernel<L, K>), dim3((unsigned)m), dim3(BIG_NT), 0, s, T, n, ldT, U,
                                ldU, S, table64, table16, b0, b1, width, look, state, states, lds, Z, ldZ);
@@ -465,5 +469,33 @@ extern "C" int lamq_ldlq_trellis16_block(double* T, int64_t m, int64_t n, int64_
     if (width > LAMQ_WMAX || width + look > BIG_TV || b1 - b0 > BIG_LAZY || m > 0x7fffffff) return LAMQ_EUNSUP;
     if (m == 0) return LAMQ_OK;
     return dispatch_big<TrellisBlockBig>(L, k, T, m, n, ldT, U, ldU, S, table64, table16, b0, b1, width, look, state,
-                                         states, lds, Z, ldZ, as_stream(stream));
+                                         states, lds, Z, ldZ, (uint32_t*)nullptr, as_stream(stream));
+}
+
+extern "C" size_t lamq_ldlq_trellis16_block_workspace_size(int64_t m, int L, int k)
+{
+    if (m < 1 || L < 13 || L > 16 || k < 1 || k > L - 12 || k > 4) return 0;
+    if ((1 << (L - k)) <= BIG_GX_MAX_R) return 0;  // the back-pointers fit in LDS
+    return (size_t)m * (size_t)(BIG_TV - 1) * BIG_NT * sizeof(uint32_t);
+}
+
+extern "C" int lamq_ldlq_trellis16_block_ws(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU,
+                                            const double* S, const double* table64, const uint16_t* table16, int L, int k,
+                                            int64_t b0, int64_t b1, int width, int look, int32_t* state, int32_t* states,
+                                            int64_t lds, double* Z, int64_t ldZ, void* workspace, size_t workspace_bytes,
+                                            void* stream)
+{
+    const size_t need = lamq_ldlq_trellis16_block_workspace_size(m, L, k);
+    if (need == 0)
+        return lamq_ldlq_trellis16_block(T, m, n, ldT, U, ldU, S, table64, table16, L, k, b0, b1, width, look, state,
+                                         states, lds, Z, ldZ, stream);
+    if (!workspace || workspace_bytes < need || ((uintptr_t)workspace % 4) != 0) return LAMQ_EINVAL;
+    if (!T || !U || !S || !table64 || !table16 || !state || !states || !Z) return LAMQ_EINVAL;
+    if (((uintptr_t)table16 % 4) != 0) return LAMQ_EINVAL;
+    if (m < 0 || n < 1 || ldT < n || ldU < n || lds < n || b0 < 0 || b1 <= b0 || b1 > n || width < 1 || look < 0)
+        return LAMQ_EINVAL;
+    if (ldZ < b1 - b0) return LAMQ_EINVAL;
+    if (width > LAMQ_WMAX || width + look > BIG_TV || b1 - b0 > BIG_LAZY || m > 0x7fffffff) return LAMQ_EUNSUP;
+    return dispatch_big<TrellisBlockBig>(L, k, T, m, n, ldT, U, ldU, S, table64, table16, b0, b1, width, look, state,
+                                         states, lds, Z, ldZ, reinterpret_cast<uint32_t*>(workspace), as_stream(stream));
 }

@@ -186,7 +186,6 @@ def ldlq_trellis_groups(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, group
     if dead is not None:
         dd = dead.to(device=dev, dtype=torch.uint8).contiguous()
         check(lib().lamq_zero_columns(ptr(T), m, n, n, ptr(dd), stream(dev)), "zero_columns")
-    block = lib().lamq_ldlq_trellis16_block if L >= BIG_L else lib().lamq_ldlq_trellis_block
     parts = []
     r0 = 0
     for rows, k, table64, table32 in groups:
@@ -198,6 +197,24 @@ def ldlq_trellis_groups(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, group
         if rows:
             parts.append((r0, int(rows), int(k), table64, t32))
         r0 += int(rows)
+    # the 16-bit-state block kernels: a group whose search keeps its back-pointers outside LDS (2^15 groups) gets a
+    # workspace of its own, allocated here on the caller's stream before the fork
+    ws = {}
+    if L >= BIG_L:
+        for r0, rows, k, _, _ in parts:
+            nb = lib().lamq_ldlq_trellis16_block_workspace_size(rows, L, k)
+            if nb:
+                ws[r0] = torch.empty(nb, dtype=torch.uint8, device=dev)
+
+    def block(Tp, rows, r0, k, table64, t32, b0, b1, zb, st_):
+        args = (ptr(Tp), rows, n, n, ptr(U), ld(U), vp(S.data_ptr() + 8 * r0), ptr(table64), ptr(t32), L, k, b0, b1, width,
+                look, vp(state.data_ptr() + 4 * r0), vp(states.data_ptr() + 4 * r0 * n), n, ptr(zb), outer)
+        if L < BIG_L:
+            return lib().lamq_ldlq_trellis_block(*args, st_)
+        w = ws.get(r0)
+        if w is None:
+            return lib().lamq_ldlq_trellis16_block(*args, st_)
+        return lib().lamq_ldlq_trellis16_block_ws(*args, ptr(w), w.numel(), st_)
     state = torch.zeros(m, dtype=torch.int32, device=dev)
     states = torch.empty(m, n, dtype=torch.int32, device=dev)
     outer = _outer_run(lazy)
@@ -221,9 +238,7 @@ def ldlq_trellis_groups(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, group
                 with torch.cuda.stream(lanes[p % len(lanes)]):
                     zb = Zp[:, b0 - B0 :]
                     ev = _event_pair(events, "block")
-                    check(block(ptr(Tp), rows, n, n, ptr(U), ld(U), vp(S.data_ptr() + 8 * r0), ptr(table64), ptr(t32), L,
-                                k, b0, b1, width, look, vp(state.data_ptr() + 4 * r0), vp(states.data_ptr() + 4 * r0 * n),
-                                n, ptr(zb), outer, stream(dev)), "ldlq_trellis_block")
+                    check(block(Tp, rows, r0, k, table64, t32, b0, b1, zb, stream(dev)), "ldlq_trellis_block")
                     _event_end(ev)
                     if len(lanes) > 1:
                         _refit_run(Tp, U, zb, b0, b1, B1, look, events)
