@@ -443,15 +443,41 @@ static bool gram256_ok(const uint16_t* X, int64_t n, int64_t ldx)
 // Token splits: enough workgroups to fill the chip, at least 1024 tokens per split. The 128 tiles aim at about
 // four workgroups per CU; the 256 tiles (one workgroup per CU) at one round of at most 256 workgroups, since a
 // short second round would cost as much as the first.
+// Token splits of a Gram launch. The 128-tile kernel: enough splits for about 1024 workgroups. The 256-tile kernel
+// (one workgroup per CU): 256 / tiles splits (one round) when those fill at least 85% of the CUs; otherwise the split
+// count whose workgroups fill the 256 CUs' rounds best (tiles * s / (rounds * 256)), the smallest such count when
+// several come within 2%, with at most max(8, 512 / tiles) splits and 512 MB of partial slabs (more splits cost a
+// larger reduction and more pipeline fills). Always at least 1024 tokens per split. At n = 4,096 (136
+// lower-triangle tiles) one split would leave 47% of the chip idle; seven fill 93% of four rounds.
 static int64_t gram_splits(int64_t N, int64_t n, bool sym, int64_t edge)
 {
     const int64_t nt = cdiv(n, edge);
     const int64_t tiles = sym ? nt * (nt + 1) / 2 : nt * nt;
-    int64_t s = edge == GT ? 256 / tiles : cdiv(1024, tiles);
     const int64_t maxs = N / 1024 > 1 ? N / 1024 : 1;
-    if (s > maxs) s = maxs;
-    if (s < 1) s = 1;
-    return s;
+    if (edge != GT) {
+        int64_t s = cdiv(1024, tiles);
+        if (s > maxs) s = maxs;
+        return s < 1 ? 1 : s;
+    }
+    int64_t s0 = 256 / tiles;
+    if (s0 > maxs) s0 = maxs;
+    if (s0 < 1) s0 = 1;
+    if ((double)(tiles * s0) / (double)(cdiv(tiles * s0, 256) * 256) >= 0.85) return s0;
+    int64_t smax = cdiv(512, tiles) > 8 ? cdiv(512, tiles) : 8;
+    const int64_t slab_cap = ((int64_t)512 << 20) / (n * n * (int64_t)sizeof(float));
+    if (smax > maxs) smax = maxs;
+    if (smax > slab_cap) smax = slab_cap;
+    int64_t best = 1;
+    double best_eff = 0.0;
+    for (int64_t s = 1; s <= smax; ++s) {
+        const int64_t wg = tiles * s, rounds = cdiv(wg, 256);
+        const double eff = (double)wg / (double)(rounds * 256);
+        if (eff > best_eff + 0.02) {
+            best = s;
+            best_eff = eff;
+        }
+    }
+    return best;
 }
 
 extern "C" size_t lamq_gram_workspace_size(int64_t N, int64_t n, int sym)
