@@ -171,7 +171,7 @@ def _golden_artifact_inputs():
 
     from conftest import GOLDEN
 
-    spec = importlib.util.spec_from_file_location("make_artifact_golden", GOLDEN / "make_artifact_golden.py")
+    spec = importlib.util.spec_from_file_location("artifact_saved", GOLDEN / "artifact_saved.py")
     mod = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(mod)
     a = dict(np.load(GOLDEN / "artifact_inputs.npz"))
