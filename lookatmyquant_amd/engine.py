@@ -4,6 +4,7 @@ are what the reference-compatible modules (codes, frame, nested, quantize, compi
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 from functools import lru_cache
 
@@ -173,6 +174,7 @@ def ldlq_trellis_groups(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, group
     without events) every group runs its whole sweep, block kernels and its own trailing updates, on a stream of
     its own, and the groups' VALU-bound searches and fp64 MFMA products overlap on the chip; the results are those
     of sweeping the groups one after the other. With events every launch is timed on the caller's stream in turn."""
+    check_tables(groups, L)
     need(X, torch.float64, "X", 2)
     need(U, torch.float64, "U", 2)
     need(S, torch.float64, "S", 1)
@@ -256,6 +258,24 @@ def ldlq_trellis_groups(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, group
     return states
 
 
+def check_tables(groups: list, L: int):
+    """Every group's table has exactly 2^L entries: the float64 table, and the float32 (L < 13) or fp16-bit int16
+    (L >= 13) copy when one is given. The kernels read 2^L entries of each, so a shorter table would be read past its
+    end."""
+    if not 1 <= L <= 16:
+        raise ValueError("L must lie in 1..16")
+    for g in groups:
+        t64, t32 = g[2], g[3] if len(g) > 3 else None
+        if not isinstance(t64, torch.Tensor) or t64.dim() != 1 or t64.numel() != 1 << L:
+            raise ValueError(f"a trellis table must be a 1-d tensor of 2^L = {1 << L} entries")
+        if t32 is not None:
+            want = torch.int16 if L >= BIG_L else torch.float32
+            if t32.dim() != 1 or t32.numel() != 1 << L or (t32.dtype != want and not (L >= BIG_L and
+                                                                                       t32.dtype == torch.float32)):
+                raise ValueError(f"the search copy of a trellis table must be a 1-d {want} tensor of 2^L = {1 << L} "
+                                 "entries")
+
+
 _GROUP_STREAMS: dict = {}
 GROUP_STREAMS = 4  # streams per device for concurrent row groups (the box's hardware queues per process)
 
@@ -313,6 +333,66 @@ def _event_pair(events: dict | None, key: str):
 def _event_end(ev):
     if ev is not None:
         ev.record()
+
+
+def viterbi_ops_per_row_step(L: int, k: int) -> int:
+    """Algorithmic fp32 operations of one trellis step of one row: a subtraction, a square and an addition per state,
+    and 2^k - 1 comparisons per group of 2^k predecessors."""
+    return 3 * (1 << L) + ((1 << k) - 1) * (1 << (L - k))
+
+
+def trellis_row_steps(n: int, width: int = 16, look: int = 8, lazy: int = 128) -> list[int]:
+    """Trellis positions searched per row in each lazy block of the row-trellis sweep (the settled and the look-ahead
+    columns of every call)."""
+    out = []
+    for b0 in range(0, n, lazy):
+        b1 = min(b0 + lazy, n)
+        tot = 0
+        for j in range(b0, b1, width):
+            w = min(width, b1 - j)
+            tot += w + min(look, n - j - w)
+        out.append(tot)
+    return out
+
+
+def trailing_flops(m: int, n: int, lazy: int = 128) -> float:
+    """Algorithmic flops of the trailing updates of one sweep of m rows (syntax.py:123): the sum over lazy blocks of
+    2 m (b1 - b0) (n - b1)."""
+    return float(sum(2 * m * (min(b0 + lazy, n) - b0) * (n - min(b0 + lazy, n)) for b0 in range(0, n, lazy)))
+
+
+class KernelTimer:
+    """Event pairs recorded on the current stream around launches, by key, with the algorithmic work (flops, ops or
+    bytes) each span does. events[key] is the list of (start, end) torch.cuda.Event pairs (the sweeps append their
+    per-launch pairs under "block" and "trailing" to the same dict)."""
+
+    def __init__(self):
+        self.events: dict = {}
+        self.work: dict = {}
+
+    @contextlib.contextmanager
+    def span(self, key: str, work: float = 0.0):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        yield
+        b.record()
+        self.events.setdefault(key, []).append((a, b))
+        self.work[key] = self.work.get(key, 0.0) + float(work)
+
+    def add_work(self, key: str, work: float):
+        self.work[key] = self.work.get(key, 0.0) + float(work)
+
+    def ms(self, key: str) -> float:
+        """Summed duration of the key's spans in ms (synchronise first)."""
+        return sum(event_ms(self.events, key))
+
+    def launches(self, key: str) -> int:
+        return len(self.events.get(key, []))
+
+
+def span(timer: KernelTimer | None, key: str, work: float = 0.0):
+    """timer.span(key, work), or nothing without a timer."""
+    return contextlib.nullcontext() if timer is None else timer.span(key, work)
 
 
 def event_ms(events: dict, key: str) -> list[float]:
@@ -443,7 +523,9 @@ def hessian_accum(H: torch.Tensor, X: torch.Tensor, w: torch.Tensor | None = Non
     """H (float32 [n, n], lower triangle) += scale * X^T diag(w) X for bf16 X [N, n]. Weights with few distinct
     values are taken class by class through the unweighted kernel (exact products): the most frequent weight w0
     over all tokens (contiguous), then (v - w0) over each other class's rows (gathered in the kernel). Other
-    weights use the hi/lo split. classes: weight_classes(w, include_zero=True), if the caller has it already."""
+    weights use the hi/lo split. classes: weight_classes(w, include_zero=True), if the caller has it already; classes
+    that leave tokens out (weight_classes without the zero class) are taken one by one, each over its own rows, so a
+    token outside every class counts with weight 0."""
     need(H, torch.float32, "H", 2)
     need(X, torch.bfloat16, "X", 2)
     N, n = X.shape
@@ -453,7 +535,9 @@ def hessian_accum(H: torch.Tensor, X: torch.Tensor, w: torch.Tensor | None = Non
         if classes is None and _tiled(X):
             classes = weight_classes(wv, include_zero=True)
         if classes is not None and _tiled(X):
-            base, _ = max(classes, key=lambda c: c[1].numel())
+            base = 0.0
+            if sum(rows.numel() for _, rows in classes) == N:  # every token in a class: a contiguous base pass
+                base, _ = max(classes, key=lambda c: c[1].numel())
             if base != 0.0:
                 nbytes = lib().lamq_gram_workspace_size(N, n, 1)
                 ws = workspace(nbytes, X.device)

@@ -176,21 +176,33 @@ def cross_target(H: torch.Tensor, D: torch.Tensor, alpha: float, lam: float = LA
     return cross_map(H, D, alpha, lam).cpu()
 
 
-def cross_map(H: torch.Tensor, D: torch.Tensor, alpha: float, lam: float = LAM) -> torch.Tensor:
-    """cross_target's M, float64 on the GPU."""
+def cross_map(H: torch.Tensor, D: torch.Tensor, alpha: float, lam: float = LAM,
+              timer: E.KernelTimer | None = None) -> torch.Tensor:
+    """cross_target's M, float64 on the GPU. timer: spans "chol" (4n^3/3 flops) and "qep_gemm" (the products:
+    2 M N K flops for a full one, M N K for a triangular one)."""
     dev = E._abi.device()
     Hg = torch.as_tensor(H).to(dev, torch.float64).contiguous()
     Dg = torch.as_tensor(D).to(dev, torch.float64).contiguous()
     n = Hg.shape[0]
-    _, U, _, _ = E.chol_inv_upper(Hg, damp=lam)
+    with E.span(timer, "chol", 4.0 * n ** 3 / 3):
+        _, U, _, _ = E.chol_inv_upper(Hg, damp=lam)
     # (H + d I)^-1 = U^T U, so M = I + alpha ((H + d I)^-1 D^T)^T = I + alpha D U^T U: two triangular products
-    P = torch.zeros(n, n, dtype=torch.float64, device=dev)
-    E.gemm_sub(P, alpha * Dg, U, transb=True, tri=1)  # P = -alpha D U^T
-    M = torch.eye(n, dtype=torch.float64, device=dev)
-    return E.gemm_sub(M, P, U, tri=2)  # M = I + alpha D U^T U
+    with E.span(timer, "qep_gemm", 2.0 * n ** 3):
+        P = torch.zeros(n, n, dtype=torch.float64, device=dev)
+        E.gemm_sub(P, alpha * Dg, U, transb=True, tri=1)  # P = -alpha D U^T
+        M = torch.eye(n, dtype=torch.float64, device=dev)
+        return E.gemm_sub(M, P, U, tri=2)  # M = I + alpha D U^T U
 
 
-def qep_targets(H: torch.Tensor, D: torch.Tensor, alpha: float, Ws: dict, lam: float = LAM) -> dict:
+def _product(A: torch.Tensor, B: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
+    """scale * A @ B on the fp64 MFMA GEMM (lamq_gemm_sub_f64 from a zero C: 0 - (-scale A) B, exact negations, so
+    the products are summed once, as a plain product sums them)."""
+    C = torch.zeros(A.shape[0], B.shape[1], dtype=torch.float64, device=A.device)
+    return E.gemm_sub(C, (-scale * A).contiguous(), B.contiguous())
+
+
+def qep_targets(H: torch.Tensor, D: torch.Tensor, alpha: float, Ws: dict, lam: float = LAM,
+                timer: E.KernelTimer | None = None) -> dict:
     """W* = W M for every matrix of a stage (quantize.py:1505), M = cross_target(H, D, alpha, lam), float64 on the
     GPU. When the stage has fewer rows than inputs M is not formed: W M = W + alpha (W D) (H + d I)^-1 =
     W + alpha (W D) U^T U, one product and two triangular ones (4 m n^2 flops against 2 n^3 + 2 m n^2)."""
@@ -199,17 +211,20 @@ def qep_targets(H: torch.Tensor, D: torch.Tensor, alpha: float, Ws: dict, lam: f
     Wg = {nm: torch.as_tensor(W).to(dev, torch.float64) for nm, W in Ws.items()}
     m = sum(W.shape[0] for W in Wg.values())
     if m >= n:
-        M = cross_map(H, D, alpha, lam)
-        return {nm: W @ M for nm, W in Wg.items()}
+        M = cross_map(H, D, alpha, lam, timer)
+        with E.span(timer, "qep_gemm", 2.0 * m * n * n):
+            return {nm: _product(W, M) for nm, W in Wg.items()}
     Hg = torch.as_tensor(H).to(dev, torch.float64).contiguous()
     Dg = torch.as_tensor(D).to(dev, torch.float64).contiguous()
-    _, U, _, _ = E.chol_inv_upper(Hg, damp=lam)
+    with E.span(timer, "chol", 4.0 * n ** 3 / 3):
+        _, U, _, _ = E.chol_inv_upper(Hg, damp=lam)
     out = {}
-    for nm, W in Wg.items():
-        Z = alpha * (W @ Dg)
-        P = torch.zeros(W.shape[0], n, dtype=torch.float64, device=dev)
-        E.gemm_sub(P, Z, U, transb=True, tri=1)  # P = -alpha W D U^T
-        out[nm] = E.gemm_sub(W.contiguous().clone(), P, U, tri=2)  # W + alpha W D U^T U
+    with E.span(timer, "qep_gemm", 4.0 * m * n * n):
+        for nm, W in Wg.items():
+            Z = _product(W, Dg, alpha)
+            P = torch.zeros(W.shape[0], n, dtype=torch.float64, device=dev)
+            E.gemm_sub(P, Z, U, transb=True, tri=1)  # P = -alpha W D U^T
+            out[nm] = E.gemm_sub(W.contiguous().clone(), P, U, tri=2)  # W + alpha W D U^T U
     return out
 
 
@@ -237,18 +252,24 @@ def stage_statistics(Xq_chunks, w_chunks=None, Xr_chunks=None):
 # ----------------------------------------------------------------------------- the batched stage path
 
 
-def stage_factor(H: torch.Tensor, in_seed: int, damp: float = 0.01):
+def stage_factor(H: torch.Tensor, in_seed: int, damp: float = 0.01, timer: E.KernelTimer | None = None):
     """The stage's factor as quantize_stage_row_groups makes it: (U, dead, info) of the rotated, damped H (no host
-    synchronisation: info is a device value, 0 when positive definite)."""
+    synchronisation: info is a device value, 0 when positive definite). timer: spans "rht" (the rotation's HBM
+    bytes, 3 passes of 16 n^2) and "chol" (4n^3/3 flops)."""
     dev = E._abi.device()
-    Hr = E.rotate_hessian(torch.as_tensor(H).to(dev, torch.float64).contiguous(), in_seed)
-    _, U, dead, info = E.chol_inv_upper(Hr, damp=damp, raise_on_fail=False)
+    Hg = torch.as_tensor(H).to(dev, torch.float64).contiguous()
+    n = Hg.shape[0]
+    with E.span(timer, "rht", 48.0 * n * n):
+        Hr = E.rotate_hessian(Hg, in_seed)
+    with E.span(timer, "chol", 4.0 * n ** 3 / 3):
+        _, U, dead, info = E.chol_inv_upper(Hr, damp=damp, raise_on_fail=False)
     return U, dead, info
 
 
 def quantize_stage_row_groups(targets: dict, groups: dict, H: torch.Tensor, in_seed: int, L: int = 12,
                               width: int = 16, look: int = 8, tables: dict | None = None, events: dict | None = None,
-                              chol_events: tuple | None = None, damp: float = 0.01, factor: tuple | None = None):
+                              chol_events: tuple | None = None, damp: float = 0.01, factor: tuple | None = None,
+                              timer: E.KernelTimer | None = None):
     """Every matrix of a stage, row group by row group, with the row trellis at the group's width: the same result
     as quantize_row_groups(target, groups, round_group) with round_group = the tr<bits> word of (target[rows], H,
     in_seed, out_rot=False), for each matrix. targets: {name: W [m, n]}; groups: {name: [{"rows", "bits"}]};
@@ -256,9 +277,24 @@ def quantize_stage_row_groups(targets: dict, groups: dict, H: torch.Tensor, in_s
     GPU, S float64 [m] on the GPU)}; the codes entries and reconstructions follow from them. events / chol_events
     ((dict, key)): torch.cuda.Event pairs around the sweep kernels / the factorization, for timing. damp: the
     Environment's damping fraction (frame.py:521). factor: stage_factor(H, in_seed, damp), if the caller has made it
-    already (for instance on another stream, next to other work); a non-positive-definite factor raises."""
-    dev = E._abi.device()
+    already (for instance on another stream, next to other work); a non-positive-definite factor raises. timer: an
+    engine.KernelTimer; every launch of the sweep is timed on this stream (one stream for all groups) under "block" and
+    "trailing", the row rotations under "rht" (16 m n bytes), and the factor as in stage_factor."""
     names = list(targets)
+    stage_tables = {}  # the table of each width, resolved before any device work
+    for bits in sorted({int(g["bits"]) for nm in names for g in groups[nm]}):
+        table = (tables or {}).get(bits)
+        if table is None:
+            if L != 12:
+                raise ValueError(f"no trellis table given for {bits} bits at L = {L}: only the 12-bit tables are cached")
+            table = C.load_table(12, bits)
+        table = table if isinstance(table, torch.Tensor) else torch.from_numpy(np.array(table, dtype=np.float64))
+        stage_tables[bits] = table.to(torch.float64)
+    dev = E._abi.device()
+    if timer is not None:
+        events = timer.events
+    if factor is None and timer is not None:
+        factor = stage_factor(H, in_seed, damp, timer)
     if factor is not None:
         U, dead, info = factor
         if int(info.item()):
@@ -279,7 +315,8 @@ def quantize_stage_row_groups(targets: dict, groups: dict, H: torch.Tensor, in_s
     X_all, S_all = {}, {}
     for nm in names:
         W = torch.as_tensor(targets[nm]).to(dev, torch.float64).contiguous()
-        X_all[nm], S_all[nm] = E.rht_rows(W, in_seed, want_rms=True)
+        with E.span(timer, "rht", 16.0 * W.numel()):
+            X_all[nm], S_all[nm] = E.rht_rows(W, in_seed, want_rms=True)
     # rows of one width across the stage's matrices go through one sweep
     by_bits: dict = {}
     for nm in names:
@@ -290,11 +327,7 @@ def quantize_stage_row_groups(targets: dict, groups: dict, H: torch.Tensor, in_s
     out = {nm: torch.empty(X_all[nm].shape, dtype=torch.int32, device=dev) for nm in names}
     idx, sweep_groups = [], []
     for bits, parts in sorted(by_bits.items()):
-        table = (tables or {}).get(bits)
-        if table is None:
-            table = C.load_table(12, bits)
-        table = table if isinstance(table, torch.Tensor) else torch.from_numpy(np.array(table, dtype=np.float64))
-        table = table.to(torch.float64)
+        table = stage_tables[bits]
         rows = 0
         for nm, r in parts:
             idx.append((nm, r.to(dev)))
@@ -308,3 +341,88 @@ def quantize_stage_row_groups(targets: dict, groups: dict, H: torch.Tensor, in_s
         out[nm].index_copy_(0, r, st[r0 : r0 + len(r)])
         r0 += len(r)
     return {nm: (out[nm], S_all[nm]) for nm in names}
+
+
+# ----------------------------------------------------------------------------- the command line
+
+
+def main(argv=None):
+    """quantize.py --program plan|<program> [--plan P.json] [--row-plan R.json] ... (quantize.py:923-989), on the
+    random-initialised Qwen3.5-4B-shaped stack (hidden 2560, GQA 32/8 x 128, MLP 9728; model loading and the text
+    data are not part of this path): synthetic calibration token ids, the stage statistics, QEP targets, codes and
+    packed codes on the GPU. Writes a summary JSON (--out), the reference's --save-codes dictionary, and with
+    --artifact an opgraph-packed-1 artifact."""
+    import argparse
+    import json
+    import time
+    from pathlib import Path
+
+    from . import stack
+    from .rowplan import load_row_plan
+
+    ap = argparse.ArgumentParser(prog="python -m lookatmyquant_amd.quantize")
+    ap.add_argument("--program", required=True, help="plan, or one program for every linear: tr3x, lm6x, fp16, ...")
+    ap.add_argument("--plan", default="", help="with --program plan: a plan JSON ({\"linears\": {\"i.name\": program}})")
+    ap.add_argument("--row-plan", default="", help="rowgroup-plan-1 JSON: original row ids and widths by full parameter "
+                                                   "name; requires --rot in-shared and --trellis-rows")
+    ap.add_argument("--trellis-rows", default="16,8", help="width,look of the row trellis (16,8)")
+    ap.add_argument("--rot", choices=["in-shared"], default="in-shared",
+                    help="one input rotation per stage, none on the output (the only rotation of this path)")
+    ap.add_argument("--cross-alpha", type=float, default=1.0, help="QEP's alpha for cross-term programs")
+    ap.add_argument("--lam", type=float, default=LAM, help="the cross term's ridge penalty")
+    ap.add_argument("--layers", type=int, default=0, help="quantize only the first n layers; 0 = all 36")
+    ap.add_argument("--calib", type=int, default=32, help="calibration windows")
+    ap.add_argument("--calib-len", type=int, default=2048)
+    ap.add_argument("--chunk", type=int, default=32, help="sequences per calibration forward")
+    ap.add_argument("--token-weights", choices=["", "digits"], default="digits",
+                    help="digits: a random 10%% of tokens weighted 10x (normalised to mean 1), the synthetic stand-in "
+                         "for the digit weights of quantize.py:593-629")
+    ap.add_argument("--seed-set", type=int, default=0, help="moves every randomized Hadamard seed")
+    ap.add_argument("--state-bits", type=int, choices=[12, 16], default=12,
+                    help="trellis state bits: 12, the reference's fitted tables; 16, the fp16 Gaussian-quantile table")
+    ap.add_argument("--redamp", action="store_true", help="damp a stage x10, x100 when its statistics are not positive "
+                                                          "definite (ldlq_gpu.py:19-23) instead of raising")
+    ap.add_argument("--save-codes", default="", help="write the codes, scales, tables and row groups here (torch.save)")
+    ap.add_argument("--artifact", default="", help="write the codes as an opgraph-packed-1 artifact in this new directory")
+    ap.add_argument("--out", required=True)
+    args = ap.parse_args(argv)
+    if args.trellis_rows != "16,8":
+        raise NotImplementedError("the fused row-trellis kernels settle 16 columns and look 8 ahead")
+    sh = stack.Shape()
+    layers = args.layers or sh.layers
+    if args.program == "plan":
+        if not args.plan:
+            ap.error("--program plan needs --plan")
+        plan = json.loads(Path(args.plan).read_text())
+    else:
+        parse(args.program)
+        plan = {"linears": {f"{i}.{nm}": args.program for i in range(layers) for nm in stack.matrix_shapes(sh)}}
+    row_plan, manifest = {}, None
+    if args.row_plan:
+        row_plan, manifest = load_row_plan(args.row_plan, stack.active_shapes(sh, plan, layers))
+    tokens, w = stack.calibration_tokens(args.calib, args.calib_len, sh.vocab)
+    torch.cuda.set_device(0)
+    t0 = time.perf_counter()
+    timer = stack.Timer()
+    out = stack.build(tokens, sh, w if args.token_weights else None, alpha=args.cross_alpha, L=args.state_bits,
+                      plan=plan, row_plan=row_plan, chunk=args.chunk, layers=layers, timer=timer, redamp=args.redamp,
+                      lam=args.lam, seed_set=args.seed_set)
+    torch.cuda.synchronize()
+    secs = time.perf_counter() - t0
+    res = {"program": args.program, "layers": layers, "weights": out["weights"],
+           "bits per weight": out["bits"] / out["weights"], "quantize seconds": round(secs, 2),
+           "seconds per layer": round(secs / layers, 3), "seconds by phase": {k: round(v, 2) for k, v in timer.t.items()},
+           "stages damped more": out["redamped"], "row plan": manifest}
+    if args.save_codes:
+        Path(args.save_codes).parent.mkdir(parents=True, exist_ok=True)
+        torch.save(stack.saved_codes(out), args.save_codes)
+    if args.artifact:
+        res["artifact"] = {k: v for k, v in stack.export_codes(out, args.artifact).items()
+                           if k in ("total_bytes", "tensor_count", "all_tensor_bytes_verified")}
+    Path(args.out).parent.mkdir(parents=True, exist_ok=True)
+    Path(args.out).write_text(json.dumps(res, indent=1))
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()

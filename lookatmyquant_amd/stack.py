@@ -25,7 +25,7 @@ import torch
 from . import artifact
 from . import engine as E
 from . import synthetic
-from .quantize import matrix_seeds, qep_targets, quantize_stage_row_groups, stage_factor
+from .quantize import LAM, matrix_seeds, parse, qep_targets, quantize_stage_row_groups, stage_factor
 from .tables import load_table, quantile_table
 
 
@@ -92,18 +92,14 @@ def _lin(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return torch.matmul(x, w.t().contiguous())
 
 
-def _attention_flash(q, k, v):
-    """Causal grouped-query attention [B, H, T, D] bf16 on the fused flash kernel only (the backend is forced, so a
-    build without it raises instead of falling back to the unfused math path)."""
-    from torch.nn.attention import SDPBackend, sdpa_kernel
-
-    with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
-        return torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True)
+ATTENTION_BATCH = 4  # sequences per batched product in the attention (their float32 scores: 2 GB at T = 2048)
 
 
-def _attention_unfused(q, k, v, sh: Shape):
-    """The same attention one sequence at a time: scores and softmax in float32, every batched product's right
-    operand contiguous."""
+def attention(q, k, v, sh: Shape):
+    """Causal grouped-query attention of [B, heads, T, head_dim] bf16 q and [B, kv_heads, T, head_dim] k, v: the scores
+    q k^T / sqrt(head_dim) as a bf16 batched product, masked and soft-maxed in float32, rounded to bf16 and multiplied
+    by v. The one path of every forward here (no fused-kernel backend, no fallback), a few sequences per batched
+    product; every right operand is contiguous."""
     B, _, T, _ = q.shape
     rep = sh.heads // sh.kv_heads
     kT = k.repeat_interleave(rep, dim=1).transpose(-1, -2).contiguous()
@@ -111,20 +107,18 @@ def _attention_unfused(q, k, v, sh: Shape):
     mask = torch.ones(T, T, dtype=torch.bool, device=q.device).triu(1)
     out = torch.empty(B, sh.heads, T, sh.head_dim, dtype=q.dtype, device=q.device)
     scale = 1.0 / float(sh.head_dim) ** 0.5
-    for b in range(B):  # one sequence at a time bounds the score matrix
-        sc = torch.matmul(q[b], kT[b]).float() * scale
+    for b0 in range(0, B, ATTENTION_BATCH):
+        b1 = min(b0 + ATTENTION_BATCH, B)
+        sc = torch.matmul(q[b0:b1], kT[b0:b1]).float().mul_(scale)
         sc.masked_fill_(mask, float("-inf"))
-        out[b] = torch.matmul(torch.softmax(sc, -1).to(q.dtype), vv[b])
+        out[b0:b1] = torch.matmul(torch.softmax(sc, -1).to(q.dtype), vv[b0:b1])
+        del sc
     return out
-
-
-_FLASH = [True]
 
 
 def attention_input_to_o(x: torch.Tensor, w: dict, sh: Shape, rope) -> torch.Tensor:
     """The o_proj input of one chunk [B, T, hidden] (normed hidden states in): q/k/v, per-head RMSNorm of q and k,
-    rotary embedding, causal grouped-query attention (the fused flash kernel where the build has it, else the
-    unfused float32-softmax path)."""
+    rotary embedding, causal grouped-query attention."""
     B, T, _ = x.shape
     q = _lin(x, w["self_attn.q_proj"]).view(B, T, sh.heads, sh.head_dim)
     k = _lin(x, w["self_attn.k_proj"]).view(B, T, sh.kv_heads, sh.head_dim)
@@ -135,14 +129,7 @@ def attention_input_to_o(x: torch.Tensor, w: dict, sh: Shape, rope) -> torch.Ten
     cos, sin = rope
     q = (q * cos + _rotate_half(q) * sin).contiguous()
     k = (k * cos + _rotate_half(k) * sin).contiguous()
-    out = None
-    if _FLASH[0]:
-        try:
-            out = _attention_flash(q, k, v)
-        except RuntimeError:
-            _FLASH[0] = False
-    if out is None:
-        out = _attention_unfused(q, k, v, sh)
+    out = attention(q, k, v, sh)
     return out.transpose(1, 2).reshape(B, T, sh.heads * sh.head_dim)
 
 
@@ -158,50 +145,115 @@ class Timer:
         self.t[key] = self.t.get(key, 0.0) + s
 
 
-@torch.no_grad()
-def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | None = None, alpha: float = 0.5,
-          L: int = 12, plan_seed: int = 7000, chunk: int = 32, layers: int | None = None, weight_seed: int = 5000,
-          timer: Timer | None = None, keep: int = 0) -> dict:
-    """The build of a random-initialised stack on calibration token ids [S, T]: per layer and stage, the two streams'
-    statistics, the QEP target, the row-group trellis codes (a 2.3 bpw row plan per matrix, bits 1-4) and the
-    quantized weights written back. Returns {"codes": {"i.name": {"states": int32 [m, n], "scales": float64 [m],
-    "in_seed", "groups": the row plan, "packed": per group the code words (engine.pack_codes, read in place)}},
-    "weights": n, "bits": total rate bits, "redamped": {"i.first matrix": damping} for stages that needed more than
-    0.01, "bad": a device flag set if any packed row was not a trellis path, "L", "tables"}; export_codes writes the
-    codes as an opgraph-packed-1 artifact. chunk: calibration sequences per forward pass (the default takes config
-    5's 32 x 2048 tokens in one, about 17 GB of activations at its peak: fewer, larger products). token_w: per-token weights [S, T] (mean 1), or None. keep: the first `keep` layers
-    also return their stages' inputs and statistics under "stages" (for tests: {(i, s): (X_q, X_ref, H, D,
-    {name: W*}, in_seed, plans)}, on the CPU)."""
-    dev = E._abi.device()
-    main = torch.cuda.current_stream(dev)
-    side = torch.cuda.Stream(dev)  # default priority
-    S_, T = tokens.shape
-    nl = sh.layers if layers is None else layers
-    timer = timer or Timer()
-    tables = {b: (quantile_table(16, 0) if L == 16 else load_table(12, b)) for b in (1, 2, 3, 4)}
-    rope = tuple(t.to(dev) for t in rope_tables(T, sh, dev))
-    chunks = [slice(c, min(c + chunk, S_)) for c in range(0, S_, chunk)]
-    wt = None if token_w is None else [token_w[cs].reshape(-1).to(dev, torch.float32) for cs in chunks]
-    wcls = None if wt is None else [E.weight_classes(wc, include_zero=True) for wc in wt]
-    # the embedding (shared by both streams: it is not quantized here)
-    g = torch.Generator(device=dev).manual_seed(weight_seed * 1000 + 999)
-    emb = (torch.randn(sh.vocab, sh.hidden, generator=g, device=dev, dtype=torch.float32) * sh.std).to(torch.bfloat16)
-    hq = [emb[tokens[cs].to(dev)] for cs in chunks]
-    hr = [h.clone() for h in hq]
-    del emb
-    codes, n_w, bits, kept, redamped = {}, 0, 0.0, {}, {}
-    bad = torch.zeros(1, dtype=torch.int32, device=dev)  # set if any packed row is not a trellis path from state 0
+def synthetic_plans(sh: Shape, layers: int, plan_seed: int = 7000, program: str = "tr2x"):
+    """The synthetic build's plan and row plan: every linear of `layers` layers on `program` (the LM2 recipe's
+    row-trellis codes with the QEP cross term), and per matrix a seeded 2.3 bpw row plan (synthetic.row_plan: eight
+    groups, bits 1-4 drawn with the LM2 histogram), keyed as load_row_plan keys them."""
     shapes = matrix_shapes(sh)
-    for i in range(nl):
+    plan = {"linears": {f"{i}.{nm}": program for i in range(layers) for nm in shapes}}
+    row_plan = {f"model.layers.{i}.{nm}.weight": synthetic.row_plan(shapes[nm][0], plan_seed + 10 * i + STAGE_INDEX[nm])
+                for i in range(layers) for nm in shapes}
+    return plan, row_plan
+
+
+def active_shapes(sh: Shape, plan: dict, layers: int) -> dict:
+    """{full parameter name: shape} of the matrices a plan quantizes with a trellis program: the matrices a row plan
+    may name (quantize.py:1196-1207)."""
+    shapes = matrix_shapes(sh)
+    return {f"model.layers.{i}.{nm}.weight": shapes[nm] for i in range(layers) for nm in shapes
+            if parse(plan["linears"][f"{i}.{nm}"])[0] == "tr"}
+
+
+class StackBuild:
+    """The build of a random-initialised stack on calibration token ids [S, T], one decoder layer per call of
+    layer(): per stage, the two streams' statistics, the QEP target of the matrices whose program asks for it, the
+    codes of every matrix (row-trellis programs by their row-plan groups, in one batched sweep per stage; Lloyd-Max
+    programs by the width-1 sweep on the stage's factor; fp16 programs kept) and the reconstruction written back, so
+    the next stage's input already sees it; then both streams advance through the layer.
+
+    plan: {"linears": {"i.name": program}} (the plan JSON of quantize.py --program plan; programs tr<k>[x],
+    lm<b>[x], fp16; x: the QEP cross-term target W M at `alpha`); row_plan: {full parameter name: [{"group", "rows",
+    "bits"}]} as load_row_plan returns it, for trellis matrices (a trellis matrix without one is a single group at its
+    program's width). Both None: synthetic_plans() for the layers built.
+
+    chunk: calibration sequences per forward pass (the default takes config 5's 32 x 2048 tokens in one: fewer,
+    larger products). token_w: per-token weights [S, T] (mean 1), or None. keep: the first `keep` layers also return
+    their stages' inputs and statistics under "stages" (for tests: {(i, s): {"Xq", "Xr" (the stage inputs of both
+    streams, bf16 [tokens, n]), "H", "D" (float64), "targets" ({name: W*}), "in_seed", "plans" (the trellis matrices'
+    row groups), "U", "dead" (the stage factor)}}, on the GPU). redamp: a stage whose damped statistics are not positive definite is damped x10 and x100
+    (as ldlq_gpu.ldlq_factor retries, ldlq_gpu.py:19-23) and listed under "redamped"; without it (the default) it
+    raises LinAlgError, as the reference's Environment does (frame.py:521-522). kernels: an engine.KernelTimer; every
+    kernel of the stages then runs on the caller's stream, one after the other, each span timed with events and
+    credited with its algorithmic work ("hessian" N n (n + 1) flops, "cross_gram" 2 N n^2, "chol" 4 n^3 / 3, "rht"
+    HBM bytes, "qep_gemm", "block" trellis ops, "trailing" flops, "pack" bytes); without it the stage factor runs on a
+    second stream next to the QEP targets and each stage's row groups are swept on streams of their own."""
+
+    def __init__(self, tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | None = None,
+                 alpha: float = 0.5, L: int = 12, plan: dict | None = None, row_plan: dict | None = None,
+                 plan_seed: int = 7000, chunk: int = 32, layers: int | None = None, weight_seed: int = 5000,
+                 timer: Timer | None = None, keep: int = 0, redamp: bool = False, lam: float = LAM,
+                 seed_set: int = 0, kernels: E.KernelTimer | None = None):
+        dev = E._abi.device()
+        self.dev, self.sh, self.alpha, self.L, self.keep, self.redamp = dev, sh, alpha, L, keep, redamp
+        self.lam, self.seed_set, self.kernels = lam, seed_set, kernels
+        self.weight_seed = weight_seed
+        self.layers = sh.layers if layers is None else layers
+        if plan is None and row_plan is None:
+            plan, row_plan = synthetic_plans(sh, self.layers, plan_seed)
+        elif plan is None:
+            raise ValueError("a row plan needs the plan it refines")
+        for i in range(self.layers):
+            for nm in matrix_shapes(sh):
+                fam = parse(plan["linears"][f"{i}.{nm}"])[0]
+                if fam not in ("tr", "lm", "fp"):
+                    raise NotImplementedError(f"program family {fam!r} is not part of this path")
+        self.plan, self.row_plan = plan, row_plan or {}
+        self.main = torch.cuda.current_stream(dev)
+        self.side = torch.cuda.Stream(dev)  # default priority
+        self.timer = timer or Timer()
+        self.tables = {b: (quantile_table(16, 0) if L == 16 else load_table(12, b)) for b in (1, 2, 3, 4)}
+        S_, T = tokens.shape
+        self.rope = tuple(t.to(dev) for t in rope_tables(T, sh, dev))
+        chunks = [slice(c, min(c + chunk, S_)) for c in range(0, S_, chunk)]
+        self.wt = None if token_w is None else [token_w[cs].reshape(-1).to(dev, torch.float32) for cs in chunks]
+        self.wcls = None if self.wt is None else [E.weight_classes(wc, include_zero=True) for wc in self.wt]
+        # the embedding (shared by both streams: it is not quantized here)
+        g = torch.Generator(device=dev).manual_seed(weight_seed * 1000 + 999)
+        emb = (torch.randn(sh.vocab, sh.hidden, generator=g, device=dev, dtype=torch.float32) * sh.std).to(torch.bfloat16)
+        self.hq = [emb[tokens[cs].to(dev)] for cs in chunks]
+        self.hr = [h.clone() for h in self.hq]
+        del emb
+        self.codes, self.n_w, self.bits, self.kept, self.redamped = {}, 0, 0.0, {}, {}
+        self.bad = torch.zeros(1, dtype=torch.int32, device=dev)  # set if a packed row is not a trellis path from 0
+        self.next_layer = 0
+
+    def program(self, i: int, nm: str) -> str:
+        return self.plan["linears"][f"{i}.{nm}"]
+
+    def groups(self, i: int, nm: str) -> list:
+        """The row groups of a trellis matrix: its row-plan entry, else one group at its program's width."""
+        g = self.row_plan.get(f"model.layers.{i}.{nm}.weight")
+        if g is not None:
+            return g
+        m = matrix_shapes(self.sh)[nm][0]
+        return [{"group": 0, "rows": list(range(m)), "bits": parse(self.program(i, nm))[1]}]
+
+    @torch.no_grad()
+    def layer(self) -> int:
+        """Builds the next layer; returns its index."""
+        i = self.next_layer
+        if i >= self.layers:
+            raise ValueError(f"the stack has {self.layers} layers")
+        sh, dev, timer = self.sh, self.dev, self.timer
         t0 = time.perf_counter()
-        wr = layer_weights(i, sh, dev, weight_seed)  # the reference layer
+        wr = layer_weights(i, sh, dev, self.weight_seed)  # the reference layer
         wq = {k: v.clone() for k, v in wr.items()}  # quantized in place, stage by stage
         # the reference stream's stage inputs (its weights never change) and its output
         xr = {s: [] for s in range(4)}
         hr_next = []
-        for c, h in enumerate(hr):
+        for h in self.hr:
             x1 = rms_norm(h, wr["input_layernorm"], sh.eps)
-            a = attention_input_to_o(x1, wr, sh, rope)
+            a = attention_input_to_o(x1, wr, sh, self.rope)
             h1 = h + _lin(a, wr["self_attn.o_proj"])
             x2 = rms_norm(h1, wr["post_attention_layernorm"], sh.eps)
             m = torch.nn.functional.silu(_lin(x2, wr["mlp.gate_proj"])) * _lin(x2, wr["mlp.up_proj"])
@@ -211,16 +263,15 @@ def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | Non
         torch.cuda.synchronize()
         timer.add("forward", time.perf_counter() - t0)
         # the quantized stream, stage by stage
+        hq = self.hq
         h1q = [None] * len(hq)
         x2q = [None] * len(hq)
         for s, names in enumerate(STAGES):
             t1 = time.perf_counter()
             if s == 0:
-                xq = [rms_norm(h, wq["input_layernorm"], sh.eps) for h in hq]
-                x1q = xq
+                xq = x1q = [rms_norm(h, wq["input_layernorm"], sh.eps) for h in hq]
             elif s == 1:
-                xq = [attention_input_to_o(x, wq, sh, rope) for x in x1q]
-                aq = xq
+                xq = aq = [attention_input_to_o(x, wq, sh, self.rope) for x in x1q]
             elif s == 2:
                 h1q = [h + _lin(a, wq["self_attn.o_proj"]) for h, a in zip(hq, aq)]
                 xq = x2q = [rms_norm(h, wq["post_attention_layernorm"], sh.eps) for h in h1q]
@@ -230,62 +281,156 @@ def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | Non
             torch.cuda.synchronize()
             t2 = time.perf_counter()
             timer.add("forward", t2 - t1)
-            H, D = _stage_statistics(xqf, wt, xr[s], wcls)
-            torch.cuda.synchronize()
-            t25 = time.perf_counter()
-            timer.add("statistics", t25 - t2)
-            _, in_seed = matrix_seeds(i, names[0], 0, names[0])
-            # the stage's factor (rotation of H, damped inverse factor) on a second stream, next to the QEP targets
-            # (their own factor of H + lambda I and products) on this one: the two are independent
-            side.wait_stream(main)
-            with torch.cuda.stream(side):
-                factor = stage_factor(H, in_seed, 0.01)
-            targets = qep_targets(H, D - H, alpha, {nm: wr[nm] for nm in names})
-            main.wait_stream(side)
-            for t in factor:
-                t.record_stream(main)
-            torch.cuda.synchronize()
-            t3 = time.perf_counter()
-            timer.add("qep_targets", t3 - t25)
-            plans = {nm: synthetic.row_plan(shapes[nm][0], plan_seed + 10 * i + STAGE_INDEX[nm]) for nm in names}
-            # a stage whose statistics the damping of the reference's Environment cannot make positive definite (float32
-            # sums of a nearly singular H, as the o_proj input of a random-initialised stack with near-uniform
-            # attention gives) is damped more, as ldlq_gpu.ldlq_factor does (ldlq_gpu.py:19-23), and counted
-            for d in (0.01, 0.1, 1.0):
-                try:
-                    res = quantize_stage_row_groups(targets, plans, H, in_seed, L=L, tables=tables, damp=d,
-                                                    factor=factor if d == 0.01 else None)
-                    break
-                except E.LinAlgError:
-                    if d == 1.0:
-                        raise
-                    redamped[f"{i}.{names[0]}"] = 10 * d
-            if i < keep:
-                kept[(i, s)] = (torch.cat(xqf).cpu(), torch.cat(xr[s]).cpu(), H.cpu(), D.cpu(),
-                                {nm: t.cpu() for nm, t in targets.items()}, in_seed, plans)
-            for nm, (st, Srow) in res.items():
-                wq[nm] = _reconstruct(st, Srow, plans[nm], tables, in_seed).to(torch.bfloat16)
-                packed = []
-                for gp in plans[nm]:
-                    rows = torch.as_tensor(gp["rows"], dtype=torch.int64, device=dev)
-                    packed.append(E.pack_codes(st, gp["bits"], rows=rows, L=L, bad=bad)[0])
-                    bits += len(gp["rows"]) * shapes[nm][1] * gp["bits"] + 16 * len(gp["rows"])
-                codes[f"{i}.{nm}"] = {"states": st, "scales": Srow, "in_seed": in_seed, "groups": plans[nm],
-                                      "packed": packed}
-                n_w += shapes[nm][0] * shapes[nm][1]
-            torch.cuda.synchronize()
-            timer.add("quantize", time.perf_counter() - t3)
-            del xq, xqf, targets, H, D
+            self._stage(i, s, names, xqf, xr[s], wr, wq)
+            del xq, xqf
         # both streams through the layer (the quantized one with its last matrix now quantized)
         t4 = time.perf_counter()
-        hq = [h1 + _lin(torch.nn.functional.silu(_lin(x, wq["mlp.gate_proj"])) * _lin(x, wq["mlp.up_proj"]),
-                        wq["mlp.down_proj"]) for h1, x in zip(h1q, x2q)]
-        hr = hr_next
+        self.hq = [h1 + _lin(torch.nn.functional.silu(_lin(x, wq["mlp.gate_proj"])) * _lin(x, wq["mlp.up_proj"]),
+                             wq["mlp.down_proj"]) for h1, x in zip(h1q, x2q)]
+        self.hr = hr_next
         del xr, wr, wq, h1q, x2q
         torch.cuda.synchronize()
         timer.add("forward", time.perf_counter() - t4)
-    return {"codes": codes, "weights": n_w, "bits": bits, "stages": kept, "redamped": redamped, "bad": bad, "L": L,
-            "tables": tables}
+        self.next_layer = i + 1
+        return i
+
+    def _stage(self, i, s, names, xqf, xrf, wr, wq):
+        dev, timer, L = self.dev, self.timer, self.L
+        shapes = matrix_shapes(self.sh)
+        progs = {nm: self.program(i, nm) for nm in names}
+        coded = [nm for nm in names if parse(progs[nm])[0] != "fp"]
+        for nm in names:
+            if nm not in coded:  # fp16: the bf16 weights stay as they are, at 16 bits per weight
+                self.n_w += shapes[nm][0] * shapes[nm][1]
+                self.bits += 16.0 * shapes[nm][0] * shapes[nm][1]
+        if not coded:
+            return
+        t2 = time.perf_counter()
+        kt = self.kernels
+        cross = [nm for nm in coded if parse(progs[nm])[2]]
+        H, D = _stage_statistics(xqf, self.wt, xrf if cross else None, self.wcls, kt)
+        torch.cuda.synchronize()
+        t25 = time.perf_counter()
+        timer.add("statistics", t25 - t2)
+        _, in_seed = matrix_seeds(i, names[0], 0, names[0], self.seed_set)
+        if kt is None:
+            # the stage's factor (rotation of H, damped inverse factor) on a second stream, next to the QEP targets
+            # (their own factor of H + lambda I and products) on this one: the two are independent
+            self.side.wait_stream(self.main)
+            with torch.cuda.stream(self.side):
+                factor = stage_factor(H, in_seed, 0.01)
+        else:
+            factor = stage_factor(H, in_seed, 0.01, kt)
+        targets = qep_targets(H, D - H, self.alpha, {nm: wr[nm] for nm in cross}, self.lam, kt) if cross else {}
+        for nm in coded:
+            if nm not in targets:
+                targets[nm] = wr[nm].double()
+        if kt is None:
+            self.main.wait_stream(self.side)
+            for t in factor:
+                t.record_stream(self.main)
+        torch.cuda.synchronize()
+        t3 = time.perf_counter()
+        timer.add("qep_targets", t3 - t25)
+        trellis = [nm for nm in coded if parse(progs[nm])[0] == "tr"]
+        plans = {nm: self.groups(i, nm) for nm in trellis}
+        factor = self._factor(H, in_seed, factor, f"{i}.{names[0]}")
+        res = {}
+        if trellis:
+            res = quantize_stage_row_groups({nm: targets[nm] for nm in trellis}, plans, H, in_seed, L=L,
+                                            tables=self.tables, factor=factor, timer=kt)
+            if kt is not None:  # the sweep's algorithmic work: trellis ops and trailing-update flops per width
+                n = shapes[trellis[0]][1]
+                steps = sum(E.trellis_row_steps(n))
+                for bits in sorted({int(g["bits"]) for nm in trellis for g in plans[nm]}):
+                    m = sum(len(g["rows"]) for nm in trellis for g in plans[nm] if int(g["bits"]) == bits)
+                    kt.add_work("block", m * steps * E.viterbi_ops_per_row_step(L, bits))
+                    kt.add_work("trailing", E.trailing_flops(m, n))
+        if i < self.keep:
+            self.kept[(i, s)] = {"Xq": torch.cat(xqf), "Xr": torch.cat(xrf), "H": H, "D": D, "targets": targets,
+                                 "in_seed": in_seed, "plans": plans, "U": factor[0], "dead": factor[1]}
+        for nm in trellis:
+            st, Srow = res[nm]
+            m, n = st.shape
+            with E.span(kt, "rht", 16.0 * m * n):
+                wq[nm] = _reconstruct(st, Srow, plans[nm], self.tables, in_seed).to(torch.bfloat16)
+            packed = []
+            for gp in plans[nm]:
+                rows = torch.as_tensor(gp["rows"], dtype=torch.int64, device=dev)
+                r = len(gp["rows"])
+                with E.span(kt, "pack", 4.0 * r * n + 4.0 * r * ((n + 31) // 32) * gp["bits"]):
+                    packed.append(E.pack_codes(st, gp["bits"], rows=rows, L=L, bad=self.bad)[0])
+                self.bits += r * n * gp["bits"] + 16 * r
+            self.codes[f"{i}.{nm}"] = {"kind": "trellis", "states": st, "scales": Srow, "in_seed": in_seed,
+                                       "groups": plans[nm], "packed": packed}
+            self.n_w += shapes[nm][0] * shapes[nm][1]
+        for nm in coded:
+            if parse(progs[nm])[0] != "lm":
+                continue
+            b = parse(progs[nm])[1]
+            idx, Srow, levels = _lloyd_max_codes(targets[nm], factor, in_seed, b)
+            Q = levels[idx.long()] * Srow[:, None]
+            wq[nm] = E.rht_rows(Q, in_seed, inverse=True).to(torch.bfloat16)
+            m, n = idx.shape
+            self.codes[f"{i}.{nm}"] = {"kind": "scalar", "states": idx, "scales": Srow, "in_seed": in_seed,
+                                       "groups": [{"group": 0, "rows": list(range(m)), "bits": b}],
+                                       "levels": levels, "packed": [E.pack_codes(idx, b, trellis=False, bad=self.bad)[0]]}
+            self.bits += m * n * b + 16 * m
+            self.n_w += m * n
+        torch.cuda.synchronize()
+        timer.add("quantize", time.perf_counter() - t3)
+
+    def _factor(self, H, in_seed, factor, key):
+        """The stage factor at the Environment's damping; with redamp, x10 and x100 more where that is not positive
+        definite (one host synchronisation reads the pivot flag)."""
+        U, dead, info = factor
+        if int(info.item()) == 0:
+            return factor
+        if not self.redamp:
+            raise E.LinAlgError(f"stage {key}: linalg.cholesky: the leading minor of order {int(info.item())} is not "
+                                "positive-definite")
+        for d in (0.1, 1.0):
+            f = stage_factor(H, in_seed, d)
+            if int(f[2].item()) == 0:
+                self.redamped[key] = d
+                return f
+        raise E.LinAlgError(f"stage {key}: not positive definite even at damping 1.0")
+
+    def result(self) -> dict:
+        return {"codes": self.codes, "weights": self.n_w, "bits": self.bits, "stages": self.kept,
+                "redamped": self.redamped, "bad": self.bad, "L": self.L, "tables": self.tables,
+                "layers": self.next_layer}
+
+
+def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | None = None, alpha: float = 0.5,
+          L: int = 12, plan: dict | None = None, row_plan: dict | None = None, plan_seed: int = 7000, chunk: int = 32,
+          layers: int | None = None, weight_seed: int = 5000, timer: Timer | None = None, keep: int = 0,
+          redamp: bool = False, lam: float = LAM, seed_set: int = 0) -> dict:
+    """The whole build of a random-initialised stack (StackBuild, layer after layer). Returns {"codes": {"i.name":
+    {"kind": "trellis" | "scalar", "states": int32 [m, n] (trellis states, or Lloyd-Max level indices), "scales":
+    float64 [m], "in_seed", "groups": the row groups, "packed": per group the code words (engine.pack_codes, read in
+    place), "levels" (scalar)}}, "weights": n, "bits": total rate bits, "redamped": {"i.first matrix": damping} (with
+    redamp), "bad": a device flag set if any packed row was not a trellis path, "L", "tables", "layers"};
+    export_codes writes the codes as an opgraph-packed-1 artifact and saved_codes as the reference's --save-codes
+    dictionary."""
+    b = StackBuild(tokens, sh, token_w, alpha, L, plan, row_plan, plan_seed, chunk, layers, weight_seed, timer, keep,
+                   redamp, lam, seed_set)
+    for _ in range(b.layers):
+        b.layer()
+    return b.result()
+
+
+def _lloyd_max_codes(target: torch.Tensor, factor: tuple, in_seed: int, b: int):
+    """An lm<b> word of one matrix on the stage's factor (quantize.py:332-347, nested.py:155-192 with one rate and
+    out_rot=False): the rotated rows X = W R_in^T, their RMS scales S, the width-1 LDLQ of X / S onto the Lloyd-Max
+    levels (first minimum). Returns (indices int32 [m, n], S float64 [m], levels float64 [2^b]), on the GPU."""
+    from . import nested as N
+
+    U, dead, _ = factor
+    X, S = E.rht_rows(torch.as_tensor(target).to(U.device, torch.float64).contiguous(), in_seed, want_rms=True)
+    levels = torch.as_tensor(N.lloyd_max(b), dtype=torch.float64).to(U.device).contiguous()
+    idx = E.ldlq_scalar((X / S[:, None]).contiguous(), U, levels, mode=0, dead=dead)
+    return idx, S, levels
 
 
 STAGE_INDEX = {nm: j for j, nm in enumerate(n for st in STAGES for n in st)}
@@ -294,43 +439,82 @@ STAGE_INDEX = {nm: j for j, nm in enumerate(n for st in STAGES for n in st)}
 def export_codes(out: dict, path) -> dict:
     """The build's codes as an opgraph-packed-1 artifact at `path` (compiler_artifact.py:307-371, 491-531): per
     matrix model.layers.{i}.{name}.weight, its row groups in plan order with the words packed during the build, fp32
-    row scales, the stage rotation's signs and each group's fp32 table; semantic metadata {"matrices": ...} only
-    (the random-initialised stack has no dense state to store). Returns write_artifact's receipt."""
-    if out["L"] != artifact.STATE_BITS:
-        raise ValueError("opgraph-packed-1 stores 12-bit trellis states")
+    row scales, the stage rotation's signs and each group's fp32 table (trellis) or levels (scalar); semantic
+    metadata {"matrices": ...} only (the random-initialised stack has no dense state to store). Returns
+    write_artifact's receipt."""
     if int(out["bad"].item()):
         raise ValueError("states are not a row trellis from zero")
+    if any(rec["kind"] == "trellis" for rec in out["codes"].values()) and out["L"] != artifact.STATE_BITS:
+        raise ValueError("opgraph-packed-1 stores 12-bit trellis states")
     tables = {b: np.asarray(t, dtype=np.float64).astype(np.float32) for b, t in out["tables"].items()}
     tensors, matrices = {}, {}
     for key, rec in out["codes"].items():
         i, nm = key.split(".", 1)
         name = f"model.layers.{i}.{nm}.weight"
         m, n = rec["states"].shape
-        groups = [(np.asarray(gp["rows"], dtype=np.int64), int(gp["bits"]), "trellis", tables[int(gp["bits"])], words)
-                  for gp, words in zip(rec["groups"], rec["packed"])]
+        if rec["kind"] == "trellis":
+            groups = [(np.asarray(gp["rows"], dtype=np.int64), int(gp["bits"]), "trellis", tables[int(gp["bits"])],
+                       words) for gp, words in zip(rec["groups"], rec["packed"])]
+        else:
+            lv = rec["levels"].float().cpu().numpy()
+            groups = [(np.arange(m, dtype=np.int64), int(rec["groups"][0]["bits"]), "scalar", lv, rec["packed"][0])]
         t, matrices[name] = artifact.encode_groups(name, (m, n), groups, rec["scales"].float().cpu().numpy(),
                                                    artifact._input_signs(n, rec["in_seed"]))
         tensors.update(t)
     return artifact.write_artifact(path, tensors, {"matrices": matrices})
 
 
-def _stage_statistics(xq: list, w: list | None, xr: list, classes: list | None = None):
-    """H = X_q^T W X_q / N and D = X_ref^T W X_q / N over the chunks (quantize.py:1416-1470), float64 on the GPU.
-    classes: per chunk, engine.weight_classes(w[c], include_zero=True) (computed once per build)."""
+def saved_codes(out: dict) -> dict:
+    """The build's codes as the reference's --save-codes dictionary (quantize.py:513-565, 1541-1553): per full
+    parameter name, a row-trellis entry {"states": int16 [m, n] (state + 4096 * table_index), "scales": float32 [m],
+    "in_seed", "table": float32 [4096 * groups], "row_groups": [{"rows", "bits", "table_index"}], "trellis_layout":
+    "row"} or a scalar entry {"codes": uint8 [m, n], "scales", "in_seed", "levels": float32}, on the CPU."""
+    saved = {}
+    for key, rec in out["codes"].items():
+        i, nm = key.split(".", 1)
+        name = f"model.layers.{i}.{nm}.weight"
+        if rec["kind"] == "scalar":
+            saved[name] = {"codes": rec["states"].cpu().to(torch.uint8), "scales": rec["scales"].float().cpu(),
+                           "in_seed": int(rec["in_seed"]), "levels": rec["levels"].float().cpu()}
+            continue
+        if out["L"] != 12:
+            raise ValueError("saved row-group codes require a 12-bit state table")
+        st = rec["states"].cpu()
+        states = torch.empty(st.shape, dtype=torch.int16)
+        tabs, groups = [], []
+        for ti, gp in enumerate(rec["groups"]):
+            rows = torch.as_tensor(gp["rows"], dtype=torch.long)
+            states[rows] = (st[rows] + 4096 * ti).to(torch.int16)
+            tabs.append(torch.as_tensor(np.asarray(out["tables"][int(gp["bits"])]), dtype=torch.float32))
+            groups.append({"rows": rows, "bits": int(gp["bits"]), "table_index": ti})
+        saved[name] = {"states": states, "scales": rec["scales"].float().cpu(), "in_seed": int(rec["in_seed"]),
+                       "table": torch.cat(tabs), "row_groups": groups, "trellis_layout": "row"}
+    return saved
+
+
+def _stage_statistics(xq: list, w: list | None, xr: list | None, classes: list | None = None,
+                      kt: E.KernelTimer | None = None):
+    """H = X_q^T W X_q / N and D = X_ref^T W X_q / N (None without xr) over the chunks (quantize.py:1416-1470),
+    float64 on the GPU. classes: per chunk, engine.weight_classes(w[c], include_zero=True) (computed once per
+    build). kt: spans "hessian" (N n (n + 1) flops, the unique entries) and "cross_gram" (2 N n^2 flops)."""
     dev = xq[0].device
     n = xq[0].shape[1]
     H = torch.zeros(n, n, dtype=torch.float32, device=dev)
-    D = torch.zeros(n, n, dtype=torch.float32, device=dev)
+    D = None if xr is None else torch.zeros(n, n, dtype=torch.float32, device=dev)
     ntok = 0
-    for c, (a, b) in enumerate(zip(xq, xr)):
+    for c, a in enumerate(xq):
         a = a.contiguous()
-        b = b.contiguous()
+        N = a.shape[0]
         wc = None if w is None else w[c]
         cc = None if classes is None else classes[c]
-        E.hessian_accum(H, a, wc, classes=cc)
-        E.cross_gram_accum(D, b, a, wc, classes=cc)
-        ntok += a.shape[0]
-    return E.hessian_finalize(H, float(ntok)), (D / ntok).double()
+        with E.span(kt, "hessian", float(N) * n * (n + 1)):
+            E.hessian_accum(H, a, wc, classes=cc)
+        if D is not None:
+            b = xr[c].contiguous()
+            with E.span(kt, "cross_gram", 2.0 * N * n * n):
+                E.cross_gram_accum(D, b, a, wc, classes=cc)
+        ntok += N
+    return E.hessian_finalize(H, float(ntok)), None if D is None else (D / ntok).double()
 
 
 def _reconstruct(states: torch.Tensor, S: torch.Tensor, groups: list, tables: dict, in_seed: int) -> torch.Tensor:
