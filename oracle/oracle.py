@@ -16,6 +16,7 @@ Parity status of each function (what pins it is listed in the test named beside 
   sweep              equals the C sweeps (ldlq_scalar, ldlq_trellis) under their projections
   column_trellis_*   per-sequence viterbi (pinned above) on the reshaped columns; brute force for tiny L
   hadamard / rht     orthogonality, |H_ij| = 1/sqrt(n), Kronecker closed forms
+  rht_apply          equals the products with the dense rht(n, seed) both ways (tests/test_oracle.py)
   hessian            fp64 closed form X^T diag(w) X / N
   kl_rows            fp64 closed form; KL(p||p) = 0; Gaussian-logit closed form
   lloyd_max          Max (1960) MSE table; GAUSS2 levels; reference vectors
@@ -282,6 +283,21 @@ def rht_signs(n: int, seed: int) -> np.ndarray:
 
 def rht(n: int, seed: int) -> np.ndarray:
     return hadamard(n) * rht_signs(n, seed)[None, :]
+
+
+def rht_apply(X, seed: int, inverse: bool = False) -> np.ndarray:
+    """X @ rht(n, seed).T (the incoherent rows, codes.py:430), or with inverse X @ rht(n, seed) (a reconstruction,
+    codes.py:459-462), through the factors hadamard(n) = kron(A, B) / sqrt(n) instead of the dense matrix: for a row
+    z of length a b laid out as an a x b matrix Z, z kron(A, B)^T = vec(A Z B^T) and z kron(A, B) = vec(A^T Z B)."""
+    X = np.asarray(X, dtype=np.float64)
+    m, n = X.shape
+    A, B = hadamard_factors(n)
+    s = rht_signs(n, seed)
+    if not inverse:
+        Z = (X * s[None, :]).reshape(m, len(A), len(B))
+        return (A @ Z @ B.T).reshape(m, n) / math.sqrt(n)
+    Z = X.reshape(m, len(A), len(B))
+    return (A.T @ Z @ B).reshape(m, n) / math.sqrt(n) * s[None, :]
 
 
 # ----------------------------------------------------------------------------- statistics and scales

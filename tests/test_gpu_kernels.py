@@ -328,8 +328,9 @@ def test_ldlq_trellis_L16_matches_reference(E, golden, config12):
 
 @pytest.mark.parametrize("k", [1, 3, 4])
 def test_ldlq_trellis_L16_other_widths_match_oracle(E, k):
-    """The 16-bit-state sweep at the widths a row plan also assigns (k = 1: the quarter-window kernel; k = 3, 4: the
-    minima-exchange kernel), 3 rows x 272 columns (two lazy blocks, the second ragged), against the C oracle."""
+    """The 16-bit-state sweep at the widths a row plan also assigns (k = 1: the minima-exchange kernel with its
+    back-pointers in a workspace; k = 3, 4: the minima-exchange kernel), 3 rows x 272 columns (two lazy blocks, the
+    second ragged), against the C oracle."""
     from lookatmyquant_amd.tables import quantile_table
 
     rng = np.random.default_rng(40 + k)
@@ -343,6 +344,29 @@ def test_ldlq_trellis_L16_other_widths_match_oracle(E, k):
     st = E.ldlq_trellis(cuda(X), cuda(S), cuda(U), cuda(tab), 16, k).cpu().numpy()
     ref = O.ldlq_trellis(X, U, S, tab, 16, k)
     assert np.array_equal(st, ref)
+
+
+def test_ldlq_trellis16_k1_without_workspace_matches_oracle(E, monkeypatch):
+    """lamq_ldlq_trellis16_block at L = 16, k = 1, the entry point without a workspace (the quarter-window kernel,
+    full path costs exchanged through LDS): the same states as the oracle and as the workspace kernel, 3 rows x 272
+    columns."""
+    from lookatmyquant_amd.tables import quantile_table
+
+    rng = np.random.default_rng(41)
+    m, n = 3, 272
+    Xa = rng.standard_normal((600, n))
+    _, U, _ = O.environment(Xa.T @ Xa / 600)
+    X = rng.standard_normal((m, n))
+    S = O.row_scale(X)
+    tab = np.asarray(quantile_table(16, 0), dtype=np.float64)
+    say("ldlq trellis L=16 k=1, 3 x 272, workspace kernel")
+    with_ws = E.ldlq_trellis(cuda(X), cuda(S), cuda(U), cuda(tab), 16, 1).cpu().numpy()
+    monkeypatch.setattr(E._abi.lib(), "lamq_ldlq_trellis16_block_workspace_size", lambda *a: 0)
+    say("ldlq trellis L=16 k=1, 3 x 272, no workspace (lamq_ldlq_trellis16_block)")
+    without = E.ldlq_trellis(cuda(X), cuda(S), cuda(U), cuda(tab), 16, 1).cpu().numpy()
+    ref = O.ldlq_trellis(X, U, S, tab, 16, 1)
+    assert np.array_equal(with_ws, ref)
+    assert np.array_equal(without, ref)
 
 
 def test_ldlq_trellis_ragged_matches_oracle(E, tables):
@@ -493,6 +517,30 @@ def test_hessian_zero_weight_class(E):
     w[rng.random(N) < 0.1] = 10.0
     say("hessian with zero-weight tokens")
     Hg = E.hessian(torch.from_numpy(X).to(torch.bfloat16).cuda(), torch.from_numpy(w).cuda()).cpu().numpy()
+    ref = O.hessian(X, w)
+    err = np.abs(Hg - ref).max() / np.abs(ref).max()
+    say(f"  max |H - H64| / max |H64| = {err:.3e}")
+    assert err < 1e-4
+
+
+def test_hessian_classes_that_leave_tokens_out(E):
+    """Classes made without the zero class (weight_classes(w, include_zero=False)) leave the zero-weight tokens out:
+    those tokens count with weight 0, not at the most frequent weight (each class then runs over its own rows)."""
+    from lookatmyquant_amd import synthetic
+
+    N, n = 3000, 264
+    X = synthetic.calibration(N, n, 34, 35)
+    rng = np.random.default_rng(36)
+    w = np.ones(N, np.float32)
+    w[rng.random(N) < 0.3] = 0.0
+    w[rng.random(N) < 0.1] = 4.0
+    wg = torch.from_numpy(w).cuda()
+    classes = E.weight_classes(wg, include_zero=False)
+    assert sum(r.numel() for _, r in classes) < N
+    say("hessian with classes that leave the zero-weight tokens out")
+    H = torch.zeros(n, n, dtype=torch.float32, device="cuda")
+    E.hessian_accum(H, torch.from_numpy(X).to(torch.bfloat16).cuda(), wg, classes=classes)
+    Hg = E.hessian_finalize(H, float(N)).cpu().numpy()
     ref = O.hessian(X, w)
     err = np.abs(Hg - ref).max() / np.abs(ref).max()
     say(f"  max |H - H64| / max |H64| = {err:.3e}")

@@ -191,10 +191,72 @@ def test_bench_refuses_more_than_one_gpu():
     assert r.returncode == 2 and "one GPU" in r.stderr
 
 
-def test_bench_workload_counts():
-    sys.path.insert(0, str(REPO))
-    import bench
+def test_workload_counts():
+    from lookatmyquant_amd import engine as E
 
-    assert sum(bench.row_steps(960, 16, 8, 128)) == 1432  # (n/16 - 1) * 24 + 16
-    assert sum(bench.row_steps(9728, 16, 8, 128)) == 14584
-    assert bench.viterbi_ops_per_row_step(16, 2) == 245760
+    assert sum(E.trellis_row_steps(960, 16, 8, 128)) == 1432  # (n/16 - 1) * 24 + 16
+    assert sum(E.trellis_row_steps(9728, 16, 8, 128)) == 14584
+    assert E.viterbi_ops_per_row_step(16, 2) == 245760
+    assert E.viterbi_ops_per_row_step(12, 2) == 15360
+    # sum over blocks of 2 m (b1 - b0) (n - b1), against the closed form for n a multiple of 128: 2 m 128^2 B(B-1)/2
+    assert E.trailing_flops(7, 1280) == 2 * 7 * 128 * 128 * 10 * 9 / 2
+
+
+def test_trellis_tables_must_have_two_to_the_L_entries():
+    """A table shorter than 2^L would be read past its end by the search kernels: refused before any launch."""
+    from lookatmyquant_amd import engine as E
+    from lookatmyquant_amd.tables import load_table, quantile_table
+
+    t12 = torch.from_numpy(load_table(12, 2).copy())
+    X = torch.zeros(4, 64, dtype=torch.float64)
+    for L, t64, t32 in ((16, t12, None), (12, t12[:100], None), (12, t12, t12[:4095].float()),
+                        (16, torch.from_numpy(np.asarray(quantile_table(16, 0), dtype=np.float64)), t12.float())):
+        with pytest.raises(ValueError, match="2\\^L"):
+            E.ldlq_trellis_groups(X, torch.ones(4, dtype=torch.float64), torch.eye(64, dtype=torch.float64),
+                                  [(4, 2, t64, t32)], L)
+    with pytest.raises(ValueError):
+        E.check_tables([(4, 2, t12, None)], 17)
+    E.check_tables([(4, 2, t12, t12.float())], 12)  # the right sizes pass
+
+
+def test_stage_without_tables_refuses_other_state_bits():
+    from lookatmyquant_amd.quantize import quantize_stage_row_groups
+
+    with pytest.raises(ValueError, match="12-bit tables"):
+        quantize_stage_row_groups({"a": torch.zeros(64, 64)}, {"a": [{"rows": list(range(64)), "bits": 2}]},
+                                  torch.eye(64), 1, L=16, factor=(None, None, torch.zeros(1, dtype=torch.int32)))
+
+
+def test_synthetic_plans_are_valid_row_plans(tmp_path):
+    """The synthetic build's row plan written as rowgroup-plan-1 reads back through the reference's validation rules
+    (rowgroup_alloc.py:268-307) for the matrices its plan puts on a trellis, at 2.3 bpw."""
+    from lookatmyquant_amd import stack
+    from lookatmyquant_amd.rowplan import load_row_plan, write_row_plan
+
+    sh = stack.Shape()
+    plan, rp = stack.synthetic_plans(sh, 2)
+    assert set(plan["linears"].values()) == {"tr2x"} and len(plan["linears"]) == 14
+    shapes = stack.active_shapes(sh, plan, 2)
+    write_row_plan(tmp_path / "r.json", rp, shapes)
+    back, manifest = load_row_plan(tmp_path / "r.json", shapes)
+    assert manifest["matrices"] == 14 and back.keys() == rp.keys()
+    for name, groups in back.items():
+        assert [g["rows"] for g in groups] == [g["rows"] for g in rp[name]]
+    bits = sum(len(g["rows"]) * shapes[nm][1] * g["bits"] for nm, gs in back.items() for g in gs)
+    assert abs(bits / sum(m * n for m, n in shapes.values()) - 2.3) < 0.06
+    # a matrix on an fp16 program is not active for a row plan
+    plan["linears"]["1.mlp.down_proj"] = "fp16"
+    assert "model.layers.1.mlp.down_proj.weight" not in stack.active_shapes(sh, plan, 2)
+
+
+def test_cli_checks_its_arguments(tmp_path):
+    """quantize.py's entry point: the row trellis is width 16, look 8; --program plan needs --plan; unknown programs
+    are refused before any work (no GPU is touched)."""
+    from lookatmyquant_amd.quantize import main
+
+    with pytest.raises(NotImplementedError):
+        main(["--program", "tr2x", "--trellis-rows", "8,4", "--out", str(tmp_path / "o.json")])
+    with pytest.raises(SystemExit):
+        main(["--program", "plan", "--out", str(tmp_path / "o.json")])
+    with pytest.raises(ValueError):
+        main(["--program", "tr9y", "--out", str(tmp_path / "o.json")])

@@ -325,6 +325,19 @@ def test_hadamard_orders(n, golden):
         assert np.array_equal(A, golden("misc")[f"had_{n}_A"]) and np.array_equal(B, golden("misc")[f"had_{n}_B"])
 
 
+@pytest.mark.parametrize("n", [64, 960, 2560])
+def test_rht_apply_is_the_dense_rotation(n):
+    """The factored rotation equals the products with the dense R = rht(n, seed) both ways, and the two undo each
+    other (a transposed factor, a missing sign or a wrong 1/sqrt(n) breaks one of these)."""
+    rng = np.random.default_rng(n)
+    X = rng.standard_normal((5, n))
+    R = O.rht(n, 1001)
+    Y = O.rht_apply(X, 1001)
+    assert np.abs(Y - X @ R.T).max() < 1e-12
+    assert np.abs(O.rht_apply(X, 1001, inverse=True) - X @ R).max() < 1e-12
+    assert np.abs(O.rht_apply(Y, 1001, inverse=True) - X).max() < 1e-12
+
+
 def test_hessian_is_the_weighted_sum_of_outer_products():
     rng = np.random.default_rng(8)
     X = rng.standard_normal((9, 5))
