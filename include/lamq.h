@@ -242,6 +242,17 @@ size_t lamq_kl_workspace_size(int64_t T);
 int lamq_kl_rows(const uint16_t* ref, const uint16_t* q, int64_t T, int64_t V, int64_t ldr, int64_t ldq,
                  const float* w, float* kl, double* sums, void* workspace, size_t workspace_bytes, void* stream);
 
+/* lamq_kl_rows without a workspace and without any allocation: no counterpart in the reference. For callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving or measurement loops, harnesses that
+ * forbid hipMalloc). The per-token partials live in a static device array of LAMQ_KL_NOALLOC_MAX_T * 2 float64
+ * (1 MiB) that each GPU holds until the process ends; its address is looked up once per device on the first call
+ * (the stream's device must be current). T > LAMQ_KL_NOALLOC_MAX_T returns LAMQ_EINVAL before any launch. Every
+ * entry of the array a call reads it has written first, so nothing needs clearing; calls that overlap on one GPU
+ * (two streams at once) share the array and race. Same arguments and results as lamq_kl_rows otherwise. */
+#define LAMQ_KL_NOALLOC_MAX_T 65536
+int lamq_kl_rows_noalloc(const uint16_t* ref, const uint16_t* q, int64_t T, int64_t V, int64_t ldr, int64_t ldq,
+                         const float* w, float* kl, double* sums, void* stream);
+
 /* ------------------------------------------------------------------------------------------------
  * Pack row-trellis states into the opgraph-packed-1 bitstream.
  * Replaces compiler_artifact.py:225-240 (pack_symbols) and :261-284 (valid_path, pack_trellis):

@@ -8,6 +8,8 @@
 // partials in a fixed order, so the result does not depend on scheduling.
 #include "common.h"
 
+#include <mutex>
+
 __device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xFFFF0000u); }
 
@@ -154,17 +156,12 @@ __global__ __launch_bounds__(256) void kl_sum_kernel(const double* __restrict__ 
 
 extern "C" size_t lamq_kl_workspace_size(int64_t T) { return T > 0 ? (size_t)T * 2 * sizeof(double) : 0; }
 
-extern "C" int lamq_kl_rows(const uint16_t* ref, const uint16_t* q, int64_t T, int64_t V, int64_t ldr, int64_t ldq,
-                            const float* w, float* kl, double* sums, void* workspace, size_t workspace_bytes, void* stream)
+// The two launches of both entry points: per-row KL into kl, w*kl and w into wkl[0..T), wkl[T..2T), then their sums.
+static int kl_launch(const uint16_t* ref, const uint16_t* q, int64_t T, int64_t V, int64_t ldr, int64_t ldq,
+                     const float* w, float* kl, double* sums, double* wkl, hipStream_t s)
 {
-    if (!ref || !q || !kl || T < 0 || V < 1 || ldr < V || ldq < V) return LAMQ_EINVAL;
-    if (T == 0) return LAMQ_OK;
-    if (!workspace || workspace_bytes < lamq_kl_workspace_size(T)) return LAMQ_EINVAL;
-    if (T > 0x7fffffff) return LAMQ_EUNSUP;
     const int vec = ((uintptr_t)ref % 16 == 0) && ((uintptr_t)q % 16 == 0) && (ldr % 8 == 0) && (ldq % 8 == 0);
-    double* wkl = reinterpret_cast<double*>(workspace);
     double* wt = wkl + T;
-    hipStream_t s = as_stream(stream);
     hipLaunchKernelGGL(kl_rows_kernel, dim3((unsigned)T), dim3(256), 0, s, ref, q, V, ldr, ldq, w, kl, wkl, wt, vec);
     LAMQ_LAUNCH_CHECK();
     if (sums) {
@@ -172,4 +169,61 @@ extern "C" int lamq_kl_rows(const uint16_t* ref, const uint16_t* q, int64_t T, i
         LAMQ_LAUNCH_CHECK();
     }
     return LAMQ_OK;
+}
+
+extern "C" int lamq_kl_rows(const uint16_t* ref, const uint16_t* q, int64_t T, int64_t V, int64_t ldr, int64_t ldq,
+                            const float* w, float* kl, double* sums, void* workspace, size_t workspace_bytes, void* stream)
+{
+    if (!ref || !q || !kl || T < 0 || V < 1 || ldr < V || ldq < V) return LAMQ_EINVAL;
+    if (T == 0) return LAMQ_OK;
+    if (!workspace || workspace_bytes < lamq_kl_workspace_size(T)) return LAMQ_EINVAL;
+    if (T > 0x7fffffff) return LAMQ_EUNSUP;
+    return kl_launch(ref, q, T, V, ldr, ldq, w, kl, sums, reinterpret_cast<double*>(workspace), as_stream(stream));
+}
+
+// The allocation-free variant's partials: one array per GPU, for the life of the process. In host code `scratch`
+// names a host-side stand-in, not device memory; kernels get the device address hipGetSymbolAddress returns for the
+// current device, looked up once per device and kept in kl_scratch_ptr.
+static __device__ __align__(256) double scratch[2 * LAMQ_KL_NOALLOC_MAX_T];
+
+#define LAMQ_MAX_DEVICES 64
+static std::mutex kl_scratch_mu;
+static void* kl_scratch_ptr[LAMQ_MAX_DEVICES];
+
+// The device address of this GPU's scratch array (the current device, which must be the stream's).
+static int kl_scratch(hipStream_t s, double** out)
+{
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= LAMQ_MAX_DEVICES) return LAMQ_EUNSUP;
+    if (s) {
+        hipDevice_t sdev = -1;
+        e = hipStreamGetDevice(s, &sdev);
+        if (e != hipSuccess) return (int)e;
+        if (sdev != dev) return LAMQ_EINVAL;
+    }
+    std::lock_guard<std::mutex> lock(kl_scratch_mu);
+    if (!kl_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        if (!p) return LAMQ_EINVAL;
+        kl_scratch_ptr[dev] = p;
+    }
+    *out = static_cast<double*>(kl_scratch_ptr[dev]);
+    return LAMQ_OK;
+}
+
+extern "C" int lamq_kl_rows_noalloc(const uint16_t* ref, const uint16_t* q, int64_t T, int64_t V, int64_t ldr,
+                                    int64_t ldq, const float* w, float* kl, double* sums, void* stream)
+{
+    if (!ref || !q || !kl || T < 0 || V < 1 || ldr < V || ldq < V) return LAMQ_EINVAL;
+    if (T > LAMQ_KL_NOALLOC_MAX_T) return LAMQ_EINVAL;
+    if (T == 0) return LAMQ_OK;
+    hipStream_t s = as_stream(stream);
+    double* wkl = nullptr;
+    const int rc = kl_scratch(s, &wkl);
+    if (rc != LAMQ_OK) return rc;
+    return kl_launch(ref, q, T, V, ldr, ldq, w, kl, sums, wkl, s);
 }

@@ -637,6 +637,36 @@ def kl_rows(ref: torch.Tensor, q: torch.Tensor, w: torch.Tensor | None = None):
     return kl, sums
 
 
+KL_NOALLOC_MAX_T = 65536  # LAMQ_KL_NOALLOC_MAX_T
+
+
+def kl_rows_noalloc(ref: torch.Tensor, q: torch.Tensor, kl: torch.Tensor, sums: torch.Tensor | None,
+                    w: torch.Tensor | None = None):
+    """kl_rows into caller-owned outputs (kl [T] float32, sums [2] float64 or None) through lamq_kl_rows_noalloc,
+    which allocates nothing: its partials live in a static per-device array of KL_NOALLOC_MAX_T tokens, shared by
+    every call on that GPU (calls that overlap on one GPU race). w, if given, must already be a contiguous float32
+    tensor on the device. T > KL_NOALLOC_MAX_T raises ValueError before any launch."""
+    need(ref, torch.bfloat16, "ref", 2)
+    need(q, torch.bfloat16, "q", 2)
+    need(kl, torch.float32, "kl", 1)
+    if ref.shape != q.shape or kl.numel() != ref.shape[0]:
+        raise ValueError("ref and q must have the same shape and kl one entry per row")
+    T, V = ref.shape
+    if T > KL_NOALLOC_MAX_T:
+        raise ValueError(f"kl_rows_noalloc takes at most {KL_NOALLOC_MAX_T} tokens per call (got {T})")
+    if sums is not None:
+        need(sums, torch.float64, "sums", 1)
+        if sums.numel() < 2:
+            raise ValueError("sums must hold two float64 values")
+    if w is not None:
+        need(w, torch.float32, "w", 1)
+        if w.numel() != T:
+            raise ValueError("one weight per token")
+    check(lib().lamq_kl_rows_noalloc(ptr(ref), ptr(q), T, V, ld(ref), ld(q), ptr(w), ptr(kl), ptr(sums),
+                                     stream(ref.device)), "kl_rows_noalloc")
+    return kl, sums
+
+
 # ----------------------------------------------------------------------------- packing (compiler_artifact.py:276-284)
 
 
