@@ -64,13 +64,18 @@ int lamq_viterbi_rows(const float* x, int64_t B, int T, int64_t ldx, const float
  *   states   [m, n] int32 output for columns [b0, b1) (row stride lds)
  *   Z        [m, b1-b0] float64 output: the block's refit coefficients z = E U_BB^-1 (row stride ldZ),
  *            the left operand of the trailing update
+ *   pre      0 <= pre <= min(b0, 1024): the look-ahead columns past b1 lack the trailing updates (syntax.py:123)
+ *            of the pre columns before b0, earlier blocks of the caller's run (the caller updates the columns past
+ *            the run in one product after the run); the block reads them as T[:, c] - Z[:, -pre:0] U[b0-pre:b0, c],
+ *            Z's pre columns before the block holding those blocks' coefficients (ldZ >= pre + b1 - b0).
+ *            pre = 0: T already holds every earlier update.
  * width divides lazy = b1-b0 except in the last block; width <= 16, width + look <= 24; b1 - b0 <= 128
  * (the reference runs 16, 8 and 128). Supported: 2 <= L <= 12 with 1 <= k <= min(4, L-1).
  * ---------------------------------------------------------------------------------------------- */
 int lamq_ldlq_trellis_block(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU,
                             const double* S, const double* table64, const float* table32, int L, int k,
                             int64_t b0, int64_t b1, int width, int look, int32_t* state, int32_t* states,
-                            int64_t lds, double* Z, int64_t ldZ, void* stream);
+                            int64_t lds, double* Z, int64_t ldZ, int64_t pre, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
  * One lazy block [b0, b1) of the width-1 LDLQ sweep onto a scalar set of K levels.
@@ -101,7 +106,7 @@ int lamq_viterbi16_rows(const float* x, int64_t B, int T, int64_t ldx, const uin
 int lamq_ldlq_trellis16_block(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU,
                               const double* S, const double* table64, const uint16_t* table16, int L, int k,
                               int64_t b0, int64_t b1, int width, int look, int32_t* state, int32_t* states,
-                              int64_t lds, double* Z, int64_t ldZ, void* stream);
+                              int64_t lds, double* Z, int64_t ldZ, int64_t pre, void* stream);
 
 /* The same fused block with the back-pointers in a caller's workspace: lamq_ldlq_trellis16_block's results, bit for
  * bit. With 2^15 groups (L = 16, k = 1) the minima-exchange search's 128 KB of group minima leave no LDS for the
@@ -112,8 +117,8 @@ size_t lamq_ldlq_trellis16_block_workspace_size(int64_t m, int L, int k);
 int lamq_ldlq_trellis16_block_ws(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU,
                                  const double* S, const double* table64, const uint16_t* table16, int L, int k,
                                  int64_t b0, int64_t b1, int width, int look, int32_t* state, int32_t* states,
-                                 int64_t lds, double* Z, int64_t ldZ, void* workspace, size_t workspace_bytes,
-                                 void* stream);
+                                 int64_t lds, double* Z, int64_t ldZ, int64_t pre, void* workspace,
+                                 size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
  * The lazy trailing update T[:, b1:n] -= Z @ U[b0:b1, b1:n] on fp64 MFMA.

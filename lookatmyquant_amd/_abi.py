@@ -21,17 +21,17 @@ SIGNATURES = {
     "lamq_viterbi_workspace_size": (_c_size, [_c_i64, _c_int, _c_int, _c_int]),
     "lamq_viterbi_rows": (_c_int, [_p, _c_i64, _c_int, _c_i64, _p, _c_int, _c_int, _p, _p, _c_i64, _p, _c_size, _p]),
     "lamq_ldlq_trellis_block": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _p, _p, _c_int, _c_int, _c_i64, _c_i64,
-                                         _c_int, _c_int, _p, _p, _c_i64, _p, _c_i64, _p]),
+                                         _c_int, _c_int, _p, _p, _c_i64, _p, _c_i64, _c_i64, _p]),
     "lamq_ldlq_scalar_block": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _p, _c_int, _c_int, _c_i64, _c_i64, _p,
                                         _c_i64, _p, _c_i64, _p]),
     "lamq_viterbi16_workspace_size": (_c_size, [_c_i64, _c_int, _c_int, _c_int]),
     "lamq_viterbi16_rows": (_c_int, [_p, _c_i64, _c_int, _c_i64, _p, _c_int, _c_int, _p, _p, _c_i64, _p, _c_size, _p]),
     "lamq_ldlq_trellis16_block": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _p, _p, _c_int, _c_int, _c_i64,
-                                           _c_i64, _c_int, _c_int, _p, _p, _c_i64, _p, _c_i64, _p]),
+                                           _c_i64, _c_int, _c_int, _p, _p, _c_i64, _p, _c_i64, _c_i64, _p]),
     "lamq_ldlq_trellis16_block_workspace_size": (ctypes.c_size_t, [_c_i64, _c_int, _c_int]),
     "lamq_ldlq_trellis16_block_ws": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _p, _p, _c_int, _c_int, _c_i64,
-                                              _c_i64, _c_int, _c_int, _p, _p, _c_i64, _p, _c_i64, _p, ctypes.c_size_t,
-                                              _p]),
+                                              _c_i64, _c_int, _c_int, _p, _p, _c_i64, _p, _c_i64, _c_i64, _p,
+                                              ctypes.c_size_t, _p]),
     "lamq_trailing_update_f64": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _c_i64, _c_i64, _c_i64, _p]),
     "lamq_gemm_sub_f64": (_c_int, [_p, _c_i64, _p, _c_i64, _p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _p]),
     "lamq_refit_step": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _c_i64, _c_i64, _c_int, _c_i64, _c_i64, _p,

@@ -115,6 +115,9 @@ __global__ __launch_bounds__(256) void gemm_sub_f64_kernel(double* C, int64_t ld
 // [k][col] B) and 16-byte aligned operands (gemm_sub_f64 checks; other shapes take the kernel above).
 #define G8_BM 128
 #define G8_BK 16
+#ifndef LAMQ_PANEL_MAX_TILES128
+#define LAMQ_PANEL_MAX_TILES128 1024  // short products with fewer 128-tiles than this take the 64-tile panel kernel
+#endif
 #define LAMQ_TRI_KGE 1
 #define LAMQ_TRI_KLE 2
 
@@ -198,9 +201,24 @@ gemm128_f64_kernel(double* __restrict__ C, int64_t ldc, const double* __restrict
         piece((int64_t)st0 * BK, st0 & 1, q, 0);
         piece((int64_t)st0 * BK, st0 & 1, q, 1);
     }
+    // D layout (16x16): lane l, register v -> row 4*v + l/16, column l%16. C is read two row-groups of 16 ahead of
+    // its writes: one wait counter covers loads and stores alike, so a read issued after a write would wait for it.
+    auto cload = [&](int i, double(&g)[4][4]) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int64_t row = tr + wr + 16 * i + 4 * v + lk;
+                const int64_t col = tc + wc + 16 * j + li;
+                g[j][v] = (row < M && col < N && (!LOWER || col <= row)) ? C[row * ldc + col] : 0.0;
+            }
+    };
+    double g0[4][4], g1[4][4];
     for (int st = st0; st < nst; ++st) {
         wait_vm<0>();     // this wave's loads of stage st have landed
         __syncthreads();  // everyone's; the other buffer (stage st - 1) is free
+        // the first row-group of C is read during the last stage's MFMAs
+        if (st == nst - 1) cload(0, g0);
         const int buf = st & 1;
         const uint8_t* As = lds[buf][0];
         const uint8_t* Bs = lds[buf][1];
@@ -225,19 +243,9 @@ gemm128_f64_kernel(double* __restrict__ C, int64_t ldc, const double* __restrict
             }
         }
     }
+    if (st0 >= nst) cload(0, g0);  // no stage ran
+    cload(1, g1);
     wait_vm<0>();
-    // D layout (16x16): lane l, register v -> row 4*v + l/16, column l%16. C is read two row-groups of 16 ahead of
-    // its writes: one wait counter covers loads and stores alike, so a read issued after a write would wait for it.
-    auto cload = [&](int i, double(&g)[4][4]) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int64_t row = tr + wr + 16 * i + 4 * v + lk;
-                const int64_t col = tc + wc + 16 * j + li;
-                g[j][v] = (row < M && col < N && (!LOWER || col <= row)) ? C[row * ldc + col] : 0.0;
-            }
-    };
     auto cstore = [&](int i, const double(&g)[4][4]) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -248,9 +256,6 @@ gemm128_f64_kernel(double* __restrict__ C, int64_t ldc, const double* __restrict
                 if (row < M && col < N && (!LOWER || col <= row)) C[row * ldc + col] = g[j][v] - acc[i][j][v];
             }
     };
-    double g0[4][4], g1[4][4];
-    cload(0, g0);
-    cload(1, g1);
     cstore(0, g0);
     cload(2, g0);
     cstore(1, g1);
@@ -259,8 +264,118 @@ gemm128_f64_kernel(double* __restrict__ C, int64_t ldc, const double* __restrict
     cstore(3, g1);
 }
 
+// Short products (K <= 128: the narrow refits of the sweep, the factor's panel products): the same C -= A op(B) (or
+// C = A op(B) with OVERWRITE) on 64x64 tiles whose whole k-range stays in LDS, in up to four stages of 32: every load
+// of every stage is issued at once (global_load_lds, 16 bytes a lane), and stage s is computed as soon as its own
+// loads have landed, while the later stages' loads are still in flight; C is read before them. Four waves of 32x32
+// (2x2 MFMA tiles). LDS layout per stage: [row][k] operands (A; B when TRANSB) 256 bytes a row, chunk c of row r at
+// c ^ (r & 15) (the 16 rows of a fragment read fall in 16 different 16-byte bank windows); [k][col] B 512 bytes a
+// k-row. Needs even K, lda, ldb (and N for a [k][col] B) and 16-byte aligned A and B, like the 128-tile kernel.
+#define GP_BK 32
+template <bool TRANSB, bool LOWER, bool OVERWRITE>
+__global__ __launch_bounds__(256) void gemm64_panel_f64_kernel(double* C, int64_t ldc, const double* A, int64_t lda,
+                                                               const double* B, int64_t ldb, int64_t M, int64_t N,
+                                                               int64_t K, const int32_t* __restrict__ info)
+{
+    constexpr int SB = 64 * GP_BK * 8;  // bytes of one operand stage (A: 64 rows x 256 B; B: 32 k-rows x 512 B)
+    constexpr int NS = 128 / GP_BK;     // most stages
+    __shared__ __align__(16) uint8_t lds[NS][2][SB];
+    if (info && *info != 0) return;
+    const int64_t tr = (int64_t)blockIdx.y * 64, tc = (int64_t)blockIdx.x * 64;
+    if (LOWER && tc > tr + 63) return;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
+    const double* zc = lamq_zero_chunk;
+    asm volatile("" : "+s"(zc));
+    const int nst = (int)cdiv(K, GP_BK);
+    const int wr = (wave >> 1) * 32, wc = (wave & 1) * 32;
+    const int li = lane & 15, lk = lane >> 4;
+    // C first: its loads are the oldest, so each stage's wait below also covers them
+    double cv[2][2][4];
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < 2; ++tj)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int64_t row = tr + wr + ti * 16 + 4 * v + lk;
+                const int64_t col = tc + wc + tj * 16 + li;
+                cv[ti][tj][v] = (!OVERWRITE && row < M && col < N && (!LOWER || col <= row)) ? C[row * ldc + col] : 0.0;
+            }
+    // stage st, operand op: 16 instructions of 1 KB, four a wave (instruction i = 4 wv + q)
+    //   [row][k]: rows 4i .. 4i + 3, lane l row 4i + l/16, slot l%16 holding chunk (l%16) ^ (row & 15)
+    //   [k][col]: k-rows 2i and 2i + 1, lane l k-row 2i + l/32, columns 2 (l%32), 2 (l%32) + 1
+    for (int st = 0; st < nst; ++st) {
+        const int64_t k0 = (int64_t)st * GP_BK;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int i = 4 * wv + q;
+            {
+                const int r = 4 * i + lane / 16, c = (lane % 16) ^ (r & 15);
+                const int64_t row = tr + r, k = k0 + 2 * c;
+                load_lds16((row < M && k < K) ? A + row * lda + k : zc, base + (uint32_t)((st * 2 + 0) * SB + i * 1024));
+            }
+            if (TRANSB) {
+                const int r = 4 * i + lane / 16, c = (lane % 16) ^ (r & 15);
+                const int64_t col = tc + r, k = k0 + 2 * c;
+                load_lds16((col < N && k < K) ? B + col * ldb + k : zc, base + (uint32_t)((st * 2 + 1) * SB + i * 1024));
+            } else {
+                const int64_t k = k0 + 2 * i + lane / 32, col = tc + 2 * (lane % 32);
+                load_lds16((k < K && col < N) ? B + k * ldb + col : zc, base + (uint32_t)((st * 2 + 1) * SB + i * 1024));
+            }
+        }
+    }
+    auto aaddr = [](int r, int kk) -> uint32_t { return (uint32_t)(r * 256 + (((kk >> 1) ^ (r & 15)) << 4) + (kk & 1) * 8); };
+    lamq_d4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = lamq_d4{0.0, 0.0, 0.0, 0.0};
+    for (int st = 0; st < nst; ++st) {
+        // this wave's loads of stages 0..st have landed when at most 8 (nst - 1 - st) of its loads are outstanding
+        switch (nst - 1 - st) {
+            case 0: wait_vm<0>(); break;
+            case 1: wait_vm<8>(); break;
+            case 2: wait_vm<16>(); break;
+            default: wait_vm<24>(); break;
+        }
+        __syncthreads();
+        const uint8_t* As = lds[st][0];
+        const uint8_t* Bs = lds[st][1];
+#pragma unroll
+        for (int k4 = 0; k4 < GP_BK; k4 += 4) {
+            const int kk = k4 + lk;
+            double a[2], b[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                a[t] = *reinterpret_cast<const double*>(As + aaddr(wr + 16 * t + li, kk));
+                b[t] = TRANSB ? *reinterpret_cast<const double*>(Bs + aaddr(wc + 16 * t + li, kk))
+                              : *reinterpret_cast<const double*>(Bs + kk * 512 + 8 * (wc + 16 * t + li));
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+    }
+    if (OVERWRITE) __syncthreads();
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < 2; ++tj)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int64_t row = tr + wr + ti * 16 + 4 * v + lk;
+                const int64_t col = tc + wc + tj * 16 + li;
+                if (row < M && col < N && (!LOWER || col <= row))
+                    C[row * ldc + col] = OVERWRITE ? acc[ti][tj][v] : cv[ti][tj][v] - acc[ti][tj][v];
+            }
+}
+
 // TRI (LAMQ_TRI_KGE, LAMQ_TRI_KLE): op(B) is triangular and the 128-tile kernel skips the stages of its zero part (the
-// other kernel reads the zeros).
+// other kernels read the zeros).
 template <bool TRANSB, bool LOWER, bool OVERWRITE = false, int TRI = 0>
 static int gemm_sub_f64(double* C, int64_t ldc, const double* A, int64_t lda, const double* B, int64_t ldb, int64_t M,
                         int64_t N, int64_t K, const int32_t* info, hipStream_t s)
@@ -271,14 +386,21 @@ static int gemm_sub_f64(double* C, int64_t ldc, const double* A, int64_t lda, co
     // (a [k][col] B chunk holds columns col, col + 1: N even keeps the pair inside the row)
     const bool chunks = (lda % 2) == 0 && (ldb % 2) == 0 && (K % 2) == 0 && (TRANSB || (N % 2) == 0) &&
                         ((uintptr_t)A % 16) == 0 && ((uintptr_t)B % 16) == 0;
-    if (!OVERWRITE && chunks && cdiv(M, G8_BM) * cdiv(N, G8_BM) >= 128) {
-        dim3 grid((unsigned)cdiv(N, G8_BM), (unsigned)cdiv(M, G8_BM));
-        hipLaunchKernelGGL((gemm128_f64_kernel<TRANSB, LOWER, G8_BK, TRI>), grid, dim3(256), 0, s, C, ldc, A, lda, B, ldb,
-                           M, N, K, info);
+    const int64_t tiles128 = cdiv(M, G8_BM) * cdiv(N, G8_BM);
+    dim3 grid((unsigned)cdiv(N, 64), (unsigned)cdiv(M, 64));
+    if (chunks && K <= 128 && (OVERWRITE || tiles128 < LAMQ_PANEL_MAX_TILES128)) {
+        hipLaunchKernelGGL((gemm64_panel_f64_kernel<TRANSB, LOWER, OVERWRITE>), grid, dim3(256), 0, s, C, ldc, A, lda, B,
+                           ldb, M, N, K, info);
         LAMQ_LAUNCH_CHECK();
         return LAMQ_OK;
     }
-    dim3 grid((unsigned)cdiv(N, 64), (unsigned)cdiv(M, 64));
+    if (!OVERWRITE && chunks && tiles128 >= 128) {
+        dim3 grid128((unsigned)cdiv(N, G8_BM), (unsigned)cdiv(M, G8_BM));
+        hipLaunchKernelGGL((gemm128_f64_kernel<TRANSB, LOWER, G8_BK, TRI>), grid128, dim3(256), 0, s, C, ldc, A, lda, B,
+                           ldb, M, N, K, info);
+        LAMQ_LAUNCH_CHECK();
+        return LAMQ_OK;
+    }
     hipLaunchKernelGGL((gemm_sub_f64_kernel<TRANSB, LOWER, OVERWRITE>), grid, dim3(256), 0, s, C, ldc, A, lda, B, ldb, M, N,
                        K, info);
     LAMQ_LAUNCH_CHECK();

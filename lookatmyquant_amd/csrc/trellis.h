@@ -15,7 +15,8 @@
 #pragma once
 #include "common.h"
 
-#define LAMQ_WMAX 16  // widest block the fused kernels settle at once
+#define LAMQ_WMAX 16      // widest block the fused kernels settle at once
+#define LAMQ_PRE_MAX 1024  // most earlier columns of a run whose updates a block takes itself (pre)
 
 template <int L, int K, int NT>
 struct VX {
@@ -335,6 +336,52 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
     }
     lds_barrier();
     return pathv;
+}
+
+// ------------------------------------------------------------------------------------------------ block row
+// The block's columns of one row as the lazy sweep sees them when the block starts: trow[c] = Tr[b0 + c] for
+// c < nplain (T holds every earlier update there), and for nplain <= c < nc (the look-ahead past the caller's run, at
+// most LAMQ_WMAX + 8 columns) trow[c] = Tr[b0 + c] - sum_{l < pre} Zr[l] U[b0 - pre + l][b0 + c]: those columns still
+// lack the trailing updates (syntax.py:123) of the run's pre earlier columns, which the caller applies past the run
+// in one product only after the run. Zr: the row's coefficients of those columns. The first wave takes the updated
+// columns, its lanes as 4 column pairs x 16 slices of l (lane = 4 * slice + pair): slice s sums l = s, s + 16, ... as
+// an fma chain in increasing l, and four butterfly steps add the slices in a fixed order (every lane ends with the
+// same bits).
+template <int NT>
+__device__ __forceinline__ void load_block_row(double* trow, const double* __restrict__ Tr, int64_t b0, int nplain,
+                                               int nc, const double* __restrict__ Zr, int pre,
+                                               const double* __restrict__ U, int64_t ldU)
+{
+    const int tid = threadIdx.x;
+    const int plain = pre > 0 ? nplain : nc;
+    for (int c = tid; c < plain; c += NT) trow[c] = Tr[b0 + c];
+    if (pre <= 0 || tid >= 64) return;
+    constexpr int SL = 16;
+    const int pr = tid & 3, sl = tid >> 2;
+    const double* Ub = U + (b0 - pre) * ldU + b0;
+    for (int c0 = nplain; c0 < nc; c0 += 8) {
+        const int c = c0 + 2 * pr;
+        const bool in0 = c < nc, in1 = c + 1 < nc;
+        double a0 = 0.0, a1 = 0.0;
+        if (in0) {
+#pragma unroll 4
+            for (int l = sl; l < pre; l += SL) {
+                const double* p = Ub + (int64_t)l * ldU + c;
+                const double z = Zr[l];
+                a0 = fma(z, p[0], a0);
+                a1 = fma(z, in1 ? p[1] : 0.0, a1);
+            }
+        }
+#pragma unroll
+        for (int o = 4; o < 64; o <<= 1) {
+            a0 += __shfl_xor(a0, o);
+            a1 += __shfl_xor(a1, o);
+        }
+        if (sl == 0) {
+            if (in0) trow[c] = Tr[b0 + c] - a0;
+            if (in1) trow[c + 1] = Tr[b0 + c + 1] - a1;
+        }
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ refit

@@ -88,7 +88,7 @@ __global__ __launch_bounds__(LAMQ_NT) void ldlq_trellis_block_kernel(
     const double* __restrict__ T, int64_t n, int64_t ldT, const double* __restrict__ U, int64_t ldU,
     const double* __restrict__ S, const double* __restrict__ table64, const float* __restrict__ table32,
     int64_t b0, int64_t b1, int width, int look, int32_t* __restrict__ state, int32_t* __restrict__ states,
-    int64_t lds, double* __restrict__ Z, int64_t ldZ)
+    int64_t lds, double* __restrict__ Z, int64_t ldZ, int pre)
 {
     using V = VX<L, K, LAMQ_NT>;
     __shared__ __align__(16) float buf[2 * V::R];
@@ -102,11 +102,11 @@ __global__ __launch_bounds__(LAMQ_NT) void ldlq_trellis_block_kernel(
 
     const int64_t row = blockIdx.x;
     const int tid = threadIdx.x;
+    const int64_t cend = (b1 + look < n) ? b1 + look : n;
+    load_block_row<LAMQ_NT>(trow, T + row * ldT, b0, (int)(b1 - b0), (int)(cend - b0), Z + row * ldZ - pre, pre, U,
+                            ldU);
     TabF32<V> tab;
     if (tid < V::ACT) tab.load(table32, tid);
-    const int64_t cend = (b1 + look < n) ? b1 + look : n;
-    const double* Tr = T + row * ldT;
-    for (int64_t c = tid; c < cend - b0; c += LAMQ_NT) trow[c] = Tr[b0 + c];
     const double Sr = S[row];
     int st = state[row];
     lds_barrier();
@@ -133,10 +133,10 @@ template <int L, int K>
 struct TrellisBlock {
     static int run(const double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU, const double* S,
                    const double* table64, const float* table32, int64_t b0, int64_t b1, int width, int look,
-                   int32_t* state, int32_t* states, int64_t lds, double* Z, int64_t ldZ, hipStream_t s)
+                   int32_t* state, int32_t* states, int64_t lds, double* Z, int64_t ldZ, int pre, hipStream_t s)
     {
         hipLaunchKernelGGL((ldlq_trellis_block_kernel<L, K>), dim3((unsigned)m), dim3(LAMQ_NT), 0, s, T, n, ldT, U, ldU, S,
-                           table64, table32, b0, b1, width, look, state, states, lds, Z, ldZ);
+                           table64, table32, b0, b1, width, look, state, states, lds, Z, ldZ, pre);
         LAMQ_LAUNCH_CHECK();
         return LAMQ_OK;
     }
@@ -145,15 +145,16 @@ struct TrellisBlock {
 extern "C" int lamq_ldlq_trellis_block(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU,
                                        const double* S, const double* table64, const float* table32, int L, int k,
                                        int64_t b0, int64_t b1, int width, int look, int32_t* state, int32_t* states,
-                                       int64_t lds, double* Z, int64_t ldZ, void* stream)
+                                       int64_t lds, double* Z, int64_t ldZ, int64_t pre, void* stream)
 {
     if (!T || !U || !S || !table64 || !table32 || !state || !states || !Z) return LAMQ_EINVAL;
     if (m < 0 || n < 1 || ldT < n || ldU < n || lds < n || b0 < 0 || b1 <= b0 || b1 > n || width < 1 || look < 0)
         return LAMQ_EINVAL;
-    if (ldZ < b1 - b0) return LAMQ_EINVAL;
+    if (pre < 0 || pre > b0 || ldZ < pre + (b1 - b0)) return LAMQ_EINVAL;
+    if (pre > LAMQ_PRE_MAX) return LAMQ_EUNSUP;
     if (width > LAMQ_WMAX || width + look > LAMQ_TV_BLK || b1 - b0 > LAMQ_LAZY_MAX || m > 0x7fffffff)
         return LAMQ_EUNSUP;
     if (m == 0) return LAMQ_OK;
     return dispatch_lk<TrellisBlock>(L, k, T, m, n, ldT, U, ldU, S, table64, table32, b0, b1, width, look, state,
-                                     states, lds, Z, ldZ, as_stream(stream));
+                                     states, lds, Z, ldZ, (int)pre, as_stream(stream));
 }

@@ -310,7 +310,7 @@ __global__ __launch_bounds__(BIG_NT) void ldlq_trellis_block_big_kernel(
     const double* __restrict__ T, int64_t n, int64_t ldT, const double* __restrict__ U, int64_t ldU,
     const double* __restrict__ S, const double* __restrict__ table64, const uint16_t* __restrict__ table16,
     int64_t b0, int64_t b1, int width, int look, int32_t* __restrict__ state, int32_t* __restrict__ states,
-    int64_t lds, double* __restrict__ Z, int64_t ldZ)
+    int64_t lds, double* __restrict__ Z, int64_t ldZ, int pre)
 {
     using V = VBig<L, K>;
     __shared__ __align__(16) float xbuf[V::QS];
@@ -327,8 +327,8 @@ __global__ __launch_bounds__(BIG_NT) void ldlq_trellis_block_big_kernel(
     uint32_t Ch[V::SPT / 2];
     load_half_table<L, K>(table16, Ch);
     const int64_t cend = (b1 + look < n) ? b1 + look : n;
-    const double* Tr = T + row * ldT;
-    for (int64_t c = tid; c < cend - b0; c += BIG_NT) trow[c] = Tr[b0 + c];
+    load_block_row<BIG_NT>(trow, T + row * ldT, b0, (int)(b1 - b0), (int)(cend - b0), Z + row * ldZ - pre, pre, U,
+                            ldU);
     const double Sr = S[row];
     int st = state[row];
     __syncthreads();
@@ -381,7 +381,7 @@ __global__ __launch_bounds__(BIG_NT) void ldlq_trellis_block_gx_kernel(
     const double* __restrict__ T, int64_t n, int64_t ldT, const double* __restrict__ U, int64_t ldU,
     const double* __restrict__ S, const double* __restrict__ table64, const uint16_t* __restrict__ table16,
     int64_t b0, int64_t b1, int width, int look, int32_t* __restrict__ state, int32_t* __restrict__ states,
-    int64_t lds, double* __restrict__ Z, int64_t ldZ, uint32_t* __restrict__ back_ws)
+    int64_t lds, double* __restrict__ Z, int64_t ldZ, uint32_t* __restrict__ back_ws, int pre)
 {
     using V = VX<L, K, BIG_NT>;
     constexpr bool DBL = V::R <= 4096;
@@ -407,11 +407,11 @@ __global__ __launch_bounds__(BIG_NT) void ldlq_trellis_block_gx_kernel(
     const int64_t row = blockIdx.x;
     uint32_t* back = BG ? back_ws + row * (int64_t)((BIG_TV - 1) * V::ACT) : sm.back;
     const int tid = threadIdx.x;
+    const int64_t cend = (b1 + look < n) ? b1 + look : n;
+    load_block_row<BIG_NT>(trow, T + row * ldT, b0, (int)(b1 - b0), (int)(cend - b0), Z + row * ldZ - pre, pre, U,
+                            ldU);
     TabF16<V> tab;
     tab.load(table16, tid);
-    const int64_t cend = (b1 + look < n) ? b1 + look : n;
-    const double* Tr = T + row * ldT;
-    for (int64_t c = tid; c < cend - b0; c += BIG_NT) trow[c] = Tr[b0 + c];
     const double Sr = S[row];
     int st = state[row];
     lds_barrier();
@@ -440,17 +440,20 @@ template <int L, int K>
 struct TrellisBlockBig {
     static int run(const double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU, const double* S,
                    const double* table64, const uint16_t* table16, int64_t b0, int64_t b1, int width, int look,
-                   int32_t* state, int32_t* states, int64_t lds, double* Z, int64_t ldZ, uint32_t* back_ws, hipStream_t s)
+                   int32_t* state, int32_t* states, int64_t lds, double* Z, int64_t ldZ, uint32_t* back_ws, int pre,
+                   hipStream_t s)
     {
         if constexpr (VX<L, K, BIG_NT>::R <= BIG_GX_MAX_R)
             hipLaunchKernelGGL((ldlq_trellis_block_gx_kernel<L, K, false>), dim3((unsigned)m), dim3(BIG_NT), 0, s, T, n,
-                               ldT, U, ldU, S, table64, table16, b0, b1, width, look, state, states, lds, Z, ldZ, nullptr);
+                               ldT, U, ldU, S, table64, table16, b0, b1, width, look, state, states, lds, Z, ldZ, nullptr,
+                               pre);
         else if (back_ws)
             hipLaunchKernelGGL((ldlq_trellis_block_gx_kernel<L, K, true>), dim3((unsigned)m), dim3(BIG_NT), 0, s, T, n,
-                               ldT, U, ldU, S, table64, table16, b0, b1, width, look, state, states, lds, Z, ldZ, back_ws);
+                               ldT, U, ldU, S, table64, table16, b0, b1, width, look, state, states, lds, Z, ldZ, back_ws,
+                               pre);
         else
             hipLaunchKernelGGL((ldlq_trellis_block_big_kernel<L, K>), dim3((unsigned)m), dim3(BIG_NT), 0, s, T, n, ldT, U,
-                               ldU, S, table64, table16, b0, b1, width, look, state, states, lds, Z, ldZ);
+                               ldU, S, table64, table16, b0, b1, width, look, state, states, lds, Z, ldZ, pre);
         LAMQ_LAUNCH_CHECK();
         return LAMQ_OK;
     }
@@ -459,17 +462,18 @@ struct TrellisBlockBig {
 extern "C" int lamq_ldlq_trellis16_block(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU,
                                          const double* S, const double* table64, const uint16_t* table16, int L, int k,
                                          int64_t b0, int64_t b1, int width, int look, int32_t* state, int32_t* states,
-                                         int64_t lds, double* Z, int64_t ldZ, void* stream)
+                                         int64_t lds, double* Z, int64_t ldZ, int64_t pre, void* stream)
 {
     if (!T || !U || !S || !table64 || !table16 || !state || !states || !Z) return LAMQ_EINVAL;
     if (((uintptr_t)table16 % 4) != 0) return LAMQ_EINVAL;
     if (m < 0 || n < 1 || ldT < n || ldU < n || lds < n || b0 < 0 || b1 <= b0 || b1 > n || width < 1 || look < 0)
         return LAMQ_EINVAL;
-    if (ldZ < b1 - b0) return LAMQ_EINVAL;
-    if (width > LAMQ_WMAX || width + look > BIG_TV || b1 - b0 > BIG_LAZY || m > 0x7fffffff) return LAMQ_EUNSUP;
+    if (pre < 0 || pre > b0 || ldZ < pre + (b1 - b0)) return LAMQ_EINVAL;
+    if (width > LAMQ_WMAX || width + look > BIG_TV || b1 - b0 > BIG_LAZY || m > 0x7fffffff || pre > LAMQ_PRE_MAX)
+        return LAMQ_EUNSUP;
     if (m == 0) return LAMQ_OK;
     return dispatch_big<TrellisBlockBig>(L, k, T, m, n, ldT, U, ldU, S, table64, table16, b0, b1, width, look, state,
-                                         states, lds, Z, ldZ, (uint32_t*)nullptr, as_stream(stream));
+                                         states, lds, Z, ldZ, (uint32_t*)nullptr, (int)pre, as_stream(stream));
 }
 
 extern "C" size_t lamq_ldlq_trellis16_block_workspace_size(int64_t m, int L, int k)
@@ -482,20 +486,22 @@ extern "C" size_t lamq_ldlq_trellis16_block_workspace_size(int64_t m, int L, int
 extern "C" int lamq_ldlq_trellis16_block_ws(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU,
                                             const double* S, const double* table64, const uint16_t* table16, int L, int k,
                                             int64_t b0, int64_t b1, int width, int look, int32_t* state, int32_t* states,
-                                            int64_t lds, double* Z, int64_t ldZ, void* workspace, size_t workspace_bytes,
-                                            void* stream)
+                                            int64_t lds, double* Z, int64_t ldZ, int64_t pre, void* workspace,
+                                            size_t workspace_bytes, void* stream)
 {
     const size_t need = lamq_ldlq_trellis16_block_workspace_size(m, L, k);
     if (need == 0)
         return lamq_ldlq_trellis16_block(T, m, n, ldT, U, ldU, S, table64, table16, L, k, b0, b1, width, look, state,
-                                         states, lds, Z, ldZ, stream);
+                                         states, lds, Z, ldZ, pre, stream);
     if (!workspace || workspace_bytes < need || ((uintptr_t)workspace % 4) != 0) return LAMQ_EINVAL;
     if (!T || !U || !S || !table64 || !table16 || !state || !states || !Z) return LAMQ_EINVAL;
     if (((uintptr_t)table16 % 4) != 0) return LAMQ_EINVAL;
     if (m < 0 || n < 1 || ldT < n || ldU < n || lds < n || b0 < 0 || b1 <= b0 || b1 > n || width < 1 || look < 0)
         return LAMQ_EINVAL;
-    if (ldZ < b1 - b0) return LAMQ_EINVAL;
-    if (width > LAMQ_WMAX || width + look > BIG_TV || b1 - b0 > BIG_LAZY || m > 0x7fffffff) return LAMQ_EUNSUP;
+    if (pre < 0 || pre > b0 || ldZ < pre + (b1 - b0)) return LAMQ_EINVAL;
+    if (width > LAMQ_WMAX || width + look > BIG_TV || b1 - b0 > BIG_LAZY || m > 0x7fffffff || pre > LAMQ_PRE_MAX)
+        return LAMQ_EUNSUP;
     return dispatch_big<TrellisBlockBig>(L, k, T, m, n, ldT, U, ldU, S, table64, table16, b0, b1, width, look, state,
-                                         states, lds, Z, ldZ, reinterpret_cast<uint32_t*>(workspace), as_stream(stream));
+                                         states, lds, Z, ldZ, reinterpret_cast<uint32_t*>(workspace), (int)pre,
+                                         as_stream(stream));
 }

@@ -208,9 +208,9 @@ def ldlq_trellis_groups(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, group
             if nb:
                 ws[r0] = torch.empty(nb, dtype=torch.uint8, device=dev)
 
-    def block(Tp, rows, r0, k, table64, t32, b0, b1, zb, st_):
+    def block(Tp, rows, r0, k, table64, t32, b0, b1, zb, pre, st_):
         args = (ptr(Tp), rows, n, n, ptr(U), ld(U), vp(S.data_ptr() + 8 * r0), ptr(table64), ptr(t32), L, k, b0, b1, width,
-                look, vp(state.data_ptr() + 4 * r0), vp(states.data_ptr() + 4 * r0 * n), n, ptr(zb), outer)
+                look, vp(state.data_ptr() + 4 * r0), vp(states.data_ptr() + 4 * r0 * n), n, ptr(zb), outer, pre)
         if L < BIG_L:
             return lib().lamq_ldlq_trellis_block(*args, st_)
         w = ws.get(r0)
@@ -231,27 +231,31 @@ def ldlq_trellis_groups(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, group
     vp = ctypes.c_void_p
     # each group's rows as views: T, Z and the outputs of rows [r0, r0 + rows)
     views = [(T.narrow(0, r0, rows), Z.narrow(0, r0, rows)) for r0, rows, _, _, _ in parts]
+    # per block, a narrow product updates the rest of its run (_refit_run); the run's last block reads its look-ahead
+    # past the run with the run's earlier blocks applied in the kernel (pre), and one product per run updates every
+    # column past the run (_refit_rest)
     for B0 in range(0, n, outer):
         B1 = min(B0 + outer, n)
         for b0 in range(B0, B1, lazy):
             b1 = min(b0 + lazy, n)
+            pre = b0 - B0 if b1 == B1 else 0
             for p, (r0, rows, k, table64, t32) in enumerate(parts):
                 Tp, Zp = views[p]
                 with torch.cuda.stream(lanes[p % len(lanes)]):
                     zb = Zp[:, b0 - B0 :]
                     ev = _event_pair(events, "block")
-                    check(block(Tp, rows, r0, k, table64, t32, b0, b1, zb, stream(dev)), "ldlq_trellis_block")
+                    check(block(Tp, rows, r0, k, table64, t32, b0, b1, zb, pre, stream(dev)), "ldlq_trellis_block")
                     _event_end(ev)
                     if len(lanes) > 1:
-                        _refit_run(Tp, U, zb, b0, b1, B1, look, events)
+                        _refit_run(Tp, U, zb, b0, b1, B1, 0, events)
             if len(lanes) == 1:  # one product over every group's rows
-                _refit_run(T, U, Z[:, b0 - B0 :], b0, b1, B1, look, events)
+                _refit_run(T, U, Z[:, b0 - B0 :], b0, b1, B1, 0, events)
         if len(lanes) == 1:
-            _refit_rest(T, U, Z, B0, B1, look, events)
+            _refit_rest(T, U, Z, B0, B1, 0, events)
         else:
             for p, (Tp, Zp) in enumerate(views):
                 with torch.cuda.stream(lanes[p % len(lanes)]):
-                    _refit_rest(Tp, U, Zp, B0, B1, look, events)
+                    _refit_rest(Tp, U, Zp, B0, B1, 0, events)
     for ln in lanes:
         if ln is not main:
             main.wait_stream(ln)
@@ -308,8 +312,9 @@ def _refit_run(T, U, zb, b0, b1, B1, look, events):
 
 
 def _refit_rest(T, U, Z, B0, B1, look, events):
-    """The columns past the outer run [B0, B1) and its look-ahead get the run's blocks at once:
-    T[:, c0:] -= Z[:, :B1-B0] U[B0:B1, c0:] with c0 = B1 + look (syntax.py:123 summed over the run's blocks)."""
+    """The columns past the outer run [B0, B1), past its first `look` (which the narrow products already updated), get
+    the run's blocks at once: T[:, c0:] -= Z[:, :B1-B0] U[B0:B1, c0:] with c0 = B1 + look (syntax.py:123 summed over
+    the run's blocks)."""
     m, n = T.shape
     c0 = B1 + look
     if c0 >= n:

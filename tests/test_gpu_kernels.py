@@ -153,6 +153,28 @@ def test_gemm_sub_triangular(E, M, N, K, transb, tri):
     assert err < 1e-13
 
 
+@pytest.mark.parametrize("M,N,K,transb", [(2560, 384, 128, False), (300, 136, 128, True), (77, 190, 64, False),
+                                           (130, 70, 64, True), (65, 66, 2, False), (200, 128, 100, True),
+                                           (19456, 256, 128, False)])
+def test_gemm_sub_short_k(E, M, N, K, transb):
+    """Short products (K <= 128: the sweep's narrow refits, the factor's panels) on the 64-tile kernel that loads a
+    tile's whole k-range into LDS at once: ragged M, N and K (zero chunks past them), both layouts of B, against a
+    float64 product on the GPU; columns outside [0, N) of a wider C untouched."""
+    g = torch.Generator(device="cuda").manual_seed(M + 3 * N + 7 * K)
+    Cw = torch.randn(M, N + 6, generator=g, device="cuda", dtype=torch.float64)
+    C = Cw[:, 2 : 2 + N]
+    A = torch.randn(M, K, generator=g, device="cuda", dtype=torch.float64)
+    Bm = torch.randn(N, K, generator=g, device="cuda", dtype=torch.float64) if transb else \
+        torch.randn(K, N, generator=g, device="cuda", dtype=torch.float64)
+    ref = Cw.clone()
+    ref[:, 2 : 2 + N] -= A @ (Bm.T if transb else Bm)
+    say(f"gemm_sub short k: M={M} N={N} K={K} transb={transb}")
+    E.gemm_sub(C, A, Bm, transb=transb)
+    err = ((Cw - ref).abs().max() / ref.abs().max()).item()
+    say(f"  max relative difference {err:.3e}")
+    assert err < 1e-13
+
+
 @pytest.mark.parametrize("n", [16, 64, 100, 200, 960, 2500])
 def test_chol_inv_upper(E, n):
     rng = np.random.default_rng(n)

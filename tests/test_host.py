@@ -52,7 +52,12 @@ def test_argument_errors_are_reported_without_a_gpu():
     ptr = lambda t: t.data_ptr()
     # width + look beyond the fused search's limit: unsupported, not a crash
     assert L.lamq_ldlq_trellis_block(ptr(p), 1, 8, 8, ptr(p), 8, ptr(p), ptr(p), ptr(p), 12, 2, 0, 8, 30, 8, ptr(q), ptr(q),
-                                     8, ptr(p), 8, None) == -2
+                                     8, ptr(p), 8, 0, None) == -2
+    # earlier run columns beyond the block's start, or a Z too narrow to hold them
+    assert L.lamq_ldlq_trellis_block(ptr(p), 1, 8, 8, ptr(p), 8, ptr(p), ptr(p), ptr(p), 12, 2, 0, 8, 4, 4, ptr(q), ptr(q),
+                                     8, ptr(p), 8, 1, None) == -1
+    assert L.lamq_ldlq_trellis16_block(ptr(p), 1, 8, 8, ptr(p), 8, ptr(p), ptr(p), ptr(p), 16, 2, 4, 8, 4, 4, ptr(q),
+                                       ptr(q), 8, ptr(p), 4, 4, None) == -1
     # a trellis width the kernels are not built for
     assert L.lamq_viterbi_rows(ptr(p), 1, 4, 4, ptr(p), 12, 7, None, ptr(q), 4, None, 0, None) == -2
     # packing: widths beyond 8, a trellis no wider than its symbols, too few code words, more rows than the source
