@@ -281,7 +281,7 @@ def run_c5(args):
     torch.cuda.empty_cache()
     # the production schedule, and the reference's own 12-bit trellis, on a few more layers (untimed by events)
     extra = {}
-    for L, n_l in ((args.L, 3), (12 if args.L != 12 else 16, 3)):
+    for L, n_l in () if args.no_extra else ((args.L, 3), (12 if args.L != 12 else 16, 3)):
         bb = stack.StackBuild(tokens, sh, w, L=L, layers=n_l, redamp=True)
         bb.layer()
         torch.cuda.synchronize()
@@ -612,6 +612,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--workload", choices=("c2", "c3", "c4", "c5"), default="c5")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MiB")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="c5: skip the extra layers timed in the production schedule and at the other state width")
     args = ap.parse_args()
     if args.steps is None:
         args.steps = {"c5": 12, "c3": 5}.get(args.workload, 10)
