@@ -1,7 +1,7 @@
 """The trellis and the LDLQ words with the reference's signatures (opgraph/codes.py), on the gfx950 kernels.
 
     viterbi(X, values, L, k, chunk=None, start=None)                      codes.py:151
-    trellis_values(L, k, T=256, seed=0, refine=None, fit=None)             codes.py:187 (cached tables)
+    trellis_values(L, k, T=256, seed=0, refine=None, fit=None)             codes.py:187 (cached, else fitted)
     is_trellis_path(states, L, k)                                          codes.py:246
     ScalarCode(domain), RowTrellisCode(L, k, T=256, width=16, look=8, seed=0, values=None)   codes.py:322,386
     TrellisCode(L, k, T=320, width=16, seed=0, values=None)                codes.py:363
@@ -12,11 +12,13 @@
 Differences a caller can see: results are computed on the GPU whatever device the inputs are on (Net cores are
 returned on the CPU, as the reference returns them); a word also carries its integer codes (`net.codes`: trellis
 states or level indices) so they need not be recovered from values (which is ambiguous for tables with repeated
-values); the fitting of new trellis tables is not part of this package (trellis_values serves the cached ones)."""
+values)."""
 
 from __future__ import annotations
 
 import math
+
+from functools import lru_cache
 
 import numpy as np
 import torch
@@ -75,12 +77,25 @@ def viterbi(X: torch.Tensor, values: torch.Tensor, L: int, k: int, chunk: int | 
 
 def trellis_values(L: int, k: int, T: int = 256, seed: int = 0, refine: int | None = None, fit: str | None = None) -> torch.Tensor:
     """A value for each of the 2^L states (codes.py:187-220), float64. The tables the reference has fitted and
-    cached (L = 12, k = 1..4, T = 256, seed 0, fit "ema") are served as stored; fitting others is not part of this
-    package (use trellis_init_values for the unrefined quantile table)."""
+    cached (L = 12, k = 1..4, T = 256, seed 0, fit "ema") are served as stored; any other (L, k, T, seed, refine, fit)
+    is fitted on the GPU (fit.fit_table, the reference's procedure; refitting a cached table reproduces it to within
+    4 units in the last place) and kept for the life of the process (the reference writes it into its cache)."""
     fit = fit or TRELLIS_FIT
-    if refine is not None:
-        raise NotImplementedError("fitting trellis tables (refine) is not part of this package")
-    return torch.from_numpy(np.array(load_table(L, k, T, seed, fit)))
+    if refine is None:
+        try:
+            return torch.from_numpy(np.array(load_table(L, k, T, seed, fit)))
+        except FileNotFoundError:
+            pass
+    return torch.from_numpy(_fitted(L, k, T, seed, refine, fit).copy())
+
+
+@lru_cache(maxsize=16)
+def _fitted(L, k, T, seed, refine, fit):
+    from .fit import fit_table
+
+    v = fit_table(L, k, T, seed, refine, fit)
+    v.setflags(write=False)
+    return v
 
 
 def trellis_init_values(L: int, seed: int = 0, dtype: str = "float64") -> torch.Tensor:

@@ -265,3 +265,15 @@ def test_cli_checks_its_arguments(tmp_path):
         main(["--program", "plan", "--out", str(tmp_path / "o.json")])
     with pytest.raises(ValueError):
         main(["--program", "tr9y", "--out", str(tmp_path / "o.json")])
+
+
+def test_trellis_fit_checks_its_arguments():
+    """Fitting covers the float32 search's trellises (L <= 12) and the two fits of codes.py:187-220; a table the
+    reference cached is served without a GPU."""
+    from lookatmyquant_amd import codes, fit
+
+    with pytest.raises(NotImplementedError):
+        fit.fit_table(16, 2)
+    with pytest.raises(ValueError):
+        fit.fit_table(12, 2, fit="kmeans")
+    assert codes.trellis_values(12, 2).shape == (4096,)
