@@ -372,6 +372,19 @@ __global__ __launch_bounds__(BIG_NT) void ldlq_trellis_block_big_kernel(
     if (tid == 0) state[row] = st;
 }
 
+// LDS of the fused minima-exchange kernel below: the block row and small arrays, the group minima (two buffers when
+// they fit, which spares each step its second barrier: 2^12 groups, and 2^13 with the back-pointers in LDS, 163,456 of
+// the 163,840 bytes), and the back-pointers unless they go to a workspace (BG).
+template <int L, int K, bool BG>
+constexpr int gx_lds_bytes(bool dbl)
+{
+    using V = VX<L, K, BIG_NT>;
+    return 8 * (BIG_LAZY + BIG_TV) + 8 * LAMQ_WMAX * LAMQ_WMAX + 8 * LAMQ_WMAX + 4 * BIG_TV + 4 * BIG_TV +
+           4 * 2 * (BIG_NT / 64) + 4 * (dbl ? 2 : 1) * V::R + 4 * (BG ? 1 : (BIG_TV - 1) * V::ACT);
+}
+template <int L, int K, bool BG>
+constexpr bool gx_double_buffered() { return gx_lds_bytes<L, K, BG>(true) <= 160 * 1024; }
+
 // The same with the minima-exchange search and the prefetched refit of trellis.h (four threads per column of the
 // in-block update).
 // BG: the back-pointers in back_ws, (BIG_TV - 1) * BIG_NT words per row, instead of LDS (the 2^15-group search,
@@ -384,7 +397,7 @@ __global__ __launch_bounds__(BIG_NT) void ldlq_trellis_block_gx_kernel(
     int64_t lds, double* __restrict__ Z, int64_t ldZ, uint32_t* __restrict__ back_ws, int pre)
 {
     using V = VX<L, K, BIG_NT>;
-    constexpr bool DBL = V::R <= 4096;
+    constexpr bool DBL = gx_double_buffered<L, K, BG>();
     // one record, small arrays first: their addresses stay within the 16-bit offset of LDS instructions
     struct alignas(16) Smem {
         double trow[BIG_LAZY + BIG_TV];

@@ -523,7 +523,7 @@ def _reconstruct(states: torch.Tensor, S: torch.Tensor, groups: list, tables: di
     Q = torch.empty(states.shape, dtype=torch.float64, device=dev)
     for gp in groups:
         rows = torch.as_tensor(gp["rows"], device=dev)
-        tab = torch.as_tensor(np.asarray(tables[gp["bits"]]), dtype=torch.float64, device=dev)
+        tab = torch.tensor(np.asarray(tables[gp["bits"]], dtype=np.float64), device=dev)
         Q.index_copy_(0, rows, tab[states.index_select(0, rows).long()] * S.index_select(0, rows)[:, None])
     return E.rht_rows(Q, in_seed, inverse=True)
 

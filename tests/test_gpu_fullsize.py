@@ -200,3 +200,20 @@ def test_config5_first_two_layers_full_shape():
             Q *= rec["scales"].cpu().numpy()[pick][:, None]
             ref = O.rht_apply(Q, kept["in_seed"], inverse=True)
             assert np.abs(Wh - ref).max() <= 1e-10 * np.abs(ref).max()
+
+
+def test_config5_build_is_reproducible():
+    """Two builds of the same two config-5 layers in one process give the same codes, bit for bit: every kernel of
+    the path reduces in a fixed order, and the forwards' bf16 products and attention repeat exactly on one GPU."""
+    from lookatmyquant_amd import stack
+
+    sh = stack.Shape()
+    tok, w = stack.calibration_tokens()
+    say("config 5: two builds of two layers, L=12")
+    a, b = (stack.build(tok, sh, w, L=12, layers=2) for _ in range(2))
+    assert a["codes"].keys() == b["codes"].keys()
+    for nm in a["codes"]:
+        assert torch.equal(a["codes"][nm]["states"], b["codes"][nm]["states"]), nm
+        assert torch.equal(a["codes"][nm]["scales"], b["codes"][nm]["scales"]), nm
+        for p, q in zip(a["codes"][nm]["packed"], b["codes"][nm]["packed"]):
+            assert torch.equal(p, q), nm

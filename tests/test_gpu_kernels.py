@@ -368,25 +368,27 @@ def test_ldlq_trellis_L16_other_widths_match_oracle(E, k):
     assert np.array_equal(st, ref)
 
 
-def test_ldlq_trellis16_k1_without_workspace_matches_oracle(E, monkeypatch):
-    """lamq_ldlq_trellis16_block at L = 16, k = 1, the entry point without a workspace (the quarter-window kernel,
-    full path costs exchanged through LDS): the same states as the oracle and as the workspace kernel, 3 rows x 272
-    columns."""
+@pytest.mark.parametrize("k", [1])
+def test_ldlq_trellis16_without_workspace_matches_oracle(E, monkeypatch, k):
+    """lamq_ldlq_trellis16_block at L = 16, the entry point without a workspace, for the width whose fused search
+    otherwise keeps its back-pointers in one (k = 1: the quarter-window kernel, full path costs exchanged through
+    LDS): the same states as the oracle and as the workspace kernel, 3 rows x 272 columns."""
     from lookatmyquant_amd.tables import quantile_table
 
-    rng = np.random.default_rng(41)
+    assert E._abi.lib().lamq_ldlq_trellis16_block_workspace_size(3, 16, k) > 0
+    rng = np.random.default_rng(40 + k)
     m, n = 3, 272
     Xa = rng.standard_normal((600, n))
     _, U, _ = O.environment(Xa.T @ Xa / 600)
     X = rng.standard_normal((m, n))
     S = O.row_scale(X)
     tab = np.asarray(quantile_table(16, 0), dtype=np.float64)
-    say("ldlq trellis L=16 k=1, 3 x 272, workspace kernel")
-    with_ws = E.ldlq_trellis(cuda(X), cuda(S), cuda(U), cuda(tab), 16, 1).cpu().numpy()
+    say(f"ldlq trellis L=16 k={k}, 3 x 272, workspace kernel")
+    with_ws = E.ldlq_trellis(cuda(X), cuda(S), cuda(U), cuda(tab), 16, k).cpu().numpy()
     monkeypatch.setattr(E._abi.lib(), "lamq_ldlq_trellis16_block_workspace_size", lambda *a: 0)
-    say("ldlq trellis L=16 k=1, 3 x 272, no workspace (lamq_ldlq_trellis16_block)")
-    without = E.ldlq_trellis(cuda(X), cuda(S), cuda(U), cuda(tab), 16, 1).cpu().numpy()
-    ref = O.ldlq_trellis(X, U, S, tab, 16, 1)
+    say(f"ldlq trellis L=16 k={k}, 3 x 272, no workspace (lamq_ldlq_trellis16_block)")
+    without = E.ldlq_trellis(cuda(X), cuda(S), cuda(U), cuda(tab), 16, k).cpu().numpy()
+    ref = O.ldlq_trellis(X, U, S, tab, 16, k)
     assert np.array_equal(with_ws, ref)
     assert np.array_equal(without, ref)
 

@@ -68,6 +68,10 @@ def test_argument_errors_are_reported_without_a_gpu():
     assert L.lamq_pack_codes(None, 8, 8, None, 8, 8, 0, 2, 12, 1, ptr(q), 8, ptr(q), None) == -1
     assert L.lamq_chol_inv_upper_workspace_size(10) >= 800
     assert L.lamq_viterbi_workspace_size(3, 100, 12, 2) == 3 * 100 * 256
+    # the fused 16-bit-state search keeps its back-pointers (23 steps x 1024 words a row) in a workspace where LDS
+    # cannot hold them (k = 1, 2^15 groups); k = 2, 3, 4 keep them in LDS
+    for k, words in ((1, 23 * 1024), (2, 0), (3, 0), (4, 0)):
+        assert L.lamq_ldlq_trellis16_block_workspace_size(5, 16, k) == 5 * 4 * words
 
 
 def test_hadamard_factors_and_signs_equal_the_reference(golden):
