@@ -31,6 +31,7 @@ counters of a profiler run.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -74,6 +75,20 @@ def trellis_line(ms: float, ops: float, launches: int) -> dict:
     line["issue_ceiling"] = round(VALU_ISSUE_TOPS, 1)
     line["frac_of_issue_ceiling"] = round(line["achieved"] / VALU_ISSUE_TOPS, 4)
     return line
+
+
+def spin_cycles(us: float) -> int:
+    """torch.cuda._sleep cycles that keep the stream busy for about `us` microseconds, measured once on this GPU."""
+    import torch
+
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(1000)
+    a.record()
+    torch.cuda._sleep(1_000_000)
+    b.record()
+    torch.cuda.synchronize()
+    per_us = 1_000_000 / max(a.elapsed_time(b) * 1e3, 1e-3)
+    return max(1, int(us * per_us))
 
 
 # ----------------------------------------------------------------------------- the CPU baseline
@@ -514,8 +529,10 @@ def run_c3(args):
     ms = (time.perf_counter() - t1) * 1e3 / args.steps
     bad = sum(int(b.item()) for _, b in out.values())
     assert bad == 0
-    # the per-kernel lines: one more build with every launch timed in turn (row groups one after the other)
-    kt = E.KernelTimer()
+    # the per-kernel lines: one more build with every launch timed in turn (row groups one after the other). The
+    # host enqueues this build's short launches more slowly than the GPU runs them, so each span starts behind a GPU
+    # spin of about 100 us (outside the span): the span then times its kernel, not the host's launch latency.
+    kt = E.KernelTimer(lead_cycles=spin_cycles(100.0))
     step(kt)
     torch.cuda.synchronize()
     weights = 2 * inter * hid + hid * inter
@@ -627,6 +644,10 @@ def main():
         print("bench.py measures one GPU: the per-matrix hot path runs on one MI355X here (rows would shard across "
               "GPUs with no communication). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    # no collector passes inside the timed regions: a generation-2 pass over the many event objects of a timed build
+    # stalls the host for tens of ms, and where the GPU has drained its queue by then, the stall lands inside a span
+    gc.collect()
+    gc.disable()
     {"c2": run_c2, "c3": run_c3, "c4": run_c4, "c5": run_c5}[args.workload](args)
     if args.copy_probe:
         copy_probe(args.copy_probe)

@@ -329,6 +329,7 @@ def _refit_rest(T, U, Z, B0, B1, look, events):
 def _event_pair(events: dict | None, key: str):
     if events is None:
         return None
+    _lead(events)
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     events.setdefault(key, []).append((a, b))
@@ -366,17 +367,32 @@ def trailing_flops(m: int, n: int, lazy: int = 128) -> float:
     return float(sum(2 * m * (min(b0 + lazy, n) - b0) * (n - min(b0 + lazy, n)) for b0 in range(0, n, lazy)))
 
 
+class EventLog(dict):
+    """key -> list of (start, end) torch.cuda.Event pairs. lead_cycles > 0: before each span's start event, a GPU spin
+    of that many cycles (torch.cuda._sleep) keeps the stream busy while the host enqueues the span, so that a span
+    times its kernel and not the host's launch latency where the host, not the GPU, sets the pace."""
+
+    lead_cycles = 0
+
+
+def _lead(events):
+    if getattr(events, "lead_cycles", 0):
+        torch.cuda._sleep(int(events.lead_cycles))
+
+
 class KernelTimer:
     """Event pairs recorded on the current stream around launches, by key, with the algorithmic work (flops, ops or
     bytes) each span does. events[key] is the list of (start, end) torch.cuda.Event pairs (the sweeps append their
-    per-launch pairs under "block" and "trailing" to the same dict)."""
+    per-launch pairs under "block" and "trailing" to the same log). lead_cycles: see EventLog."""
 
-    def __init__(self):
-        self.events: dict = {}
+    def __init__(self, lead_cycles: int = 0):
+        self.events = EventLog()
+        self.events.lead_cycles = int(lead_cycles)
         self.work: dict = {}
 
     @contextlib.contextmanager
     def span(self, key: str, work: float = 0.0):
+        _lead(self.events)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
         yield

@@ -642,9 +642,10 @@ def test_kl_rows(E, T, V):
                          torch.from_numpy(w).cuda())
     ref, mean = O.kl_rows(r, q, w)
     kl = kl.cpu().numpy().astype(np.float64)
-    err = np.abs(kl - ref).max() / np.abs(ref).max()
-    say(f"  max relative KL error {err:.3e}")
-    assert err < 1e-4
+    # per token: float32 chunk sums against the float64 oracle
+    err = (np.abs(kl - ref) / np.abs(ref)).max()
+    say(f"  largest per-token relative KL error {err:.3e}")
+    assert np.all(np.abs(kl - ref) <= 1e-4 * np.abs(ref) + 1e-9)
     s = sums.cpu().numpy()
     assert abs(s[0] / s[1] - mean) < 1e-4 * abs(mean)
 
