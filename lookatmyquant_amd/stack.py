@@ -485,7 +485,7 @@ def saved_codes(out: dict) -> dict:
         for ti, gp in enumerate(rec["groups"]):
             rows = torch.as_tensor(gp["rows"], dtype=torch.long)
             states[rows] = (st[rows] + 4096 * ti).to(torch.int16)
-            tabs.append(torch.as_tensor(np.asarray(out["tables"][int(gp["bits"])]), dtype=torch.float32))
+            tabs.append(torch.tensor(np.asarray(out["tables"][int(gp["bits"])], dtype=np.float32)))
             groups.append({"rows": rows, "bits": int(gp["bits"]), "table_index": ti})
         saved[name] = {"states": states, "scales": rec["scales"].float().cpu(), "in_seed": int(rec["in_seed"]),
                        "table": torch.cat(tabs), "row_groups": groups, "trellis_layout": "row"}

@@ -74,7 +74,9 @@ def logits(T: int, V: int, seed_ref: int = 401, seed_noise: int = 402, noise: fl
 def row_plan(m: int, seed: int, groups: int = 8, target_bpw: float = 2.30,
              probs=(0.122, 0.434, 0.378, 0.066)) -> list[dict]:
     """A rowgroup plan for one matrix: a random permutation of the rows cut into `groups` groups (multiples of 64
-    rows), bits 1-4 drawn with the LM2 histogram and adjusted until the mean is within 0.05 of `target_bpw`."""
+    rows), bits 1-4 drawn with the LM2 histogram and adjusted until the mean is within 0.125 of `target_bpw`; then
+    64 rows at a time move between groups one bit apart until the mean bits per row is within 32 / m of it (2.3
+    exactly at the configurations' row counts that are multiples of 320)."""
     rng = np.random.default_rng(seed)
     perm = rng.permutation(m)
     size = m // groups // 64 * 64
@@ -82,13 +84,24 @@ def row_plan(m: int, seed: int, groups: int = 8, target_bpw: float = 2.30,
     bits = rng.choice([1, 2, 3, 4], size=groups, p=np.asarray(probs) / np.sum(probs))
     for _ in range(64):
         mean = float(np.dot(bits, sizes) / m)
-        if abs(mean - target_bpw) < 0.05:
+        if abs(mean - target_bpw) <= 0.125:
             break
         i = int(rng.integers(groups))
         if mean < target_bpw and bits[i] < 4:
             bits[i] += 1
         elif mean > target_bpw and bits[i] > 1:
             bits[i] -= 1
+    for _ in range(4 * m // 64):
+        d = target_bpw * m - float(np.dot(bits, sizes))
+        if abs(d) <= 32:
+            break
+        up = 1 if d > 0 else -1
+        pairs = [(i, j) for i in range(groups) for j in range(groups) if bits[j] - bits[i] == up and sizes[i] > 64]
+        if not pairs:
+            break
+        i, j = pairs[int(rng.integers(len(pairs)))]
+        sizes[i] -= 64
+        sizes[j] += 64
     out, r0 = [], 0
     for g, (s, b) in enumerate(zip(sizes, bits)):
         out.append({"group": g, "rows": sorted(int(v) for v in perm[r0 : r0 + s]), "bits": int(b)})

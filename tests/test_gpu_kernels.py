@@ -28,7 +28,8 @@ def E():
 
 
 def cuda(a, dtype=None):
-    t = torch.as_tensor(np.ascontiguousarray(a))
+    a = np.ascontiguousarray(a)
+    t = torch.as_tensor(a if a.flags.writeable else a.copy())
     if dtype is not None:
         t = t.to(dtype)
     return t.cuda()

@@ -112,3 +112,44 @@ def test_attention_matches_a_float64_reference():
     say(f"  max |diff| against float64: {err:.3e}")
     assert err < 3e-2
     assert torch.equal(got[:, :, 0], vd[:, :, 0].float().bfloat16().double())  # the first position attends to itself
+
+
+def test_cli_plan_driven_build(tmp_path):
+    """python -m lookatmyquant_amd.quantize (quantize.py:923-989's arguments): one layer of the Qwen3.5-4B-shaped stack
+    from a plan file and a rowgroup-plan-1 file, with the saved codes and the artifact written; then the same layer
+    under one program for every linear."""
+    import json
+
+    from lookatmyquant_amd import stack
+    from lookatmyquant_amd.quantize import main
+    from lookatmyquant_amd.rowplan import write_row_plan
+
+    sh = stack.Shape()
+    plan, rp = stack.synthetic_plans(sh, 1)
+    (tmp_path / "plan.json").write_text(json.dumps(plan))
+    write_row_plan(tmp_path / "rows.json", rp, stack.active_shapes(sh, plan, 1))
+    small = ["--layers", "1", "--calib", "4", "--calib-len", "256", "--redamp"]
+    print("quantize --program plan, one layer", flush=True)
+    main(["--program", "plan", "--plan", str(tmp_path / "plan.json"), "--row-plan", str(tmp_path / "rows.json"),
+          *small, "--save-codes", str(tmp_path / "codes.pt"), "--artifact", str(tmp_path / "art"),
+          "--out", str(tmp_path / "res.json")])
+    res = json.loads((tmp_path / "res.json").read_text())
+    shapes = stack.matrix_shapes(sh)
+    assert res["layers"] == 1 and res["weights"] == sum(m * n for m, n in shapes.values())
+    assert abs(res["bits per weight"] - 2.3) < 0.1
+    assert res["row plan"]["matrices"] == 7
+    assert res["artifact"]["all_tensor_bytes_verified"] and res["artifact"]["tensor_count"] > 7
+    saved = torch.load(tmp_path / "codes.pt", weights_only=True)
+    assert sorted(saved) == sorted(f"model.layers.0.{nm}.weight" for nm in shapes)
+    for name, e in saved.items():
+        m, n = shapes[name.split(".", 3)[3][: -len(".weight")]]
+        assert e["states"].shape == (m, n) and e["trellis_layout"] == "row"
+        rows = torch.cat([g["rows"] for g in e["row_groups"]])
+        assert torch.equal(rows.sort().values, torch.arange(m))  # every row in exactly one group
+        for g in e["row_groups"]:
+            s = e["states"][g["rows"]].long() - 4096 * g["table_index"]
+            assert int(s.min()) >= 0 and int(s.max()) < 4096
+    print("quantize --program tr3x, one layer", flush=True)
+    main(["--program", "tr3x", *small, "--out", str(tmp_path / "res3.json")])
+    res3 = json.loads((tmp_path / "res3.json").read_text())
+    assert abs(res3["bits per weight"] - 3.0) < 0.01 and res3["row plan"] is None
