@@ -120,6 +120,27 @@ int lamq_ldlq_trellis16_block_ws(double* T, int64_t m, int64_t n, int64_t ldT, c
                                  int64_t lds, double* Z, int64_t ldZ, int64_t pre, void* workspace,
                                  size_t workspace_bytes, void* stream);
 
+/* The fused block of every row group of a stage in one launch (the per-group sweeps of quantize.py:502-565 over a
+ * stage's row groups, quantize_row_groups, as one batched sweep): group g is the rows [r0, r0 + rows) of T, S, state,
+ * states and Z, swept at its k with its tables, and its workspace (lamq_ldlq_trellis16_block_workspace_size(rows, L,
+ * k) bytes) where that is not 0. The states, Z and T are lamq_ldlq_trellis16_block_ws's for each group, bit for bit;
+ * one launch over all the rows leaves no idle tail between the groups' launches. At most
+ * LAMQ_TRELLIS_MAX_GROUPS groups; their row ranges lie in [0, m) and do not overlap. */
+#define LAMQ_TRELLIS_MAX_GROUPS 8
+typedef struct {
+    int64_t r0;
+    int64_t rows;
+    int k;
+    const double* table64;
+    const uint16_t* table16;
+    void* workspace;
+    size_t workspace_bytes;
+} lamq_trellis_group;
+int lamq_ldlq_trellis16_block_groups(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU,
+                                     const double* S, int L, const lamq_trellis_group* groups, int ngroups,
+                                     int64_t b0, int64_t b1, int width, int look, int32_t* state, int32_t* states,
+                                     int64_t lds, double* Z, int64_t ldZ, int64_t pre, void* stream);
+
 /* ------------------------------------------------------------------------------------------------
  * The lazy trailing update T[:, b1:n] -= Z @ U[b0:b1, b1:n] on fp64 MFMA.
  * Replaces opgraph/syntax.py:122-123 (and opgraph/ldlq_gpu.py:48).

@@ -32,6 +32,8 @@ SIGNATURES = {
     "lamq_ldlq_trellis16_block_ws": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _p, _p, _c_int, _c_int, _c_i64,
                                               _c_i64, _c_int, _c_int, _p, _p, _c_i64, _p, _c_i64, _c_i64, _p,
                                               ctypes.c_size_t, _p]),
+    "lamq_ldlq_trellis16_block_groups": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _c_int, _p, _c_int,
+                                                  _c_i64, _c_i64, _c_int, _c_int, _p, _p, _c_i64, _p, _c_i64, _c_i64, _p]),
     "lamq_trailing_update_f64": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _c_i64, _c_i64, _c_i64, _p]),
     "lamq_gemm_sub_f64": (_c_int, [_p, _c_i64, _p, _c_i64, _p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _p]),
     "lamq_refit_step": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _c_i64, _c_i64, _c_int, _c_i64, _c_i64, _p,
@@ -56,6 +58,14 @@ SIGNATURES = {
     "lamq_pack_trellis": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _p, _c_i64, _p, _p]),
     "lamq_pack_codes": (_c_int, [_p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _p, _c_i64, _p, _p]),
 }
+
+
+class TrellisGroup(ctypes.Structure):
+    """lamq_trellis_group of include/lamq.h: one row group of lamq_ldlq_trellis16_block_groups."""
+
+    _fields_ = [("r0", _c_i64), ("rows", _c_i64), ("k", _c_int), ("table64", _p), ("table16", _p), ("workspace", _p),
+                ("workspace_bytes", _c_size)]
+
 
 _LIB = None
 

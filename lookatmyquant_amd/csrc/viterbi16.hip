@@ -390,26 +390,33 @@ constexpr bool gx_double_buffered() { return gx_lds_bytes<L, K, BG>(true) <= 160
 // BG: the back-pointers in back_ws, (BIG_TV - 1) * BIG_NT words per row, instead of LDS (the 2^15-group search,
 // whose 128 KB of group minima leave no LDS for them)
 template <int L, int K, bool BG>
-__global__ __launch_bounds__(BIG_NT) void ldlq_trellis_block_gx_kernel(
-    const double* __restrict__ T, int64_t n, int64_t ldT, const double* __restrict__ U, int64_t ldU,
-    const double* __restrict__ S, const double* __restrict__ table64, const uint16_t* __restrict__ table16,
-    int64_t b0, int64_t b1, int width, int look, int32_t* __restrict__ state, int32_t* __restrict__ states,
-    int64_t lds, double* __restrict__ Z, int64_t ldZ, uint32_t* __restrict__ back_ws, int pre)
+struct alignas(16) GxSmem {
+    using V = VX<L, K, BIG_NT>;
+    static constexpr bool DBL = gx_double_buffered<L, K, BG>();
+    // small arrays first: their addresses stay within the 16-bit offset of LDS instructions
+    double trow[BIG_LAZY + BIG_TV];
+    double ubb[LAMQ_WMAX * LAMQ_WMAX];
+    double zs[LAMQ_WMAX];
+    float xs[BIG_TV];
+    int path[BIG_TV];
+    float red[2 * (BIG_NT / 64)];
+    float buf[(DBL ? 2 : 1) * V::R];
+    uint32_t back[BG ? 1 : (BIG_TV - 1) * V::ACT];
+};
+
+// One row's lazy block [b0, b1): `row` indexes T, S, state, states and Z; `wrow` the row's back-pointer slot in back_ws
+// (BG).
+template <int L, int K, bool BG>
+__device__ __forceinline__ void gx_block_row(GxSmem<L, K, BG>& sm, int64_t row, int64_t wrow,
+                                             const double* __restrict__ T, int64_t n, int64_t ldT,
+                                             const double* __restrict__ U, int64_t ldU, const double* __restrict__ S,
+                                             const double* __restrict__ table64, const uint16_t* __restrict__ table16,
+                                             int64_t b0, int64_t b1, int width, int look, int32_t* __restrict__ state,
+                                             int32_t* __restrict__ states, int64_t lds, double* __restrict__ Z,
+                                             int64_t ldZ, uint32_t* __restrict__ back_ws, int pre)
 {
     using V = VX<L, K, BIG_NT>;
-    constexpr bool DBL = gx_double_buffered<L, K, BG>();
-    // one record, small arrays first: their addresses stay within the 16-bit offset of LDS instructions
-    struct alignas(16) Smem {
-        double trow[BIG_LAZY + BIG_TV];
-        double ubb[LAMQ_WMAX * LAMQ_WMAX];
-        double zs[LAMQ_WMAX];
-        float xs[BIG_TV];
-        int path[BIG_TV];
-        float red[2 * (BIG_NT / 64)];
-        float buf[(DBL ? 2 : 1) * V::R];
-        uint32_t back[BG ? 1 : (BIG_TV - 1) * V::ACT];
-    };
-    __shared__ Smem sm;
+    constexpr bool DBL = GxSmem<L, K, BG>::DBL;
     double* trow = sm.trow;
     double* ubb = sm.ubb;
     double* zs = sm.zs;
@@ -417,8 +424,7 @@ __global__ __launch_bounds__(BIG_NT) void ldlq_trellis_block_gx_kernel(
     int* path = sm.path;
     float* red = sm.red;
     float* buf = sm.buf;
-    const int64_t row = blockIdx.x;
-    uint32_t* back = BG ? back_ws + row * (int64_t)((BIG_TV - 1) * V::ACT) : sm.back;
+    uint32_t* back = BG ? back_ws + wrow * (int64_t)((BIG_TV - 1) * V::ACT) : sm.back;
     const int tid = threadIdx.x;
     const int64_t cend = (b1 + look < n) ? b1 + look : n;
     load_block_row<BIG_NT>(trow, T + row * ldT, b0, (int)(b1 - b0), (int)(cend - b0), Z + row * ldZ - pre, pre, U,
@@ -447,6 +453,94 @@ __global__ __launch_bounds__(BIG_NT) void ldlq_trellis_block_gx_kernel(
         st = path[w - 1];
     }
     if (tid == 0) state[row] = st;
+}
+
+template <int L, int K, bool BG>
+__global__ __launch_bounds__(BIG_NT) void ldlq_trellis_block_gx_kernel(
+    const double* __restrict__ T, int64_t n, int64_t ldT, const double* __restrict__ U, int64_t ldU,
+    const double* __restrict__ S, const double* __restrict__ table64, const uint16_t* __restrict__ table16,
+    int64_t b0, int64_t b1, int width, int look, int32_t* __restrict__ state, int32_t* __restrict__ states,
+    int64_t lds, double* __restrict__ Z, int64_t ldZ, uint32_t* __restrict__ back_ws, int pre)
+{
+    __shared__ GxSmem<L, K, BG> sm;
+    gx_block_row<L, K, BG>(sm, blockIdx.x, blockIdx.x, T, n, ldT, U, ldU, S, table64, table16, b0, b1, width, look, state,
+                           states, lds, Z, ldZ, back_ws, pre);
+}
+
+// ------------------------------------------------------------------------------------------------ row groups at once
+// One launch for every row group of a stage: the groups differ in bits per weight (k), and a launch per group ends in
+// a tail of idle CUs (one 1024-thread row per CU, so ceil(rows / 256) rounds), which one launch over all their rows
+// does not have. Workgroup b takes row b of the concatenated groups, finds its group (a uniform scan of at most
+// LAMQ_TRELLIS_MAX_GROUPS entries) and runs that width's search in that width's LDS layout over one shared array.
+struct GxGroup {
+    int64_t r0, rows;
+    const double* table64;
+    const uint16_t* table16;
+    uint32_t* back_ws;
+    int k;
+};
+struct GxGroups {
+    GxGroup g[LAMQ_TRELLIS_MAX_GROUPS];
+    int count;
+};
+
+// back-pointers outside LDS: more groups than LDS holds next to their minima
+template <int L, int K>
+constexpr bool gx_back_global() { return VX<L, K, BIG_NT>::R > BIG_GX_MAX_R; }
+
+template <int L, int K>
+constexpr int gx_smem_bytes() { return (int)sizeof(GxSmem<L, K, gx_back_global<L, K>()>); }
+
+template <int L>
+constexpr int gx_groups_smem_bytes()
+{
+    int b = 0;
+    if constexpr (L - 12 >= 1) b = gx_smem_bytes<L, 1>() > b ? gx_smem_bytes<L, 1>() : b;
+    if constexpr (L - 12 >= 2) b = gx_smem_bytes<L, 2>() > b ? gx_smem_bytes<L, 2>() : b;
+    if constexpr (L - 12 >= 3) b = gx_smem_bytes<L, 3>() > b ? gx_smem_bytes<L, 3>() : b;
+    if constexpr (L - 12 >= 4) b = gx_smem_bytes<L, 4>() > b ? gx_smem_bytes<L, 4>() : b;
+    return b;
+}
+
+template <int L, int K>
+__device__ __forceinline__ void gx_group_row(uint8_t* raw, const GxGroup& G, int64_t b, const double* T, int64_t n,
+                                             int64_t ldT, const double* U, int64_t ldU, const double* S, int64_t b0,
+                                             int64_t b1, int width, int look, int32_t* state, int32_t* states,
+                                             int64_t lds, double* Z, int64_t ldZ, int pre)
+{
+    constexpr bool BG = gx_back_global<L, K>();
+    gx_block_row<L, K, BG>(*reinterpret_cast<GxSmem<L, K, BG>*>(raw), G.r0 + b, b, T, n, ldT, U, ldU, S, G.table64,
+                           G.table16, b0, b1, width, look, state, states, lds, Z, ldZ, G.back_ws, pre);
+}
+
+template <int L>
+__global__ __launch_bounds__(BIG_NT) void ldlq_trellis_groups_gx_kernel(
+    const double* __restrict__ T, int64_t n, int64_t ldT, const double* __restrict__ U, int64_t ldU,
+    const double* __restrict__ S, int64_t b0, int64_t b1, int width, int look, int32_t* __restrict__ state,
+    int32_t* __restrict__ states, int64_t lds, double* __restrict__ Z, int64_t ldZ, int pre, GxGroups groups)
+{
+    __shared__ __align__(16) uint8_t raw[gx_groups_smem_bytes<L>()];
+    int64_t b = blockIdx.x;
+    int i = 0;
+    while (i + 1 < groups.count && b >= groups.g[i].rows) {
+        b -= groups.g[i].rows;
+        ++i;
+    }
+    const GxGroup& G = groups.g[i];
+    switch (G.k) {
+    case 1:
+        if constexpr (L - 12 >= 1) gx_group_row<L, 1>(raw, G, b, T, n, ldT, U, ldU, S, b0, b1, width, look, state, states, lds, Z, ldZ, pre);
+        break;
+    case 2:
+        if constexpr (L - 12 >= 2) gx_group_row<L, 2>(raw, G, b, T, n, ldT, U, ldU, S, b0, b1, width, look, state, states, lds, Z, ldZ, pre);
+        break;
+    case 3:
+        if constexpr (L - 12 >= 3) gx_group_row<L, 3>(raw, G, b, T, n, ldT, U, ldU, S, b0, b1, width, look, state, states, lds, Z, ldZ, pre);
+        break;
+    default:
+        if constexpr (L - 12 >= 4) gx_group_row<L, 4>(raw, G, b, T, n, ldT, U, ldU, S, b0, b1, width, look, state, states, lds, Z, ldZ, pre);
+        break;
+    }
 }
 
 template <int L, int K>
@@ -517,4 +611,60 @@ extern "C" int lamq_ldlq_trellis16_block_ws(double* T, int64_t m, int64_t n, int
     return dispatch_big<TrellisBlockBig>(L, k, T, m, n, ldT, U, ldU, S, table64, table16, b0, b1, width, look, state,
                                          states, lds, Z, ldZ, reinterpret_cast<uint32_t*>(workspace), (int)pre,
                                          as_stream(stream));
+}
+
+template <int L>
+static void launch_groups(const GxGroups& gg, int64_t total, double* T, int64_t n, int64_t ldT, const double* U,
+                          int64_t ldU, const double* S, int64_t b0, int64_t b1, int width, int look, int32_t* state,
+                          int32_t* states, int64_t lds, double* Z, int64_t ldZ, int pre, hipStream_t s)
+{
+    hipLaunchKernelGGL((ldlq_trellis_groups_gx_kernel<L>), dim3((unsigned)total), dim3(BIG_NT), 0, s, T, n, ldT, U, ldU,
+                       S, b0, b1, width, look, state, states, lds, Z, ldZ, pre, gg);
+}
+
+extern "C" int lamq_ldlq_trellis16_block_groups(double* T, int64_t m, int64_t n, int64_t ldT, const double* U,
+                                                int64_t ldU, const double* S, int L, const lamq_trellis_group* groups,
+                                                int ngroups, int64_t b0, int64_t b1, int width, int look,
+                                                int32_t* state, int32_t* states, int64_t lds, double* Z, int64_t ldZ,
+                                                int64_t pre, void* stream)
+{
+    if (!T || !U || !S || !state || !states || !Z || !groups) return LAMQ_EINVAL;
+    if (ngroups < 1 || ngroups > LAMQ_TRELLIS_MAX_GROUPS) return LAMQ_EINVAL;
+    if (m < 0 || n < 1 || ldT < n || ldU < n || lds < n || b0 < 0 || b1 <= b0 || b1 > n || width < 1 || look < 0)
+        return LAMQ_EINVAL;
+    if (pre < 0 || pre > b0 || ldZ < pre + (b1 - b0)) return LAMQ_EINVAL;
+    if (width > LAMQ_WMAX || width + look > BIG_TV || b1 - b0 > BIG_LAZY || m > 0x7fffffff || pre > LAMQ_PRE_MAX)
+        return LAMQ_EUNSUP;
+    if (L < 13 || L > 16) return LAMQ_EUNSUP;
+    GxGroups gg{};
+    int64_t total = 0;
+    for (int i = 0; i < ngroups; ++i) {
+        const lamq_trellis_group& g = groups[i];
+        if (g.r0 < 0 || g.rows < 0 || g.r0 > m - g.rows) return LAMQ_EINVAL;
+        if (!g.table64 || !g.table16 || ((uintptr_t)g.table16 % 4) != 0) return LAMQ_EINVAL;
+        if (g.k < 1 || g.k > 4 || g.k > L - 12) return LAMQ_EUNSUP;
+        const size_t need = lamq_ldlq_trellis16_block_workspace_size(g.rows, L, g.k);
+        if (need && (!g.workspace || g.workspace_bytes < need || ((uintptr_t)g.workspace % 4) != 0)) return LAMQ_EINVAL;
+        for (int j = 0; j < i; ++j)  // the row ranges do not overlap
+            if (g.rows && groups[j].rows && g.r0 < groups[j].r0 + groups[j].rows && groups[j].r0 < g.r0 + g.rows)
+                return LAMQ_EINVAL;
+        gg.g[i].r0 = g.r0;
+        gg.g[i].rows = g.rows;
+        gg.g[i].table64 = g.table64;
+        gg.g[i].table16 = g.table16;
+        gg.g[i].back_ws = reinterpret_cast<uint32_t*>(g.workspace);
+        gg.g[i].k = g.k;
+        total += g.rows;
+    }
+    gg.count = ngroups;
+    if (total == 0) return LAMQ_OK;
+    hipStream_t s = as_stream(stream);
+    switch (L) {
+    case 13: launch_groups<13>(gg, total, T, n, ldT, U, ldU, S, b0, b1, width, look, state, states, lds, Z, ldZ, (int)pre, s); break;
+    case 14: launch_groups<14>(gg, total, T, n, ldT, U, ldU, S, b0, b1, width, look, state, states, lds, Z, ldZ, (int)pre, s); break;
+    case 15: launch_groups<15>(gg, total, T, n, ldT, U, ldU, S, b0, b1, width, look, state, states, lds, Z, ldZ, (int)pre, s); break;
+    default: launch_groups<16>(gg, total, T, n, ldT, U, ldU, S, b0, b1, width, look, state, states, lds, Z, ldZ, (int)pre, s); break;
+    }
+    LAMQ_LAUNCH_CHECK();
+    return LAMQ_OK;
 }

@@ -170,10 +170,12 @@ def ldlq_trellis_groups(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, group
                         events: dict | None = None, concurrent: bool | None = None) -> torch.Tensor:
     """ldlq_trellis over consecutive row groups that share U but not the code: groups = [(rows, k, table64,
     table32 or None)] in row order, summing to X's rows. Rows do not interact (the block kernel and the trailing
-    update work row by row), so each group's sweep is independent of the others: with `concurrent` (the default
-    without events) every group runs its whole sweep, block kernels and its own trailing updates, on a stream of
-    its own, and the groups' VALU-bound searches and fp64 MFMA products overlap on the chip; the results are those
-    of sweeping the groups one after the other. With events every launch is timed on the caller's stream in turn."""
+    update work row by row), so each group's sweep is independent of the others. With 16-bit states (L >= BIG_L) all
+    groups go through one launch per lazy block (lamq_ldlq_trellis16_block_groups) and one trailing product over all
+    rows. Below that, with `concurrent` (the default without events) every group runs its whole sweep, block kernels
+    and its own trailing updates, on a stream of its own, and the groups' VALU-bound searches and fp64 MFMA products
+    overlap on the chip. Either way the results are those of sweeping the groups one after the other. With events
+    every launch is timed on the caller's stream in turn."""
     check_tables(groups, L)
     need(X, torch.float64, "X", 2)
     need(U, torch.float64, "U", 2)
@@ -221,10 +223,19 @@ def ldlq_trellis_groups(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, group
     states = torch.empty(m, n, dtype=torch.int32, device=dev)
     outer = _outer_run(lazy)
     Z = torch.empty(m, outer, dtype=torch.float64, device=dev)
+    # the 16-bit-state groups go through one launch per lazy block (lamq_ldlq_trellis16_block_groups): every group's
+    # rows in one grid, so no group's launch ends in a tail of idle CUs and no stream per group is needed
+    merged = None
+    if L >= BIG_L and len(parts) > 1:
+        merged = (_abi.TrellisGroup * len(parts))()
+        for i, (r0, rows, k, table64, t32) in enumerate(parts):
+            w = ws.get(r0)
+            merged[i] = _abi.TrellisGroup(r0, rows, k, table64.data_ptr(), t32.data_ptr(),
+                                          None if w is None else w.data_ptr(), 0 if w is None else w.numel())
     if concurrent is None:
         concurrent = events is None
     main = torch.cuda.current_stream(dev)
-    lanes = _group_streams(dev) if concurrent and len(parts) > 1 else [main]
+    lanes = _group_streams(dev) if concurrent and len(parts) > 1 and merged is None else [main]
     for ln in lanes:
         if ln is not main:
             ln.wait_stream(main)
@@ -239,7 +250,14 @@ def ldlq_trellis_groups(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, group
         for b0 in range(B0, B1, lazy):
             b1 = min(b0 + lazy, n)
             pre = b0 - B0 if b1 == B1 else 0
-            for p, (r0, rows, k, table64, t32) in enumerate(parts):
+            if merged is not None:
+                ev = _event_pair(events, "block")
+                check(lib().lamq_ldlq_trellis16_block_groups(
+                    ptr(T), m, n, n, ptr(U), ld(U), ptr(S), L, ctypes.addressof(merged), len(parts), b0, b1, width,
+                    look, ptr(state), ptr(states), n, vp(Z.data_ptr() + 8 * (b0 - B0)), outer, pre, stream(dev)),
+                    "ldlq_trellis16_block_groups")
+                _event_end(ev)
+            for p, (r0, rows, k, table64, t32) in enumerate(parts if merged is None else ()):
                 Tp, Zp = views[p]
                 with torch.cuda.stream(lanes[p % len(lanes)]):
                     zb = Zp[:, b0 - B0 :]

@@ -56,6 +56,28 @@ def test_argument_errors_are_reported_without_a_gpu():
     # earlier run columns beyond the block's start, or a Z too narrow to hold them
     assert L.lamq_ldlq_trellis_block(ptr(p), 1, 8, 8, ptr(p), 8, ptr(p), ptr(p), ptr(p), 12, 2, 0, 8, 4, 4, ptr(q), ptr(q),
                                      8, ptr(p), 8, 1, None) == -1
+    # row groups in one launch: overlapping rows, rows past m, a width the 16-bit trellis lacks, k = 1 at L = 16
+    # without the workspace its back-pointers need, too many groups
+    from ctypes import addressof
+
+    def groups(*gs):
+        arr = (_abi.TrellisGroup * len(gs))()
+        for i, (r0, rows, k, wsb) in enumerate(gs):
+            arr[i] = _abi.TrellisGroup(r0, rows, k, ptr(p), ptr(q), ptr(p) if wsb else None, wsb)
+        return arr
+
+    def call(arr, count=None, Lbits=16):
+        return L.lamq_ldlq_trellis16_block_groups(ptr(p), 8, 8, 8, ptr(p), 8, ptr(p), Lbits, addressof(arr),
+                                                  len(arr) if count is None else count, 0, 8, 4, 4, ptr(q), ptr(q), 8,
+                                                  ptr(p), 8, 0, None)
+
+    assert call(groups((0, 5, 2, 0), (4, 4, 3, 0))) == -1
+    assert call(groups((0, 5, 2, 0), (5, 4, 3, 0))) == -1
+    assert call(groups((0, 4, 5, 0))) == -2
+    assert call(groups((0, 4, 3, 0)), Lbits=14) == -2
+    assert call(groups((0, 4, 1, 0))) == -1
+    assert call(groups((0, 4, 1, 8)), count=0) == -1
+    assert call(groups(*[(i, 1, 2, 0) for i in range(9)])) == -1
     assert L.lamq_ldlq_trellis16_block(ptr(p), 1, 8, 8, ptr(p), 8, ptr(p), ptr(p), ptr(p), 16, 2, 4, 8, 4, 4, ptr(q),
                                        ptr(q), 8, ptr(p), 4, 4, None) == -1
     # a trellis width the kernels are not built for
