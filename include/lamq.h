@@ -311,6 +311,19 @@ int lamq_pack_trellis(const int32_t* states, int64_t m, int64_t n, int64_t lds, 
 int lamq_pack_codes(const int32_t* src, int64_t ld, int64_t src_rows, const int64_t* rows, int64_t m, int64_t n,
                     int32_t base, int k, int L, int trellis, uint32_t* codes, int64_t ldc, int32_t* bad, void* stream);
 
+/* ------------------------------------------------------------------------------------------------
+ * The causal softmax of the calibration forwards' attention (the forward of the model the reference's capture runs,
+ * quantize.py:1029, 1626-1694: transformers' causal attention, scores times scaling, the causal mask, softmax in
+ * float32, cast back to bf16), fused into one pass over bf16 scores:
+ *   P[r, c] = bf16( exp(s[r, c] - m_r) / sum_c' exp(s[r, c'] - m_r) ),  s = float(S[r, c]) * scale for c <= r % T,
+ *   -inf past it;  m_r = max_c s[r, c].
+ *   S, P   [rows, T] bf16 bits (row strides lds, ldp; 16-byte aligned, strides multiples of 8); rows run over
+ *          (sequence, head, query), query r % T. P may be S (same stride); otherwise they may not overlap.
+ *   T % 8 == 0, T <= 4096; scale > 0.
+ * ---------------------------------------------------------------------------------------------- */
+int lamq_causal_softmax_bf16(const uint16_t* S, uint16_t* P, int64_t rows, int T, int64_t lds, int64_t ldp,
+                             float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,108 @@
+// The causal softmax of the calibration forwards' attention, fused: bf16 scores in, bf16 probabilities out, one
+// pass. Row r of the scores is query r % T of its (sequence, head); column c is kept where c <= r % T and masked to
+// -inf past it. In float32, as the unfused chain computes it: s = float(score) * scale, m = the row's maximum,
+// e = exp(s - m), p = e / sum(e), rounded to bf16 (nearest, ties to even). One wave per row: every lane holds T / 64
+// of the row's values in registers (16-byte loads of eight consecutive scores), the maximum and the sum are wave
+// reductions in a fixed order, so a row's result does not depend on anything else that runs. The row is read whole
+// before it is written, so P may be S.
+#include "common.h"
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f)
+{
+    const uint32_t u = __float_as_uint(f);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;  // finite, non-negative inputs: no NaN case
+}
+
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+// NC chunks of 512 columns (64 lanes x 8); T <= 512 * NC
+template <int NC>
+__global__ __launch_bounds__(256) void causal_softmax_bf16_kernel(const uint16_t* __restrict__ S,
+                                                                  uint16_t* __restrict__ P, int64_t rows, int T,
+                                                                  int64_t lds, int64_t ldp, float scale)
+{
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;  // the whole wave
+    const int lane = threadIdx.x & 63;
+    const int qi = (int)(row % T);
+    const uint16_t* s = S + row * lds;
+    float v[NC][8];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int col0 = c * 512 + 8 * lane;
+        uint4 u = make_uint4(0u, 0u, 0u, 0u);
+        if (col0 < T) u = *reinterpret_cast<const uint4*>(s + col0);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int col = col0 + e;
+            const float f = bf16_bits_to_f32((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu) * scale;
+            v[c][e] = (col < T && col <= qi) ? f : -__builtin_inff();
+        }
+    }
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m = fmaxf(m, v[c][e]);
+    m = wave_max(m);  // finite: column 0 is never masked
+    float sum = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            v[c][e] = expf(v[c][e] - m);  // exp(-inf) = 0 for the masked columns
+            sum += v[c][e];
+        }
+    sum = wave_sum(sum);
+    uint16_t* p = P + row * ldp;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int col0 = c * 512 + 8 * lane;
+        if (col0 >= T) continue;
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            w[e] = f32_to_bf16_bits(v[c][2 * e] / sum) | (f32_to_bf16_bits(v[c][2 * e + 1] / sum) << 16);
+        *reinterpret_cast<uint4*>(p + col0) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+extern "C" int lamq_causal_softmax_bf16(const uint16_t* S, uint16_t* P, int64_t rows, int T, int64_t lds, int64_t ldp,
+                                        float scale, void* stream)
+{
+    if (!S || !P || rows < 0 || T < 1 || lds < T || ldp < T) return LAMQ_EINVAL;
+    if (((uintptr_t)S % 16) != 0 || ((uintptr_t)P % 16) != 0 || lds % 8 != 0 || ldp % 8 != 0) return LAMQ_EINVAL;
+    if (T % 8 != 0 || T > 4096) return LAMQ_EUNSUP;
+    if (!(scale > 0.0f) || !(scale < 3.0e38f)) return LAMQ_EINVAL;
+    if (P != S && ((P < S && P + rows * ldp > S) || (S < P && S + rows * lds > P))) return LAMQ_EINVAL;
+    if (P == S && ldp != lds) return LAMQ_EINVAL;
+    if (rows == 0) return LAMQ_OK;
+    if (cdiv(rows, 4) > 0x7fffffff) return LAMQ_EUNSUP;
+    const dim3 grid((unsigned)cdiv(rows, 4));
+    hipStream_t s = as_stream(stream);
+    if (T <= 512)
+        hipLaunchKernelGGL(causal_softmax_bf16_kernel<1>, grid, dim3(256), 0, s, S, P, rows, T, lds, ldp, scale);
+    else if (T <= 1024)
+        hipLaunchKernelGGL(causal_softmax_bf16_kernel<2>, grid, dim3(256), 0, s, S, P, rows, T, lds, ldp, scale);
+    else if (T <= 2048)
+        hipLaunchKernelGGL(causal_softmax_bf16_kernel<4>, grid, dim3(256), 0, s, S, P, rows, T, lds, ldp, scale);
+    else
+        hipLaunchKernelGGL(causal_softmax_bf16_kernel<8>, grid, dim3(256), 0, s, S, P, rows, T, lds, ldp, scale);
+    LAMQ_LAUNCH_CHECK();
+    return LAMQ_OK;
+}

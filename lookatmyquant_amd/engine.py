@@ -385,6 +385,23 @@ def trailing_flops(m: int, n: int, lazy: int = 128) -> float:
     return float(sum(2 * m * (min(b0 + lazy, n) - b0) * (n - min(b0 + lazy, n)) for b0 in range(0, n, lazy)))
 
 
+def causal_softmax(scores: torch.Tensor, scale: float, out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16 probabilities of bf16 attention scores [..., T, T] (rows: sequence, head, query): the causal mask, the
+    scale and a float32 softmax in one pass (lamq_causal_softmax_bf16). out may be scores itself."""
+    need(scores, torch.bfloat16, "scores")
+    T = scores.shape[-1]
+    if scores.dim() < 2 or scores.shape[-2] != T or not scores.is_contiguous():
+        raise ValueError("scores must be a contiguous [..., T, T] tensor")
+    out = torch.empty_like(scores) if out is None else out
+    need(out, torch.bfloat16, "out")
+    if out.shape != scores.shape or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor of the scores' shape")
+    rows = scores.numel() // T
+    check(lib().lamq_causal_softmax_bf16(ptr(scores), ptr(out), rows, T, T, T, float(scale), stream(scores.device)),
+          "causal_softmax")
+    return out
+
+
 class EventLog(dict):
     """key -> list of (start, end) torch.cuda.Event pairs. lead_cycles > 0: before each span's start event, a GPU spin
     of that many cycles (torch.cuda._sleep) keeps the stream busy while the host enqueues the span, so that a span

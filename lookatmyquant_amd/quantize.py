@@ -388,6 +388,9 @@ def main(argv=None):
     args = ap.parse_args(argv)
     if args.trellis_rows != "16,8":
         raise NotImplementedError("the fused row-trellis kernels settle 16 columns and look 8 ahead")
+    if args.calib_len % 8 or args.calib_len > 4096:
+        raise NotImplementedError("the forwards' fused attention softmax takes sequence lengths that are multiples of 8 "
+                                  "up to 4096")
     sh = stack.Shape()
     layers = args.layers or sh.layers
     if args.program == "plan":

@@ -92,26 +92,25 @@ def _lin(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return torch.matmul(x, w.t().contiguous())
 
 
-ATTENTION_BATCH = 4  # sequences per batched product in the attention (their float32 scores: 2 GB at T = 2048)
+ATTENTION_BATCH = 4  # sequences per batched product in the attention (their bf16 scores: 1 GB at T = 2048)
 
 
 def attention(q, k, v, sh: Shape):
     """Causal grouped-query attention of [B, heads, T, head_dim] bf16 q and [B, kv_heads, T, head_dim] k, v: the scores
-    q k^T / sqrt(head_dim) as a bf16 batched product, masked and soft-maxed in float32, rounded to bf16 and multiplied
-    by v. The one path of every forward here (no fused-kernel backend, no fallback), a few sequences per batched
-    product; every right operand is contiguous."""
+    q k^T as a bf16 batched product; scaled by 1/sqrt(head_dim), masked and soft-maxed in float32 and rounded to bf16
+    in one pass over them (engine.causal_softmax, in place); multiplied by v. The one path of every forward here (no
+    fused-attention backend, no fallback), a few sequences per batched product; every right operand is contiguous."""
     B, _, T, _ = q.shape
     rep = sh.heads // sh.kv_heads
     kT = k.repeat_interleave(rep, dim=1).transpose(-1, -2).contiguous()
     vv = v.repeat_interleave(rep, dim=1).contiguous()
-    mask = torch.ones(T, T, dtype=torch.bool, device=q.device).triu(1)
     out = torch.empty(B, sh.heads, T, sh.head_dim, dtype=q.dtype, device=q.device)
     scale = 1.0 / float(sh.head_dim) ** 0.5
     for b0 in range(0, B, ATTENTION_BATCH):
         b1 = min(b0 + ATTENTION_BATCH, B)
-        sc = torch.matmul(q[b0:b1], kT[b0:b1]).float().mul_(scale)
-        sc.masked_fill_(mask, float("-inf"))
-        out[b0:b1] = torch.matmul(torch.softmax(sc, -1).to(q.dtype), vv[b0:b1])
+        sc = torch.matmul(q[b0:b1], kT[b0:b1])
+        E.causal_softmax(sc, scale, out=sc)
+        out[b0:b1] = torch.matmul(sc, vv[b0:b1])
         del sc
     return out
 

@@ -88,6 +88,30 @@ def test_small_stack_build(tmp_path):
             assert np.array_equal(stored[k + ".scales"], rec["scales"].float().cpu().numpy()[rows])
 
 
+@pytest.mark.parametrize("T", [8, 64, 520, 2048, 4096])
+def test_causal_softmax_matches_a_float64_reference(T):
+    """engine.causal_softmax on bf16 scores [2, 3, T, T]: every kept entry within one bf16 rounding (2^-8 relative)
+    of the float64 softmax of float(score) * scale under the causal mask, every masked entry exactly 0; in place and
+    out of place alike, bit for bit."""
+    from lookatmyquant_amd import engine as E
+
+    g = torch.Generator(device="cuda").manual_seed(T)
+    sc = (torch.randn(2, 3, T, T, generator=g, device="cuda") * 4).to(torch.bfloat16)
+    scale = 1.0 / 128 ** 0.5
+    print(f"causal softmax T={T}", flush=True)
+    p = E.causal_softmax(sc, scale)
+    q = sc.clone()
+    E.causal_softmax(q, scale, out=q)
+    assert torch.equal(p, q)
+    ref = sc.double().cpu() * scale
+    mask = torch.ones(T, T, dtype=torch.bool).triu(1)
+    ref = torch.softmax(ref.masked_fill(mask, float("-inf")), -1)
+    got = p.double().cpu()
+    assert torch.all(got[..., mask] == 0)
+    err = (got - ref).abs()
+    assert torch.all(err <= 2.0 ** -8 * ref + 1e-30), float((err / ref.clamp(min=1e-300)).max())
+
+
 def test_attention_matches_a_float64_reference():
     """The stack's one attention path (causal grouped-query, bf16 products, float32 softmax) against the same
     attention in float64 on the CPU from the same bf16 inputs, over a batch that spans two of its sequence groups

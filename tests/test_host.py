@@ -78,6 +78,15 @@ def test_argument_errors_are_reported_without_a_gpu():
     assert call(groups((0, 4, 1, 0))) == -1
     assert call(groups((0, 4, 1, 8)), count=0) == -1
     assert call(groups(*[(i, 1, 2, 0) for i in range(9)])) == -1
+    # the fused causal softmax: a length not a multiple of 8 or past 4096, a short stride, a bad scale, overlapping
+    # output, a misaligned pointer
+    b = torch.empty(4096, dtype=torch.int16)
+    assert L.lamq_causal_softmax_bf16(ptr(b), ptr(b), 4, 12, 16, 16, 0.5, None) == -2
+    assert L.lamq_causal_softmax_bf16(ptr(b), ptr(b), 1, 4104, 4104, 4104, 0.5, None) == -2
+    assert L.lamq_causal_softmax_bf16(ptr(b), ptr(b), 4, 16, 8, 16, 0.5, None) == -1
+    assert L.lamq_causal_softmax_bf16(ptr(b), ptr(b), 4, 16, 16, 16, 0.0, None) == -1
+    assert L.lamq_causal_softmax_bf16(ptr(b), ptr(b) + 16, 4, 16, 16, 16, 0.5, None) == -1
+    assert L.lamq_causal_softmax_bf16(ptr(b) + 2, ptr(b) + 2, 4, 16, 16, 16, 0.5, None) == -1
     assert L.lamq_ldlq_trellis16_block(ptr(p), 1, 8, 8, ptr(p), 8, ptr(p), ptr(p), ptr(p), 16, 2, 4, 8, 4, 4, ptr(q),
                                        ptr(q), 8, ptr(p), 4, 4, None) == -1
     # a trellis width the kernels are not built for
