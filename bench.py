@@ -1,6 +1,6 @@
 """Benchmark of the per-matrix quantization hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--L 16|12] [--no-cpu] [--workload c5|c2|c3|c4] [--copy-probe MiB]
+    python bench.py [--steps K] [--warmup W] [--L 16|12] [--no-cpu] [--workload c5|c1|c2|c3|c4] [--copy-probe MiB]
 
 The default workload is config 5, the build of a random-initialised Qwen3.5-4B-shaped stack (36 layers x 7 linears:
 q/k/v/o [4096|1024|1024 x 2560, 2560 x 4096], gate/up [9728 x 2560], down [2560 x 9728]), and a step is one decoder
@@ -20,6 +20,8 @@ stage's bit widths swept on streams of their own, the stage factor next to the Q
 after the timed region and reported as well.
 
 The other workloads (one JSON line each):
+  --workload c1  config 1, one 960x960 q_proj with the 3-bit Lloyd-Max code: rotation, factor, width-1 sweep and
+                 packed codes per step
   --workload c2  config 2, one 960x960 q_proj: rotation, factor, row-trellis sweep and packed codes per step
   --workload c3  config 3, one Qwen3.5-4B-shaped MLP block: Hessians of [131072, 2560] and [131072, 9728] with digit
                  token weights, one factor per stage, the row-plan sweeps of gate/up and down, packed codes
@@ -47,6 +49,7 @@ METRIC = "weights quantized/sec (LDLQ+trellis) & Viterbi rows/sec; % MFMA/HBM ro
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 MFMA_F64_PEAK_TFLOPS = 78.6
 FP32_VECTOR_PEAK_TFLOPS = 157.3
+FP64_VECTOR_PEAK_TFLOPS = 78.6
 HBM_PEAK_GBS = 8000.0
 # the trellis search's own ceiling: one non-packed, non-fused fp32 VALU op per lane per clock (the search rounds after
 # every subtraction, square and addition, and packed FP32 is disabled): 256 CUs x 4 SIMDs x 16 lanes x 2.4 GHz
@@ -390,6 +393,108 @@ def cpu_baseline_c2(W, H, table, L, k, in_seed, threads, budget_s=8.0):
             "seconds_total_extrapolated": round(total, 3)}
 
 
+def scalar_ops_per_row(n: int, K: int, lazy: int = 128) -> float:
+    """Algorithmic work of the width-1 sweep per row (syntax.py:106-121 with the search of nested.py:127-140): per
+    entry the search's K subtractions, K squares and K - 1 comparisons and the division z = E / U_jj; per lazy block
+    of w columns the in-block rank-1 refits, w (w - 1) / 2 fused multiply-adds of two flops each."""
+    ops = 0.0
+    for b0 in range(0, n, lazy):
+        w = min(lazy, n - b0)
+        ops += w * (3 * K) + w * (w - 1)
+    return ops
+
+
+def run_c1(args):
+    """Config 1: one 960x960 q_proj with the 3-bit Lloyd-Max code (nested.py:127-140's one-rate sweep)."""
+    import numpy as np
+    import torch
+
+    from lookatmyquant_amd import engine as E
+    from lookatmyquant_amd import synthetic
+    from lookatmyquant_amd.nested import lloyd_max
+
+    torch.cuda.set_device(0)
+    bits, lazy = 3, 128
+    in_seed = 201
+    W, H = synthetic.config12()
+    m, n = W.shape
+    dev = torch.device("cuda", 0)
+    Wg = torch.from_numpy(W.astype(np.float64)).to(dev)
+    Hg = torch.from_numpy(H).to(dev)
+    levels = lloyd_max(bits).to(dev)
+    K = levels.numel()
+
+    def step(events=None):
+        X, S = E.rht_rows(Wg, in_seed, want_rms=True)
+        Hr = E.rotate_hessian(Hg, in_seed)
+        _, U, dead, info = E.chol_inv_upper(Hr, raise_on_fail=False)
+        idx = E.ldlq_scalar(X / S[:, None], U, levels, mode=0, lazy=lazy, dead=dead, events=events)
+        codes, bad = E.pack_codes(idx, bits, trellis=False)
+        return idx, codes, info, bad
+
+    for _ in range(args.warmup):
+        idx, codes, info, bad = step()
+    torch.cuda.synchronize()
+    assert int(info.item()) == 0 and int(bad.item()) == 0
+    events = E.EventLog()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        idx, codes, info, bad = step(events)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    blk = E.event_ms(events, "block")
+    trl = E.event_ms(events, "trailing")
+    work = m * scalar_ops_per_row(n, K, lazy) * args.steps
+    line = kernel_line(sum(blk), work, FP64_VECTOR_PEAK_TFLOPS, "TFLOP/s", "valu", 1e12, len(blk))
+    out = {
+        "metric": METRIC, "value": round(m * n / (ms * 1e-3), 1), "unit": "weights/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f64 (sweep and search)", "data": "synthetic",
+        "config": {"workload": f"config 1: one 960x960 q_proj, width-1 block LDLQ onto the {bits}-bit Lloyd-Max levels "
+                               f"(lazy {lazy}), H from 16384 bf16 tokens, rotation + factor + sweep + packed codes per "
+                               "step", "rows": m, "columns": n, "bits": bits},
+        "roofline": {"kernel": "ldlq_scalar_block_kernel", "bound": "valu", "achieved": line["achieved"],
+                     "peak": FP64_VECTOR_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": line["frac"], "traffic": None,
+                     "avg_launch_us": line.get("avg_launch_us"), "launches_per_step": len(blk) // args.steps,
+                     "work": "per entry 3K search operations; per lazy block of w columns w (w - 1) flops of in-block "
+                             "refits (fp64 FMAs)"},
+        "phase_ms": {"block_kernels": round(sum(blk) / args.steps, 4),
+                     "trailing_updates": round(sum(trl) / args.steps, 4)},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline_c1(W, H, levels.cpu().numpy(), in_seed, lazy)
+    print(json.dumps(out))
+
+
+def cpu_baseline_c1(W, H, levels, in_seed, lazy):
+    """The C oracle on config 1, all of it: rotation, Hessian rotation and factor (numpy/LAPACK on every host thread),
+    then the width-1 sweep of every row (one row per thread at once)."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import oracle as O
+
+    _, threads = host_threads()
+    m, n = W.shape
+    with threadpool_limits(limits=threads):
+        t0 = time.perf_counter()
+        R = O.rht(n, in_seed)
+        X = np.asarray(W, dtype=np.float64) @ R.T
+        S = O.row_scale(X)
+        Hr = R @ H @ R.T
+        _, U, dead = O.environment(Hr)
+        t_fixed = time.perf_counter() - t0
+    T0 = X / S[:, None]
+    with threadpool_limits(limits=1):
+        t_rows = _rows_parallel(lambda c: O.ldlq_scalar(T0[c], U, levels, 0, lazy=lazy,
+                                                        dead=dead if dead.any() else None), list(range(m)), threads)
+    total = t_fixed + t_rows
+    return {"value": round(m * n / total, 1), "unit": "weights/s", "cores": threads, "kind": "port",
+            "sample": f"C oracle: rotation, R H R^T and U (numpy LAPACK) ({t_fixed:.2f} s) and the sweep of all {m} rows "
+                      f"({t_rows:.2f} s), {threads} threads",
+            "seconds_total": round(total, 3)}
+
+
 def run_c2(args):
     import numpy as np
     import torch
@@ -629,7 +734,7 @@ def main():
                          "reference's production trellis)")
     ap.add_argument("--k", type=int, default=2, help="c2: bits per weight")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", choices=("c2", "c3", "c4", "c5"), default="c5")
+    ap.add_argument("--workload", choices=("c1", "c2", "c3", "c4", "c5"), default="c5")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MiB")
     ap.add_argument("--no-extra", action="store_true",
                     help="c5: skip the extra layers timed in the production schedule and at the other state width")
@@ -648,7 +753,7 @@ def main():
     # stalls the host for tens of ms, and where the GPU has drained its queue by then, the stall lands inside a span
     gc.collect()
     gc.disable()
-    {"c2": run_c2, "c3": run_c3, "c4": run_c4, "c5": run_c5}[args.workload](args)
+    {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c4": run_c4, "c5": run_c5}[args.workload](args)
     if args.copy_probe:
         copy_probe(args.copy_probe)
 

@@ -10,49 +10,124 @@
 //          lower level), q = lv[index]*S
 //   z = (t - q) / U[j][j];  T[col] = T[col] - z*U[j][col] for col in (j, b1)   (syntax.py:117-121,
 //   a K = 1 product: rounded, then subtracted)
+// The columns are a chain (each z needs the refits of all before it), so a step's cost is its latency: the upper
+// triangle of the block's diagonal part of U, U[b0:b1, b0:b1], is staged in LDS once per workgroup of R rows (one
+// wave each; 66 KB, two workgroups a CU), and each step reads its U row and diagonal from there instead of from
+// memory. R = 4 while the rows fill the CUs four at a time; past that 8 or 16 rows share a workgroup, so that each
+// SIMD interleaves up to eight rows' chains.
 // ------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void ldlq_scalar_block_kernel(const double* __restrict__ T, int64_t m, int64_t ldT,
+#define SC_MAXW 128
+// row r of the staged triangle (columns r .. SC_MAXW - 1) starts at sc_tri(r)
+__host__ __device__ constexpr int sc_tri(int r) { return r * SC_MAXW - r * (r - 1) / 2; }
+#define SC_REGK 16  // level sets up to this size are searched from registers
+// P: 0 (levels read from LDS), or a power of two >= K (levels held in registers, P of them)
+template <int P, int R, int MODE>
+__global__ __launch_bounds__(64 * R) void ldlq_scalar_block_kernel(const double* __restrict__ T, int64_t m, int64_t ldT,
                                                                 const double* __restrict__ U, int64_t ldU,
                                                                 const double* __restrict__ S,
-                                                                const double* __restrict__ levels, int K, int mode,
+                                                                const double* __restrict__ levels, int K,
                                                                 int64_t b0, int64_t b1, int32_t* __restrict__ idx,
                                                                 int64_t ldi, double* __restrict__ Z, int64_t ldZ)
 {
+    __shared__ double ub[sc_tri(SC_MAXW)];  // U[b0 + r][b0 + c], c >= r, at sc_tri(r) + c - r
     __shared__ double lv[256];
     __shared__ double mid[256];
-    for (int i = threadIdx.x; i < K; i += 256) lv[i] = levels[i];
+    const int bw = (int)(b1 - b0);
+    constexpr int NTH = 64 * R;
+    for (int i = threadIdx.x; i < K; i += NTH) lv[i] = levels[i];
+    // eight loads in flight per thread before their stores (each store waits for its load); element e of the staged
+    // block is row e / SC_MAXW, column e % SC_MAXW
+    for (int e0 = threadIdx.x; e0 < bw * SC_MAXW; e0 += NTH * 8) {
+        double v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int e = e0 + NTH * u, r = e / SC_MAXW, c = e % SC_MAXW;
+            v[u] = (r < bw && c < bw && c >= r) ? U[(b0 + r) * ldU + b0 + c] : 0.0;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int e = e0 + NTH * u, r = e / SC_MAXW, c = e % SC_MAXW;
+            if (e < bw * SC_MAXW && c >= r) ub[sc_tri(r) + c - r] = v[u];
+        }
+    }
     __syncthreads();
-    for (int i = threadIdx.x; i + 1 < K; i += 256) mid[i] = (lv[i + 1] + lv[i]) / 2;
+    for (int i = threadIdx.x; i + 1 < K; i += NTH) mid[i] = (lv[i + 1] + lv[i]) / 2;
     __syncthreads();
     const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t row = (int64_t)blockIdx.x * R + (threadIdx.x >> 6);
     if (row >= m) return;
-    const int bw = (int)(b1 - b0);
+    // up to P levels and midpoints in registers (the same values in every lane)
+    constexpr bool REG = P > 0;
+    constexpr int NR = REG ? P : 1;
+    double lr[NR], mr[NR];
+    if (REG) {
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            if (MODE == 0) lr[i] = i < K ? lv[i] : 0.0;
+            if (MODE == 1) mr[i] = i + 1 < K ? mid[i] : __builtin_inf();
+        }
+    }
     const double* Tr = T + row * ldT + b0;
     double t0 = lane < bw ? Tr[lane] : 0.0;
     double t1 = lane + 64 < bw ? Tr[lane + 64] : 0.0;
-    const double Sr = mode == 1 ? S[row] : 1.0;
+    const double Sr = MODE == 1 ? S[row] : 1.0;
     for (int c = 0; c < bw; ++c) {
-        const double t = c < 64 ? __shfl(t0, c) : __shfl(t1, c - 64);
+        const double t = c < 64 ? readlane_f64(t0, c) : readlane_f64(t1, c - 64);
         int best = 0;
         double q;
-        if (mode == 0) {
-            const double d0 = t - lv[0];
-            double bd = d0 * d0;
-            for (int i = 1; i < K; ++i) {
-                double d = t - lv[i];
-                d = d * d;
-                if (d < bd) { bd = d; best = i; }
+        if constexpr (MODE == 0) {
+            if (REG) {
+                // a tournament over the squared distances with strict comparisons, the left (lower) index keeping a
+                // tie: the first argmin, as the sequential scan finds it
+                double d[NR], lq[NR];
+                int bi[NR];
+#pragma unroll
+                for (int i = 0; i < NR; ++i) {
+                    const double e = t - lr[i];
+                    d[i] = i < K ? e * e : __builtin_inf();
+                    bi[i] = i;
+                    lq[i] = lr[i];
+                }
+#pragma unroll
+                for (int span = 1; span < NR; span *= 2)
+#pragma unroll
+                    for (int i = 0; i + span < NR; i += 2 * span)
+                        if (d[i + span] < d[i]) {
+                            d[i] = d[i + span];
+                            bi[i] = bi[i + span];
+                            lq[i] = lq[i + span];
+                        }
+                best = bi[0];
+                q = lq[0];
+            } else {
+                const double d0 = t - lv[0];
+                double bd = d0 * d0;
+                for (int i = 1; i < K; ++i) {
+                    double d = t - lv[i];
+                    d = d * d;
+                    if (d < bd) { bd = d; best = i; }
+                }
+                q = lv[best];
             }
-            q = lv[best];
         } else {
             const double ts = t / Sr;
-            while (best < K - 1 && ts > mid[best]) ++best;
+            if (REG) {
+                // bucketize on the midpoints: the midpoints passed before the first that ts does not exceed (halfway
+                // goes to the lower level), as the scan below counts them
+                bool up = true;
+#pragma unroll
+                for (int i = 0; i + 1 < NR; ++i) {
+                    up = up && ts > mr[i];
+                    best += up ? 1 : 0;
+                }
+            } else {
+                while (best < K - 1 && ts > mid[best]) ++best;
+            }
             q = lv[best] * Sr;
         }
         const int64_t j = b0 + c;
-        const double zj = (t - q) / U[j * ldU + j];
-        const double* Uj = U + j * ldU + b0;
+        const double* Uj = ub + sc_tri(c) - c;  // Uj[col] = U[b0 + c][b0 + col] for col >= c
+        const double zj = (t - q) / Uj[c];
         if (lane > c && lane < bw) {
             const double p = zj * Uj[lane];
             t0 = t0 - p;
@@ -68,6 +143,46 @@ __global__ __launch_bounds__(256) void ldlq_scalar_block_kernel(const double* __
     }
 }
 
+template <int P, int MODE>
+static int scalar_launch_r(int R, const double* T, int64_t m, int64_t ldT, const double* U, int64_t ldU,
+                           const double* S, const double* levels, int K, int64_t b0, int64_t b1, int32_t* idx,
+                           int64_t ldi, double* Z, int64_t ldZ, hipStream_t s)
+{
+    if (R == 16)
+        hipLaunchKernelGGL((ldlq_scalar_block_kernel<P, 16, MODE>), dim3((unsigned)cdiv(m, 16)), dim3(1024), 0, s, T, m,
+                           ldT, U, ldU, S, levels, K, b0, b1, idx, ldi, Z, ldZ);
+    else if (R == 8)
+        hipLaunchKernelGGL((ldlq_scalar_block_kernel<P, 8, MODE>), dim3((unsigned)cdiv(m, 8)), dim3(512), 0, s, T, m, ldT,
+                           U, ldU, S, levels, K, b0, b1, idx, ldi, Z, ldZ);
+    else
+        hipLaunchKernelGGL((ldlq_scalar_block_kernel<P, 4, MODE>), dim3((unsigned)cdiv(m, 4)), dim3(256), 0, s, T, m, ldT,
+                           U, ldU, S, levels, K, b0, b1, idx, ldi, Z, ldZ);
+    LAMQ_LAUNCH_CHECK();
+    return LAMQ_OK;
+}
+
+template <int MODE>
+static int scalar_launch_p(int P, int R, const double* T, int64_t m, int64_t ldT, const double* U, int64_t ldU,
+                           const double* S, const double* levels, int K, int64_t b0, int64_t b1, int32_t* idx,
+                           int64_t ldi, double* Z, int64_t ldZ, hipStream_t s)
+{
+    switch (P) {
+    case 2: return scalar_launch_r<2, MODE>(R, T, m, ldT, U, ldU, S, levels, K, b0, b1, idx, ldi, Z, ldZ, s);
+    case 4: return scalar_launch_r<4, MODE>(R, T, m, ldT, U, ldU, S, levels, K, b0, b1, idx, ldi, Z, ldZ, s);
+    case 8: return scalar_launch_r<8, MODE>(R, T, m, ldT, U, ldU, S, levels, K, b0, b1, idx, ldi, Z, ldZ, s);
+    case SC_REGK: return scalar_launch_r<SC_REGK, MODE>(R, T, m, ldT, U, ldU, S, levels, K, b0, b1, idx, ldi, Z, ldZ, s);
+    default: return scalar_launch_r<0, MODE>(R, T, m, ldT, U, ldU, S, levels, K, b0, b1, idx, ldi, Z, ldZ, s);
+    }
+}
+
+static int scalar_launch(int P, int R, const double* T, int64_t m, int64_t ldT, const double* U, int64_t ldU,
+                         const double* S, const double* levels, int K, int mode, int64_t b0, int64_t b1, int32_t* idx,
+                         int64_t ldi, double* Z, int64_t ldZ, hipStream_t s)
+{
+    if (mode == 0) return scalar_launch_p<0>(P, R, T, m, ldT, U, ldU, S, levels, K, b0, b1, idx, ldi, Z, ldZ, s);
+    return scalar_launch_p<1>(P, R, T, m, ldT, U, ldU, S, levels, K, b0, b1, idx, ldi, Z, ldZ, s);
+}
+
 extern "C" int lamq_ldlq_scalar_block(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU,
                                       const double* S, const double* levels, int K, int mode, int64_t b0, int64_t b1,
                                       int32_t* idx, int64_t ldi, double* Z, int64_t ldZ, void* stream)
@@ -76,12 +191,12 @@ extern "C" int lamq_ldlq_scalar_block(double* T, int64_t m, int64_t n, int64_t l
     if (m < 0 || n < 1 || ldT < n || ldU < n || ldi < n || b0 < 0 || b1 <= b0 || b1 > n || K < 1 || K > 256)
         return LAMQ_EINVAL;
     if (ldZ < b1 - b0) return LAMQ_EINVAL;
-    if (b1 - b0 > 128) return LAMQ_EUNSUP;
+    if (b1 - b0 > SC_MAXW) return LAMQ_EUNSUP;
     if (m == 0) return LAMQ_OK;
-    hipLaunchKernelGGL(ldlq_scalar_block_kernel, dim3((unsigned)cdiv(m, 4)), dim3(256), 0, as_stream(stream), T, m, ldT, U,
-                       ldU, S, levels, K, mode, b0, b1, idx, ldi, Z, ldZ);
-    LAMQ_LAUNCH_CHECK();
-    return LAMQ_OK;
+    // rows per workgroup: as many as keep at least 256 workgroups (one per CU), between 4 and 16
+    const int R = m >= 16 * 256 ? 16 : (m >= 8 * 256 ? 8 : 4);
+    const int P = K <= 2 ? 2 : (K <= 4 ? 4 : (K <= 8 ? 8 : (K <= SC_REGK ? SC_REGK : 0)));
+    return scalar_launch(P, R, T, m, ldT, U, ldU, S, levels, K, mode, b0, b1, idx, ldi, Z, ldZ, as_stream(stream));
 }
 
 extern "C" int lamq_trailing_update_f64(double* T, int64_t m, int64_t n, int64_t ldT, const double* Z, int64_t ldZ,

@@ -457,9 +457,10 @@ def event_ms(events: dict, key: str) -> list[float]:
 
 
 def ldlq_scalar(T0: torch.Tensor, U: torch.Tensor, levels: torch.Tensor, mode: int = 0, S: torch.Tensor | None = None,
-                lazy: int = 128, dead: torch.Tensor | None = None) -> torch.Tensor:
+                lazy: int = 128, dead: torch.Tensor | None = None, events: dict | None = None) -> torch.Tensor:
     """Level indices [m, n] int32 of the width-1 LDLQ onto `levels` (mode 0: T0 = X/S and the first argmin of the
-    squared distance; mode 1: T0 = X and bucketize(t/S) on midpoints, q*S)."""
+    squared distance; mode 1: T0 = X and bucketize(t/S) on midpoints, q*S). events: as ldlq_trellis's ("block" the
+    scalar block kernel, "trailing" the products)."""
     need(T0, torch.float64, "T0", 2)
     need(U, torch.float64, "U", 2)
     need(levels, torch.float64, "levels", 1)
@@ -482,10 +483,12 @@ def ldlq_scalar(T0: torch.Tensor, U: torch.Tensor, levels: torch.Tensor, mode: i
         for b0 in range(B0, B1, lazy):
             b1 = min(b0 + lazy, n)
             zb = Z[:, b0 - B0 :]
+            ev = _event_pair(events, "block")
             check(lib().lamq_ldlq_scalar_block(ptr(T), m, n, n, ptr(U), ld(U), ptr(S), ptr(levels), levels.numel(), mode,
                                                b0, b1, ptr(idx), n, ptr(zb), outer, s), "ldlq_scalar_block")
-            _refit_run(T, U, zb, b0, b1, B1, 0, None)
-        _refit_rest(T, U, Z, B0, B1, 0, None)
+            _event_end(ev)
+            _refit_run(T, U, zb, b0, b1, B1, 0, events)
+        _refit_rest(T, U, Z, B0, B1, 0, events)
     return idx
 
 

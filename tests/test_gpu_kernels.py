@@ -520,6 +520,28 @@ def test_ldlq_scalar_bucketize_mode_matches_oracle(E):
     assert np.array_equal(idx, O.ldlq_scalar(X, U, lv, 1, S))
 
 
+@pytest.mark.parametrize("K,m", [(2, 40), (3, 40), (5, 40), (8, 40), (16, 40), (17, 40), (40, 40), (8, 2100),
+                                 (5, 4200), (40, 4200)])
+def test_ldlq_scalar_level_counts_match_oracle(E, K, m):
+    """The width-1 sweep at every level count the kernel specialises (K <= 2, 4, 8, 16 searched from registers by a
+    tournament, more from LDS by the scan) and every workgroup size (4, 8 and 16 rows sharing the staged U block),
+    both searches (mode 0: first argmin; mode 1: bucketize on midpoints), against the oracle: m rows x 300 columns
+    (two full lazy blocks and a ragged one)."""
+    rng = np.random.default_rng(100 + K + m)
+    n = 300
+    Xa = rng.standard_normal((2 * n, n))
+    _, U, _ = O.environment(Xa.T @ Xa / (2 * n))
+    X = rng.standard_normal((m, n))
+    S = O.row_scale(X)
+    lv = np.sort(rng.standard_normal(K)) * 1.5
+    lv[K // 2] = lv[K // 2 - 1] if K > 3 else lv[K // 2]  # a repeated level: ties go to the lower index
+    say(f"ldlq scalar K={K} m={m}")
+    T0 = X / S[:, None]
+    assert np.array_equal(E.ldlq_scalar(cuda(T0), cuda(U), cuda(lv), mode=0).cpu().numpy(), O.ldlq_scalar(T0, U, lv, 0))
+    assert np.array_equal(E.ldlq_scalar(cuda(X), cuda(U), cuda(lv), mode=1, S=cuda(S)).cpu().numpy(),
+                          O.ldlq_scalar(X, U, lv, 1, S))
+
+
 def test_end_to_end_gpu_factor_config2(E, golden, tables, config12):
     """Hessian rotation and U on the GPU too: the reference states at config 2, bit for bit."""
     W, H = config12
