@@ -89,6 +89,16 @@ int lamq_ldlq_scalar_block(double* T, int64_t m, int64_t n, int64_t ldT, const d
                            const double* S, const double* levels, int K, int mode, int64_t b0, int64_t b1,
                            int32_t* idx, int64_t ldi, double* Z, int64_t ldZ, void* stream);
 
+/* The same width-1 block for R rates at once. Replaces opgraph/nested.py:104-147 (multirate_sweep without output
+ * shaping): T and Z hold the rates' copies of the m rows stacked rate-major ([R*m, n] and [R*m, b1-b0]: copy r of row i
+ * is row r*m + i, X.repeat(R, 1)); one index per entry, idx[i][j] = first argmin_k sum_r w_r (t_r - tables[r*K + k])^2
+ * (each term the weight times the rounded square, summed in rate order); copy r settles on tables[r*K + idx] and is
+ * refit for its own error. U == NULL: no refit, every column alone (the sweep without H; Z unused).
+ * 1 <= R <= 4, K <= 256, b1 - b0 <= 128. */
+int lamq_ldlq_multirate_block(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU,
+                              const double* tables, int R, int K, const double* weights, int64_t b0, int64_t b1,
+                              int32_t* idx, int64_t ldi, double* Z, int64_t ldZ, void* stream);
+
 /* ------------------------------------------------------------------------------------------------
  * The 16-bit-state trellis (13 <= L <= 16, 1 <= k <= min(4, L-12)): the same two operations as
  * lamq_viterbi_rows and lamq_ldlq_trellis_block (the same references, the same arithmetic and tie rules)

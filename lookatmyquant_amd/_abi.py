@@ -24,6 +24,8 @@ SIGNATURES = {
                                          _c_int, _c_int, _p, _p, _c_i64, _p, _c_i64, _c_i64, _p]),
     "lamq_ldlq_scalar_block": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _p, _c_int, _c_int, _c_i64, _c_i64, _p,
                                         _c_i64, _p, _c_i64, _p]),
+    "lamq_ldlq_multirate_block": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _c_int, _c_int, _p, _c_i64, _c_i64,
+                                           _p, _c_i64, _p, _c_i64, _p]),
     "lamq_viterbi16_workspace_size": (_c_size, [_c_i64, _c_int, _c_int, _c_int]),
     "lamq_viterbi16_rows": (_c_int, [_p, _c_i64, _c_int, _c_i64, _p, _c_int, _c_int, _p, _p, _c_i64, _p, _c_size, _p]),
     "lamq_ldlq_trellis16_block": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _p, _p, _c_int, _c_int, _c_i64,

@@ -143,6 +143,118 @@ __global__ __launch_bounds__(64 * R) void ldlq_scalar_block_kernel(const double*
     }
 }
 
+// ------------------------------------------------------------------------------------------------
+// ldlq_multirate_block: the same sweep for R rates at once (opgraph/nested.py:104-147 without output shaping). The
+// rates' copies of the rows are stacked rate-major in T and Z (copy r of row i is row r*m + i, as X.repeat(R, 1)); one
+// wave takes row i and its R copies, lane c holding columns b0+c and b0+64+c of each. Per column one index for all
+// copies: first argmin_i sum_r w_r (t_r - tab[r][i])^2, each term w_r times the rounded square, summed in rate order;
+// then copy r settles on tab[r][index] and is refit for its own error: z_r = (t_r - tab[r][index]) / U[j][j],
+// T_r[col] -= z_r U[j][col]. U == NULL: no refit (every column alone, the sweep without H).
+// ------------------------------------------------------------------------------------------------
+#define MR_MAXR 4
+template <int R>
+__global__ __launch_bounds__(256) void ldlq_multirate_block_kernel(const double* __restrict__ T, int64_t m, int64_t ldT,
+                                                                   const double* __restrict__ U, int64_t ldU,
+                                                                   const double* __restrict__ tables, int K,
+                                                                   const double* __restrict__ weights, int64_t b0,
+                                                                   int64_t b1, int32_t* __restrict__ idx, int64_t ldi,
+                                                                   double* __restrict__ Z, int64_t ldZ)
+{
+    __shared__ double ub[sc_tri(SC_MAXW)];
+    __shared__ double tab[MR_MAXR * 256];
+    const int bw = (int)(b1 - b0);
+    for (int i = threadIdx.x; i < R * K; i += 256) tab[i] = tables[i];
+    if (U) {
+        for (int e0 = threadIdx.x; e0 < bw * SC_MAXW; e0 += 256 * 8) {
+            double v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int e = e0 + 256 * u, r = e / SC_MAXW, c = e % SC_MAXW;
+                v[u] = (r < bw && c < bw && c >= r) ? U[(b0 + r) * ldU + b0 + c] : 0.0;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int e = e0 + 256 * u, r = e / SC_MAXW, c = e % SC_MAXW;
+                if (e < bw * SC_MAXW && c >= r) ub[sc_tri(r) + c - r] = v[u];
+            }
+        }
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= m) return;
+    double w[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) w[r] = weights[r];
+    double t0[R], t1[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const double* Tr = T + (r * m + row) * ldT + b0;
+        t0[r] = lane < bw ? Tr[lane] : 0.0;
+        t1[r] = lane + 64 < bw ? Tr[lane + 64] : 0.0;
+    }
+    for (int c = 0; c < bw; ++c) {
+        double t[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) t[r] = c < 64 ? readlane_f64(t0[r], c) : readlane_f64(t1[r], c - 64);
+        int best = 0;
+        double bc = 0.0;
+        for (int i = 0; i < K; ++i) {
+            double cost = 0.0;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const double d = t[r] - tab[r * K + i];
+                const double p = w[r] * (d * d);
+                cost = r == 0 ? p : cost + p;
+            }
+            if (i == 0 || cost < bc) {
+                bc = cost;
+                best = i;
+            }
+        }
+        const int64_t j = b0 + c;
+        if (lane == (c & 63)) idx[row * ldi + j] = best;
+        if (!U) continue;
+        const double* Uj = ub + sc_tri(c) - c;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const double zr = (t[r] - tab[r * K + best]) / Uj[c];
+            if (lane > c && lane < bw) {
+                const double pr = zr * Uj[lane];
+                t0[r] = t0[r] - pr;
+            }
+            if (lane + 64 > c && lane + 64 < bw) {
+                const double pr = zr * Uj[lane + 64];
+                t1[r] = t1[r] - pr;
+            }
+            if (lane == (c & 63)) Z[(r * m + row) * ldZ + c] = zr;
+        }
+    }
+}
+
+extern "C" int lamq_ldlq_multirate_block(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU,
+                                         const double* tables, int R, int K, const double* weights, int64_t b0,
+                                         int64_t b1, int32_t* idx, int64_t ldi, double* Z, int64_t ldZ, void* stream)
+{
+    if (!T || !tables || !weights || !idx || (U && !Z)) return LAMQ_EINVAL;
+    if (m < 0 || n < 1 || ldT < n || (U && ldU < n) || ldi < n || b0 < 0 || b1 <= b0 || b1 > n || K < 1 || K > 256)
+        return LAMQ_EINVAL;
+    if (U && ldZ < b1 - b0) return LAMQ_EINVAL;
+    if (R < 1 || R > MR_MAXR) return LAMQ_EUNSUP;
+    if (b1 - b0 > SC_MAXW) return LAMQ_EUNSUP;
+    if (m == 0) return LAMQ_OK;
+    const dim3 grid((unsigned)cdiv(m, 4));
+    hipStream_t s = as_stream(stream);
+    switch (R) {
+    case 1: hipLaunchKernelGGL(ldlq_multirate_block_kernel<1>, grid, dim3(256), 0, s, T, m, ldT, U, ldU, tables, K, weights, b0, b1, idx, ldi, Z, ldZ); break;
+    case 2: hipLaunchKernelGGL(ldlq_multirate_block_kernel<2>, grid, dim3(256), 0, s, T, m, ldT, U, ldU, tables, K, weights, b0, b1, idx, ldi, Z, ldZ); break;
+    case 3: hipLaunchKernelGGL(ldlq_multirate_block_kernel<3>, grid, dim3(256), 0, s, T, m, ldT, U, ldU, tables, K, weights, b0, b1, idx, ldi, Z, ldZ); break;
+    default: hipLaunchKernelGGL(ldlq_multirate_block_kernel<4>, grid, dim3(256), 0, s, T, m, ldT, U, ldU, tables, K, weights, b0, b1, idx, ldi, Z, ldZ); break;
+    }
+    LAMQ_LAUNCH_CHECK();
+    return LAMQ_OK;
+}
+
 template <int P, int MODE>
 static int scalar_launch_r(int R, const double* T, int64_t m, int64_t ldT, const double* U, int64_t ldU,
                            const double* S, const double* levels, int K, int64_t b0, int64_t b1, int32_t* idx,

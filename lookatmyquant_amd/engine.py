@@ -492,6 +492,54 @@ def ldlq_scalar(T0: torch.Tensor, U: torch.Tensor, levels: torch.Tensor, mode: i
     return idx
 
 
+def ldlq_multirate(X: torch.Tensor, U: torch.Tensor | None, tables: torch.Tensor, weights: torch.Tensor,
+                   lazy: int = 128, dead: torch.Tensor | None = None, events: dict | None = None) -> torch.Tensor:
+    """Indices [m, n] int32 of the width-1 sweep of X (units of the row scale) for R rates at once
+    (nested.py:104-147): per entry the first argmin over the table index of sum_r w_r (t_r - tables[r, i])^2, each rate's
+    copy of the row refit for its own value under U (lamq_ldlq_multirate_block over X.repeat(R, 1)); U None: every
+    column alone."""
+    need(X, torch.float64, "X", 2)
+    need(tables, torch.float64, "tables", 2)
+    need(weights, torch.float64, "weights", 1)
+    if U is not None:
+        need(U, torch.float64, "U", 2)
+    R, K = tables.shape
+    if weights.numel() != R:
+        raise ValueError("one weight per rate")
+    if lazy > 128:
+        raise NotImplementedError("the width-1 block kernel keeps at most 128 columns of a row in registers")
+    m, n = X.shape
+    dev = X.device
+    s = stream(dev)
+    T = X.repeat(R, 1).contiguous()
+    if dead is not None and U is not None:
+        dd = dead.to(device=dev, dtype=torch.uint8).contiguous()
+        check(lib().lamq_zero_columns(ptr(T), R * m, n, n, ptr(dd), s), "zero_columns")
+    idx = torch.empty(m, n, dtype=torch.int32, device=dev)
+    tab = tables.contiguous()
+    wts = weights.contiguous()
+    if U is None:
+        for b0 in range(0, n, lazy):
+            b1 = min(b0 + lazy, n)
+            check(lib().lamq_ldlq_multirate_block(ptr(T), m, n, n, None, n, ptr(tab), R, K, ptr(wts), b0, b1, ptr(idx), n,
+                                                  None, 1, s), "ldlq_multirate_block")
+        return idx
+    outer = _outer_run(lazy)
+    Z = torch.empty(R * m, outer, dtype=torch.float64, device=dev)
+    for B0 in range(0, n, outer):
+        B1 = min(B0 + outer, n)
+        for b0 in range(B0, B1, lazy):
+            b1 = min(b0 + lazy, n)
+            zb = Z[:, b0 - B0 :]
+            ev = _event_pair(events, "block")
+            check(lib().lamq_ldlq_multirate_block(ptr(T), m, n, n, ptr(U), ld(U), ptr(tab), R, K, ptr(wts), b0, b1,
+                                                  ptr(idx), n, ptr(zb), outer, s), "ldlq_multirate_block")
+            _event_end(ev)
+            _refit_run(T, U, zb, b0, b1, B1, 0, events)
+        _refit_rest(T, U, Z, B0, B1, 0, events)
+    return idx
+
+
 def refit_step(T: torch.Tensor, U: torch.Tensor, Q: torch.Tensor, j: int, b0: int, b1: int, Z: torch.Tensor):
     """E = T[:, j:j+w] - Q, z = E U_BB^-1, T[:, j+w:b1] -= z U[j:j+w, j+w:b1], Z[:, j-b0:j-b0+w] = z (in place)."""
     need(T, torch.float64, "T", 2)

@@ -1,15 +1,18 @@
-"""Lloyd-Max and compander level sets, and the one-rate LDLQ onto them (opgraph/nested.py), on the gfx950 kernels.
+"""Lloyd-Max and compander level sets, and the LDLQ onto them for one or several rates (opgraph/nested.py), on the
+gfx950 kernels.
 
     gaussian_centroids, gaussian_mse, compander_bounds, compander_levels      nested.py:44-68
     lloyd_max(bits, iters=500), lloyd_max_levels(n, iters=500)                nested.py:71-82
     nested_tables(top, rates, alpha)                                          nested.py:150-152
-    multirate_sweep(X, H, tables, weights, G=None, block=32)                  nested.py:104-147 (one rate)
+    multirate_sweep(X, H, tables, weights, G=None, block=32)                  nested.py:104-147
     nested_words(Ws, H, seeds, top, rates, alpha, weights, levels=None, in_seed=None, out_rot=True)   nested.py:155
 
 The level tables are small host computations in float64 with torch's special functions, as the reference does
 them (so the levels are the same bits). The sweep is the width-1 LDLQ kernel: each column's index is the first
-minimum of (t - level)^2 over the levels, then the later columns are re-solved under U. Several rates at once
-and output-side shaping (G) are not part of this path."""
+minimum of (t - level)^2 over the levels (one rate at weight 1), or of sum_r w_r (t_r - tables[r, i])^2 over the
+rates' copies of the row (several rates: lamq_ldlq_multirate_block), then the later columns are re-solved under U.
+Output-side shaping (G, one matrix at one rate with its rows settled against each other) is not part of this path
+and raises NotImplementedError."""
 
 from __future__ import annotations
 
@@ -86,45 +89,62 @@ def nested_tables(top: int, rates: list[int], alpha: float) -> torch.Tensor:
 
 def multirate_sweep(X: torch.Tensor, H: torch.Tensor | None, tables: torch.Tensor, weights: torch.Tensor,
                     G: torch.Tensor | None = None, block: int = 32) -> torch.Tensor:
-    """One index per entry of X (already in units of the row scale) for one rate (nested.py:104-147): with H, the
-    width-1 LDLQ sweep under U; without H, the nearest level. Returns int64 indices on the CPU."""
-    tables = torch.as_tensor(tables, dtype=torch.float64)
-    if tables.dim() != 2 or tables.shape[0] != 1 or G is not None:
-        raise NotImplementedError("several rates at once and output shaping are not part of this path")
+    """One index per entry of X (already in units of the row scale) for R rates at once (nested.py:104-147): the first
+    minimum of sum_r w_r (t_r - tables[r, i])^2, each rate's copy of the row keeping its own running target; with H,
+    the width-1 LDLQ sweep under U; without H, every column alone. Returns int64 indices on the CPU."""
+    if G is not None:
+        raise NotImplementedError("output shaping (G) is not part of this path")
     dev = E._abi.device()
-    lv = tables[0].to(dev).contiguous()
+    tables = torch.as_tensor(tables, dtype=torch.float64)
+    if tables.dim() != 2:
+        raise ValueError("tables must be [rates, levels]")
     x = torch.as_tensor(X).to(dev, torch.float64).contiguous()
-    if H is None:
-        # first minimum of (t - lv)^2 per entry: a zero-row environment is not needed, every column alone
-        d = (x[:, :, None] - lv[None, None, :]) ** 2
-        return d.argmin(-1).cpu()
-    _, U, dead, _ = E.chol_inv_upper(torch.as_tensor(H).to(dev, torch.float64).contiguous())
-    return E.ldlq_scalar(x, U, lv, mode=0, dead=dead).to(torch.int64).cpu()
+    U = dead = None
+    if H is not None:
+        _, U, dead, _ = E.chol_inv_upper(torch.as_tensor(H).to(dev, torch.float64).contiguous())
+    return _sweep(x, U, dead, tables.to(dev), torch.as_tensor(weights, dtype=torch.float64).to(dev)).to(torch.int64).cpu()
+
+
+def _sweep(x, U, dead, tables, weights):
+    """The index array [m, n] int32 on the device: one rate at weight 1 through the width-1 kernel (the joint cost is
+    then the squared distance), several rates (or another weight) through the multi-rate kernel."""
+    if tables.shape[0] == 1 and float(weights[0]) == 1.0:
+        lv = tables[0].contiguous()
+        if U is None:
+            # first minimum of (t - lv)^2 per entry: every column alone
+            return ((x[:, :, None] - lv[None, None, :]) ** 2).argmin(-1).to(torch.int32)
+        return E.ldlq_scalar(x, U, lv, mode=0, dead=dead)
+    return E.ldlq_multirate(x, U, tables.contiguous(), weights.contiguous(), dead=dead)
 
 
 def nested_words(Ws: list, H: torch.Tensor | None, seeds: list[int], top: int, rates: list[int], alpha: float,
                  weights: list[float], levels: torch.Tensor | None = None, in_seed: int | None = None,
                  out_rot: bool = True, G: torch.Tensor | None = None, block: int = 32) -> dict:
-    """Incoherence (shared input transform) -> per-row RMS scale -> LDLQ onto one rate's levels -> {rate: [Net]}
-    (nested.py:155-192). With `levels` the code is that set (a dedicated code, as quantize.word's lm<b>)."""
-    if len(rates) != 1 or G is not None:
-        raise NotImplementedError("several rates at once and output shaping are not part of this path")
+    """Incoherence (shared input transform) -> per-row RMS scale -> LDLQ onto a `top`-bit nested code for every rate in
+    `rates` at once (weights price the rates' squared errors) -> {rate: [Net per matrix]}, each rate reading the shared
+    indices with its own levels (nested.py:155-192). With `levels` (one rate only) the code is that set (a dedicated
+    code, as quantize.word's lm<b>)."""
+    if G is not None:
+        raise NotImplementedError("output shaping (G) is not part of this path")
+    if levels is not None and len(rates) != 1:
+        raise ValueError("a dedicated code has one rate")
     dev, X, S, rin = _prepare(Ws, seeds, True, in_seed, out_rot)
     if levels is None:
-        tab = nested_tables(top, rates, alpha)[0]
-        dom = NESTED(rates[0], alpha)
+        tables = nested_tables(top, rates, alpha)
     else:
-        tab = torch.as_tensor(levels, dtype=torch.float64)
-        dom = SET(tab.tolist(), bits=math.log2(len(tab)))
-    lv = tab.to(dev).contiguous()
-    x = X / S[:, None]
-    if H is None:
-        idx = ((x[:, :, None] - lv[None, None, :]) ** 2).argmin(-1).to(torch.int32)
-    else:
+        tables = torch.as_tensor(levels, dtype=torch.float64)[None]
+    x = (X / S[:, None]).contiguous()
+    U = dead = None
+    if H is not None:
         Hr = E.rotate_hessian(torch.as_tensor(H).to(dev, torch.float64).contiguous(), rin)
         _, U, dead, _ = E.chol_inv_upper(Hr)
-        idx = E.ldlq_scalar(x.contiguous(), U, lv, mode=0, dead=dead)
-    idx = idx.cpu()
-    values = tab[idx.long()]
+    idx = _sweep(x, U, dead, tables.to(dev), torch.as_tensor(weights, dtype=torch.float64).to(dev)).cpu()
     rows_label = "u" if out_rot else "o"
-    return {rates[0]: _nets(Ws, seeds, X, values, S.cpu(), dom, rows_label, rin, out_rot, True, idx)}
+    out = {}
+    for r, b in enumerate(rates):
+        if levels is not None:
+            dom = SET(tables[r].tolist(), bits=math.log2(tables.shape[1]))
+        else:
+            dom = NESTED(b, alpha)
+        out[b] = _nets(Ws, seeds, X, tables[r][idx.long()], S.cpu(), dom, rows_label, rin, out_rot, True, idx)
+    return out

@@ -14,6 +14,8 @@ Parity status of each function (what pins it is listed in the test named beside 
   ldlq_factor        U^T U = (H + d mean(diag H) I)^-1 at the first d that factors; the retry path
   ldlq_round         the eager GPTQ loop of ldlq_gpu.py (reference vectors of ldlq_scalar); lazy-block invariance
   sweep              equals the C sweeps (ldlq_scalar, ldlq_trellis) under their projections
+  multirate_sweep    the reference's own vectors for three and four rates, with and without H (tests/golden/multirate.npz);
+                     one rate at weight 1 equals ldlq_scalar
   column_trellis_*   per-sequence viterbi (pinned above) on the reshaped columns; brute force for tiny L
   hadamard / rht     orthogonality, |H_ij| = 1/sqrt(n), Kronecker closed forms
   rht_apply          equals the products with the dense rht(n, seed) both ways (tests/test_oracle.py)
@@ -196,6 +198,33 @@ def sweep(W, U, project, width: int = 1, lazy: int = 128, dead=None) -> np.ndarr
         if b1 < n:
             T[:, b1:] -= Z @ U[b0:b1, b1:]
     return before
+
+
+def multirate_sweep(X, H, tables, weights, lazy: int = 128) -> np.ndarray:
+    """opgraph/nested.py:104-147 without output shaping: one index per entry of X (units of the row scale) for R rates
+    at once, idx = first argmin_i sum_r w_r (t_r - tables[r, i])^2 (w_r times the rounded square, the rates summed in
+    order); with H the width-1 sweep of X.repeat(R, 1) (the rates' copies of each row, rate-major) under
+    Environment(H)'s U, each copy refit for its own rate's value; without H every column alone."""
+    X = np.asarray(X, dtype=np.float64)
+    tables = np.asarray(tables, dtype=np.float64)
+    w = np.asarray(weights, dtype=np.float64)
+    R, m = tables.shape[0], X.shape[0]
+    idx = np.empty(X.shape, dtype=np.int64)
+
+    def project(j, col, T):
+        t = np.asarray(col).reshape(R, m)
+        cost = (w[:, None, None] * (t[:, :, None] - tables[:, None, :]) ** 2).sum(0)
+        i = cost.argmin(1)
+        idx[:, j] = i
+        return tables[:, i].reshape(-1, 1)
+
+    if H is None:
+        for j in range(X.shape[1]):
+            project(j, np.tile(X[:, j], R), None)
+        return idx
+    _, U, dead = environment(H)
+    sweep(np.tile(X, (R, 1)), U, project, width=1, lazy=lazy, dead=dead if dead.any() else None)
+    return idx
 
 
 def column_trellis_states(X, table64, L: int, k: int, T: int) -> np.ndarray:

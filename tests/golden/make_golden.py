@@ -9,7 +9,8 @@ opgraph/model.py, which reads a SmolLM2-360M config.json from the Hugging Face c
 its own model (none of the functions called here use those sizes); this script points HOME at a temporary
 directory holding that public config so the import succeeds offline.
 
-    python tests/golden/make_golden.py          # rewrites tests/golden/*.npz
+    python tests/golden/make_golden.py                    # rewrites tests/golden/*.npz
+    python tests/golden/make_golden.py --only multirate   # rewrites tests/golden/multirate.npz alone
 """
 
 from __future__ import annotations
@@ -187,5 +188,38 @@ def main():
     print(f"done in {time.time() - t0:.0f}s")
 
 
+def multirate(torch, N):
+    """multirate_sweep (nested.py:104-147) for several rates at once: the joint index of each entry minimises the
+    weighted sum of the rates' squared errors, each rate's copy of the row keeping its own running target. Three cases
+    on synthetic inputs: three rates of a 3-bit nested code with H, the same without H, and four rates of a 4-bit
+    nested code with H holding a dead input."""
+    t1 = time.time()
+    out = {}
+    rng = np.random.default_rng(31)
+    cases = (("r3", 3, [1, 2, 3], [0.25, 0.5, 1.0], True, None), ("r3_noH", 3, [1, 2, 3], [0.25, 0.5, 1.0], False, None),
+             ("r4", 4, [1, 2, 3, 4], [1.0, 0.5, 0.3, 0.2], True, 17))
+    for name, top, rates, weights, with_h, dead in cases:
+        m, n = 48, 200
+        X = rng.standard_normal((m, n))
+        Xa = rng.standard_normal((2 * n, n))
+        if dead is not None:
+            Xa[:, dead] = 0.0
+        H = Xa.T @ Xa / (2 * n)
+        tables = N.nested_tables(top, rates, 0.4)
+        idx = N.multirate_sweep(torch.from_numpy(X), torch.from_numpy(H) if with_h else None, tables,
+                                torch.tensor(weights, dtype=torch.float64))
+        out[f"{name}_X"], out[f"{name}_H"] = X, H
+        out[f"{name}_tables"], out[f"{name}_weights"] = tables.numpy(), np.array(weights)
+        out[f"{name}_idx"] = idx.numpy().astype(np.int16)
+    np.savez_compressed(OUT / "multirate.npz", **out)
+    print(f"multirate written ({time.time() - t1:.0f}s)", flush=True)
+
+
 if __name__ == "__main__":
-    main()
+    if sys.argv[1:] == ["--only", "multirate"]:
+        torch_, _, N_, _ = import_reference()
+        multirate(torch_, N_)
+    else:
+        main()
+        torch_, _, N_, _ = import_reference()
+        multirate(torch_, N_)

@@ -558,3 +558,47 @@ def test_rounded_matches_the_oracle(config12, tables):
     _, states_g = rounded(torch.from_numpy(W), R, groups_g, scale_g, env, rows=rows_g)
     assert torch.equal(states_g, states[rows_g])
     assert torch.allclose(scale_g[rows_g], scale[rows_g], rtol=1e-6, atol=0)
+
+
+@pytest.mark.parametrize("case", ["r3", "r3_noH", "r4"])
+def test_multirate_sweep_matches_the_reference(golden, case):
+    """nested.multirate_sweep for several rates at once (nested.py:104-147) on the GPU: the reference's indices
+    (three rates of a 3-bit nested code with and without H, four rates of a 4-bit code with a dead input)."""
+    from lookatmyquant_amd import nested as N
+
+    g = golden("multirate")
+    H = None if case.endswith("noH") else torch.from_numpy(g[f"{case}_H"])
+    say(f"multirate {case}")
+    idx = N.multirate_sweep(torch.from_numpy(g[f"{case}_X"]), H, torch.from_numpy(g[f"{case}_tables"]),
+                            torch.from_numpy(g[f"{case}_weights"]))
+    assert np.array_equal(idx.numpy(), g[f"{case}_idx"])
+
+
+def test_multirate_kernel_matches_the_oracle_across_runs():
+    """lamq_ldlq_multirate_block over two outer runs and several workgroups (300 rows x 700 columns, two rates of a
+    4-bit nested code with unequal weights) against the oracle, and nested_words' three rates reading the shared
+    indices with their own levels."""
+    from lookatmyquant_amd import engine as E
+    from lookatmyquant_amd import nested as N
+
+    rng = np.random.default_rng(9)
+    m, n = 300, 700
+    X = rng.standard_normal((m, n))
+    Xa = rng.standard_normal((2 * n, n))
+    H = Xa.T @ Xa / (2 * n)
+    tables = N.nested_tables(4, [2, 4], 0.4)
+    w = torch.tensor([0.7, 0.3], dtype=torch.float64)
+    say("multirate 300 x 700, two rates")
+    _, U, dead, _ = E.chol_inv_upper(torch.from_numpy(H).cuda())
+    idx = E.ldlq_multirate(torch.from_numpy(X).cuda(), U, tables.cuda(), w.cuda(), dead=dead).cpu().numpy()
+    ref = O.multirate_sweep(X, H, tables.numpy(), w.numpy())
+    assert np.array_equal(idx, ref)
+    W = torch.from_numpy(rng.standard_normal((64, 256)) * 0.02)
+    Hs = torch.from_numpy(Xa[:, :256].T @ Xa[:, :256] / (2 * n))
+    out = N.nested_words([W], Hs, [300], 3, [1, 2, 3], 0.4, [0.2, 0.3, 0.5], in_seed=301, out_rot=False)
+    assert sorted(out) == [1, 2, 3]
+    codes = out[3][0].codes
+    for b, tab in zip([1, 2, 3], N.nested_tables(3, [1, 2, 3], 0.4)):
+        net = out[b][0]
+        assert torch.equal(net.codes, codes)  # one index per entry, read by every rate
+        assert torch.allclose(net.cores["W"].data, tab[codes.long()].to(net.cores["W"].data))

@@ -87,6 +87,13 @@ def test_argument_errors_are_reported_without_a_gpu():
     assert L.lamq_causal_softmax_bf16(ptr(b), ptr(b), 4, 16, 16, 16, 0.0, None) == -1
     assert L.lamq_causal_softmax_bf16(ptr(b), ptr(b) + 16, 4, 16, 16, 16, 0.5, None) == -1
     assert L.lamq_causal_softmax_bf16(ptr(b) + 2, ptr(b) + 2, 4, 16, 16, 16, 0.5, None) == -1
+    # the multi-rate sweep: more than four rates, no levels, a refit without Z
+    assert L.lamq_ldlq_multirate_block(ptr(p), 1, 8, 8, ptr(p), 8, ptr(p), 5, 2, ptr(p), 0, 8, ptr(q), 8, ptr(p), 8,
+                                       None) == -2
+    assert L.lamq_ldlq_multirate_block(ptr(p), 1, 8, 8, ptr(p), 8, ptr(p), 2, 0, ptr(p), 0, 8, ptr(q), 8, ptr(p), 8,
+                                       None) == -1
+    assert L.lamq_ldlq_multirate_block(ptr(p), 1, 8, 8, ptr(p), 8, ptr(p), 2, 4, ptr(p), 0, 8, ptr(q), 8, None, 8,
+                                       None) == -1
     assert L.lamq_ldlq_trellis16_block(ptr(p), 1, 8, 8, ptr(p), 8, ptr(p), ptr(p), ptr(p), 16, 2, 4, 8, 4, 4, ptr(q),
                                        ptr(q), 8, ptr(p), 4, 4, None) == -1
     # a trellis width the kernels are not built for

@@ -414,3 +414,25 @@ def test_ldlq_noise_oracle_invariants():
     assert np.array_equal(back, W)
     out_in, Er_in, _ = O.ldlq_noise(W, H, 0.015, 7, eta, row_rotation=False)
     assert np.abs((out_in - W) @ Ri.T - Er_in).max() < 1e-12 * np.abs(Er_in).max()
+
+
+@pytest.mark.parametrize("case", ["r3", "r3_noH", "r4"])
+def test_multirate_sweep_matches_the_reference(golden, case):
+    """nested.py:104-147 for several rates at once: the reference's indices (tests/golden/multirate.npz: three rates of
+    a 3-bit nested code with and without H, four rates of a 4-bit code with a dead input)."""
+    g = golden("multirate")
+    H = g[f"{case}_H"] if not case.endswith("noH") else None
+    idx = O.multirate_sweep(g[f"{case}_X"], H, g[f"{case}_tables"], g[f"{case}_weights"])
+    assert np.array_equal(idx, g[f"{case}_idx"])
+
+
+def test_one_rate_multirate_is_the_scalar_sweep():
+    """One rate at weight 1: the joint cost is the squared distance, so the sweep is ldlq_scalar's (mode 0)."""
+    rng = np.random.default_rng(3)
+    m, n = 20, 150
+    X = rng.standard_normal((m, n))
+    Xa = rng.standard_normal((300, n))
+    H = Xa.T @ Xa / 300
+    lv = np.sort(rng.standard_normal(8))
+    _, U, _ = O.environment(H)
+    assert np.array_equal(O.multirate_sweep(X, H, lv[None], [1.0]), O.ldlq_scalar(X, U, lv, 0))
