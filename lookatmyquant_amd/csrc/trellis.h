@@ -183,9 +183,37 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
     }
     int cur = 0;
     float x = xs[0];
+    // From a given start state, position t reaches only the 2^(K (t+1)) states of one aligned range,
+    // [(start << K (t+1)) mod 2^L, + 2^(K (t+1))); every other state's cost is +inf there. A wave none of whose member
+    // states h*R + r lies in that range only stores +inf minima for its groups (the values the full computation would
+    // give) and no back-pointers (a traced path never reads a group whose minimum is +inf). Only for L >= 16: at
+    // L = 12 a step is short enough that the test costs more than the skipped waves save.
+    constexpr bool SKIP = L >= 16;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     for (int t = 0; t < TV - 1; ++t) {
         const float xn = xs[t + 1];
-        if (act) {
+        bool live = true;
+        if (SKIP && start >= 0 && K * (t + 1) < L) {
+            const int span = 1 << (K * (t + 1));
+            const int base = (int)(((uint32_t)start << (K * (t + 1))) & (uint32_t)(V::NS - 1));
+            const int w0 = wv * 64 * G;  // the wave's first group
+            live = false;
+#pragma unroll
+            for (int h = 0; h < NB; ++h) {
+                const int lo = h * R + w0;
+                live = live || (lo < base + span && base < lo + 64 * G);
+            }
+        }
+        if (act && !live) {
+            constexpr int CKI = V::RUN ? NB : G;
+            float* dst = buf + (DBL ? (cur ^ 1) * R : 0);
+            float infs[CKI];
+#pragma unroll
+            for (int i = 0; i < CKI; ++i) infs[i] = __builtin_inff();
+#pragma unroll
+            for (int e = 0; e < G / CKI; ++e) lds_store_swz<CKI>(dst, G * tid + e * CKI, infs);
+        }
+        if (act && live) {
             tab.hold();
             uint32_t bits = 0;
             float* dst = buf + (DBL ? (cur ^ 1) * R : 0);

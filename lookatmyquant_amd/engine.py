@@ -365,18 +365,49 @@ def viterbi_ops_per_row_step(L: int, k: int) -> int:
     return 3 * (1 << L) + ((1 << k) - 1) * (1 << (L - k))
 
 
-def trellis_row_steps(n: int, width: int = 16, look: int = 8, lazy: int = 128) -> list[int]:
-    """Trellis positions searched per row in each lazy block of the row-trellis sweep (the settled and the look-ahead
-    columns of every call)."""
+def trellis_call_lengths(n: int, width: int = 16, look: int = 8, lazy: int = 128) -> list[list[int]]:
+    """Positions of each search call per row, by lazy block of the row-trellis sweep: the w settled columns of the
+    call and its look-ahead columns (codes.py:386-404 via syntax.py:106-123)."""
     out = []
     for b0 in range(0, n, lazy):
         b1 = min(b0 + lazy, n)
-        tot = 0
+        calls = []
         for j in range(b0, b1, width):
             w = min(width, b1 - j)
-            tot += w + min(look, n - j - w)
-        out.append(tot)
+            calls.append(w + min(look, n - j - w))
+        out.append(calls)
     return out
+
+
+def trellis_row_steps(n: int, width: int = 16, look: int = 8, lazy: int = 128) -> list[int]:
+    """Trellis positions searched per row in each lazy block of the row-trellis sweep (the settled and the look-ahead
+    columns of every call)."""
+    return [sum(c) for c in trellis_call_lengths(n, width, look, lazy)]
+
+
+def viterbi_search_ops(L: int, k: int, T: int) -> int:
+    """Algorithmic fp32 operations of one search of T positions from a fixed start state, counting reachable states
+    only. Position t reaches the 2^a states, a = min(L, k (t + 1)), whose low a bits are free: each costs a
+    subtraction, a square and an addition. Forming position t's costs takes 2^k - 1 comparisons in each group of
+    predecessors (the states sharing their low L - k bits) only as far as the group holds several reachable ones:
+    with a' = min(L, k t) reachable bits at t - 1, 2^min(a', L - k) groups of 2^max(0, a' - L + k) members. Once
+    k t >= L every term equals viterbi_ops_per_row_step(L, k); the shorter first positions are the part of the
+    reference's full-array recurrence (codes.py:164-179) whose states are +inf."""
+    ops = 0
+    for t in range(T):
+        a = min(L, k * (t + 1))
+        ops += 3 * (1 << a)
+        if t > 0:
+            ap = min(L, k * t)
+            members = 1 << max(0, ap - (L - k))
+            ops += (members - 1) * (1 << min(ap, L - k))
+    return ops
+
+
+def trellis_block_ops(n: int, L: int, k: int, width: int = 16, look: int = 8, lazy: int = 128) -> list[int]:
+    """Reachable-state operations (viterbi_search_ops) of the searches of one row, by lazy block. Every call of the
+    row-trellis sweep has a fixed start state: the previous call's last settled state, 0 for the first."""
+    return [sum(viterbi_search_ops(L, k, T) for T in c) for c in trellis_call_lengths(n, width, look, lazy)]
 
 
 def trailing_flops(m: int, n: int, lazy: int = 128) -> float:

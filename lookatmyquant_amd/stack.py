@@ -343,7 +343,8 @@ class StackBuild:
                 steps = sum(E.trellis_row_steps(n))
                 for bits in sorted({int(g["bits"]) for nm in trellis for g in plans[nm]}):
                     m = sum(len(g["rows"]) for nm in trellis for g in plans[nm] if int(g["bits"]) == bits)
-                    kt.add_work("block", m * steps * E.viterbi_ops_per_row_step(L, bits))
+                    kt.add_work("block", m * sum(E.trellis_block_ops(n, L, bits)))  # reachable states
+                    kt.add_work("block_full", m * steps * E.viterbi_ops_per_row_step(L, bits))  # every state
                     kt.add_work("trailing", E.trailing_flops(m, n))
         if i < self.keep:
             self.kept[(i, s)] = {"Xq": torch.cat(xqf), "Xr": torch.cat(xrf), "H": H, "D": D, "targets": targets,

@@ -249,6 +249,42 @@ def test_workload_counts():
     assert E.trailing_flops(7, 1280) == 2 * 7 * 128 * 128 * 10 * 9 / 2
 
 
+@pytest.mark.parametrize("L,k,T,start", [(6, 1, 9, 0), (6, 2, 5, 0), (6, 2, 5, 45), (6, 3, 4, 7), (8, 2, 7, 0),
+                                         (8, 4, 4, 200), (12, 2, 24, 0)])
+def test_reachable_search_ops_match_brute_force(L, k, T, start):
+    """The reachable-state operation count of one search against an enumeration of the trellis itself: states
+    s_t = (s_{t-1} 2^k + b) mod 2^L from the given start; each reachable state costs 3 operations, and each
+    predecessor group (states sharing their low L - k bits) holding c reachable states costs c - 1 comparisons."""
+    from lookatmyquant_amd import engine as E
+
+    mask, low = (1 << L) - 1, (1 << (L - k)) - 1
+    prev = {start}
+    ops = 0
+    for t in range(T):
+        cur = {((s << k) | b) & mask for s in prev for b in range(1 << k)}
+        ops += 3 * len(cur)
+        if t > 0:
+            groups = {}
+            for s in prev:
+                groups[s & low] = groups.get(s & low, 0) + 1
+            ops += sum(c - 1 for c in groups.values())
+        prev = cur
+    assert E.viterbi_search_ops(L, k, T) == ops
+    # once every state is reachable, each further position costs the full per-step count
+    full = -(-L // k) + 1
+    if T > full:
+        assert E.viterbi_search_ops(L, k, T) - E.viterbi_search_ops(L, k, T - 1) == E.viterbi_ops_per_row_step(L, k)
+
+
+def test_trellis_block_ops_cover_every_call():
+    from lookatmyquant_amd import engine as E
+
+    calls = E.trellis_call_lengths(960, 16, 8, 128)
+    assert [sum(c) for c in calls] == E.trellis_row_steps(960, 16, 8, 128)
+    assert sum(len(c) for c in calls) == 960 // 16 and calls[-1][-1] == 16
+    assert E.trellis_block_ops(960, 12, 2) == [sum(E.viterbi_search_ops(12, 2, T) for T in c) for c in calls]
+
+
 def test_trellis_tables_must_have_two_to_the_L_entries():
     """A table shorter than 2^L would be read past its end by the search kernels: refused before any launch."""
     from lookatmyquant_amd import engine as E
