@@ -57,9 +57,9 @@ VALU_ISSUE_TOPS = 256 * 4 * 16 * 2.4e9 / 1e12
 
 # HBM bytes per launch of the dominant kernel from two rocprofv3 counter runs (FETCH_SIZE, WRITE_SIZE), scaled by a
 # 1 GiB copy's readings; keyed by (workload, kernel, L)
-MEASURED_TRAFFIC = {("c2", "ldlq_trellis_block_gx_kernel", 16): 11172003,
-                    ("c5", "ldlq_trellis_block_gx_kernel", 16): 241592801,
-                    ("c5", "ldlq_trellis_block_kernel", 12): 6286687}
+MEASURED_TRAFFIC = {("c2", "ldlq_trellis_block_gx_kernel", 16): 11125146,
+                    ("c5", "ldlq_trellis_groups_gx_kernel", 16): 260869872,
+                    ("c5", "ldlq_trellis_block_kernel", 12): 6285132}
 
 
 def kernel_line(ms: float, work: float, peak: float, unit: str, bound: str, scale: float, launches: int = 0) -> dict:
@@ -294,7 +294,9 @@ def run_c5(args):
     for k, v in kern.items():
         v["ms_per_step"] = round(v["ms"] / args.steps, 3)
     blk = kern["ldlq_trellis_block"]
-    kname = "ldlq_trellis_block_gx_kernel" if args.L >= E.BIG_L else "ldlq_trellis_block_kernel"
+    # at L >= 13 each lazy block of a stage is one launch over all its row groups (k = 1..4 by workgroup); at L = 12
+    # each group is its own launch, the groups on concurrent streams
+    kname = "ldlq_trellis_groups_gx_kernel" if args.L >= E.BIG_L else "ldlq_trellis_block_kernel"
     roofline = {"kernel": kname + " (k = 1..4)", "bound": "valu", "achieved": blk["achieved"],
                 "peak": FP32_VECTOR_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": blk["frac"],
                 "traffic": MEASURED_TRAFFIC.get(("c5", kname, args.L)), "avg_launch_us": blk.get("avg_launch_us"),
