@@ -109,6 +109,22 @@ struct TabF16 {
     }
 };
 
+// f(IntC<v>{}) for the uniform v in [I, N): a chain of scalar branches, so that f indexes registers statically
+template <int I>
+struct IntC {
+    static constexpr int value = I;
+};
+template <int I, int N, class F>
+__device__ __forceinline__ void uniform_switch(int v, F& f)
+{
+    if constexpr (I < N) {
+        if (v == I)
+            f(IntC<I>{});
+        else
+            uniform_switch<I + 1, N>(v, f);
+    }
+}
+
 // Search one path of TV steps; path[0..TV) is complete when this returns (it ends with a barrier).
 //   xs: TV float32 targets (LDS or global). start < 0 leaves the first state free, else only the states
 //   (start << K | b) & (2^L - 1) may begin (codes.py:164-167). buf: DBL ? 2R : R floats of LDS (with one
@@ -184,18 +200,29 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
     int cur = 0;
     float x = xs[0];
     // From a given start state, position t reaches only the 2^(K (t+1)) states of one aligned range,
-    // [(start << K (t+1)) mod 2^L, + 2^(K (t+1))); every other state's cost is +inf there. A wave none of whose member
-    // states h*R + r lies in that range only stores +inf minima for its groups (the values the full computation would
-    // give) and no back-pointers (a traced path never reads a group whose minimum is +inf). Only for L >= 16: at
-    // L = 12 a step is short enough that the test costs more than the skipped waves save.
+    // [(start << K (t+1)) mod 2^L, + 2^(K (t+1))); every other state's cost is +inf there, and so is the group minimum
+    // in bv of each of them (a state is reachable exactly when a state of its predecessor group is). Two savings follow,
+    // both giving the values the full computation gives. A wave none of whose member states h*R + r lies in the range
+    // only stores +inf minima for its groups, and no back-pointers (a traced path never reads a group whose minimum
+    // is +inf). While the range spans at most R states (K (t+1) <= L - K) it lies in the slab of one h, hl: every
+    // other member of a group is +inf, so the group's minimum is its member hl's cost, bv[hl] + (x - C)^2 (+inf for
+    // the groups outside the range, as bv is there), and hl is the winner wherever that is finite. Only for L >= 16:
+    // at L = 12 a step is short enough that the wave test costs more than the skipped waves save.
     constexpr bool SKIP = L >= 16;
+    constexpr uint32_t REP = [] {  // hl in every group's K-bit field of a back-pointer word
+        uint32_t r = 0;
+        for (int g = 0; g < G; ++g) r |= 1u << (g * K);
+        return r;
+    }();
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int st0 = __builtin_amdgcn_readfirstlane(start);
     for (int t = 0; t < TV - 1; ++t) {
         const float xn = xs[t + 1];
         bool live = true;
-        if (SKIP && start >= 0 && K * (t + 1) < L) {
+        int base = 0;
+        if (SKIP && st0 >= 0 && K * (t + 1) < L) {
             const int span = 1 << (K * (t + 1));
-            const int base = (int)(((uint32_t)start << (K * (t + 1))) & (uint32_t)(V::NS - 1));
+            base = (int)(((uint32_t)st0 << (K * (t + 1))) & (uint32_t)(V::NS - 1));
             const int w0 = wv * 64 * G;  // the wave's first group
             live = false;
 #pragma unroll
@@ -204,6 +231,7 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
                 live = live || (lo < base + span && base < lo + 64 * G);
             }
         }
+        const bool one_h = SKIP && st0 >= 0 && K * (t + 1) <= L - K;
         if (act && !live) {
             constexpr int CKI = V::RUN ? NB : G;
             float* dst = buf + (DBL ? (cur ^ 1) * R : 0);
@@ -213,7 +241,24 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
 #pragma unroll
             for (int e = 0; e < G / CKI; ++e) lds_store_swz<CKI>(dst, G * tid + e * CKI, infs);
         }
-        if (act && live) {
+        if (act && live && one_h) {
+            tab.hold();
+            float* dst = buf + (DBL ? (cur ^ 1) * R : 0);
+            auto step1 = [&](auto hc) {
+                constexpr int HL = decltype(hc)::value;
+                constexpr int CK = V::RUN ? NB : G;
+#pragma unroll
+                for (int e = 0; e < G / CK; ++e) {
+                    float best[CK];
+#pragma unroll
+                    for (int gg = 0; gg < CK; ++gg) best[gg] = bv[HL][e] + tab.dsq(x, HL * G + e * CK + gg);
+                    lds_store_swz<CK>(dst, G * tid + e * CK, best);
+                }
+                back[t * V::ACT + tid] = (BackT)((uint32_t)HL * REP);
+            };
+            uniform_switch<0, NB>(base >> (L - K), step1);
+        }
+        if (act && live && !one_h) {
             tab.hold();
             uint32_t bits = 0;
             float* dst = buf + (DBL ? (cur ^ 1) * R : 0);
