@@ -109,14 +109,17 @@ __global__ __launch_bounds__(256) void gemm_sub_f64_kernel(double* C, int64_t ld
 //   [row][k] operands (A; B when TRANSB): rows of BK doubles, chunk c of row r at c ^ (r & 15) for 16 chunks a
 //     row (BK = 32), c ^ ((r >> 1) & 7) for 8 (BK = 16: rows 2m and 2m + 1 sit 128 bytes apart in the banks):
 //     the 16 rows of a fragment read hit 16 different 16-byte bank windows;
-//   [k][col] operands (B): 1 KB rows of 128 columns, chunk c of row k at c ^ 8*(k & 1): the two k-rows read
-//     together sit 128 bytes apart in the banks.
+//   [k][col] operands (B): 1 KB rows of 128 columns, chunk c of row k at c ^ 8*(k & LAMQ_KSW_MASK): the four k-rows
+//     of a fragment read sit 128 bytes apart in the banks.
 // Rows past M / N and k past K load zero chunks. Needs even leading dimensions, even K (and even N for a
 // [k][col] B) and 16-byte aligned operands (gemm_sub_f64 checks; other shapes take the kernel above).
 #define G8_BM 128
 #define G8_BK 16
 #ifndef LAMQ_PANEL_MAX_TILES128
 #define LAMQ_PANEL_MAX_TILES128 1024  // short products with fewer 128-tiles than this take the 64-tile panel kernel
+#endif
+#ifndef LAMQ_KSW_MASK
+#define LAMQ_KSW_MASK 3  // [k][col] B operands: k-row k's 16-byte chunks XOR 8*(k & LAMQ_KSW_MASK)
 #endif
 #define LAMQ_TRI_KGE 1
 #define LAMQ_TRI_KLE 2
@@ -163,7 +166,7 @@ gemm128_f64_kernel(double* __restrict__ C, int64_t ldc, const double* __restrict
         load_lds16(g, m);
     };
     auto load_kcol = [&](const double* X, int64_t ldx, int64_t c0, int64_t k0, int i, uint32_t m) {
-        const int c = lane ^ (8 * (i & 1));
+        const int c = lane ^ (8 * (i & LAMQ_KSW_MASK));
         const int64_t k = k0 + i, col = c0 + 2 * c;
         const bool ok = k < K && col < N;
         const double* g = ok ? X + k * ldx + col : zc;
@@ -189,7 +192,7 @@ gemm128_f64_kernel(double* __restrict__ C, int64_t ldc, const double* __restrict
     // fragment addresses (bytes within an operand stage) for k = k4 + lk
     auto aaddr = [&](int row, int k) -> uint32_t { return (uint32_t)(row * RB + (((k >> 1) ^ rsw(row)) << 4) + (k & 1) * 8); };
     auto baddr = [&](int col, int k) -> uint32_t {
-        return TRANSB ? aaddr(col, k) : (uint32_t)(k * 1024 + (((col >> 1) ^ (8 * (k & 1))) << 4) + (col & 1) * 8);
+        return TRANSB ? aaddr(col, k) : (uint32_t)(k * 1024 + (((col >> 1) ^ (8 * (k & LAMQ_KSW_MASK))) << 4) + (col & 1) * 8);
     };
 
     int st0 = 0, nst = (int)cdiv(K, BK);
@@ -270,7 +273,8 @@ gemm128_f64_kernel(double* __restrict__ C, int64_t ldc, const double* __restrict
 // loads have landed, while the later stages' loads are still in flight; C is read before them. Four waves of 32x32
 // (2x2 MFMA tiles). LDS layout per stage: [row][k] operands (A; B when TRANSB) 256 bytes a row, chunk c of row r at
 // c ^ (r & 15) (the 16 rows of a fragment read fall in 16 different 16-byte bank windows); [k][col] B 512 bytes a
-// k-row. Needs even K, lda, ldb (and N for a [k][col] B) and 16-byte aligned A and B, like the 128-tile kernel.
+// k-row, chunk c of k-row k at c ^ 8*(k & LAMQ_KSW_MASK) (the four k-rows of a fragment read 128 bytes apart). Needs
+// even K, lda, ldb (and N for a [k][col] B) and 16-byte aligned A and B, like the 128-tile kernel.
 #define GP_BK 32
 template <bool TRANSB, bool LOWER, bool OVERWRITE>
 __global__ __launch_bounds__(256) void gemm64_panel_f64_kernel(double* C, int64_t ldc, const double* A, int64_t lda,
@@ -321,12 +325,16 @@ __global__ __launch_bounds__(256) void gemm64_panel_f64_kernel(double* C, int64_
                 const int64_t col = tc + r, k = k0 + 2 * c;
                 load_lds16((col < N && k < K) ? B + col * ldb + k : zc, base + (uint32_t)((st * 2 + 1) * SB + i * 1024));
             } else {
-                const int64_t k = k0 + 2 * i + lane / 32, col = tc + 2 * (lane % 32);
+                const int kr = 2 * i + lane / 32;
+                const int64_t k = k0 + kr, col = tc + 2 * ((lane % 32) ^ (8 * (kr & LAMQ_KSW_MASK)));
                 load_lds16((k < K && col < N) ? B + k * ldb + col : zc, base + (uint32_t)((st * 2 + 1) * SB + i * 1024));
             }
         }
     }
     auto aaddr = [](int r, int kk) -> uint32_t { return (uint32_t)(r * 256 + (((kk >> 1) ^ (r & 15)) << 4) + (kk & 1) * 8); };
+    auto kbaddr = [](int col, int kk) -> uint32_t {
+        return (uint32_t)(kk * 512 + (((col >> 1) ^ (8 * (kk & LAMQ_KSW_MASK))) << 4) + (col & 1) * 8);
+    };
     lamq_d4 acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -351,7 +359,7 @@ __global__ __launch_bounds__(256) void gemm64_panel_f64_kernel(double* C, int64_
             for (int t = 0; t < 2; ++t) {
                 a[t] = *reinterpret_cast<const double*>(As + aaddr(wr + 16 * t + li, kk));
                 b[t] = TRANSB ? *reinterpret_cast<const double*>(Bs + aaddr(wc + 16 * t + li, kk))
-                              : *reinterpret_cast<const double*>(Bs + kk * 512 + 8 * (wc + 16 * t + li));
+                              : *reinterpret_cast<const double*>(Bs + kbaddr(wc + 16 * t + li, kk));
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i)
@@ -374,6 +382,114 @@ __global__ __launch_bounds__(256) void gemm64_panel_f64_kernel(double* C, int64_
             }
 }
 
+// Short products with B as [k][col] (the sweep's narrow refits, K <= 128 by default): C -= A B on TM x TN tiles whose
+// four waves split K instead of the tile. The k-range is cut into chunks of 8 and each wave takes a quarter of the
+// chunks; it accumulates the whole tile over its quarter with its operands loaded straight into registers, one chunk
+// ahead of its MFMAs: lane l (group g = l/16, i = l%16) loads A[row i][k0 + 2g .. k0 + 2g + 1] as one 16-byte load and
+// B[k0 + 2g][col i], B[k0 + 2g + 1][col i], and the chunk is two MFMA k-steps over the k-sets {k0 + 2g} and
+// {k0 + 2g + 1}. No wave waits for another until the end, where the four partial tiles meet in LDS and are summed in
+// a fixed order, (w0 + w1) + (w2 + w3), and subtracted from C once. A workgroup's operands are read once, with no
+// LDS staging, so a CU holds several workgroups (LDS 4 TM TN doubles each), and small tiles give a product of a few
+// thousand rows enough workgroups to fill the chip, where the 64-tile kernel's one workgroup per CU (its k-range in
+// LDS) left most CUs idle. Needs even K and lda and a 16-byte aligned A (the chunks condition of gemm_sub_f64).
+#ifndef LAMQ_SPLITK_DEPTH
+#define LAMQ_SPLITK_DEPTH 2  // chunks of 8 k in flight per wave (measured: 2 beats 4 and 8)
+#endif
+template <int TM, int TN>
+__global__ __launch_bounds__(256) void gemm_splitk_f64_kernel(double* __restrict__ C, int64_t ldc,
+                                                              const double* __restrict__ A, int64_t lda,
+                                                              const double* __restrict__ B, int64_t ldb, int64_t M,
+                                                              int64_t N, int64_t K, const int32_t* __restrict__ info)
+{
+    constexpr int MT = TM / 16, NT = TN / 16;
+    constexpr int PV = MT * NT * 4;  // partial values per lane
+    __shared__ double part[4][PV * 64];
+    if (info && *info != 0) return;
+    const int64_t tr = (int64_t)blockIdx.y * TM, tc = (int64_t)blockIdx.x * TN;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int li = lane & 15, lg = lane >> 4;
+    const int64_t nch = (K + 7) >> 3, per = (nch + 3) >> 2;
+    const int64_t ch0 = wave * per, ch1 = ch0 + per < nch ? ch0 + per : nch;
+    lamq_d4 acc[MT][NT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[i][j] = lamq_d4{0.0, 0.0, 0.0, 0.0};
+    typedef double lamq_d2 __attribute__((ext_vector_type(2)));
+    const double* arow[MT];
+    bool aok[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+        const int64_t row = tr + 16 * i + li;
+        aok[i] = row < M;
+        arow[i] = A + (aok[i] ? row : 0) * lda;
+    }
+    bool bok[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) bok[j] = tc + 16 * j + li < N;
+    // one chunk's operands: a[i] = A[row][k, k + 1], b[j][e] = B[k + e][col] with k = 8 ch + 2 g (K even: k < K holds
+    // for both or neither of the pair)
+    auto load = [&](int64_t ch, lamq_d2 (&a)[MT], double (&b)[NT][2]) {
+        const int64_t k = 8 * ch + 2 * lg;
+        const bool kok = k < K;
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            a[i] = (aok[i] && kok) ? *reinterpret_cast<const lamq_d2*>(arow[i] + k) : lamq_d2{0.0, 0.0};
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const int64_t col = tc + 16 * j + li;
+            b[j][0] = (bok[j] && kok) ? B[k * ldb + col] : 0.0;
+            b[j][1] = (bok[j] && kok) ? B[(k + 1) * ldb + col] : 0.0;
+        }
+    };
+    // a ring of LAMQ_SPLITK_DEPTH chunks in flight: chunk c lives in slot (c - ch0) % D, reloaded with chunk c + D as
+    // soon as its MFMAs are issued
+    constexpr int D = LAMQ_SPLITK_DEPTH;
+    lamq_d2 a[D][MT];
+    double b[D][NT][2];
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+        if (ch0 + d < ch1) load(ch0 + d, a[d], b[d]);
+    for (int64_t ch = ch0; ch < ch1; ch += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (ch + d < ch1) {
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+#pragma unroll
+                    for (int i = 0; i < MT; ++i)
+#pragma unroll
+                        for (int j = 0; j < NT; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[d][i][e], b[d][j][e], acc[i][j], 0, 0, 0);
+                if (ch + d + D < ch1) load(ch + d + D, a[d], b[d]);
+            }
+        }
+    }
+    // partials in LDS, value p of lane l at p * 64 + l (p = (i NT + j) 4 + v)
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) part[wave][((i * NT + j) * 4 + v) * 64 + lane] = acc[i][j][v];
+    __syncthreads();
+    // each thread sums the four partials of TM TN / 256 outputs, columns fastest across threads; output (r, c) is
+    // value ((r/16) NT + c/16) 4 + (r%16)/4 of lane 16 (r%4) + c%16 (the 16x16 MFMA result layout)
+#pragma unroll
+    for (int q = 0; q < TM * TN / 256; ++q) {
+        const int o = q * 256 + (int)threadIdx.x;
+        const int r = o / TN, c = o % TN;
+        const int idx = (((r >> 4) * NT + (c >> 4)) * 4 + ((r & 15) >> 2)) * 64 + ((r & 3) << 4) + (c & 15);
+        const double s = (part[0][idx] + part[1][idx]) + (part[2][idx] + part[3][idx]);
+        const int64_t row = tr + r, col = tc + c;
+        if (row < M && col < N) C[row * ldc + col] -= s;
+    }
+}
+
+#ifndef LAMQ_SPLITK_MAXK
+#define LAMQ_SPLITK_MAXK 128  // [k][col] products up to this K (not LOWER, not OVERWRITE) take the split-K kernel
+#endif
+
 // TRI (LAMQ_TRI_KGE, LAMQ_TRI_KLE): op(B) is triangular and the 128-tile kernel skips the stages of its zero part (the
 // other kernels read the zeros).
 template <bool TRANSB, bool LOWER, bool OVERWRITE = false, int TRI = 0>
@@ -388,6 +504,12 @@ static int gemm_sub_f64(double* C, int64_t ldc, const double* A, int64_t lda, co
                         ((uintptr_t)A % 16) == 0 && ((uintptr_t)B % 16) == 0;
     const int64_t tiles128 = cdiv(M, G8_BM) * cdiv(N, G8_BM);
     dim3 grid((unsigned)cdiv(N, 64), (unsigned)cdiv(M, 64));
+    if (!TRANSB && !LOWER && !OVERWRITE && TRI == 0 && chunks && K <= LAMQ_SPLITK_MAXK && cdiv(M, 32) <= 65535) {
+        hipLaunchKernelGGL((gemm_splitk_f64_kernel<32, 32>), dim3((unsigned)cdiv(N, 32), (unsigned)cdiv(M, 32)), dim3(256),
+                           0, s, C, ldc, A, lda, B, ldb, M, N, K, info);
+        LAMQ_LAUNCH_CHECK();
+        return LAMQ_OK;
+    }
     if (chunks && K <= 128 && (OVERWRITE || tiles128 < LAMQ_PANEL_MAX_TILES128)) {
         hipLaunchKernelGGL((gemm64_panel_f64_kernel<TRANSB, LOWER, OVERWRITE>), grid, dim3(256), 0, s, C, ldc, A, lda, B,
                            ldb, M, N, K, info);

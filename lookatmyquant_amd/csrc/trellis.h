@@ -216,23 +216,33 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
     }();
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int st0 = __builtin_amdgcn_readfirstlane(start);
+    // whether some member state of this wave is reachable at position p (always, once every state is)
+    const auto wave_live = [&](int p) {
+        if (!SKIP || st0 < 0 || K * (p + 1) >= L) return true;
+        const int span = 1 << (K * (p + 1));
+        const int base = (int)(((uint32_t)st0 << (K * (p + 1))) & (uint32_t)(V::NS - 1));
+        const int w0 = wv * 64 * G;  // the wave's first group
+        bool lv = false;
+#pragma unroll
+        for (int h = 0; h < NB; ++h) {
+            const int lo = h * R + w0;
+            lv = lv || (lo < base + span && base < lo + 64 * G);
+        }
+        return lv;
+    };
+    // A wave none of whose members is reachable stores +inf minima only where its groups' entries in the target buffer
+    // may hold finite values: stale from an earlier search (both buffers at the start) or written at an earlier
+    // position. dirty0/1 track that per buffer, so a wave that stays unreachable stores its +inf once per buffer; and a
+    // wave unreachable at the next position skips the loads of its members' minima (it computes nothing there).
+    bool dirty0 = true, dirty1 = true;
+    bool live = wave_live(0);
     for (int t = 0; t < TV - 1; ++t) {
         const float xn = xs[t + 1];
-        bool live = true;
-        int base = 0;
-        if (SKIP && st0 >= 0 && K * (t + 1) < L) {
-            const int span = 1 << (K * (t + 1));
-            base = (int)(((uint32_t)st0 << (K * (t + 1))) & (uint32_t)(V::NS - 1));
-            const int w0 = wv * 64 * G;  // the wave's first group
-            live = false;
-#pragma unroll
-            for (int h = 0; h < NB; ++h) {
-                const int lo = h * R + w0;
-                live = live || (lo < base + span && base < lo + 64 * G);
-            }
-        }
+        const int base = (SKIP && st0 >= 0 && K * (t + 1) < L)
+                             ? (int)(((uint32_t)st0 << (K * (t + 1))) & (uint32_t)(V::NS - 1)) : 0;
         const bool one_h = SKIP && st0 >= 0 && K * (t + 1) <= L - K;
-        if (act && !live) {
+        const bool tgt1 = DBL && cur == 0;  // the buffer this step writes: cur ^ 1 (DBL), else the only one
+        if (act && !live && (tgt1 ? dirty1 : dirty0)) {
             constexpr int CKI = V::RUN ? NB : G;
             float* dst = buf + (DBL ? (cur ^ 1) * R : 0);
             float infs[CKI];
@@ -241,6 +251,10 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
 #pragma unroll
             for (int e = 0; e < G / CKI; ++e) lds_store_swz<CKI>(dst, G * tid + e * CKI, infs);
         }
+        if (tgt1)
+            dirty1 = live;
+        else
+            dirty0 = live;
         if (act && live && one_h) {
             tab.hold();
             float* dst = buf + (DBL ? (cur ^ 1) * R : 0);
@@ -289,11 +303,13 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
                         // a two-level tournament with strict comparisons (a tie keeps the left, lower, side): the
                         // winning pair hi = (min(c2,c3) < min(c0,c1)), then within it lo; h = 2 hi + lo enters bits
                         // [2g, 2g+2) as two carry-ins (bits = 2 bits + bit), the comparisons staying lane masks
-                        const float m01 = fminf(c[0], c[1]), m23 = fminf(c[2], c[3]);
-                        const uint64_t hi = __builtin_amdgcn_ballot_w64(m23 < m01);
+                        // (the minimum as one v_min3 of m01, c2, c3; the right pair wins exactly when it is below m01)
+                        const float m01 = fminf(c[0], c[1]);
+                        const float mb = fminf(m01, fminf(c[2], c[3]));
+                        const uint64_t hi = __builtin_amdgcn_ballot_w64(mb < m01);
                         const uint64_t lo = (hi & __builtin_amdgcn_ballot_w64(c[3] < c[2])) |
                                             (~hi & __builtin_amdgcn_ballot_w64(c[1] < c[0]));
-                        best[gg] = fminf(m01, m23);
+                        best[gg] = mb;
                         bits = shift_in(bits, hi);
                         bits = shift_in(bits, lo);
                     } else {
@@ -315,17 +331,19 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
         lds_barrier();
         cur ^= 1;
         x = xn;
-        if (act) {
+        live = wave_live(t + 1);
+        if (act && live) {
 #pragma unroll
             for (int h = 0; h < NB; ++h) lds_load_swz<M>(buf + (DBL ? cur * R : 0), ent[h], bv[h]);
         }
         if (!DBL) lds_barrier();
     }
     hook();
-    // final costs, the lowest state on ties (a thread's states increase with (h, g))
+    // final costs, the lowest state on ties (a thread's states increase with (h, g)); a wave with no reachable member
+    // there keeps +inf
     float bvv = __builtin_inff();
     int bi = 0x7fffffff;
-    if (act) {
+    if (act && live) {
         tab.hold();
 #pragma unroll
         for (int h = 0; h < NB; ++h)

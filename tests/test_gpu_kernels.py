@@ -158,9 +158,10 @@ def test_gemm_sub_triangular(E, M, N, K, transb, tri):
                                            (130, 70, 64, True), (65, 66, 2, False), (200, 128, 100, True),
                                            (19456, 256, 128, False)])
 def test_gemm_sub_short_k(E, M, N, K, transb):
-    """Short products (K <= 128: the sweep's narrow refits, the factor's panels) on the 64-tile kernel that loads a
-    tile's whole k-range into LDS at once: ragged M, N and K (zero chunks past them), both layouts of B, against a
-    float64 product on the GPU; columns outside [0, N) of a wider C untouched."""
+    """Short products (K <= 128): with B as [k][col] (the sweep's narrow refits) on the split-K kernel (four waves, a
+    quarter of the k-range each, partial tiles summed in LDS), with B as [col][k] (the factor's panels) on the 64-tile
+    kernel that loads a tile's whole k-range into LDS at once: ragged M, N and K (zeros past them), against a float64
+    product on the GPU; columns outside [0, N) of a wider C untouched."""
     g = torch.Generator(device="cuda").manual_seed(M + 3 * N + 7 * K)
     Cw = torch.randn(M, N + 6, generator=g, device="cuda", dtype=torch.float64)
     C = Cw[:, 2 : 2 + N]
@@ -172,6 +173,23 @@ def test_gemm_sub_short_k(E, M, N, K, transb):
     say(f"gemm_sub short k: M={M} N={N} K={K} transb={transb}")
     E.gemm_sub(C, A, Bm, transb=transb)
     err = ((Cw - ref).abs().max() / ref.abs().max()).item()
+    say(f"  max relative difference {err:.3e}")
+    assert err < 1e-13
+
+
+@pytest.mark.parametrize("M,N,K", [(2560, 9216, 512), (2560, 1536, 512), (6144, 1536, 512), (19456, 2048, 512),
+                                   (300, 1000, 136)])
+def test_gemm_sub_deep_rounds(E, M, N, K):
+    """The sweep's deep products (B as [k][col], K = 512 at the config-5 and config-3 stage shapes) on the LDS-staged
+    128-tile kernel, and a small one on the 64-tile kernel; against a float64 product on the GPU."""
+    g = torch.Generator(device="cuda").manual_seed(M + 5 * N + 11 * K)
+    C = torch.randn(M, N, generator=g, device="cuda", dtype=torch.float64)
+    A = torch.randn(M, K, generator=g, device="cuda", dtype=torch.float64)
+    Bm = torch.randn(K, N, generator=g, device="cuda", dtype=torch.float64)
+    ref = C - A @ Bm
+    say(f"gemm_sub deep: M={M} N={N} K={K}")
+    got = E.gemm_sub(C, A, Bm)
+    err = ((got - ref).abs().max() / ref.abs().max()).item()
     say(f"  max relative difference {err:.3e}")
     assert err < 1e-13
 
