@@ -189,11 +189,11 @@ int lamq_zero_columns(double* T, int64_t m, int64_t n, int64_t ldT, const uint8_
  *   info  [1] int32 device output: 0, or j+1 when the leading minor of order j+1 of J H J is not
  *         positive definite (torch.linalg.LinAlgError in the reference)
  *   workspace: lamq_chol_inv_upper_workspace_size(n) bytes
- * Part of the work runs on an internal stream (one per calling stream and device, up to eight, created on first use,
- * default priority), ordered after the work already on `stream` and joined back into `stream` before the call
- * returns, so the results are ordered on `stream` like any other entry point's; factorizations enqueued on
- * different streams run side by side. Calls from several host threads on one stream serialise their enqueue on a
- * lock.
+ * lamq_chol_inv_upper enqueues everything on `stream`. lamq_chol_inv_upper_ex may be given a second stream of the
+ * caller's, `side_stream` (NULL: none), on which the inverse half of the steps runs, ordered after the work already
+ * on `stream` and joined back into `stream` before the call returns (events made and released by the call), so the
+ * results are ordered on `stream` either way; the library keeps no streams or other state of its own. Concurrent
+ * calls must not share a side stream unless their inverses may run one after the other (the results are the same).
  * ---------------------------------------------------------------------------------------------- */
 size_t lamq_chol_inv_upper_workspace_size(int64_t n);
 /* flags of lamq_chol_inv_upper_ex: LAMQ_CHOL_KEEP_DEAD leaves a zero diagonal as it is (no unit diagonal at dead
@@ -201,7 +201,7 @@ size_t lamq_chol_inv_upper_workspace_size(int64_t n);
 #define LAMQ_CHOL_KEEP_DEAD 1
 int lamq_chol_inv_upper_ex(const double* H, int64_t n, int64_t ldH, double damp, int flags, double* Hd,
                            int64_t ldHd, double* U, int64_t ldU, uint8_t* dead, int32_t* info, void* workspace,
-                           size_t workspace_bytes, void* stream);
+                           size_t workspace_bytes, void* stream, void* side_stream);
 int lamq_chol_inv_upper(const double* H, int64_t n, int64_t ldH, double damp, double* Hd, int64_t ldHd,
                         double* U, int64_t ldU, uint8_t* dead, int32_t* info, void* workspace,
                         size_t workspace_bytes, void* stream);

@@ -44,7 +44,7 @@ SIGNATURES = {
     "lamq_chol_inv_upper_workspace_size": (_c_size, [_c_i64]),
     "lamq_chol_inv_upper": (_c_int, [_p, _c_i64, _c_i64, _c_dbl, _p, _c_i64, _p, _c_i64, _p, _p, _p, _c_size, _p]),
     "lamq_chol_inv_upper_ex": (_c_int, [_p, _c_i64, _c_i64, _c_dbl, _c_int, _p, _c_i64, _p, _c_i64, _p, _p, _p, _c_size,
-                                        _p]),
+                                        _p, _p]),
     "lamq_rht_rows": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _p, _c_int, _p, _c_int, _c_int, _p, _p]),
     "lamq_transpose_f64": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p]),
     "lamq_row_rms": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _p]),

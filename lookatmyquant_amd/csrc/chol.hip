@@ -10,7 +10,6 @@
 // X_k = Lkk^-1 B_k.
 #include "gemm_f64.h"
 
-#include <mutex>
 
 #define NBK 64
 #ifndef LAMQ_NB2
@@ -304,58 +303,8 @@ __global__ void reverse_kernel(double* __restrict__ U, int64_t n, int64_t ldU, c
     U[i * ldU + j] = 0.0;
 }
 
-// One internal stream per device (default priority) with the events that order it against the caller's stream.
-// The enqueue of one factorization holds the device's mutex, so calls from several host threads do not interleave
-// their use of the events.
-struct SideStream {
-    std::mutex mu;
-    bool used = false;
-    hipStream_t owner = nullptr;  // the caller's stream this side stream serves
-    hipStream_t s = nullptr;
-    hipEvent_t fork = nullptr, step = nullptr, join = nullptr;
-};
-#define LAMQ_MAX_DEVICES 64
-#define LAMQ_SIDE_PER_DEVICE 8
-static SideStream g_side[LAMQ_MAX_DEVICES][LAMQ_SIDE_PER_DEVICE];
-static std::mutex g_side_init;
-
-// The side stream of the caller's stream on the current device, made on first use: factorizations enqueued on
-// different streams (for instance two of them run side by side) get different side streams, so that neither's
-// inverse waits behind the other's. Beyond LAMQ_SIDE_PER_DEVICE caller streams, callers share side streams (their
-// inverses then run one after the other; the results are the same).
-static int side_stream(hipStream_t caller, SideStream** out)
-{
-    int dev = 0;
-    LAMQ_HIP_CHECK(hipGetDevice(&dev));
-    if (dev < 0 || dev >= LAMQ_MAX_DEVICES) return LAMQ_EUNSUP;
-    std::lock_guard<std::mutex> lock(g_side_init);
-    SideStream* row = g_side[dev];
-    for (int i = 0; i < LAMQ_SIDE_PER_DEVICE; ++i)
-        if (row[i].used && row[i].owner == caller) {
-            *out = &row[i];
-            return LAMQ_OK;
-        }
-    for (int i = 0; i < LAMQ_SIDE_PER_DEVICE; ++i) {
-        SideStream& ss = row[i];
-        if (ss.used) continue;
-        hipStream_t st = nullptr;
-        hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
-        LAMQ_HIP_CHECK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
-        for (int j = 0; j < 3; ++j) LAMQ_HIP_CHECK(hipEventCreateWithFlags(&ev[j], hipEventDisableTiming));
-        ss.fork = ev[0];
-        ss.step = ev[1];
-        ss.join = ev[2];
-        ss.s = st;
-        ss.owner = caller;
-        ss.used = true;
-        *out = &ss;
-        return LAMQ_OK;
-    }
-    *out = &row[(uintptr_t)caller % LAMQ_SIDE_PER_DEVICE];
-    return LAMQ_OK;
-}
-
-// The blocked steps of the factorization (stream s) and of the inverse (stream si).
+// The blocked steps of the factorization (stream s) and of the inverse (stream si, which may be s: then the step
+// events are not used).
 static int chol_steps(double* A, int64_t n, double* Linv, double* U, int64_t ldU, int32_t* info, hipStream_t s,
                       hipStream_t si, hipEvent_t step)
 {
@@ -377,8 +326,10 @@ static int chol_steps(double* A, int64_t n, double* Linv, double* U, int64_t ldU
             hipLaunchKernelGGL(diag_block_kernel, dim3(pg), dim3(256), 0, s, A, n, k0, nb, rest, Lk, info);
             LAMQ_LAUNCH_CHECK();
             int rc;
-            LAMQ_HIP_CHECK(hipEventRecord(step, s));
-            LAMQ_HIP_CHECK(hipStreamWaitEvent(si, step, 0));
+            if (si != s) {
+                LAMQ_HIP_CHECK(hipEventRecord(step, s));
+                LAMQ_HIP_CHECK(hipStreamWaitEvent(si, step, 0));
+            }
             const int64_t pc = pe - (k0 + nb);
             if (rest > 0 && pc > 0) {
                 rc = gemm_sub_f64<true, true>(A + (k0 + nb) * n + k0 + nb, n, P, n, P, n, rest, pc, nb, info, s);
@@ -413,9 +364,21 @@ extern "C" size_t lamq_chol_inv_upper_workspace_size(int64_t n)
     return (size_t)n * (size_t)n * sizeof(double) + (size_t)cdiv(n, NBK) * NBK * NBK * sizeof(double) + 256;
 }
 
+// Events of one factorization whose inverse runs on a side stream, made and released by the call (the library keeps
+// no state between calls). A released event that is still recorded on a stream lives until the stream reaches it.
+struct CholEvents {
+    hipEvent_t fork = nullptr, step = nullptr, join = nullptr;
+    ~CholEvents()
+    {
+        if (fork) (void)hipEventDestroy(fork);
+        if (step) (void)hipEventDestroy(step);
+        if (join) (void)hipEventDestroy(join);
+    }
+};
+
 extern "C" int lamq_chol_inv_upper_ex(const double* H, int64_t n, int64_t ldH, double damp, int flags, double* Hd,
                                       int64_t ldHd, double* U, int64_t ldU, uint8_t* dead, int32_t* info, void* workspace,
-                                      size_t workspace_bytes, void* stream)
+                                      size_t workspace_bytes, void* stream, void* side_stream)
 {
     if (!H || !U || !info || !workspace || n < 1 || ldH < n || ldU < n || (Hd && ldHd < n)) return LAMQ_EINVAL;
     if (flags & ~LAMQ_CHOL_KEEP_DEAD) return LAMQ_EINVAL;
@@ -423,11 +386,14 @@ extern "C" int lamq_chol_inv_upper_ex(const double* H, int64_t n, int64_t ldH, d
     if (workspace_bytes < lamq_chol_inv_upper_workspace_size(n)) return LAMQ_EINVAL;
     if (n > (int64_t)1 << 20) return LAMQ_EUNSUP;
     hipStream_t s = as_stream(stream);
-    SideStream* side = nullptr;
-    int rc = side_stream(s, &side);
-    if (rc) return rc;
-    std::lock_guard<std::mutex> lock(side->mu);
-    hipStream_t si = side->s;
+    hipStream_t si = side_stream ? as_stream(side_stream) : s;
+    const bool fork = si != s;
+    CholEvents ev;
+    if (fork) {
+        LAMQ_HIP_CHECK(hipEventCreateWithFlags(&ev.fork, hipEventDisableTiming));
+        LAMQ_HIP_CHECK(hipEventCreateWithFlags(&ev.step, hipEventDisableTiming));
+        LAMQ_HIP_CHECK(hipEventCreateWithFlags(&ev.join, hipEventDisableTiming));
+    }
     double* A = reinterpret_cast<double*>(workspace);
     double* Linv = A + n * n;  // cdiv(n, NBK) blocks of NBK x NBK
     double* delta = Linv + cdiv(n, NBK) * NBK * NBK;
@@ -436,19 +402,25 @@ extern "C" int lamq_chol_inv_upper_ex(const double* H, int64_t n, int64_t ldH, d
     const dim3 g2((unsigned)cdiv(n, 64), (unsigned)cdiv(n, 16)), b2(64, 16);
     hipLaunchKernelGGL(prep_kernel, g2, b2, 0, s, H, n, ldH, delta, keep_dead, A, Hd, ldHd);
     LAMQ_LAUNCH_CHECK();
-    // The inverse X = L^-1 runs on the side stream, one 64-column step behind the factorization: its step k needs
-    // Lkk^-1 and the panel L_ik of the factor's step k (an event after that step's panel solve), nothing the
-    // factor writes later. The factor's in-panel and trailing updates and the inverse's products then overlap.
-    LAMQ_HIP_CHECK(hipEventRecord(side->fork, s));
-    LAMQ_HIP_CHECK(hipStreamWaitEvent(si, side->fork, 0));
+    // The inverse X = L^-1 runs on the side stream (when one is given), one 64-column step behind the factorization:
+    // its step k needs Lkk^-1 and the panel L_ik of the factor's step k (an event after that step's panel solve),
+    // nothing the factor writes later. The factor's in-panel and trailing updates and the inverse's products then
+    // overlap. Without a side stream both run in order on the caller's stream.
+    if (fork) {
+        LAMQ_HIP_CHECK(hipEventRecord(ev.fork, s));
+        LAMQ_HIP_CHECK(hipStreamWaitEvent(si, ev.fork, 0));
+    }
     hipLaunchKernelGGL(identity_kernel, g2, b2, 0, si, U, n, ldU);
     LAMQ_LAUNCH_CHECK();
-    rc = chol_steps(A, n, Linv, U, ldU, info, s, si, side->step);
-    // the caller's stream waits for the side stream, also after a failed launch
-    const hipError_t e1 = hipEventRecord(side->join, si);
-    const hipError_t e2 = e1 == hipSuccess ? hipStreamWaitEvent(s, side->join, 0) : e1;
+    int rc = chol_steps(A, n, Linv, U, ldU, info, s, si, ev.step);
+    if (fork) {
+        // the caller's stream waits for the side stream, also after a failed launch
+        const hipError_t e1 = hipEventRecord(ev.join, si);
+        const hipError_t e2 = e1 == hipSuccess ? hipStreamWaitEvent(s, ev.join, 0) : e1;
+        if (rc) return rc;
+        if (e2 != hipSuccess) return (int)e2;
+    }
     if (rc) return rc;
-    if (e2 != hipSuccess) return (int)e2;
     hipLaunchKernelGGL(reverse_kernel, g2, b2, 0, s, U, n, ldU, info);
     LAMQ_LAUNCH_CHECK();
     return LAMQ_OK;
@@ -458,5 +430,6 @@ extern "C" int lamq_chol_inv_upper(const double* H, int64_t n, int64_t ldH, doub
                                    double* U, int64_t ldU, uint8_t* dead, int32_t* info, void* workspace,
                                    size_t workspace_bytes, void* stream)
 {
-    return lamq_chol_inv_upper_ex(H, n, ldH, damp, 0, Hd, ldHd, U, ldU, dead, info, workspace, workspace_bytes, stream);
+    return lamq_chol_inv_upper_ex(H, n, ldH, damp, 0, Hd, ldHd, U, ldU, dead, info, workspace, workspace_bytes, stream,
+                                  nullptr);
 }

@@ -442,6 +442,16 @@ __global__ __launch_bounds__(256) void gemm_splitk_f64_kernel(double* __restrict
             b[j][1] = (bok[j] && kok) ? B[(k + 1) * ldb + col] : 0.0;
         }
     };
+    // this thread's outputs of C, read now so that their latency overlaps the k-loop (TM TN / 256 per thread, columns
+    // fastest across threads, as the epilogue writes them)
+    constexpr int QO = TM * TN / 256;
+    double cpre[QO];
+#pragma unroll
+    for (int q = 0; q < QO; ++q) {
+        const int o = q * 256 + (int)threadIdx.x;
+        const int64_t row = tr + o / TN, col = tc + o % TN;
+        cpre[q] = (row < M && col < N) ? C[row * ldc + col] : 0.0;
+    }
     // a ring of LAMQ_SPLITK_DEPTH chunks in flight: chunk c lives in slot (c - ch0) % D, reloaded with chunk c + D as
     // soon as its MFMAs are issued
     constexpr int D = LAMQ_SPLITK_DEPTH;
@@ -476,13 +486,13 @@ __global__ __launch_bounds__(256) void gemm_splitk_f64_kernel(double* __restrict
     // each thread sums the four partials of TM TN / 256 outputs, columns fastest across threads; output (r, c) is
     // value ((r/16) NT + c/16) 4 + (r%16)/4 of lane 16 (r%4) + c%16 (the 16x16 MFMA result layout)
 #pragma unroll
-    for (int q = 0; q < TM * TN / 256; ++q) {
+    for (int q = 0; q < QO; ++q) {
         const int o = q * 256 + (int)threadIdx.x;
         const int r = o / TN, c = o % TN;
         const int idx = (((r >> 4) * NT + (c >> 4)) * 4 + ((r & 15) >> 2)) * 64 + ((r & 3) << 4) + (c & 15);
         const double s = (part[0][idx] + part[1][idx]) + (part[2][idx] + part[3][idx]);
         const int64_t row = tr + r, col = tc + c;
-        if (row < M && col < N) C[row * ldc + col] -= s;
+        if (row < M && col < N) C[row * ldc + col] = cpre[q] - s;
     }
 }
 

@@ -129,4 +129,4 @@ extern "C" int lamq_pack_trellis(const int32_t* states, int64_t m, int64_t n, in
     return lamq_pack_codes(states, lds, m, nullptr, m, n, 0, k, L, 1, codes, ldc, bad, stream);
 }
 
-extern "C" int lamq_abi_version(void) { return 100; }
+extern "C" int lamq_abi_version(void) { return 101; }

@@ -129,6 +129,20 @@ def unrotate_columns(X: torch.Tensor, seed: int) -> torch.Tensor:
 CHOL_KEEP_DEAD = 1
 
 
+_SIDE_STREAMS: dict = {}
+
+
+def _side_stream(dev: torch.device) -> torch.cuda.Stream:
+    """The stream on which the factor's inverse half runs beside the current stream: one per (device, calling stream),
+    made on first use at the default priority, so that factorizations enqueued on different streams stay independent
+    (lamq_chol_inv_upper_ex forks from and joins back into the calling stream)."""
+    cur = torch.cuda.current_stream(dev)
+    key = (cur.device.index, cur.cuda_stream)
+    if key not in _SIDE_STREAMS:
+        _SIDE_STREAMS[key] = torch.cuda.Stream(device=cur.device)
+    return _SIDE_STREAMS[key]
+
+
 def chol_inv_upper(H: torch.Tensor, damp: float = 0.01, raise_on_fail: bool = True, keep_dead: bool = False):
     """(Hd, U, dead, info): the damped H, the upper Cholesky factor of its inverse, the dead-column mask and the
     failing pivot (0 when H is positive definite after damping; raises LinAlgError then unless told not to).
@@ -144,8 +158,8 @@ def chol_inv_upper(H: torch.Tensor, damp: float = 0.01, raise_on_fail: bool = Tr
     nbytes = lib().lamq_chol_inv_upper_workspace_size(n)
     ws = workspace(nbytes, H.device)
     check(lib().lamq_chol_inv_upper_ex(ptr(H), n, ld(H), float(damp), CHOL_KEEP_DEAD if keep_dead else 0, ptr(Hd), n,
-                                       ptr(U), n, ptr(dead), ptr(info), ptr(ws), nbytes, stream(H.device)),
-          "chol_inv_upper")
+                                       ptr(U), n, ptr(dead), ptr(info), ptr(ws), nbytes, stream(H.device),
+                                       _side_stream(H.device).cuda_stream), "chol_inv_upper")
     if raise_on_fail:
         bad = int(info.item())
         if bad:

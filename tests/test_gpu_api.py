@@ -423,7 +423,7 @@ def test_chol_keep_dead_flag():
     out = torch.empty(n, n, dtype=torch.float64, device="cuda")
     inf = torch.zeros(1, dtype=torch.int32, device="cuda")
     rc = lib.lamq_chol_inv_upper_ex(Ht.data_ptr(), n, n, 0.01, 2, None, 0, out.data_ptr(), n, None, inf.data_ptr(),
-                                    ws.data_ptr(), ws.numel(), None)
+                                    ws.data_ptr(), ws.numel(), None, None)
     assert rc == -1  # LAMQ_EINVAL
 
 

@@ -242,7 +242,7 @@ def test_chol_inv_upper_large_inverse_identity(E, n):
 
 
 def test_chol_inv_upper_on_two_streams(E):
-    """Two factorizations enqueued on two streams (each with its own internal inverse stream) run side by side and
+    """Two factorizations enqueued on two streams (each with its own side stream for the inverse) run side by side and
     give the factors they give one after the other, bit for bit."""
     g = torch.Generator(device="cuda").manual_seed(23)
     Hs = []
@@ -266,6 +266,30 @@ def test_chol_inv_upper_on_two_streams(E):
         for (Hd, U, dead, info), r in zip(out, ref):
             assert int(info.item()) == 0
             assert torch.equal(U, r)
+
+
+def test_chol_inv_upper_without_a_side_stream(E):
+    """lamq_chol_inv_upper (no side stream: every step on the caller's stream) and lamq_chol_inv_upper_ex with a side
+    stream for the inverse give the same factor bit for bit, and the damped H the same."""
+    n = 1500
+    g = torch.Generator(device="cuda").manual_seed(29)
+    A = torch.randn(2 * n, n, generator=g, device="cuda", dtype=torch.float64)
+    H = (A.T @ A / (2 * n)).contiguous()
+    say("chol_inv_upper: n = 1500 with and without a side stream")
+    Hd, U, _, info = E.chol_inv_upper(H)
+    lib = E._abi.lib()
+    nb = lib.lamq_chol_inv_upper_workspace_size(n)
+    ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    U1 = torch.empty(n, n, dtype=torch.float64, device="cuda")
+    Hd1 = torch.empty(n, n, dtype=torch.float64, device="cuda")
+    info1 = torch.empty(1, dtype=torch.int32, device="cuda")
+    rc = lib.lamq_chol_inv_upper(H.data_ptr(), n, n, 0.01, Hd1.data_ptr(), n, U1.data_ptr(), n, None, info1.data_ptr(),
+                                 ws.data_ptr(), nb, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert int(info.item()) == 0 and int(info1.item()) == 0
+    assert torch.equal(U1, U)
+    assert torch.equal(Hd1, Hd)
 
 
 @pytest.mark.parametrize("n,k", [(300, 3), (300, 37), (300, 250)])

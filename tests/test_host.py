@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     lib = _abi.lib()  # loads the gfx950 library; binding fails on a missing symbol
     for n in names:
         assert hasattr(lib, n)
-    assert lib.lamq_abi_version() == 100
+    assert lib.lamq_abi_version() == 101
 
 
 def test_library_symbols_are_c_abi():
