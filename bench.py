@@ -57,8 +57,8 @@ VALU_ISSUE_TOPS = 256 * 4 * 16 * 2.4e9 / 1e12
 
 # HBM bytes per launch of the dominant kernel from two rocprofv3 counter runs (FETCH_SIZE, WRITE_SIZE), scaled by a
 # 1 GiB copy's readings; keyed by (workload, kernel, L)
-MEASURED_TRAFFIC = {("c2", "ldlq_trellis_block_gx_kernel", 16): 11197133,
-                    ("c5", "ldlq_trellis_groups_gx_kernel", 16): 262272589,
+MEASURED_TRAFFIC = {("c2", "ldlq_trellis_block_gx_kernel", 16): 10119877,
+                    ("c5", "ldlq_trellis_groups_gx_kernel", 16): 265452184,
                     ("c5", "ldlq_trellis_block_kernel", 12): 6285132}
 
 
