@@ -391,7 +391,7 @@ __global__ __launch_bounds__(256) void gemm64_panel_f64_kernel(double* C, int64_
 // a fixed order, (w0 + w1) + (w2 + w3), and subtracted from C once. A workgroup's operands are read once, with no
 // LDS staging, so a CU holds several workgroups (LDS 4 TM TN doubles each), and small tiles give a product of a few
 // thousand rows enough workgroups to fill the chip, where the 64-tile kernel's one workgroup per CU (its k-range in
-// LDS) left most CUs idle. Needs even K and lda and a 16-byte aligned A (the chunks condition of gemm_sub_f64).
+// LDS) left most CUs idle. Needs even K and lda and a 16-byte aligned A.
 #ifndef LAMQ_SPLITK_DEPTH
 #define LAMQ_SPLITK_DEPTH 2  // chunks of 8 k in flight per wave (measured: 2 beats 4 and 8)
 #endif
@@ -514,7 +514,9 @@ static int gemm_sub_f64(double* C, int64_t ldc, const double* A, int64_t lda, co
                         ((uintptr_t)A % 16) == 0 && ((uintptr_t)B % 16) == 0;
     const int64_t tiles128 = cdiv(M, G8_BM) * cdiv(N, G8_BM);
     dim3 grid((unsigned)cdiv(N, 64), (unsigned)cdiv(M, 64));
-    if (!TRANSB && !LOWER && !OVERWRITE && TRI == 0 && chunks && K <= LAMQ_SPLITK_MAXK && cdiv(M, 32) <= 65535) {
+    // the split-K kernel loads A in 16-byte pairs (even lda and K, a 16-byte aligned A) and B element by element
+    const bool pairs = (lda % 2) == 0 && (K % 2) == 0 && ((uintptr_t)A % 16) == 0;
+    if (!TRANSB && !LOWER && !OVERWRITE && TRI == 0 && pairs && K <= LAMQ_SPLITK_MAXK && cdiv(M, 32) <= 65535) {
         hipLaunchKernelGGL((gemm_splitk_f64_kernel<32, 32>), dim3((unsigned)cdiv(N, 32), (unsigned)cdiv(M, 32)), dim3(256),
                            0, s, C, ldc, A, lda, B, ldb, M, N, K, info);
         LAMQ_LAUNCH_CHECK();

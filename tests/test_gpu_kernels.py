@@ -156,7 +156,7 @@ def test_gemm_sub_triangular(E, M, N, K, transb, tri):
 
 @pytest.mark.parametrize("M,N,K,transb", [(2560, 384, 128, False), (300, 136, 128, True), (77, 190, 64, False),
                                            (130, 70, 64, True), (65, 66, 2, False), (200, 128, 100, True),
-                                           (19456, 256, 128, False)])
+                                           (203, 130, 100, False), (33, 31, 16, False), (19456, 256, 128, False)])
 def test_gemm_sub_short_k(E, M, N, K, transb):
     """Short products (K <= 128): with B as [k][col] (the sweep's narrow refits) on the split-K kernel (four waves, a
     quarter of the k-range each, partial tiles summed in LDS), with B as [col][k] (the factor's panels) on the 64-tile
