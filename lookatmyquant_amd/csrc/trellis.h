@@ -236,7 +236,8 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
     // wave unreachable at the next position skips the loads of its members' minima (it computes nothing there).
     bool dirty0 = true, dirty1 = true;
     bool live = wave_live(0);
-    for (int t = 0; t < TV - 1; ++t) {
+    // one step of the search, position t, reading minima buffer cur (written into cur ^ 1 with two buffers)
+    const auto step = [&](const int t, int& cur) {
         const float xn = xs[t + 1];
         const int base = (SKIP && st0 >= 0 && K * (t + 1) < L)
                              ? (int)(((uint32_t)st0 << (K * (t + 1))) & (uint32_t)(V::NS - 1)) : 0;
@@ -337,6 +338,23 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
             for (int h = 0; h < NB; ++h) lds_load_swz<M>(buf + (DBL ? cur * R : 0), ent[h], bv[h]);
         }
         if (!DBL) lds_barrier();
+    };
+    if constexpr (L <= 12 && DBL) {
+        // a step at L <= 12 is short: two steps per iteration, each with its buffer a constant (immediate LDS offsets
+        // instead of addresses formed every step)
+        int t = 0;
+        for (; t + 1 < TV - 1; t += 2) {
+            int c0 = 0, c1 = 1;
+            step(t, c0);
+            step(t + 1, c1);
+        }
+        if (t < TV - 1) {
+            int c0 = 0;
+            step(t, c0);
+        }
+        cur = (TV - 1) & 1;
+    } else {
+        for (int t = 0; t < TV - 1; ++t) step(t, cur);
     }
     hook();
     // final costs, the lowest state on ties (a thread's states increase with (h, g)); a wave with no reachable member
