@@ -71,7 +71,19 @@ __global__ __launch_bounds__(64 * R) void ldlq_scalar_block_kernel(const double*
     double t0 = lane < bw ? Tr[lane] : 0.0;
     double t1 = lane + 64 < bw ? Tr[lane + 64] : 0.0;
     const double Sr = MODE == 1 ? S[row] : 1.0;
+    // the U row a step uses (its diagonal and this lane's two columns) is read one step ahead, off the chain of
+    // dependent operations; entries left of the diagonal are read too (inside the staged triangle) and not used
+    const auto urow = [&](int c, double& ud, double& u0, double& u1) {
+        const double* Uj = ub + sc_tri(c) - c;  // Uj[col] = U[b0 + c][b0 + col] for col >= c
+        ud = Uj[c];
+        u0 = Uj[lane];
+        u1 = Uj[lane + 64];
+    };
+    double ud_n, u0_n, u1_n;
+    urow(0, ud_n, u0_n, u1_n);
     for (int c = 0; c < bw; ++c) {
+        const double ud = ud_n, u0 = u0_n, u1 = u1_n;
+        if (c + 1 < bw) urow(c + 1, ud_n, u0_n, u1_n);
         const double t = c < 64 ? readlane_f64(t0, c) : readlane_f64(t1, c - 64);
         int best = 0;
         double q;
@@ -126,14 +138,13 @@ __global__ __launch_bounds__(64 * R) void ldlq_scalar_block_kernel(const double*
             q = lv[best] * Sr;
         }
         const int64_t j = b0 + c;
-        const double* Uj = ub + sc_tri(c) - c;  // Uj[col] = U[b0 + c][b0 + col] for col >= c
-        const double zj = (t - q) / Uj[c];
+        const double zj = (t - q) / ud;
         if (lane > c && lane < bw) {
-            const double p = zj * Uj[lane];
+            const double p = zj * u0;
             t0 = t0 - p;
         }
         if (lane + 64 > c && lane + 64 < bw) {
-            const double p = zj * Uj[lane + 64];
+            const double p = zj * u1;
             t1 = t1 - p;
         }
         if (lane == (c & 63)) {
