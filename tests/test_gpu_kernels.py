@@ -86,6 +86,40 @@ def test_viterbi_big_tables_match_oracle(E, L, k):
     assert np.array_equal(free, O.viterbi(x[:2], tab, L, k))
 
 
+@pytest.mark.parametrize("k", [1, 2, 3, 4])
+def test_viterbi_L16_ties_match_oracle(E, k):
+    """A 16-bit-state table of three values (every state -1, 0 or 1) and targets on and between them: path costs
+    tie at every step, so every group's winner is decided by the lowest-h rule (the tournaments of k = 2, 3, 4 and the
+    strict compare of k = 1), against the oracle, whose tie rule brute force pins at small L. Fixed starts over 24
+    positions (back-pointers in LDS) and free starts over 40 (in the workspace)."""
+    rng = np.random.default_rng(160 + k)
+    tab = rng.choice([-1.0, 0.0, 1.0], 1 << 16)
+    x = rng.choice([-1.0, -0.5, 0.0, 0.25, 0.5, 1.0], (4, 40)).astype(np.float32)
+    st = rng.integers(0, 1 << 16, 4)
+    C = cuda(tab.astype(np.float32))
+    say(f"viterbi L=16 k={k}, three-valued table")
+    got = E.viterbi_rows(cuda(x[:, :24]), C, 16, k, start=cuda(st, torch.int32)).cpu().numpy()
+    assert np.array_equal(got, O.viterbi(x[:, :24], tab, 16, k, start=st))
+    free = E.viterbi_rows(cuda(x[:2]), C, 16, k).cpu().numpy()
+    assert np.array_equal(free, O.viterbi(x[:2], tab, 16, k))
+
+
+@pytest.mark.parametrize("k", [2, 3, 4])
+def test_ldlq_trellis_L16_ties_match_oracle(E, k):
+    """The fused 16-bit-state sweep with the three-valued table (ties at every step of every search), 3 rows x 160
+    columns, against the C oracle."""
+    rng = np.random.default_rng(170 + k)
+    m, n = 3, 160
+    Xa = rng.standard_normal((400, n))
+    _, U, _ = O.environment(Xa.T @ Xa / 400)
+    X = rng.standard_normal((m, n))
+    S = O.row_scale(X)
+    tab = rng.choice([-1.0, 0.0, 1.0], 1 << 16)
+    say(f"ldlq trellis L=16 k={k}, three-valued table")
+    st = E.ldlq_trellis(cuda(X), cuda(S), cuda(U), cuda(tab), 16, k).cpu().numpy()
+    assert np.array_equal(st, O.ldlq_trellis(X, U, S, tab, 16, k))
+
+
 def test_viterbi_L16_long_paths_use_workspace(E):
     from lookatmyquant_amd.tables import quantile_table
 
