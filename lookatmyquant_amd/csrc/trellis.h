@@ -88,8 +88,10 @@ template <class V>
 struct TabF16 {
     static_assert(V::G % 2 == 0, "members in pairs");
     uint32_t v[V::SPT / 2];
+    const uint16_t* src;  // the whole table (the one-wave ramp of a fixed start reads other threads' states there)
     __device__ __forceinline__ void load(const uint16_t* __restrict__ C16, int t)
     {
+        src = C16;
 #pragma unroll
         for (int h = 0; h < V::NB; ++h)
 #pragma unroll
@@ -122,6 +124,21 @@ __device__ __forceinline__ void uniform_switch(int v, F& f)
             f(IntC<I>{});
         else
             uniform_switch<I + 1, N>(v, f);
+    }
+}
+
+// The one-wave ramp of a fixed start (viterbi_gx): a lane's states at position t (the ancestors of its 2^LQ states at
+// position T0).
+template <int K, int T0, int LQ>
+constexpr int ramp_nts(int t) { return K * (T0 - t) >= LQ ? 1 : ((1 << LQ) >> (K * (T0 - t))); }
+
+// f(IntC<I>{}), f(IntC<I + 1>{}), ..., f(IntC<N - 1>{})
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F& f)
+{
+    if constexpr (I < N) {
+        f(IntC<I>{});
+        static_for<I + 1, N>(f);
     }
 }
 
@@ -190,13 +207,23 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
 #pragma unroll
     for (int h = 0; h < NB; ++h) ent[h] = V::RUN ? h * (R >> K) + M * tid : (h * R + G * tid) >> K;
     float bv[NB][M];
-    {
+    // ent[h] = ent[0] + h (R >> K); where that stride is a multiple of 256 the swizzle keeps it (swz(x + 256 i) =
+    // swz(x) + 256 i), so every h reads at one swizzled index plus a constant offset (one register, not NB)
+    constexpr bool EOFF = (R >> K) % 256 == 0;
+    const auto load_minima = [&](const float* b, int h) {
+        if constexpr (EOFF)
+            lds_load_swz<M>(b + h * (R >> K), ent[0], bv[h]);
+        else
+            lds_load_swz<M>(b, ent[h], bv[h]);
+    };
+    // the group minima before position 0: 0 for the start's group (every group with a free start), else +inf
+    const auto start_minima = [&]() {
         const int rs = start >= 0 ? (start & (R - 1)) : -1;
 #pragma unroll
         for (int h = 0; h < NB; ++h)
 #pragma unroll
             for (int e = 0; e < M; ++e) bv[h][e] = (rs < 0 || ent[h] + e == rs) ? 0.0f : __builtin_inff();
-    }
+    };
     int cur = 0;
     float x = xs[0];
     // From a given start state, position t reaches only the 2^(K (t+1)) states of one aligned range,
@@ -335,11 +362,12 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
         live = wave_live(t + 1);
         if (act && live) {
 #pragma unroll
-            for (int h = 0; h < NB; ++h) lds_load_swz<M>(buf + (DBL ? cur * R : 0), ent[h], bv[h]);
+            for (int h = 0; h < NB; ++h) load_minima(buf + (DBL ? cur * R : 0), h);
         }
         if (!DBL) lds_barrier();
     };
     if constexpr (L <= 12 && DBL) {
+        start_minima();
         // a step at L <= 12 is short: two steps per iteration, each with its buffer a constant (immediate LDS offsets
         // instead of addresses formed every step)
         int t = 0;
@@ -354,7 +382,106 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
         }
         cur = (TV - 1) & 1;
     } else {
-        for (int t = 0; t < TV - 1; ++t) step(t, cur);
+        int tb = 0;
+        if constexpr (SKIP && (K == 2 || K == 3)) {
+            // From a fixed start the first positions reach few states: position t the 2^(K (t+1)) states
+            // base_t + i (i < 2^(K (t+1))), base_t = (start << K (t+1)) mod 2^L, each with exactly one reachable
+            // predecessor, base_(t-1) + (i >> K). While that holds (one slab, K (t+1) <= L - K) the path cost of
+            // base_t + i is the cost of that predecessor plus (x_t - C)^2, the value the full step forms (the group
+            // minimum over one finite member is that member). Positions 0 .. T0 (at most 1,024 states at T0) are
+            // therefore taken by wave 0 alone, each lane following the ancestors of its Q states at T0
+            // (Q l .. Q l + Q - 1) with no exchange between lanes and no barrier, the table entries read from
+            // memory; it writes those states' costs as the group minima of position T0 and the back-pointer
+            // words of the groups each position reaches (winner hl = base_t >> (L - K) in every field, as the
+            // one-slab step writes them). Every other thread stores +inf into its own entries outside that range,
+            // so minima buffer 0 holds exactly the minima of position T0 and the steps go on from T0 + 1. For
+            // k = 2 and 3 (k = 2: positions 0-4, k = 3: 0-2); at k = 1 the second path costs the kernel spilled
+            // registers, at k = 4 it would replace two steps only.
+            constexpr int LS = 10 < L - K ? 10 : L - K;
+            constexpr int T0 = LS / K - 1;
+            constexpr int LQ = K * (T0 + 1) - 6;
+            constexpr int Q = 1 << LQ;
+            static_assert(LQ >= 2 && Q <= 16 && 64 * Q >= G && (1 << (K * (T0 + 1))) <= R, "one-wave ramp shape");
+            if (st0 >= 0 && T0 <= TV - 2) {
+                constexpr int SPAN = 64 * Q;
+                const uint32_t su = (uint32_t)st0;
+                const int rb = (int)((su << (K * (T0 + 1))) & (uint32_t)(R - 1));
+                if (act && !(G * tid >= rb && G * tid < rb + SPAN)) {
+                    constexpr int CKI = G < 4 ? G : 4;
+                    float infs[CKI];
+#pragma unroll
+                    for (int i = 0; i < CKI; ++i) infs[i] = __builtin_inff();
+#pragma unroll
+                    for (int e = 0; e < G / CKI; ++e) lds_store_swz<CKI>(buf, G * tid + e * CKI, infs);
+                }
+                if (tid < 64) {
+                    // the path costs of this lane's ancestors, position by position (at most Q / NB of them before
+                    // T0); position T0 in chunks of four states, each stored as soon as it is formed (few registers
+                    // live at once: the search loop's allocation is the kernel's)
+                    float cp[Q / NB > 0 ? Q / NB : 1];
+                    cp[0] = 0.0f;  // the start's group minimum
+                    const auto back_words = [&](int t, uint32_t base) {  // the owners of the groups t reaches
+                        const int span = 1 << (K * (t + 1));
+                        const int no = span >= G ? span / G : 1;
+                        const int olo = (int)(base & (uint32_t)(R - 1)) / G;
+                        if (tid < no) back[t * V::ACT + olo + tid] = (BackT)((base >> (L - K)) * REP);
+                    };
+                    const auto pos = [&](auto tc) {
+                        constexpr int t = decltype(tc)::value;
+                        constexpr int SH = K * (T0 - t);
+                        constexpr int NTS = ramp_nts<K, T0, LQ>(t);  // this lane's states at position t
+                        const uint32_t base = (su << (K * (t + 1))) & (uint32_t)(V::NS - 1);
+                        const uint16_t* c16 = tab.src + base + (((uint32_t)Q * (uint32_t)tid) >> SH);
+                        const float xt = xs[t];
+                        float cn[NTS];
+#pragma unroll
+                        for (int j = 0; j < NTS; j += 2) {
+                            const uint32_t w = NTS == 1 ? (uint32_t)c16[0] : *reinterpret_cast<const uint32_t*>(c16 + j);
+                            const float d0 = xmc_lo(xt, w);
+                            cn[j] = cp[j >> K] + d0 * d0;
+                            if (j + 1 < NTS) {
+                                const float d1 = xmc_hi(xt, w);
+                                cn[j + 1] = cp[(j + 1) >> K] + d1 * d1;
+                            }
+                        }
+#pragma unroll
+                        for (int j = 0; j < NTS; ++j) cp[j] = cn[j];
+                        back_words(t, base);
+                    };
+                    static_for<0, T0>(pos);
+                    {
+                        const uint32_t base = (su << (K * (T0 + 1))) & (uint32_t)(V::NS - 1);
+                        const uint16_t* c16 = tab.src + base + (uint32_t)Q * (uint32_t)tid;
+                        const float xt = xs[T0];
+#pragma unroll
+                        for (int c = 0; c < Q; c += 4) {
+                            const uint32_t w0 = *reinterpret_cast<const uint32_t*>(c16 + c);
+                            const uint32_t w1 = *reinterpret_cast<const uint32_t*>(c16 + c + 2);
+                            const float d[4] = {xmc_lo(xt, w0), xmc_hi(xt, w0), xmc_lo(xt, w1), xmc_hi(xt, w1)};
+                            float cn[4];
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) cn[j] = cp[(c + j) >> K] + d[j] * d[j];
+                            lds_store_swz<4>(buf, rb + Q * tid + c, cn);
+                        }
+                        back_words(T0, base);
+                    }
+                }
+                lds_barrier();
+                dirty0 = wave_live(T0);
+                dirty1 = true;
+                cur = 0;
+                x = xs[T0 + 1];
+                live = wave_live(T0 + 1);
+                if (act && live) {
+#pragma unroll
+                    for (int h = 0; h < NB; ++h) load_minima(buf, h);
+                }
+                if (!DBL) lds_barrier();
+                tb = T0 + 1;
+            }
+        }
+        if (tb == 0) start_minima();
+        for (int t = tb; t < TV - 1; ++t) step(t, cur);
     }
     hook();
     // final costs, the lowest state on ties (a thread's states increase with (h, g)); a wave with no reachable member
