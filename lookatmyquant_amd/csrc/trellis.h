@@ -179,6 +179,36 @@ __device__ __forceinline__ void wave_argmin(float& v, int& i)
     argmin_dpp<0x143, 0xC>(v, i);  // row_bcast31 into rows 2 and 3
 }
 
+// the minimum of the wave (float or int) by the same DPP moves; lane 63 ends up with it
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float fmin_dpp(float v)
+{
+    return fminf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROWS, 0xF, false)));
+}
+__device__ __forceinline__ float wave_min(float v)
+{
+    v = fmin_dpp<0xB1, 0xF>(v);
+    v = fmin_dpp<0x4E, 0xF>(v);
+    v = fmin_dpp<0x141, 0xF>(v);
+    v = fmin_dpp<0x140, 0xF>(v);
+    v = fmin_dpp<0x142, 0xA>(v);
+    return fmin_dpp<0x143, 0xC>(v);
+}
+template <int CTRL, int ROWS>
+__device__ __forceinline__ int imin_dpp(int v)
+{
+    return min(v, __builtin_amdgcn_update_dpp(v, v, CTRL, ROWS, 0xF, false));
+}
+__device__ __forceinline__ int wave_imin(int v)
+{
+    v = imin_dpp<0xB1, 0xF>(v);
+    v = imin_dpp<0x4E, 0xF>(v);
+    v = imin_dpp<0x141, 0xF>(v);
+    v = imin_dpp<0x140, 0xF>(v);
+    v = imin_dpp<0x142, 0xA>(v);
+    return imin_dpp<0x143, 0xC>(v);
+}
+
 // Search one path of TV steps. With PATHREG (TV <= 64) the path comes back in a register of wave 0, lane c holding
 // path[c] (the return value), and is also stored to path[0..TV) (LDS or global); otherwise lane 0 of wave 0 stores
 // path[] as the traceback goes and the return value is 0. Ends with a barrier after which path[] is complete.
@@ -219,10 +249,11 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
     // the group minima before position 0: 0 for the start's group (every group with a free start), else +inf
     const auto start_minima = [&]() {
         const int rs = start >= 0 ? (start & (R - 1)) : -1;
+        const int d = rs - ent[0];  // ent[h] + e == rs exactly when d == h (R >> K) + e
 #pragma unroll
         for (int h = 0; h < NB; ++h)
 #pragma unroll
-            for (int e = 0; e < M; ++e) bv[h][e] = (rs < 0 || ent[h] + e == rs) ? 0.0f : __builtin_inff();
+            for (int e = 0; e < M; ++e) bv[h][e] = (rs < 0 || d == h * (R >> K) + e) ? 0.0f : __builtin_inff();
     };
     int cur = 0;
     float x = xs[0];
@@ -415,6 +446,10 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
                     for (int e = 0; e < G / CKI; ++e) lds_store_swz<CKI>(buf, G * tid + e * CKI, infs);
                 }
                 if (tid < 64) {
+                    // the lane index through an opaque move: the addresses below are formed here, not hoisted out of
+                    // the caller's loop over searches (held across it, they would take registers the steps need)
+                    uint32_t ln = (uint32_t)tid;
+                    asm volatile("" : "+v"(ln));
                     // the path costs of this lane's ancestors, position by position (at most Q / NB of them before
                     // T0); position T0 in chunks of four states, each stored as soon as it is formed (few registers
                     // live at once: the search loop's allocation is the kernel's)
@@ -424,14 +459,14 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
                         const int span = 1 << (K * (t + 1));
                         const int no = span >= G ? span / G : 1;
                         const int olo = (int)(base & (uint32_t)(R - 1)) / G;
-                        if (tid < no) back[t * V::ACT + olo + tid] = (BackT)((base >> (L - K)) * REP);
+                        if ((int)ln < no) back[t * V::ACT + olo + (int)ln] = (BackT)((base >> (L - K)) * REP);
                     };
                     const auto pos = [&](auto tc) {
                         constexpr int t = decltype(tc)::value;
                         constexpr int SH = K * (T0 - t);
                         constexpr int NTS = ramp_nts<K, T0, LQ>(t);  // this lane's states at position t
                         const uint32_t base = (su << (K * (t + 1))) & (uint32_t)(V::NS - 1);
-                        const uint16_t* c16 = tab.src + base + (((uint32_t)Q * (uint32_t)tid) >> SH);
+                        const uint16_t* c16 = tab.src + base + (((uint32_t)Q * ln) >> SH);
                         const float xt = xs[t];
                         float cn[NTS];
 #pragma unroll
@@ -451,7 +486,7 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
                     static_for<0, T0>(pos);
                     {
                         const uint32_t base = (su << (K * (T0 + 1))) & (uint32_t)(V::NS - 1);
-                        const uint16_t* c16 = tab.src + base + (uint32_t)Q * (uint32_t)tid;
+                        const uint16_t* c16 = tab.src + base + (uint32_t)Q * ln;
                         const float xt = xs[T0];
 #pragma unroll
                         for (int c = 0; c < Q; c += 4) {
@@ -461,7 +496,7 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
                             float cn[4];
 #pragma unroll
                             for (int j = 0; j < 4; ++j) cn[j] = cp[(c + j) >> K] + d[j] * d[j];
-                            lds_store_swz<4>(buf, rb + Q * tid + c, cn);
+                            lds_store_swz<4>(buf, rb + Q * (int)ln + c, cn);
                         }
                         back_words(T0, base);
                     }
@@ -483,29 +518,76 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
         if (tb == 0) start_minima();
         for (int t = tb; t < TV - 1; ++t) step(t, cur);
     }
-    hook();
-    // final costs, the lowest state on ties (a thread's states increase with (h, g)); a wave with no reachable member
-    // there keeps +inf
-    float bvv = __builtin_inff();
-    int bi = 0x7fffffff;
-    if (act && live) {
-        tab.hold();
+    int* redi = reinterpret_cast<int*>(red + NT / 64);
+    constexpr bool TWOPASS = L > 12;  // (at L <= 12 a thread holds at most 16 states: one pass with the index)
+    if constexpr (TWOPASS) {
+        // final costs in two passes: the minimum of this thread's states (a v_min3 tree per h; a wave with no reachable
+        // member there keeps +inf) and the block's minimum M, then the lowest state attaining M, looked for only in the
+        // threads whose own minimum is M (typically one) and there only under the h whose minimum is M (NB <= 8)
+        constexpr bool KEEPH = NB <= 8;
+        float mh[KEEPH ? NB : 1];
+        float mine = __builtin_inff();
+        if (act && live) {
+            tab.hold();
 #pragma unroll
-        for (int h = 0; h < NB; ++h)
+            for (int h = 0; h < NB; ++h) {
+                float m = __builtin_inff();
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float c = bv[h][V::RUN ? (g >> K) : 0] + tab.dsq(x, h * G + g);
-                if ((h == 0 && g == 0) || c < bvv) {
-                    bvv = c;
-                    bi = h * R + G * tid + g;
+                for (int g = 0; g < G; ++g) m = fminf(m, bv[h][V::RUN ? (g >> K) : 0] + tab.dsq(x, h * G + g));
+                if constexpr (KEEPH) mh[h] = m;
+                mine = fminf(mine, m);
+            }
+        }
+        const float wmin = wave_min(mine);
+        if ((tid & 63) == 63) red[tid >> 6] = wmin;
+        hook();  // (after the first pass, whose registers the caller's loads would otherwise share)
+        lds_barrier();
+        float mb = red[0];
+#pragma unroll
+        for (int wv = 1; wv < NT / 64; ++wv) mb = fminf(mb, red[wv]);
+        int bi = 0x7fffffff;
+        if (act && live && mine == mb) {
+            tab.hold();
+            // x through an opaque move: the costs are formed again here, not kept from the first pass (64 registers)
+            float xo = x;
+            asm volatile("" : "+v"(xo));
+#pragma unroll
+            for (int h = 0; h < NB; ++h) {
+                if (bi == 0x7fffffff && (!KEEPH || mh[KEEPH ? h : 0] == mb)) {
+#pragma unroll
+                    for (int g = 0; g < G; ++g) {
+                        const float c = bv[h][V::RUN ? (g >> K) : 0] + tab.dsq(xo, h * G + g);
+                        bi = (c == mb && bi == 0x7fffffff) ? h * R + G * tid + g : bi;
+                    }
                 }
             }
-    }
-    wave_argmin(bvv, bi);
-    int* redi = reinterpret_cast<int*>(red + NT / 64);
-    if ((tid & 63) == 63) {
-        red[tid >> 6] = bvv;
-        redi[tid >> 6] = bi;
+        }
+        const int wbi = wave_imin(bi);
+        if ((tid & 63) == 63) redi[tid >> 6] = wbi;
+    } else {
+        hook();
+        // final costs, the lowest state on ties (a thread's states increase with (h, g)); a wave with no reachable
+        // member there keeps +inf
+        float bvv = __builtin_inff();
+        int bi = 0x7fffffff;
+        if (act && live) {
+            tab.hold();
+#pragma unroll
+            for (int h = 0; h < NB; ++h)
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const float c = bv[h][V::RUN ? (g >> K) : 0] + tab.dsq(x, h * G + g);
+                    if ((h == 0 && g == 0) || c < bvv) {
+                        bvv = c;
+                        bi = h * R + G * tid + g;
+                    }
+                }
+        }
+        wave_argmin(bvv, bi);
+        if ((tid & 63) == 63) {
+            red[tid >> 6] = bvv;
+            redi[tid >> 6] = bi;
+        }
     }
     if (BACK_GLOBAL)
         __syncthreads();
@@ -513,15 +595,20 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
         lds_barrier();
     int pathv = 0;
     if (tid < 64) {
-        // wave 0 traces back; every lane combines the waves' minima, so s is uniform
-        float v = red[0];
+        // wave 0 traces back; every lane combines the waves' results, so s is uniform
         int s = redi[0];
+        if constexpr (TWOPASS) {
 #pragma unroll
-        for (int wv = 1; wv < NT / 64; ++wv)
-            if (red[wv] < v || (red[wv] == v && redi[wv] < s)) {
-                v = red[wv];
-                s = redi[wv];
-            }
+            for (int wv = 1; wv < NT / 64; ++wv) s = min(s, redi[wv]);
+        } else {
+            float v = red[0];
+#pragma unroll
+            for (int wv = 1; wv < NT / 64; ++wv)
+                if (red[wv] < v || (red[wv] == v && redi[wv] < s)) {
+                    v = red[wv];
+                    s = redi[wv];
+                }
+        }
         s = __builtin_amdgcn_readfirstlane(s);
         const auto emit = [&](int c, int sc) {
             if (PATHREG)
