@@ -218,9 +218,10 @@ __device__ __forceinline__ int wave_imin(int v)
 //   back: (TV-1) * ACT entries (LDS or global), entry t*ACT + owner holding the winning h of each of the
 //   owner's groups for the step that produced B_{t+1}. red: 2*(NT/64) words of LDS.
 //   Final state: the lowest among the minimal costs (codes.py:173); traceback codes.py:176-179.
-// hook() runs once the forward pass is done (the caller's chance to issue loads that the final argmin and the
-// traceback then cover). BACK_GLOBAL: back-pointers in global memory, published to the tracing wave by a full
-// barrier (otherwise only LDS is ordered, and the caller's outstanding loads stay in flight).
+// hook() runs once the forward pass is done (the caller's chance to issue loads that the end of the final argmin and
+// the traceback then cover; at L > 12 after the argmin's two passes over the states). BACK_GLOBAL: back-pointers in
+// global memory, published to the tracing wave by a full barrier (otherwise only LDS is ordered, and the caller's
+// outstanding loads stay in flight).
 template <int L, int K, int NT, bool DBL, bool BACK_GLOBAL = false, bool PATHREG = false, typename BackT, class Tab,
           class Hook = NoHook>
 __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* buf, BackT* back, int* path, float* red,
@@ -540,7 +541,6 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
         }
         const float wmin = wave_min(mine);
         if ((tid & 63) == 63) red[tid >> 6] = wmin;
-        hook();  // (after the first pass, whose registers the caller's loads would otherwise share)
         lds_barrier();
         float mb = red[0];
 #pragma unroll
@@ -562,6 +562,7 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
                 }
             }
         }
+        hook();  // (after both passes, whose registers the caller's loads would otherwise share)
         const int wbi = wave_imin(bi);
         if ((tid & 63) == 63) redi[tid >> 6] = wbi;
     } else {
