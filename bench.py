@@ -57,9 +57,9 @@ VALU_ISSUE_TOPS = 256 * 4 * 16 * 2.4e9 / 1e12
 
 # HBM bytes per launch of the dominant kernel from two rocprofv3 counter runs (FETCH_SIZE, WRITE_SIZE), scaled by a
 # 1 GiB copy's readings; keyed by (workload, kernel, L)
-MEASURED_TRAFFIC = {("c2", "ldlq_trellis_block_gx_kernel", 16): 10119877,
-                    ("c5", "ldlq_trellis_groups_gx_kernel", 16): 265452184,
-                    ("c5", "ldlq_trellis_block_kernel", 12): 6285132}
+MEASURED_TRAFFIC = {("c2", "ldlq_trellis_block_gx_kernel", 16): 8965206,
+                    ("c5", "ldlq_trellis_groups_gx_kernel", 16): 303817646,
+                    ("c5", "ldlq_trellis_block_kernel", 12): 6301544}
 
 
 def kernel_line(ms: float, work: float, peak: float, unit: str, bound: str, scale: float, launches: int = 0) -> dict:
