@@ -499,6 +499,16 @@ __global__ __launch_bounds__(256) void gemm_splitk_f64_kernel(double* __restrict
 #ifndef LAMQ_SPLITK_MAXK
 #define LAMQ_SPLITK_MAXK 128  // [k][col] products up to this K (not LOWER, not OVERWRITE) take the split-K kernel
 #endif
+// Deeper [k][col] products (K <= LAMQ_SPLITK_DEEPK) take it too where the 128-tile kernel's workgroups would fill the
+// chip's 512 slots (two a CU) poorly: fewer than LAMQ_SPLITK_TILES128 tiles, or a second round holding under 64 of
+// them. Measured at K = 512 (the sweep's deep products): 20-80 tiles 5.7-17 -> 19-35 TFLOP/s, 300-320 tiles 35-38 ->
+// 44-46, 560 tiles 43 -> 47; at 384-480 and 608 tiles the two kernels are even or the 128-tile one is ahead.
+#ifndef LAMQ_SPLITK_TILES128
+#define LAMQ_SPLITK_TILES128 384
+#endif
+#ifndef LAMQ_SPLITK_DEEPK
+#define LAMQ_SPLITK_DEEPK 1024
+#endif
 
 // TRI (LAMQ_TRI_KGE, LAMQ_TRI_KLE): op(B) is triangular and the 128-tile kernel skips the stages of its zero part (the
 // other kernels read the zeros).
@@ -516,7 +526,9 @@ static int gemm_sub_f64(double* C, int64_t ldc, const double* A, int64_t lda, co
     dim3 grid((unsigned)cdiv(N, 64), (unsigned)cdiv(M, 64));
     // the split-K kernel loads A in 16-byte pairs (even lda and K, a 16-byte aligned A) and B element by element
     const bool pairs = (lda % 2) == 0 && (K % 2) == 0 && ((uintptr_t)A % 16) == 0;
-    if (!TRANSB && !LOWER && !OVERWRITE && TRI == 0 && pairs && K <= LAMQ_SPLITK_MAXK && cdiv(M, 32) <= 65535) {
+    const bool thin = tiles128 < LAMQ_SPLITK_TILES128 || (tiles128 > 512 && tiles128 < 1024 && tiles128 % 512 < 64);
+    if (!TRANSB && !LOWER && !OVERWRITE && TRI == 0 && pairs && cdiv(M, 32) <= 65535 &&
+        (K <= LAMQ_SPLITK_MAXK || (K <= LAMQ_SPLITK_DEEPK && thin))) {
         hipLaunchKernelGGL((gemm_splitk_f64_kernel<32, 32>), dim3((unsigned)cdiv(N, 32), (unsigned)cdiv(M, 32)), dim3(256),
                            0, s, C, ldc, A, lda, B, ldb, M, N, K, info);
         LAMQ_LAUNCH_CHECK();

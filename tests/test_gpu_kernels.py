@@ -212,10 +212,13 @@ def test_gemm_sub_short_k(E, M, N, K, transb):
 
 
 @pytest.mark.parametrize("M,N,K", [(2560, 9216, 512), (2560, 1536, 512), (6144, 1536, 512), (19456, 2048, 512),
-                                   (300, 1000, 136)])
+                                   (300, 1000, 136), (2560, 3584, 512), (2500, 700, 512), (77, 130, 1024),
+                                   (2560, 128, 512)])
 def test_gemm_sub_deep_rounds(E, M, N, K):
-    """The sweep's deep products (B as [k][col], K = 512 at the config-5 and config-3 stage shapes) on the LDS-staged
-    128-tile kernel, and a small one on the 64-tile kernel; against a float64 product on the GPU."""
+    """The sweep's deep products (B as [k][col], K = 512 at the config-5 and config-3 stage shapes): on the LDS-staged
+    128-tile kernel where its tiles fill the CUs' slots, on the split-K kernel where they would not (fewer than 384
+    tiles of 128, or 512 + under 64: 2560 x 1536, 2560 x 3584, ragged 2500 x 700 and 77 x 130 at K = 1024, the last
+    run's 2560 x 128); against a float64 product on the GPU."""
     g = torch.Generator(device="cuda").manual_seed(M + 5 * N + 11 * K)
     C = torch.randn(M, N, generator=g, device="cuda", dtype=torch.float64)
     A = torch.randn(M, K, generator=g, device="cuda", dtype=torch.float64)
