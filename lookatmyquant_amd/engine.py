@@ -91,6 +91,19 @@ def rht_rows(X: torch.Tensor, seed: int, inverse: bool = False, want_rms: bool =
     return (y, rms) if want_rms else y
 
 
+def rht_flops(rows: int, n: int) -> float:
+    """Algorithmic fp64 work of rht_rows over `rows` rows of width n: the two Kronecker factors' products, 2n(a + b)
+    flops a row (a x b = n)."""
+    a, b = _factor_sizes(n)
+    return 2.0 * rows * n * (a + b)
+
+
+@lru_cache(maxsize=64)
+def _factor_sizes(n: int) -> tuple:
+    A, B = hadamard_factors(n)
+    return A.shape[0], B.shape[0]
+
+
 def row_rms(X: torch.Tensor) -> torch.Tensor:
     """S_r = max(sqrt(mean_j X_rj^2), 1e-12) (codes.py:436)."""
     need(X, torch.float64, "X", 2)

@@ -254,12 +254,12 @@ def stage_statistics(Xq_chunks, w_chunks=None, Xr_chunks=None):
 
 def stage_factor(H: torch.Tensor, in_seed: int, damp: float = 0.01, timer: E.KernelTimer | None = None):
     """The stage's factor as quantize_stage_row_groups makes it: (U, dead, info) of the rotated, damped H (no host
-    synchronisation: info is a device value, 0 when positive definite). timer: spans "rht" (the rotation's HBM
-    bytes, 3 passes of 16 n^2) and "chol" (4n^3/3 flops)."""
+    synchronisation: info is a device value, 0 when positive definite). timer: spans "rht" (R H R^T: two
+    passes of rht_rows, 2n(a + b) flops a row, and a transpose) and "chol" (4n^3/3 flops)."""
     dev = E._abi.device()
     Hg = torch.as_tensor(H).to(dev, torch.float64).contiguous()
     n = Hg.shape[0]
-    with E.span(timer, "rht", 48.0 * n * n):
+    with E.span(timer, "rht", 2.0 * E.rht_flops(n, n)):
         Hr = E.rotate_hessian(Hg, in_seed)
     with E.span(timer, "chol", 4.0 * n ** 3 / 3):
         _, U, dead, info = E.chol_inv_upper(Hr, damp=damp, raise_on_fail=False)
@@ -279,7 +279,7 @@ def quantize_stage_row_groups(targets: dict, groups: dict, H: torch.Tensor, in_s
     Environment's damping fraction (frame.py:521). factor: stage_factor(H, in_seed, damp), if the caller has made it
     already (for instance on another stream, next to other work); a non-positive-definite factor raises. timer: an
     engine.KernelTimer; every launch of the sweep is timed on this stream (one stream for all groups) under "block" and
-    "trailing", the row rotations under "rht" (16 m n bytes), and the factor as in stage_factor."""
+    "trailing", the row rotations under "rht" (2n(a + b) flops a row), and the factor as in stage_factor."""
     names = list(targets)
     stage_tables = {}  # the table of each width, resolved before any device work
     for bits in sorted({int(g["bits"]) for nm in names for g in groups[nm]}):
@@ -315,7 +315,7 @@ def quantize_stage_row_groups(targets: dict, groups: dict, H: torch.Tensor, in_s
     X_all, S_all = {}, {}
     for nm in names:
         W = torch.as_tensor(targets[nm]).to(dev, torch.float64).contiguous()
-        with E.span(timer, "rht", 16.0 * W.numel()):
+        with E.span(timer, "rht", E.rht_flops(W.shape[0], W.shape[1])):
             X_all[nm], S_all[nm] = E.rht_rows(W, in_seed, want_rms=True)
     # rows of one width across the stage's matrices go through one sweep
     by_bits: dict = {}

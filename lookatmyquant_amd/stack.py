@@ -229,6 +229,13 @@ class StackBuild:
     def program(self, i: int, nm: str) -> str:
         return self.plan["linears"][f"{i}.{nm}"]
 
+    def device_tables(self) -> dict:
+        """The trellis tables as float64 tensors on the device, made once."""
+        if getattr(self, "_dtables", None) is None:
+            self._dtables = {b: torch.as_tensor(np.asarray(t, dtype=np.float64)).to(self.dev)
+                             for b, t in self.tables.items()}
+        return self._dtables
+
     def groups(self, i: int, nm: str) -> list:
         """The row groups of a trellis matrix: its row-plan entry, else one group at its program's width."""
         g = self.row_plan.get(f"model.layers.{i}.{nm}.weight")
@@ -337,7 +344,7 @@ class StackBuild:
         res = {}
         if trellis:
             res = quantize_stage_row_groups({nm: targets[nm] for nm in trellis}, plans, H, in_seed, L=L,
-                                            tables=self.tables, factor=factor, timer=kt)
+                                            tables=self.device_tables(), factor=factor, timer=kt)
             if kt is not None:  # the sweep's algorithmic work: trellis ops and trailing-update flops per width
                 n = shapes[trellis[0]][1]
                 steps = sum(E.trellis_row_steps(n))
@@ -352,8 +359,10 @@ class StackBuild:
         for nm in trellis:
             st, Srow = res[nm]
             m, n = st.shape
-            with E.span(kt, "rht", 16.0 * m * n):
-                wq[nm] = _reconstruct(st, Srow, plans[nm], self.tables, in_seed).to(torch.bfloat16)
+            Q = _decode(st, Srow, plans[nm], self.device_tables())
+            with E.span(kt, "rht", E.rht_flops(m, n)):
+                Wh = E.rht_rows(Q, in_seed, inverse=True)
+            wq[nm] = Wh.to(torch.bfloat16)
             packed = []
             for gp in plans[nm]:
                 rows = torch.as_tensor(gp["rows"], dtype=torch.int64, device=dev)
@@ -517,15 +526,25 @@ def _stage_statistics(xq: list, w: list | None, xr: list | None, classes: list |
     return E.hessian_finalize(H, float(ntok)), None if D is None else (D / ntok).double()
 
 
-def _reconstruct(states: torch.Tensor, S: torch.Tensor, groups: list, tables: dict, in_seed: int) -> torch.Tensor:
-    """W_hat = diag(S) table[states] R_in (codes.py:413-462 with out_rot=False), row group by row group."""
+def _decode(states: torch.Tensor, S: torch.Tensor, groups: list, tables: dict) -> torch.Tensor:
+    """diag(S) table[states], each row through its group's table: tables {bits: float64 table on the device}. The
+    tables are read as one concatenation, each row's states offset to its width's table, in one gather."""
     dev = states.device
-    Q = torch.empty(states.shape, dtype=torch.float64, device=dev)
+    widths = sorted(tables)
+    cat = torch.cat([tables[b] for b in widths])
+    size = tables[widths[0]].numel()
+    base = torch.empty(states.shape[0], dtype=torch.int64)
     for gp in groups:
-        rows = torch.as_tensor(gp["rows"], device=dev)
-        tab = torch.tensor(np.asarray(tables[gp["bits"]], dtype=np.float64), device=dev)
-        Q.index_copy_(0, rows, tab[states.index_select(0, rows).long()] * S.index_select(0, rows)[:, None])
-    return E.rht_rows(Q, in_seed, inverse=True)
+        base[np.asarray(gp["rows"], dtype=np.int64)] = widths.index(int(gp["bits"])) * size
+    base = base.to(dev, non_blocking=True)
+    return cat[states.long() + base[:, None]] * S[:, None]
+
+
+def _reconstruct(states: torch.Tensor, S: torch.Tensor, groups: list, tables: dict, in_seed: int) -> torch.Tensor:
+    """W_hat = diag(S) table[states] R_in (codes.py:413-462 with out_rot=False)."""
+    dev = states.device
+    dt = {b: torch.as_tensor(np.asarray(t, dtype=np.float64)).to(dev) for b, t in tables.items()}
+    return E.rht_rows(_decode(states, S, groups, dt), in_seed, inverse=True)
 
 
 def calibration_tokens(sequences: int = 32, T: int = 2048, vocab: int = 151936, seed: int = 501, digit_share: float = 0.1,
