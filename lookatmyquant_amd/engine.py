@@ -254,8 +254,11 @@ def ldlq_trellis_groups(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, group
     # rows in one grid, so no group's launch ends in a tail of idle CUs and no stream per group is needed
     merged = None
     if L >= BIG_L and len(parts) > 1:
+        # the grid takes the groups in the table's order, widest first: the costliest rows are dispatched first, so
+        # the launch ends on its cheapest rows (a shorter tail of partly idle CUs); rows are independent, so the
+        # order changes no result
         merged = (_abi.TrellisGroup * len(parts))()
-        for i, (r0, rows, k, table64, t32) in enumerate(parts):
+        for i, (r0, rows, k, table64, t32) in enumerate(sorted(parts, key=lambda p: -p[2])):
             w = ws.get(r0)
             merged[i] = _abi.TrellisGroup(r0, rows, k, table64.data_ptr(), t32.data_ptr(),
                                           None if w is None else w.data_ptr(), 0 if w is None else w.numel())
