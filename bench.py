@@ -618,6 +618,7 @@ def run_c3(args):
     torch.cuda.synchronize()
     setup_s = time.perf_counter() - t0
     stages = [({"gate": Wg, "up": Wu}, X1, 1301), ({"down": Wd}, X2, 3301)]  # in_seed of layer 0's stages
+    plan_rows = {nm: E.device_rows(p, dev) for nm, p in plans.items()}
 
     def step(kt):
         """One build of the block. kt None: the production schedule (each row group's sweep on its own stream); a
@@ -631,8 +632,7 @@ def run_c3(args):
             res = quantize_stage_row_groups(sub, {nm: plans[nm] for nm in sub}, H, in_seed, L=L, tables=tables,
                                             timer=kt)
             for nm, (st, S) in res.items():
-                for g in plans[nm]:
-                    rows = torch.as_tensor(g["rows"], device=dev)
+                for g, rows in zip(plans[nm], plan_rows[nm]):
                     out[(nm, g["group"])] = E.pack_trellis(st.index_select(0, rows).contiguous(), g["bits"], L,
                                                            check_paths=False)
         return out

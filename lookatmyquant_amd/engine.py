@@ -8,6 +8,7 @@ import contextlib
 import ctypes
 from functools import lru_cache
 
+import numpy as np
 import torch
 
 from . import _abi
@@ -89,6 +90,16 @@ def rht_rows(X: torch.Tensor, seed: int, inverse: bool = False, want_rms: bool =
     check(lib().lamq_rht_rows(ptr(X), rows, n, ld(X), ptr(y), ld(y), ptr(s), ptr(A), A.shape[0], ptr(B), B.shape[0],
                               1 if inverse else 0, ptr(rms), stream(X.device)), "rht_rows")
     return (y, rms) if want_rms else y
+
+
+def device_rows(groups: list, dev) -> list:
+    """Each row group's row indices ({"rows": [...]}) as an int64 tensor on the device, through one pinned buffer
+    and one asynchronous copy: no per-group upload that would make the host wait for the stream."""
+    sizes = [len(g["rows"]) for g in groups]
+    host = torch.empty(sum(sizes), dtype=torch.int64, pin_memory=True)
+    if sizes and sum(sizes):
+        host.numpy()[:] = np.concatenate([np.asarray(g["rows"], dtype=np.int64).reshape(-1) for g in groups])
+    return list(torch.split(host.to(dev, non_blocking=True), sizes))
 
 
 def rht_flops(rows: int, n: int) -> float:

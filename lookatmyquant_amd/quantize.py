@@ -320,8 +320,8 @@ def quantize_stage_row_groups(targets: dict, groups: dict, H: torch.Tensor, in_s
     # rows of one width across the stage's matrices go through one sweep
     by_bits: dict = {}
     for nm in names:
-        for g in groups[nm]:
-            by_bits.setdefault(int(g["bits"]), []).append((nm, torch.as_tensor(g["rows"], dtype=torch.long)))
+        for g, r in zip(groups[nm], E.device_rows(groups[nm], dev)):
+            by_bits.setdefault(int(g["bits"]), []).append((nm, r))
     # all of the stage's rows go through one sweep: the block kernel runs width by width on consecutive row
     # groups, and each trailing update covers every row at once
     out = {nm: torch.empty(X_all[nm].shape, dtype=torch.int32, device=dev) for nm in names}
@@ -330,7 +330,7 @@ def quantize_stage_row_groups(targets: dict, groups: dict, H: torch.Tensor, in_s
         table = stage_tables[bits]
         rows = 0
         for nm, r in parts:
-            idx.append((nm, r.to(dev)))
+            idx.append((nm, r))
             rows += len(r)
         sweep_groups.append((rows, bits, table.to(dev), None))
     X = torch.cat([X_all[nm].index_select(0, r) for nm, r in idx])

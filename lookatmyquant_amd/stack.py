@@ -364,8 +364,7 @@ class StackBuild:
                 Wh = E.rht_rows(Q, in_seed, inverse=True)
             wq[nm] = Wh.to(torch.bfloat16)
             packed = []
-            for gp in plans[nm]:
-                rows = torch.as_tensor(gp["rows"], dtype=torch.int64, device=dev)
+            for gp, rows in zip(plans[nm], E.device_rows(plans[nm], dev)):
                 r = len(gp["rows"])
                 with E.span(kt, "pack", 4.0 * r * n + 4.0 * r * ((n + 31) // 32) * gp["bits"]):
                     packed.append(E.pack_codes(st, gp["bits"], rows=rows, L=L, bad=self.bad)[0])
@@ -533,9 +532,9 @@ def _decode(states: torch.Tensor, S: torch.Tensor, groups: list, tables: dict) -
     widths = sorted(tables)
     cat = torch.cat([tables[b] for b in widths])
     size = tables[widths[0]].numel()
-    base = torch.empty(states.shape[0], dtype=torch.int64)
+    base = torch.empty(states.shape[0], dtype=torch.int64, pin_memory=True)
     for gp in groups:
-        base[np.asarray(gp["rows"], dtype=np.int64)] = widths.index(int(gp["bits"])) * size
+        base.numpy()[np.asarray(gp["rows"], dtype=np.int64)] = widths.index(int(gp["bits"])) * size
     base = base.to(dev, non_blocking=True)
     return cat[states.long() + base[:, None]] * S[:, None]
 
