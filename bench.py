@@ -260,7 +260,7 @@ def run_c5(args):
     torch.cuda.synchronize()
     kt.events.clear()
     kt.work.clear()
-    timer.t.clear()
+    timer.clear()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         b.layer()

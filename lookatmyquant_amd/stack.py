@@ -16,7 +16,6 @@ the statistics, factors, rotations and sweeps on this package's kernels.
 
 from __future__ import annotations
 
-import time
 from dataclasses import dataclass
 
 import numpy as np
@@ -137,11 +136,31 @@ def _flat(x: torch.Tensor) -> torch.Tensor:
 
 
 class Timer:
-    def __init__(self):
-        self.t = {}
+    """Seconds per phase of the build, from events recorded on the current stream at the phase boundaries: the GPU
+    time from one boundary to the next, with no host synchronisation in the build (the events are read when `t` is)."""
 
-    def add(self, key, s):
-        self.t[key] = self.t.get(key, 0.0) + s
+    def __init__(self):
+        self._spans, self._t = [], {}
+
+    @staticmethod
+    def mark() -> torch.cuda.Event:
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        return e
+
+    def add(self, key: str, start: torch.cuda.Event, end: torch.cuda.Event):
+        self._spans.append((key, start, end))
+
+    @property
+    def t(self) -> dict:
+        for key, a, b in self._spans:
+            b.synchronize()
+            self._t[key] = self._t.get(key, 0.0) + a.elapsed_time(b) / 1e3
+        self._spans = []
+        return self._t
+
+    def clear(self):
+        self._spans, self._t = [], {}
 
 
 def synthetic_plans(sh: Shape, layers: int, plan_seed: int = 7000, program: str = "tr2x"):
@@ -251,7 +270,7 @@ class StackBuild:
         if i >= self.layers:
             raise ValueError(f"the stack has {self.layers} layers")
         sh, dev, timer = self.sh, self.dev, self.timer
-        t0 = time.perf_counter()
+        t0 = timer.mark()
         wr = layer_weights(i, sh, dev, self.weight_seed)  # the reference layer
         wq = {k: v.clone() for k, v in wr.items()}  # quantized in place, stage by stage
         # the reference stream's stage inputs (its weights never change) and its output
@@ -266,14 +285,13 @@ class StackBuild:
             hr_next.append(h1 + _lin(m, wr["mlp.down_proj"]))
             for s, x in enumerate((x1, a, x2, m)):
                 xr[s].append(_flat(x))
-        torch.cuda.synchronize()
-        timer.add("forward", time.perf_counter() - t0)
+        timer.add("forward", t0, timer.mark())
         # the quantized stream, stage by stage
         hq = self.hq
         h1q = [None] * len(hq)
         x2q = [None] * len(hq)
         for s, names in enumerate(STAGES):
-            t1 = time.perf_counter()
+            t1 = timer.mark()
             if s == 0:
                 xq = x1q = [rms_norm(h, wq["input_layernorm"], sh.eps) for h in hq]
             elif s == 1:
@@ -284,19 +302,16 @@ class StackBuild:
             else:
                 xq = [torch.nn.functional.silu(_lin(x, wq["mlp.gate_proj"])) * _lin(x, wq["mlp.up_proj"]) for x in x2q]
             xqf = [_flat(x) for x in xq]
-            torch.cuda.synchronize()
-            t2 = time.perf_counter()
-            timer.add("forward", t2 - t1)
+            timer.add("forward", t1, timer.mark())
             self._stage(i, s, names, xqf, xr[s], wr, wq)
             del xq, xqf
         # both streams through the layer (the quantized one with its last matrix now quantized)
-        t4 = time.perf_counter()
+        t4 = timer.mark()
         self.hq = [h1 + _lin(torch.nn.functional.silu(_lin(x, wq["mlp.gate_proj"])) * _lin(x, wq["mlp.up_proj"]),
                              wq["mlp.down_proj"]) for h1, x in zip(h1q, x2q)]
         self.hr = hr_next
         del xr, wr, wq, h1q, x2q
-        torch.cuda.synchronize()
-        timer.add("forward", time.perf_counter() - t4)
+        timer.add("forward", t4, timer.mark())
         self.next_layer = i + 1
         return i
 
@@ -311,13 +326,12 @@ class StackBuild:
                 self.bits += 16.0 * shapes[nm][0] * shapes[nm][1]
         if not coded:
             return
-        t2 = time.perf_counter()
+        t2 = timer.mark()
         kt = self.kernels
         cross = [nm for nm in coded if parse(progs[nm])[2]]
         H, D = _stage_statistics(xqf, self.wt, xrf if cross else None, self.wcls, kt)
-        torch.cuda.synchronize()
-        t25 = time.perf_counter()
-        timer.add("statistics", t25 - t2)
+        t25 = timer.mark()
+        timer.add("statistics", t2, t25)
         _, in_seed = matrix_seeds(i, names[0], 0, names[0], self.seed_set)
         if kt is None:
             # the stage's factor (rotation of H, damped inverse factor) on a second stream, next to the QEP targets
@@ -335,9 +349,8 @@ class StackBuild:
             self.main.wait_stream(self.side)
             for t in factor:
                 t.record_stream(self.main)
-        torch.cuda.synchronize()
-        t3 = time.perf_counter()
-        timer.add("qep_targets", t3 - t25)
+        t3 = timer.mark()
+        timer.add("qep_targets", t25, t3)
         trellis = [nm for nm in coded if parse(progs[nm])[0] == "tr"]
         plans = {nm: self.groups(i, nm) for nm in trellis}
         factor = self._factor(H, in_seed, factor, f"{i}.{names[0]}")
@@ -385,8 +398,7 @@ class StackBuild:
                                        "levels": levels, "packed": [E.pack_codes(idx, b, trellis=False, bad=self.bad)[0]]}
             self.bits += m * n * b + 16 * m
             self.n_w += m * n
-        torch.cuda.synchronize()
-        timer.add("quantize", time.perf_counter() - t3)
+        timer.add("quantize", t3, timer.mark())
 
     def _factor(self, H, in_seed, factor, key):
         """The stage factor at the Environment's damping; with redamp, x10 and x100 more where that is not positive
