@@ -1,0 +1,183 @@
+// Causal grouped-query attention of the calibration forwards, fused: the score matrix never reaches memory.
+//
+// One workgroup per (sequence, head, block of 128 queries); its four waves take 32 queries each and walk the key
+// blocks of 32 up to their own diagonal, independently (no barrier: a wave stops where its queries end). Per key
+// block a wave forms S^T = K Q^T (32 keys x 32 queries: the head dim, 128, as eight 16-deep steps of
+// v_mfma_f32_32x32x16_bf16, float32 sums), masks it causally, updates each query's running maximum and sum (the
+// online softmax: exp2 with the scale and log2(e) folded into the scores), rounds the probabilities to bf16 and
+// accumulates O^T += V^T P^T (128 x 32, float32) with the earlier sums rescaled. At the end O = O^T / sum, rounded
+// to bf16 (nearest, ties to even).
+//
+// Operand layouts (32x32x16 bf16 MFMA): A[m][k] has lane l holding m = l % 32 and k = 8 (l / 32) .. + 7; B[k][n]
+// has lane l holding n = l % 32 and the same k; the result has lane l holding column l % 32 and rows
+// 8 (v / 4) + 4 (l / 32) + v % 4 of register v. So S^T's result is P^T's B operand as it stands, with its k order
+// (keys {0-3, 8-11} in lanes 0-31 and {4-7, 12-15} in lanes 32-63 for the first 16 keys, +16 for the second): the
+// V^T operand takes the same order, as two transposing LDS reads (ds_read_b64_tr_b16: a 16-lane group reads a 4 x 16
+// block, lane i receiving the four rows of column i) of four consecutive keys each. Q's fragments (B of S^T: eight
+// consecutive head-dim values of one query) stay in registers; K's (A of S^T) come straight from memory as 16-byte
+// loads. Each wave keeps its own copy of the key block's V rows in LDS: 256-byte rows whose 16-byte chunks are
+// XOR-swizzled by 4 (row & 3), so the 32 lanes a transposing read serves at once touch 16 different chunks of four
+// rows (all 64 banks once).
+#include "common.h"
+
+typedef __bf16 lamq_at_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float lamq_at_f32x16 __attribute__((ext_vector_type(16)));
+
+#define AT_D 128   // head dim
+#define AT_QW 32   // queries per wave
+#define AT_KB 32   // keys per block
+#define AT_QB 128  // queries per workgroup
+
+__device__ __forceinline__ uint32_t at_sw(int row, int chunk)
+{
+    return (uint32_t)(row * (AT_D * 2) + ((chunk ^ (4 * (row & 3))) << 4));
+}
+
+__global__ __launch_bounds__(256) void attention_causal_kernel(
+    const uint16_t* __restrict__ Q, int64_t sqb, int64_t sqh, int64_t sqt, const uint16_t* __restrict__ K,
+    int64_t skb, int64_t skh, int64_t skt, const uint16_t* __restrict__ V, int64_t svb, int64_t svh, int64_t svt,
+    uint16_t* __restrict__ O, int64_t sob, int64_t soh, int64_t sot, int rep, int T, float scale_log2)
+{
+    __shared__ __align__(16) uint8_t lds[4][AT_KB * AT_D * 2];
+    const int nqb = (T + AT_QB - 1) / AT_QB;
+    const int qb = nqb - 1 - (int)blockIdx.x;  // the longest query blocks first
+    const int h = (int)blockIdx.y, b = (int)blockIdx.z;
+    const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
+    const int q0 = qb * AT_QB + AT_QW * wave;
+    if (q0 >= T) return;  // the whole wave
+    const int li = lane & 31, hi = lane >> 5, g = lane >> 4, i16 = lane & 15;
+    const uint16_t* Qp = Q + b * sqb + (int64_t)h * sqh;
+    const uint16_t* Kp = K + b * skb + (int64_t)(h / rep) * skh;
+    const uint16_t* Vp = V + b * svb + (int64_t)(h / rep) * svh;
+    const int myq = q0 + li;  // this lane's query (past T: computed, not stored)
+    const int qrow = myq < T ? myq : T - 1;
+    lamq_at_bf16x8 qf[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qf[j] = *reinterpret_cast<const lamq_at_bf16x8*>(Qp + qrow * sqt + 16 * j + 8 * hi);
+    lamq_at_f32x16 o[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[t][v] = 0.0f;
+    float mrun = -__builtin_inff(), lrun = 0.0f;
+    const int last = (q0 + AT_QW < T ? q0 + AT_QW : T) - 1;  // the wave's last query
+    const int nkb = last / AT_KB + 1;
+    uint8_t* vl = lds[wave];
+    const uint32_t vbase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)vl;
+    using v2u = uint32_t __attribute__((ext_vector_type(2)));
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int k0 = kb * AT_KB;
+        // K fragments (A of S^T): key k0 + li, head dims 16 j + 8 hi .. + 7; V rows: chunk c = lane + 64 i is row
+        // c / 16, 16-byte chunk c % 16 (rows past T read row T - 1: finite values that meet zero probabilities)
+        const int krow = k0 + li < T ? k0 + li : T - 1;
+        lamq_at_bf16x8 kf[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) kf[j] = *reinterpret_cast<const lamq_at_bf16x8*>(Kp + krow * skt + 16 * j + 8 * hi);
+        uint4 vr[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int c = lane + 64 * i, r = c >> 4;
+            const int row = k0 + r < T ? k0 + r : T - 1;
+            vr[i] = *reinterpret_cast<const uint4*>(Vp + row * svt + 8 * (c & 15));
+        }
+        lamq_at_f32x16 s;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) s[v] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[j], qf[j], s, 0, 0, 0);
+        // causal mask, scale, the running maximum of each query (its 32 keys: 16 here, 16 in lane l ^ 32)
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int key = k0 + 8 * (v >> 2) + 4 * hi + (v & 3);
+            const float x = (key <= myq && key < T) ? s[v] * scale_log2 : -__builtin_inff();
+            s[v] = x;
+            mx = fmaxf(mx, x);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mnew = fmaxf(mrun, mx);  // finite from the first block on: key 0 is never masked
+        const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);  // 0 on the first block
+        float ps = 0.0f;
+        lamq_at_bf16x8 pf[2];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const float p = __builtin_amdgcn_exp2f(s[v] - mnew);  // masked: exp2(-inf) = 0
+            ps += p;
+            pf[v >> 3][v & 7] = (__bf16)p;
+        }
+        ps += __shfl_xor(ps, 32);
+        lrun = lrun * alpha + ps;
+        mrun = mnew;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) o[t][v] *= alpha;
+        // the block's V rows into this wave's LDS copy; the wave's own reads below come after them in order
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int c = lane + 64 * i;
+            *reinterpret_cast<uint4*>(vl + at_sw(c >> 4, c & 15)) = vr[i];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi) {
+                // lane: head dim 32 t + li; keys 16 mi + 4 hi + {0..3} and + 8 (the P^T order); the group's lane i16
+                // points at row 16 mi + 4 hi + i16 / 4, columns 32 t + 16 (g & 1) + 4 (i16 % 4) .. + 3
+                const int row = 16 * mi + 4 * hi + (i16 >> 2);
+                const int col = 32 * t + 16 * (g & 1) + 4 * (i16 & 3);
+                const uint32_t a0 = vbase + at_sw(row, col >> 3) + 8 * ((col >> 2) & 1);
+                const uint32_t a1 = vbase + at_sw(row + 8, col >> 3) + 8 * ((col >> 2) & 1);
+                v2u lo, hi2;
+                asm volatile("ds_read_b64_tr_b16 %0, %2\n\tds_read_b64_tr_b16 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+                             : "=v"(lo), "=v"(hi2)
+                             : "v"(a0), "v"(a1)
+                             : "memory");
+                const uint32_t __attribute__((ext_vector_type(4))) w = {lo[0], lo[1], hi2[0], hi2[1]};
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(lamq_at_bf16x8, w), pf[mi], o[t], 0, 0,
+                                                               0);
+            }
+        // the next block rewrites the LDS copy: every read of this one has returned (waited above)
+    }
+    if (myq >= T) return;
+    const float inv = 1.0f / lrun;
+    uint16_t* Op = O + b * sob + (int64_t)h * soh + (int64_t)myq * sot;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            // registers 4 r .. 4 r + 3: head dims 32 t + 8 r + 4 hi + {0..3}
+            uint32_t w2[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const __bf16 x0 = (__bf16)(o[t][4 * r + 2 * e] * inv), x1 = (__bf16)(o[t][4 * r + 2 * e + 1] * inv);
+                w2[e] = (uint32_t)__builtin_bit_cast(uint16_t, x0) | ((uint32_t)__builtin_bit_cast(uint16_t, x1) << 16);
+            }
+            *reinterpret_cast<uint2*>(Op + 32 * t + 8 * r + 4 * hi) = make_uint2(w2[0], w2[1]);
+        }
+}
+
+// out[b, t, h, :] = softmax(q[b, h, t, :] k[b, h / rep, :t + 1, :]^T * scale) v[b, h / rep, :t + 1, :], bf16 in and out;
+// every tensor's head dim (128) contiguous, the other strides in elements.
+extern "C" int lamq_attention_causal_bf16(const uint16_t* q, int64_t sqb, int64_t sqh, int64_t sqt, const uint16_t* k,
+                                          int64_t skb, int64_t skh, int64_t skt, const uint16_t* v, int64_t svb,
+                                          int64_t svh, int64_t svt, uint16_t* out, int64_t sob, int64_t soh,
+                                          int64_t sot, int64_t B, int64_t H, int64_t Hkv, int64_t T, int64_t D,
+                                          float scale, void* stream)
+{
+    if (!q || !k || !v || !out || B < 0 || H < 1 || Hkv < 1 || T < 0 || H % Hkv != 0) return LAMQ_EINVAL;
+    if (D != AT_D) return LAMQ_EUNSUP;
+    if (!(scale > 0.0f) || !(scale < 3.0e38f)) return LAMQ_EINVAL;
+    const int64_t strides[12] = {sqb, sqh, sqt, skb, skh, skt, svb, svh, svt, sob, soh, sot};
+    for (int64_t s : strides)
+        if (s < 0 || s % 8 != 0) return LAMQ_EINVAL;  // 16-byte rows of eight bf16
+    if (((uintptr_t)q % 16) || ((uintptr_t)k % 16) || ((uintptr_t)v % 16) || ((uintptr_t)out % 8)) return LAMQ_EINVAL;
+    if (B == 0 || T == 0) return LAMQ_OK;
+    if (B > 65535 || H > 65535 || T > 0x7fffff) return LAMQ_EUNSUP;
+    const dim3 grid((unsigned)cdiv(T, AT_QB), (unsigned)H, (unsigned)B);
+    hipLaunchKernelGGL(attention_causal_kernel, grid, dim3(256), 0, as_stream(stream), q, sqb, sqh, sqt, k, skb, skh, skt,
+                       v, svb, svh, svt, out, sob, soh, sot, (int)(H / Hkv), (int)T, scale * 1.4426950408889634f);
+    LAMQ_LAUNCH_CHECK();
+    return LAMQ_OK;
+}

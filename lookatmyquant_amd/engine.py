@@ -474,6 +474,31 @@ def causal_softmax(scores: torch.Tensor, scale: float, out: torch.Tensor | None 
     return out
 
 
+def attention_causal(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal grouped-query attention, fused (lamq_attention_causal_bf16): q [B, H, T, 128], k and v [B, Hkv, T, 128]
+    bf16, any strides with the head dim contiguous; query head h reads key/value head h // (H / Hkv). Returns out
+    [B, H, T, 128] bf16, by default a view of a [B, T, H, 128] buffer (the o_proj input's layout)."""
+    for t, nm in ((q, "q"), (k, "k"), (v, "v")):
+        need(t, torch.bfloat16, nm, 4)
+        if t.stride(3) != 1:
+            raise ValueError(f"{nm} must have a contiguous head dim")
+    B, H, T, D = q.shape
+    Hkv = k.shape[1]
+    if k.shape != (B, Hkv, T, D) or v.shape != k.shape or H % Hkv:
+        raise ValueError("k and v must be [B, Hkv, T, D] with Hkv dividing q's heads")
+    if out is None:
+        out = torch.empty(B, T, H, D, dtype=q.dtype, device=q.device).transpose(1, 2)
+    need(out, torch.bfloat16, "out", 4)
+    if out.shape != q.shape or out.stride(3) != 1:
+        raise ValueError("out must be [B, H, T, D] with a contiguous head dim")
+    check(lib().lamq_attention_causal_bf16(ptr(q), q.stride(0), q.stride(1), q.stride(2), ptr(k), k.stride(0),
+                                           k.stride(1), k.stride(2), ptr(v), v.stride(0), v.stride(1), v.stride(2),
+                                           ptr(out), out.stride(0), out.stride(1), out.stride(2), B, H, Hkv, T, D,
+                                           float(scale), stream(q.device)), "attention_causal")
+    return out
+
+
 class EventLog(dict):
     """key -> list of (start, end) torch.cuda.Event pairs. lead_cycles > 0: before each span's start event, a GPU spin
     of that many cycles (torch.cuda._sleep) keeps the stream busy while the host enqueues the span, so that a span

@@ -91,27 +91,12 @@ def _lin(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return torch.matmul(x, w.t().contiguous())
 
 
-ATTENTION_BATCH = 4  # sequences per batched product in the attention (their bf16 scores: 1 GB at T = 2048)
-
-
 def attention(q, k, v, sh: Shape):
-    """Causal grouped-query attention of [B, heads, T, head_dim] bf16 q and [B, kv_heads, T, head_dim] k, v: the scores
-    q k^T as a bf16 batched product; scaled by 1/sqrt(head_dim), masked and soft-maxed in float32 and rounded to bf16
-    in one pass over them (engine.causal_softmax, in place); multiplied by v. The one path of every forward here (no
-    fused-attention backend, no fallback), a few sequences per batched product; every right operand is contiguous."""
-    B, _, T, _ = q.shape
-    rep = sh.heads // sh.kv_heads
-    kT = k.repeat_interleave(rep, dim=1).transpose(-1, -2).contiguous()
-    vv = v.repeat_interleave(rep, dim=1).contiguous()
-    out = torch.empty(B, sh.heads, T, sh.head_dim, dtype=q.dtype, device=q.device)
-    scale = 1.0 / float(sh.head_dim) ** 0.5
-    for b0 in range(0, B, ATTENTION_BATCH):
-        b1 = min(b0 + ATTENTION_BATCH, B)
-        sc = torch.matmul(q[b0:b1], kT[b0:b1])
-        E.causal_softmax(sc, scale, out=sc)
-        out[b0:b1] = torch.matmul(sc, vv[b0:b1])
-        del sc
-    return out
+    """Causal grouped-query attention of [B, heads, T, head_dim] bf16 q and [B, kv_heads, T, head_dim] k, v (any
+    strides with the head dim contiguous), fused in one kernel (engine.attention_causal: scores in registers, an
+    online float32 softmax, bf16 probabilities times v). The one path of every forward here (no other backend, no
+    fallback). Returns [B, heads, T, head_dim], a view of a [B, T, heads, head_dim] buffer."""
+    return E.attention_causal(q, k, v, 1.0 / float(sh.head_dim) ** 0.5)
 
 
 def attention_input_to_o(x: torch.Tensor, w: dict, sh: Shape, rope) -> torch.Tensor:
@@ -123,10 +108,10 @@ def attention_input_to_o(x: torch.Tensor, w: dict, sh: Shape, rope) -> torch.Ten
     v = _lin(x, w["self_attn.v_proj"]).view(B, T, sh.kv_heads, sh.head_dim)
     q = rms_norm(q, w["self_attn.q_norm"], sh.eps).transpose(1, 2)
     k = rms_norm(k, w["self_attn.k_norm"], sh.eps).transpose(1, 2)
-    v = v.transpose(1, 2).contiguous()
+    v = v.transpose(1, 2)
     cos, sin = rope
-    q = (q * cos + _rotate_half(q) * sin).contiguous()
-    k = (k * cos + _rotate_half(k) * sin).contiguous()
+    q = q * cos + _rotate_half(q) * sin
+    k = k * cos + _rotate_half(k) * sin
     out = attention(q, k, v, sh)
     return out.transpose(1, 2).reshape(B, T, sh.heads * sh.head_dim)
 

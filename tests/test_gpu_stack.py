@@ -112,11 +112,38 @@ def test_causal_softmax_matches_a_float64_reference(T):
     assert torch.all(err <= 2.0 ** -8 * ref + 1e-30), float((err / ref.clamp(min=1e-300)).max())
 
 
+@pytest.mark.parametrize("B,H,Hkv,T", [(2, 32, 8, 2048), (3, 4, 4, 33), (1, 8, 2, 1)])
+def test_fused_attention_shapes_against_float64(B, H, Hkv, T):
+    """The fused attention at the config-5 shape (GQA 32/8, T = 2,048), a ragged T with one query block partly past it
+    and T = 1, from strided q and k (the layouts the forward hands over) against float64 on the CPU: each output
+    within 2e-2 of |v| ~ 1 (the probabilities are rounded to bf16 before the product with v) and the output of query
+    0, which sees only key 0, equal to v[0]."""
+    from lookatmyquant_amd import engine as E
+
+    g = torch.Generator(device="cuda").manual_seed(B * 1000 + T)
+    q = torch.randn(B, T, H, 128, generator=g, device="cuda").bfloat16().transpose(1, 2)
+    k = torch.randn(B, T, Hkv, 128, generator=g, device="cuda").bfloat16().transpose(1, 2)
+    v = torch.randn(B, Hkv, T, 128, generator=g, device="cuda").bfloat16()
+    say(f"fused attention B={B} H={H} Hkv={Hkv} T={T}")
+    got = E.attention_causal(q, k, v, 128 ** -0.5).float().cpu().double()
+    rep = H // Hkv
+    for b in range(B):
+        for h in range(0, H, max(1, H // 4)):
+            qd, kd, vd = (t[b, hh].float().cpu().double() for t, hh in ((q, h), (k, h // rep), (v, h // rep)))
+            sc = qd @ kd.T / 128 ** 0.5
+            sc = sc.masked_fill(torch.ones(T, T, dtype=torch.bool).triu(1), float("-inf"))
+            ref = torch.softmax(sc, -1) @ vd
+            err = (got[b, h] - ref).abs().max().item()
+            assert err < 2e-2, (b, h, err)
+            assert torch.equal(got[b, h, 0], vd[0].float().bfloat16().double())
+    assert torch.isfinite(got).all()
+
+
 def test_attention_matches_a_float64_reference():
     """The stack's one attention path (causal grouped-query, bf16 products, float32 softmax) against the same
     attention in float64 on the CPU from the same bf16 inputs, over a batch that spans two of its sequence groups
-    (6 sequences, 4 per batched product). The scores are rounded to bf16 and the probabilities too before the last
-    product, so the tolerance is a few bf16 units of |v| ~ 1."""
+    (6 sequences). The probabilities are rounded to bf16 before the product with v, so the tolerance is a few bf16
+    units of |v| ~ 1."""
     from lookatmyquant_amd import stack
 
     sh = stack.Shape(hidden=512, heads=8, kv_heads=4, head_dim=128, inter=1024, layers=1, vocab=1000)
