@@ -65,14 +65,20 @@ __global__ __launch_bounds__(256) void attention_causal_kernel(
     uint8_t* vl = lds[wave];
     const uint32_t vbase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)vl;
     using v2u = uint32_t __attribute__((ext_vector_type(2)));
-    for (int kb = 0; kb < nkb; ++kb) {
-        const int k0 = kb * AT_KB;
-        // K fragments (A of S^T): key k0 + li, head dims 16 j + 8 hi .. + 7; V rows: chunk c = lane + 64 i is row
-        // c / 16, 16-byte chunk c % 16 (rows past T read row T - 1: finite values that meet zero probabilities)
+    // K fragments (A of S^T): key k0 + li, head dims 16 j + 8 hi .. + 7 (rows past T read row T - 1: finite values
+    // that meet zero probabilities)
+    auto load_k = [&](int k0, lamq_at_bf16x8 (&kf)[8]) {
         const int krow = k0 + li < T ? k0 + li : T - 1;
-        lamq_at_bf16x8 kf[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) kf[j] = *reinterpret_cast<const lamq_at_bf16x8*>(Kp + krow * skt + 16 * j + 8 * hi);
+    };
+    // (the next block's K loaded during this block would take 64 more registers and one wave per SIMD: 8.1 ms
+    // instead of 4.8 at the config-5 shape)
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int k0 = kb * AT_KB;
+        lamq_at_bf16x8 kf[8];
+        load_k(k0, kf);
+        // V rows: chunk c = lane + 64 i is row c / 16, 16-byte chunk c % 16
         uint4 vr[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -119,22 +125,35 @@ __global__ __launch_bounds__(256) void attention_causal_kernel(
             *reinterpret_cast<uint4*>(vl + at_sw(c >> 4, c & 15)) = vr[i];
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        // all sixteen transposing reads first, one wait, then the eight MFMAs. Lane: head dim 32 t + li; keys
+        // 16 mi + 4 hi + {0..3} and + 8 (the P^T order); the group's lane i16 points at row 16 mi + 4 hi + i16 / 4,
+        // columns 32 t + 16 (g & 1) + 4 (i16 % 4) .. + 3
+        v2u lo[4][2], hi2[4][2];
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi) {
-                // lane: head dim 32 t + li; keys 16 mi + 4 hi + {0..3} and + 8 (the P^T order); the group's lane i16
-                // points at row 16 mi + 4 hi + i16 / 4, columns 32 t + 16 (g & 1) + 4 (i16 % 4) .. + 3
                 const int row = 16 * mi + 4 * hi + (i16 >> 2);
                 const int col = 32 * t + 16 * (g & 1) + 4 * (i16 & 3);
                 const uint32_t a0 = vbase + at_sw(row, col >> 3) + 8 * ((col >> 2) & 1);
                 const uint32_t a1 = vbase + at_sw(row + 8, col >> 3) + 8 * ((col >> 2) & 1);
-                v2u lo, hi2;
-                asm volatile("ds_read_b64_tr_b16 %0, %2\n\tds_read_b64_tr_b16 %1, %3\n\ts_waitcnt lgkmcnt(0)"
-                             : "=v"(lo), "=v"(hi2)
+                asm volatile("ds_read_b64_tr_b16 %0, %2\n\tds_read_b64_tr_b16 %1, %3"
+                             : "=v"(lo[t][mi]), "=v"(hi2[t][mi])
                              : "v"(a0), "v"(a1)
                              : "memory");
-                const uint32_t __attribute__((ext_vector_type(4))) w = {lo[0], lo[1], hi2[0], hi2[1]};
+            }
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(lo[0][0]), "+v"(lo[0][1]), "+v"(lo[1][0]), "+v"(lo[1][1]), "+v"(lo[2][0]), "+v"(lo[2][1]),
+                       "+v"(lo[3][0]), "+v"(lo[3][1]), "+v"(hi2[0][0]), "+v"(hi2[0][1]), "+v"(hi2[1][0]),
+                       "+v"(hi2[1][1]), "+v"(hi2[2][0]), "+v"(hi2[2][1]), "+v"(hi2[3][0]), "+v"(hi2[3][1])
+                     :
+                     : "memory");
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi) {
+                const uint32_t __attribute__((ext_vector_type(4))) w = {lo[t][mi][0], lo[t][mi][1], hi2[t][mi][0],
+                                                                        hi2[t][mi][1]};
                 o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(lamq_at_bf16x8, w), pf[mi], o[t], 0, 0,
                                                                0);
             }
