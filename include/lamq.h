@@ -344,6 +344,13 @@ int lamq_causal_softmax_bf16(const uint16_t* S, uint16_t* P, int64_t rows, int T
  *   aligned. H % Hkv == 0; head dim 128 (LAMQ_EUNSUP otherwise); scale > 0.
  * Replaces the bf16 q k^T product, lamq_causal_softmax_bf16 and the product with v in the forwards.
  * ---------------------------------------------------------------------------------------------- */
+/* RMSNorm of the forwards (the calibration model's RMSNorm, quantize.py:1029, in float32 and back to bf16):
+ *   Y[r, :] = bf16( float(bf16(x * rsqrt(mean(x^2) + eps))) * float(g) ),  x = float(X[r, :])
+ *   X [rows, n] (row stride ldx), Y [rows, n] (ldy), g [n], bf16 bits; n, ldx, ldy multiples of 8, X, Y, g 16-byte
+ *   aligned; n <= 10,240 (LAMQ_EUNSUP above). Replaces the pow / mean / rsqrt / mul chain of the forwards. */
+int lamq_rms_norm_bf16(const uint16_t* X, int64_t rows, int64_t n, int64_t ldx, const uint16_t* g, uint16_t* Y,
+                       int64_t ldy, float eps, void* stream);
+
 int lamq_attention_causal_bf16(const uint16_t* q, int64_t sqb, int64_t sqh, int64_t sqt, const uint16_t* k,
                                int64_t skb, int64_t skh, int64_t skt, const uint16_t* v, int64_t svb, int64_t svh,
                                int64_t svt, uint16_t* out, int64_t sob, int64_t soh, int64_t sot, int64_t B, int64_t H,

@@ -12,7 +12,7 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f)
 {
     const uint32_t u = __float_as_uint(f);
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;  // finite, non-negative inputs: no NaN case
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;  // nearest, ties to even, for finite values of either sign
 }
 
 __device__ __forceinline__ float wave_max(float v)
@@ -103,6 +103,91 @@ extern "C" int lamq_causal_softmax_bf16(const uint16_t* S, uint16_t* P, int64_t 
         hipLaunchKernelGGL(causal_softmax_bf16_kernel<4>, grid, dim3(256), 0, s, S, P, rows, T, lds, ldp, scale);
     else
         hipLaunchKernelGGL(causal_softmax_bf16_kernel<8>, grid, dim3(256), 0, s, S, P, rows, T, lds, ldp, scale);
+    LAMQ_LAUNCH_CHECK();
+    return LAMQ_OK;
+}
+
+// RMSNorm of the forwards (Qwen3's RMSNorm as the calibration model computes it, in float32 and back):
+//   y = bf16( float(bf16(x * rsqrt(mean(x^2) + eps))) * float(g) ),  x = float(X[r, :]).
+// P lanes per row (P divides 64), C 16-byte chunks of eight values per lane: the row in registers, the sum of squares
+// as a segmented wave reduction in a fixed order, one read and one write of the row.
+template <int P, int C>
+__global__ __launch_bounds__(256) void rms_norm_bf16_kernel(const uint16_t* __restrict__ X, int64_t rows, int n,
+                                                            int64_t ldx, const uint16_t* __restrict__ g,
+                                                            uint16_t* __restrict__ Y, int64_t ldy, float eps)
+{
+    const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int64_t row = wave * (64 / P) + lane / P;
+    const int sl = lane % P;
+    const bool live = row < rows;  // lanes past the last row still take part in the reductions
+    const uint16_t* x = X + (live ? row : 0) * ldx;
+    float v[C][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int col0 = 8 * (sl + P * c);
+        uint4 u = make_uint4(0u, 0u, 0u, 0u);
+        if (live && col0 < n) u = *reinterpret_cast<const uint4*>(x + col0);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            v[c][e] = bf16_bits_to_f32((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+            ss += v[c][e] * v[c][e];
+        }
+    }
+#pragma unroll
+    for (int off = P / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    const float r = rsqrtf(ss / (float)n + eps);
+    if (!live) return;
+    uint16_t* y = Y + row * ldy;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int col0 = 8 * (sl + P * c);
+        if (col0 >= n) continue;
+        const uint4 gu = *reinterpret_cast<const uint4*>(g + col0);
+        const uint32_t gw[4] = {gu.x, gu.y, gu.z, gu.w};
+        uint32_t out[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            uint32_t pair = 0;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int k = 2 * e + h;
+                const float t = bf16_bits_to_f32(f32_to_bf16_bits(v[c][k] * r));
+                const float gv = bf16_bits_to_f32((gw[k >> 1] >> (16 * (k & 1))) & 0xFFFFu);
+                pair |= f32_to_bf16_bits(t * gv) << (16 * h);
+            }
+            out[e] = pair;
+        }
+        *reinterpret_cast<uint4*>(y + col0) = make_uint4(out[0], out[1], out[2], out[3]);
+    }
+}
+
+extern "C" int lamq_rms_norm_bf16(const uint16_t* X, int64_t rows, int64_t n, int64_t ldx, const uint16_t* g,
+                                  uint16_t* Y, int64_t ldy, float eps, void* stream)
+{
+    if (!X || !g || !Y || rows < 0 || n < 1 || ldx < n || ldy < n || !(eps >= 0.0f)) return LAMQ_EINVAL;
+    if (n % 8 || ldx % 8 || ldy % 8 || ((uintptr_t)X % 16) || ((uintptr_t)Y % 16) || ((uintptr_t)g % 16))
+        return LAMQ_EINVAL;
+    if (n > 8 * 64 * 20) return LAMQ_EUNSUP;
+    if (rows == 0) return LAMQ_OK;
+    hipStream_t s = as_stream(stream);
+#define RMS_LAUNCH(P, C)                                                                                              \
+    do {                                                                                                              \
+        const int64_t waves = cdiv(rows, 64 / (P));                                                                   \
+        if (cdiv(waves, 4) > 0x7fffffff) return LAMQ_EUNSUP;                                                          \
+        hipLaunchKernelGGL((rms_norm_bf16_kernel<P, C>), dim3((unsigned)cdiv(waves, 4)), dim3(256), 0, s, X, rows,      \
+                           (int)n, ldx, g, Y, ldy, eps);                                                              \
+    } while (0)
+    if (n <= 128) RMS_LAUNCH(16, 1);
+    else if (n <= 512) RMS_LAUNCH(64, 1);
+    else if (n <= 1024) RMS_LAUNCH(64, 2);
+    else if (n <= 2048) RMS_LAUNCH(64, 4);
+    else if (n <= 2560) RMS_LAUNCH(64, 5);
+    else if (n <= 4096) RMS_LAUNCH(64, 8);
+    else RMS_LAUNCH(64, 20);
+#undef RMS_LAUNCH
     LAMQ_LAUNCH_CHECK();
     return LAMQ_OK;
 }

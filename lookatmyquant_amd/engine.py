@@ -474,6 +474,24 @@ def causal_softmax(scores: torch.Tensor, scale: float, out: torch.Tensor | None 
     return out
 
 
+def rms_norm(x: torch.Tensor, g: torch.Tensor, eps: float) -> torch.Tensor:
+    """bf16(bf16(x rsqrt(mean(x^2) + eps)) g) over the last dim of a bf16 x (float32 inside), one pass
+    (lamq_rms_norm_bf16). x's rows may be strided (the last dim contiguous, one row stride); returns a new contiguous
+    tensor of x's shape."""
+    need(x, torch.bfloat16, "x")
+    need(g, torch.bfloat16, "g", 1)
+    n = x.shape[-1]
+    if g.numel() != n:
+        raise ValueError("g must have the last dim of x")
+    X = x.reshape(-1, n)
+    if X.dim() == 2 and X.shape[0] > 1 and X.stride(1) != 1:
+        raise ValueError("x must have a contiguous last dim")
+    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    check(lib().lamq_rms_norm_bf16(ptr(X), X.shape[0], n, X.stride(0) if X.shape[0] > 1 else n, ptr(g.contiguous()),
+                                   ptr(y), n, float(eps), stream(x.device)), "rms_norm")
+    return y
+
+
 def attention_causal(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
                      out: torch.Tensor | None = None) -> torch.Tensor:
     """Causal grouped-query attention, fused (lamq_attention_causal_bf16): q [B, H, T, 128], k and v [B, Hkv, T, 128]

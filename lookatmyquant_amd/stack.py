@@ -70,8 +70,8 @@ def layer_weights(i: int, sh: Shape, dev, seed: int = 5000) -> dict:
 
 
 def rms_norm(x: torch.Tensor, g: torch.Tensor, eps: float) -> torch.Tensor:
-    xf = x.float()
-    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype) * g
+    """Qwen3's RMSNorm in float32 and back: bf16(bf16(x rsqrt(mean(x^2) + eps)) g), one kernel (engine.rms_norm)."""
+    return E.rms_norm(x, g, eps)
 
 
 def rope_tables(T: int, sh: Shape, dev):

@@ -112,6 +112,25 @@ def test_causal_softmax_matches_a_float64_reference(T):
     assert torch.all(err <= 2.0 ** -8 * ref + 1e-30), float((err / ref.clamp(min=1e-300)).max())
 
 
+@pytest.mark.parametrize("shape", [(3, 77, 2560), (2, 5, 32, 128), (1000, 4096), (7, 9728), (1, 8)])
+def test_rms_norm_matches_the_float32_chain(shape):
+    """engine.rms_norm against the float32 chain it replaces, xf * rsqrt(mean(xf^2) + eps) rounded to bf16, times g in
+    bf16: equal up to one bf16 rounding of the product (the sum of squares is reduced in another order), at the
+    forward's widths (hidden 2,560, head dim 128, 4,096, 9,728) and a width of 8."""
+    from lookatmyquant_amd import engine as E
+
+    g0 = torch.Generator(device="cuda").manual_seed(sum(shape))
+    x = (torch.randn(*shape, generator=g0, device="cuda") * 3).bfloat16()
+    g = (1 + 0.1 * torch.randn(shape[-1], generator=g0, device="cuda")).bfloat16()
+    say(f"rms_norm {shape}")
+    got = E.rms_norm(x, g, 1e-6).float()
+    xf = x.float()
+    ref = ((xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).bfloat16() * g).float()
+    rel = ((got - ref).abs() / ref.abs().clamp_min(1e-30)).max().item()
+    assert rel <= 2 ** -7, rel
+    assert (got == ref).float().mean().item() > 0.99
+
+
 @pytest.mark.parametrize("B,H,Hkv,T", [(2, 32, 8, 2048), (3, 4, 4, 33), (1, 8, 2, 1)])
 def test_fused_attention_shapes_against_float64(B, H, Hkv, T):
     """The fused attention at the config-5 shape (GQA 32/8, T = 2,048), a ragged T with one query block partly past it
