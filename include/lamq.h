@@ -351,6 +351,11 @@ int lamq_causal_softmax_bf16(const uint16_t* S, uint16_t* P, int64_t rows, int T
 int lamq_rms_norm_bf16(const uint16_t* X, int64_t rows, int64_t n, int64_t ldx, const uint16_t* g, uint16_t* Y,
                        int64_t ldy, float eps, void* stream);
 
+/* The MLP gate of the forwards (silu(gate) * up, in float32 with the bf16 rounding after each of the two as the
+ * unfused chain rounds): y = bf16(float(bf16(a / (1 + exp(-a)))) * float(b)), n elements (a multiple of 8) of
+ * 16-byte aligned contiguous bf16 a, b, y. */
+int lamq_swiglu_bf16(const uint16_t* a, const uint16_t* b, uint16_t* y, int64_t n, void* stream);
+
 int lamq_attention_causal_bf16(const uint16_t* q, int64_t sqb, int64_t sqh, int64_t sqt, const uint16_t* k,
                                int64_t skb, int64_t skh, int64_t skt, const uint16_t* v, int64_t svb, int64_t svh,
                                int64_t svt, uint16_t* out, int64_t sob, int64_t soh, int64_t sot, int64_t B, int64_t H,

@@ -474,6 +474,18 @@ def causal_softmax(scores: torch.Tensor, scale: float, out: torch.Tensor | None 
     return out
 
 
+def swiglu(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """silu(a) * b for contiguous bf16 a, b of one shape, rounded to bf16 after the silu and after the product, as
+    the unfused chain rounds (lamq_swiglu_bf16)."""
+    need(a, torch.bfloat16, "a")
+    need(b, torch.bfloat16, "b")
+    if a.shape != b.shape or not a.is_contiguous() or not b.is_contiguous() or a.numel() % 8:
+        raise ValueError("a and b must be contiguous tensors of one shape, a multiple of 8 elements")
+    y = torch.empty_like(a)
+    check(lib().lamq_swiglu_bf16(ptr(a), ptr(b), ptr(y), a.numel(), stream(a.device)), "swiglu")
+    return y
+
+
 def rms_norm(x: torch.Tensor, g: torch.Tensor, eps: float) -> torch.Tensor:
     """bf16(bf16(x rsqrt(mean(x^2) + eps)) g) over the last dim of a bf16 x (float32 inside), one pass
     (lamq_rms_norm_bf16). x's rows may be strided (the last dim contiguous, one row stride); returns a new contiguous

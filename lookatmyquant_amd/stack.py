@@ -87,8 +87,9 @@ def _rotate_half(x):
 
 
 def _lin(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-    """x W^T with a contiguous right operand (x [.., n] bf16, W [m, n])."""
-    return torch.matmul(x, w.t().contiguous())
+    """x W^T (x [.., n] bf16, W [m, n]) as a linear layer computes it: one 2-d product with W read transposed in
+    place (no batched product, no copy of W per call)."""
+    return torch.nn.functional.linear(x, w)
 
 
 def attention(q, k, v, sh: Shape):
@@ -266,7 +267,7 @@ class StackBuild:
             a = attention_input_to_o(x1, wr, sh, self.rope)
             h1 = h + _lin(a, wr["self_attn.o_proj"])
             x2 = rms_norm(h1, wr["post_attention_layernorm"], sh.eps)
-            m = torch.nn.functional.silu(_lin(x2, wr["mlp.gate_proj"])) * _lin(x2, wr["mlp.up_proj"])
+            m = E.swiglu(_lin(x2, wr["mlp.gate_proj"]), _lin(x2, wr["mlp.up_proj"]))
             hr_next.append(h1 + _lin(m, wr["mlp.down_proj"]))
             for s, x in enumerate((x1, a, x2, m)):
                 xr[s].append(_flat(x))
@@ -285,14 +286,14 @@ class StackBuild:
                 h1q = [h + _lin(a, wq["self_attn.o_proj"]) for h, a in zip(hq, aq)]
                 xq = x2q = [rms_norm(h, wq["post_attention_layernorm"], sh.eps) for h in h1q]
             else:
-                xq = [torch.nn.functional.silu(_lin(x, wq["mlp.gate_proj"])) * _lin(x, wq["mlp.up_proj"]) for x in x2q]
+                xq = [E.swiglu(_lin(x, wq["mlp.gate_proj"]), _lin(x, wq["mlp.up_proj"])) for x in x2q]
             xqf = [_flat(x) for x in xq]
             timer.add("forward", t1, timer.mark())
             self._stage(i, s, names, xqf, xr[s], wr, wq)
             del xq, xqf
         # both streams through the layer (the quantized one with its last matrix now quantized)
         t4 = timer.mark()
-        self.hq = [h1 + _lin(torch.nn.functional.silu(_lin(x, wq["mlp.gate_proj"])) * _lin(x, wq["mlp.up_proj"]),
+        self.hq = [h1 + _lin(E.swiglu(_lin(x, wq["mlp.gate_proj"]), _lin(x, wq["mlp.up_proj"])),
                              wq["mlp.down_proj"]) for h1, x in zip(h1q, x2q)]
         self.hr = hr_next
         del xr, wr, wq, h1q, x2q

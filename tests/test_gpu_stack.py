@@ -112,6 +112,22 @@ def test_causal_softmax_matches_a_float64_reference(T):
     assert torch.all(err <= 2.0 ** -8 * ref + 1e-30), float((err / ref.clamp(min=1e-300)).max())
 
 
+def test_swiglu_matches_the_unfused_chain():
+    """engine.swiglu against torch's silu(a) * b in bf16 (each rounded to bf16): equal up to one bf16 rounding where
+    the exponentials differ in their last bit, over the config-5 MLP width and large |a|."""
+    from lookatmyquant_amd import engine as E
+
+    g = torch.Generator(device="cuda").manual_seed(9)
+    a = (torch.randn(300, 9728, generator=g, device="cuda") * 4).bfloat16()
+    b = torch.randn(300, 9728, generator=g, device="cuda").bfloat16()
+    say("swiglu 300 x 9728")
+    got = E.swiglu(a, b).float()
+    ref = (torch.nn.functional.silu(a) * b).float()
+    rel = ((got - ref).abs() / ref.abs().clamp_min(1e-30)).max().item()
+    assert rel <= 2 ** -7, rel
+    assert (got == ref).float().mean().item() > 0.99
+
+
 @pytest.mark.parametrize("shape", [(3, 77, 2560), (2, 5, 32, 128), (1000, 4096), (7, 9728), (1, 8)])
 def test_rms_norm_matches_the_float32_chain(shape):
     """engine.rms_norm against the float32 chain it replaces, xf * rsqrt(mean(xf^2) + eps) rounded to bf16, times g in
