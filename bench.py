@@ -161,13 +161,14 @@ def cpu_sweep_rows(n: int, L: int, k: int, table, threads: int, rows_per_thread:
     return wall / rows
 
 
-def cpu_fixed_parts(n: int, threads: int, sample_tokens: int = 4096, seed: int = 0) -> dict:
+def cpu_fixed_parts(n: int, threads: int, sample_tokens: int = 4096, seed: int = 0, qep: bool = True,
+                    m: int | None = None) -> dict:
     """Seconds of a stage's per-matrix statistics and algebra on the CPU (numpy/LAPACK on `threads` threads) at width n,
     by how each part scales, as the reference computes them (quantize.py:1457-1470, 1330-1335, 1503; codes.py:129-132,
-    430-439; frame.py:515-522): "stats" the weighted Hessian and the QEP cross-Gram in float32 over `sample_tokens`
-    tokens (N n^2), "cubic" the QEP solve, the dense rotation R H R^T and the damped Cholesky-inverse factor (n^3),
-    "rows" the target product W M and the rows' rotation W R^T for n rows (m n^2), "rht" the dense rotation matrix
-    itself (n^2)."""
+    430-439; frame.py:515-522): "stats" the weighted Hessian (and with qep the QEP cross-Gram) in float32 over
+    `sample_tokens` tokens (N n^2), "cubic" the QEP solve (with qep), the dense rotation R H R^T and the damped
+    Cholesky-inverse factor (n^3), "rows" the rows' rotation W R^T (with qep after the target product W M) for m rows
+    (default n; m n^2), "rht" the dense rotation matrix itself (n^2)."""
     import numpy as np
     from threadpoolctl import threadpool_limits
 
@@ -177,29 +178,51 @@ def cpu_fixed_parts(n: int, threads: int, sample_tokens: int = 4096, seed: int =
     X = rng.standard_normal((sample_tokens, n), dtype=np.float32)
     Xr = X + np.float32(0.01) * rng.standard_normal((sample_tokens, n), dtype=np.float32)
     w = rng.random(sample_tokens, dtype=np.float32) + np.float32(0.5)
-    W = rng.standard_normal((n, n))
+    W = rng.standard_normal((n if m is None else m, n))
     out = {}
     with threadpool_limits(limits=threads):
         t = time.perf_counter()
         Xw = X * w[:, None]
         H = X.T @ Xw
-        D = Xr.T @ Xw
+        D = Xr.T @ Xw if qep else None
         out["stats"] = time.perf_counter() - t
         t = time.perf_counter()
         R = O.rht(n, 1)
         out["rht"] = time.perf_counter() - t
         H = H.astype(np.float64) / sample_tokens
-        D = D.astype(np.float64) / sample_tokens
         t = time.perf_counter()
-        M = np.eye(n) + 0.5 * np.linalg.solve(H + 0.1 * np.mean(np.diag(H)) * np.eye(n), (D - H).T).T
+        if qep:
+            D = D.astype(np.float64) / sample_tokens
+            M = np.eye(n) + 0.5 * np.linalg.solve(H + 0.1 * np.mean(np.diag(H)) * np.eye(n), (D - H).T).T
         Hr = R @ H @ R.T
         O.environment(Hr)
         out["cubic"] = time.perf_counter() - t
         t = time.perf_counter()
-        target = W @ M
+        target = W @ M if qep else W
         _ = target @ R.T
         out["rows"] = time.perf_counter() - t
     return out
+
+
+def extrapolate_layer(per_row: dict, fx: dict, stages: list, plans_one_layer: dict, tokens: int, n0: int,
+                      sample_tokens: int, row_steps) -> tuple[float, float]:
+    """(fixed, sweep) seconds of one layer from the sampled figures: per_row {bits: seconds per row at width n0 with
+    the host's threads all busy, i.e. wall time / rows of a batch of one row per thread}, fx cpu_fixed_parts(n0),
+    stages [(n, {name: m})], plans_one_layer {name: row groups}, row_steps(n) the trellis row-steps of a row of width
+    n. The sweep of a row of width n costs per_row[bits] * row_steps(n) / row_steps(n0); the statistics scale with
+    tokens x n^2, the solve, R H R^T and the factor with n^3, the target and row rotation with m n^2 and the rotation
+    matrix with n^2."""
+    fixed = sweep = 0.0
+    for n, ms in stages:
+        m = sum(ms.values())
+        r = n / n0
+        fixed += (fx["stats"] * tokens / sample_tokens * r * r + fx["cubic"] * r ** 3 + fx["rows"] * (m / n0) * r * r
+                  + fx["rht"] * r * r)
+        ratio = row_steps(n) / row_steps(n0)
+        for nm in ms:
+            for g in plans_one_layer[nm]:
+                sweep += len(g["rows"]) * per_row[int(g["bits"])] * ratio
+    return fixed, sweep
 
 
 def cpu_baseline_c5(L: int, threads: int, sh, plans_one_layer: dict, tokens: int) -> dict:
@@ -218,23 +241,16 @@ def cpu_baseline_c5(L: int, threads: int, sh, plans_one_layer: dict, tokens: int
     per_row = {k: cpu_sweep_rows(n0, L, k, tables[k], threads) for k in (1, 2, 3, 4)}
     fx = cpu_fixed_parts(n0, threads, sample_tokens)
     shapes = stack.matrix_shapes(sh)
-    fixed = sweep = 0.0
-    for names in stack.STAGES:
-        n = shapes[names[0]][1]
-        m = sum(shapes[nm][0] for nm in names)
-        r = n / n0
-        fixed += (fx["stats"] * tokens / sample_tokens * r * r + fx["cubic"] * r ** 3 + fx["rows"] * (m / n0) * r * r
-                  + fx["rht"] * r * r)
-        ratio = sum(E.trellis_row_steps(n)) / sum(E.trellis_row_steps(n0))
-        for nm in names:
-            for g in plans_one_layer[nm]:
-                sweep += len(g["rows"]) * per_row[int(g["bits"])] * ratio / threads
+    stages = [(shapes[names[0]][1], {nm: shapes[nm][0] for nm in names}) for names in stack.STAGES]
+    fixed, sweep = extrapolate_layer(per_row, fx, stages, plans_one_layer, tokens, n0, sample_tokens,
+                                     lambda n: sum(E.trellis_row_steps(n)))
     weights = sum(shapes[nm][0] * shapes[nm][1] for names in stack.STAGES for nm in names)
     total = fixed + sweep
     return {"value": round(weights / total, 1), "unit": "weights/s", "cores": threads, "kind": "port",
             "seconds_per_layer_extrapolated": round(total, 2), "of_which_sweeps": round(sweep, 2),
             "sample_seconds": round(time.perf_counter() - t0, 1),
-            "seconds_per_row_n2560": {str(k): round(v, 4) for k, v in per_row.items()}}
+            "seconds_per_row_n2560": {str(k): round(v, 4) for k, v in per_row.items()},
+            "fixed_parts_n2560": {k: round(v, 4) for k, v in fx.items()}}
 
 
 # ----------------------------------------------------------------------------- config 5 (the default)
@@ -472,19 +488,23 @@ def run_c1(args):
                      "trailing_updates": round(sum(trl) / args.steps, 4)},
     }
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline_c1(W, H, levels.cpu().numpy(), in_seed, lazy)
+        aff, eff = host_threads()
+        base = cpu_baseline_c1(W, H, levels.cpu().numpy(), in_seed, lazy, eff)
+        eight = base if eff == 8 else cpu_baseline_c1(W, H, levels.cpu().numpy(), in_seed, lazy, 8)
+        base["affinity_cpus"] = aff
+        base["at_8_threads"] = {"value": eight["value"], "cores": 8, "sample": eight["sample"]}
+        out["cpu_baseline"] = base
     print(json.dumps(out))
 
 
-def cpu_baseline_c1(W, H, levels, in_seed, lazy):
-    """The C oracle on config 1, all of it: rotation, Hessian rotation and factor (numpy/LAPACK on every host thread),
-    then the width-1 sweep of every row (one row per thread at once)."""
+def cpu_baseline_c1(W, H, levels, in_seed, lazy, threads):
+    """The C oracle on config 1, all of it: rotation, Hessian rotation and factor (numpy/LAPACK on `threads` host
+    threads), then the width-1 sweep of every row (one row per thread at once)."""
     import numpy as np
     from threadpoolctl import threadpool_limits
 
     from oracle import oracle as O
 
-    _, threads = host_threads()
     m, n = W.shape
     with threadpool_limits(limits=threads):
         t0 = time.perf_counter()
@@ -588,6 +608,43 @@ def run_c2(args):
 # ----------------------------------------------------------------------------- config 3
 
 
+def cpu_baseline_c3(L: int, threads: int, plans: dict, N: int, stage_rows: list, rows_per_thread: int = 1,
+                    sample_tokens: int = 4096) -> dict:
+    """The CPU restatement's time for config 3 at `threads` threads, each part measured at the stage's own width: per
+    stage (n = 2,560: gate and up; n = 9,728: down) the weighted Hessian in float32 on `sample_tokens` of the N tokens
+    (scaled by N / sample_tokens: its cost is linear in the tokens), the dense rotation matrix, R H R^T, the damped
+    Cholesky-inverse factor and the rotation of the stage's rows W R^T in full (numpy/LAPACK), and the row sweep
+    (the C oracle, one row per thread in flight) for each bit width on threads x rows_per_thread rows, extrapolated by
+    the plan's row count of that width (rows are independent given U and S)."""
+    from lookatmyquant_amd.tables import load_table, quantile_table
+
+    t0 = time.perf_counter()
+    tables = {b: (quantile_table(16, 0) if L == 16 else load_table(12, b)) for b in (1, 2, 3, 4)}
+    fixed = sweep = 0.0
+    parts = {}
+    for n, names in stage_rows:
+        m = sum(len(g["rows"]) for nm in names for g in plans[nm])
+        fx = cpu_fixed_parts(n, threads, sample_tokens, qep=False, m=m)
+        fixed += fx["stats"] * N / sample_tokens + fx["rht"] + fx["cubic"] + fx["rows"]
+        per_row = {}
+        for k in (1, 2, 3, 4):
+            rows_k = sum(len(g["rows"]) for nm in names for g in plans[nm] if int(g["bits"]) == k)
+            if rows_k:
+                per_row[k] = cpu_sweep_rows(n, L, k, tables[k], threads, rows_per_thread)
+                sweep += rows_k * per_row[k]
+        parts[str(n)] = {"fixed": {p: round(v, 4) for p, v in fx.items()},
+                         "seconds_per_row": {str(k): round(v, 5) for k, v in per_row.items()}}
+    total = fixed + sweep
+    weights = sum(len(g["rows"]) * n for n, names in stage_rows for nm in names for g in plans[nm])
+    return {"value": round(weights / total, 1), "unit": "weights/s", "cores": threads, "kind": "port",
+            "seconds_total_extrapolated": round(total, 3), "of_which_sweeps": round(sweep, 3),
+            "sample_seconds": round(time.perf_counter() - t0, 1), "by_width": parts,
+            "sample": f"C oracle + numpy/LAPACK on {threads} threads: per stage the weighted Hessian (float32) on "
+                      f"{sample_tokens} of {N} tokens scaled by tokens, the dense rotation, R H R^T, the damped "
+                      f"Cholesky-inverse factor and W R^T in full; the row sweep on {threads * rows_per_thread} rows "
+                      f"per bit width (one row per thread in flight), extrapolated by the plan's rows"}
+
+
 def run_c3(args):
     """Config 3: one MLP block (gate/up stage on the hidden input, down stage on the intermediate)."""
     import torch
@@ -675,7 +732,7 @@ def run_c3(args):
                                                "mfma", 1e12, kt.launches("trailing")),
             "rht": kernel_line(kt.ms("rht"), kt.work["rht"], MFMA_F64_PEAK_TFLOPS, "TFLOP/s", "mfma", 1e12,
                                kt.launches("rht"))}
-    print(json.dumps({
+    line = {
         "metric": METRIC, "value": round(weights / (ms * 1e-3), 1), "unit": "weights/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16->f32 (Hessian), f64/f32 (sweep)", "data": "synthetic",
@@ -684,7 +741,17 @@ def run_c3(args):
                                f"bits 1-4, row trellis L={L}, one factor per stage, packed codes per group",
                    "L": L, "tokens": N, "weights": weights, "setup_s": round(setup_s, 1)},
         "viterbi_row_steps_per_s": round(row_steps_total / (ms * 1e-3), 1),
-        "kernels": kern}))
+        "kernels": kern}
+    if not args.no_cpu:
+        aff, eff = host_threads()
+        stage_rows = [(hid, ("gate", "up")), (inter, ("down",))]
+        base = cpu_baseline_c3(L, eff, plans, N, stage_rows)
+        eight = base if eff == 8 else cpu_baseline_c3(L, 8, plans, N, stage_rows)
+        base["affinity_cpus"] = aff
+        base["at_8_threads"] = {"value": eight["value"], "cores": 8,
+                                "seconds_total_extrapolated": eight["seconds_total_extrapolated"]}
+        line["cpu_baseline"] = base
+    print(json.dumps(line))
 
 
 # ----------------------------------------------------------------------------- config 4
@@ -714,6 +781,13 @@ def run_c4(args):
             kl, sums = E.kl_rows(ref, q)
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t1) * 1e3 / args.steps
+    cpu = None
+    if not args.no_cpu:
+        aff, eff = host_threads()
+        cpu = cpu_baseline_c4(ref, q, eff, T)
+        eight = cpu if eff == 8 else cpu_baseline_c4(ref, q, 8, T)
+        cpu["affinity_cpus"] = aff
+        cpu["at_8_threads"] = {"value": eight["value"], "cores": 8, "sample": eight["sample"]}
     print(json.dumps({
         "metric": "KL evaluations/s (per-token KL over paired bf16 logits)", "value": round(1e3 / ms, 2),
         "unit": "evals/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
@@ -722,7 +796,32 @@ def run_c4(args):
         "config": {"workload": "config 4: one KL evaluation over [8192, 151936] bf16 logit pairs per step",
                    "tokens": T, "vocab": V, "mean_kl": float(sums[0] / sums[1])},
         "kernels": {"kl_rows": kernel_line(kt.ms("kl"), kt.work["kl"], HBM_PEAK_GBS, "GB/s", "hbm", 1e9,
-                                           kt.launches("kl"))}}))
+                                           kt.launches("kl"))},
+        **({"cpu_baseline": cpu} if cpu else {})}))
+
+
+def cpu_baseline_c4(ref, q, threads: int, T: int, sample_tokens: int = 1024) -> dict:
+    """The C oracle's KL (compiler.py:177-188 in float64) on the first `sample_tokens` token rows of the same logits,
+    the rows split across `threads` host threads, scaled to one evaluation of T tokens (tokens are independent)."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as O
+
+    r = ref[:sample_tokens].cpu().view(torch.int16).numpy().view(np.uint16)
+    qq = q[:sample_tokens].cpu().view(torch.int16).numpy().view(np.uint16)
+    from concurrent.futures import ThreadPoolExecutor
+
+    cuts = [i * sample_tokens // threads for i in range(threads + 1)]  # contiguous token blocks, one per thread
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(max_workers=threads) as ex:
+        list(ex.map(lambda i: O.kl_rows(r[cuts[i]:cuts[i + 1]], qq[cuts[i]:cuts[i + 1]]), range(threads)))
+    wall = time.perf_counter() - t0
+    per_eval = wall * T / sample_tokens
+    return {"value": round(1.0 / per_eval, 4), "unit": "evals/s", "cores": threads, "kind": "port",
+            "seconds_per_eval_extrapolated": round(per_eval, 3),
+            "sample": f"C oracle (float64) on the first {sample_tokens} of {T} token rows, {threads} threads "
+                      f"({wall:.2f} s), scaled by tokens"}
 
 
 def copy_probe(mib: int):

@@ -334,16 +334,6 @@ int lamq_pack_codes(const int32_t* src, int64_t ld, int64_t src_rows, const int6
 int lamq_causal_softmax_bf16(const uint16_t* S, uint16_t* P, int64_t rows, int T, int64_t lds, int64_t ldp,
                              float scale, void* stream);
 
-/* ----------------------------------------------------------------------------------------------
- * Causal grouped-query attention of the forwards, fused (the same attention as above, quantize.py:1029 and the
- * layer loop 1626-1694, with the scores kept in registers: an online softmax over key blocks of 32, exp2 with the
- * scale folded in, probabilities rounded to bf16 for the product with v, float32 sums):
- *   out[b, t, h, :] = sum_{u <= t} softmax_u(q[b, h, t, :] . k[b, h / (H / Hkv), u, :] * scale) v[b, h / (H / Hkv), u, :]
- *   q [B, H, T, 128], k, v [B, Hkv, T, 128], out [B, H, T, 128] bf16 bits, each given by its (batch, head, token)
- *   strides in elements with the head dim contiguous; strides multiples of 8, q, k, v 16-byte and out 8-byte
- *   aligned. H % Hkv == 0; head dim 128 (LAMQ_EUNSUP otherwise); scale > 0.
- * Replaces the bf16 q k^T product, lamq_causal_softmax_bf16 and the product with v in the forwards.
- * ---------------------------------------------------------------------------------------------- */
 /* RMSNorm of the forwards (the calibration model's RMSNorm, quantize.py:1029, in float32 and back to bf16):
  *   Y[r, :] = bf16( float(bf16(x * rsqrt(mean(x^2) + eps))) * float(g) ),  x = float(X[r, :])
  *   X [rows, n] (row stride ldx), Y [rows, n] (ldy), g [n], bf16 bits; n, ldx, ldy multiples of 8, X, Y, g 16-byte
@@ -356,6 +346,17 @@ int lamq_rms_norm_bf16(const uint16_t* X, int64_t rows, int64_t n, int64_t ldx, 
  * 16-byte aligned contiguous bf16 a, b, y. */
 int lamq_swiglu_bf16(const uint16_t* a, const uint16_t* b, uint16_t* y, int64_t n, void* stream);
 
+/* ----------------------------------------------------------------------------------------------
+ * Causal grouped-query attention of the forwards, fused (the attention lamq_causal_softmax_bf16 serves, quantize.py:1029 and the
+ * layer loop 1626-1694, with the scores kept in registers: an online softmax over key blocks of 32, exp2 with the
+ * scale folded in, probabilities rounded to bf16 for the product with v, float32 sums):
+ *   out[b, t, h, :] = sum_{u <= t} softmax_u(q[b, h, t, :] . k[b, h / (H / Hkv), u, :] * scale) v[b, h / (H / Hkv), u, :]
+ *   q [B, H, T, 128], k, v [B, Hkv, T, 128], out [B, H, T, 128] bf16 bits, each given by its (batch, head, token)
+ *   strides in elements with the head dim contiguous; strides multiples of 8, q, k, v 16-byte and out 8-byte
+ *   aligned. H % Hkv == 0; head dim 128 (LAMQ_EUNSUP otherwise); scale > 0.
+ * Replaces the bf16 q k^T product, lamq_causal_softmax_bf16 and the product with v in the forwards.
+ * T from 1 to 8,388,607; B, H at most 65,535 (LAMQ_EUNSUP above).
+ * ---------------------------------------------------------------------------------------------- */
 int lamq_attention_causal_bf16(const uint16_t* q, int64_t sqb, int64_t sqh, int64_t sqt, const uint16_t* k,
                                int64_t skb, int64_t skh, int64_t skt, const uint16_t* v, int64_t svb, int64_t svh,
                                int64_t svt, uint16_t* out, int64_t sob, int64_t soh, int64_t sot, int64_t B, int64_t H,

@@ -610,6 +610,11 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
                     s = redi[wv];
                 }
         }
+        // no state attains the minimum only when every final cost is NaN (a NaN target: each cost of that position and
+        // every later one is NaN; in one pass the result may then come from a thread that owns no states); the
+        // reference's argmin then returns the first entry, state 0, and the traceback below stays inside the
+        // back-pointers
+        s = (uint32_t)s < (uint32_t)V::NS ? s : 0;
         s = __builtin_amdgcn_readfirstlane(s);
         const auto emit = [&](int c, int sc) {
             if (PATHREG)

@@ -388,9 +388,8 @@ def main(argv=None):
     args = ap.parse_args(argv)
     if args.trellis_rows != "16,8":
         raise NotImplementedError("the fused row-trellis kernels settle 16 columns and look 8 ahead")
-    if args.calib_len % 8 or args.calib_len > 4096:
-        raise NotImplementedError("the forwards' fused attention softmax takes sequence lengths that are multiples of 8 "
-                                  "up to 4096")
+    if not 1 <= args.calib_len <= 0x7FFFFF:
+        raise NotImplementedError("the forwards' fused attention takes sequence lengths of 1 to 8388607 tokens")
     sh = stack.Shape()
     layers = args.layers or sh.layers
     if args.program == "plan":
@@ -418,7 +417,9 @@ def main(argv=None):
            "stages damped more": out["redamped"], "row plan": manifest}
     if args.save_codes:
         Path(args.save_codes).parent.mkdir(parents=True, exist_ok=True)
-        torch.save(stack.saved_codes(out), args.save_codes)
+        calibration = {"windows": args.calib, "tokens per window": args.calib_len,
+                       "token weights": args.token_weights or "none"}
+        torch.save(stack.saved_codes(out, manifest if args.row_plan else None, calibration), args.save_codes)
     if args.artifact:
         res["artifact"] = {k: v for k, v in stack.export_codes(out, args.artifact).items()
                            if k in ("total_bytes", "tensor_count", "all_tensor_bytes_verified")}

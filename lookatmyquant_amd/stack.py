@@ -237,7 +237,8 @@ class StackBuild:
     def device_tables(self) -> dict:
         """The trellis tables as float64 tensors on the device, made once."""
         if getattr(self, "_dtables", None) is None:
-            self._dtables = {b: torch.as_tensor(np.asarray(t, dtype=np.float64)).to(self.dev)
+            # (np.array copies: the cached tables are read-only)
+            self._dtables = {b: torch.from_numpy(np.array(t, dtype=np.float64)).to(self.dev)
                              for b, t in self.tables.items()}
         return self._dtables
 
@@ -371,6 +372,8 @@ class StackBuild:
             self.codes[f"{i}.{nm}"] = {"kind": "trellis", "states": st, "scales": Srow, "in_seed": in_seed,
                                        "groups": plans[nm], "packed": packed}
             self.n_w += shapes[nm][0] * shapes[nm][1]
+            if i < self.keep:  # the weights the quantized stream goes on with (bf16 of the decoded reconstruction)
+                self.kept[(i, s)].setdefault("Wq", {})[nm] = wq[nm]
         for nm in coded:
             if parse(progs[nm])[0] != "lm":
                 continue
@@ -470,11 +473,17 @@ def export_codes(out: dict, path) -> dict:
     return artifact.write_artifact(path, tensors, {"matrices": matrices})
 
 
-def saved_codes(out: dict) -> dict:
-    """The build's codes as the reference's --save-codes dictionary (quantize.py:513-565, 1541-1553): per full
-    parameter name, a row-trellis entry {"states": int16 [m, n] (state + 4096 * table_index), "scales": float32 [m],
-    "in_seed", "table": float32 [4096 * groups], "row_groups": [{"rows", "bits", "table_index"}], "trellis_layout":
-    "row"} or a scalar entry {"codes": uint8 [m, n], "scales", "in_seed", "levels": float32}, on the CPU."""
+SOURCE_MODEL = "random-initialised Qwen3.5-4B-shaped stack (hidden 2560, GQA 32/8 x 128, MLP 9728)"
+
+
+def saved_codes(out: dict, row_plan: dict | None = None, calibration: dict | None = None) -> dict:
+    """The build's codes as the reference's --save-codes file (quantize.py:1737-1739): {"matrices": per full parameter
+    name, a row-trellis entry {"states": int16 [m, n] (state + 4096 * table_index), "scales": float32 [m], "in_seed",
+    "table": float32 [4096 * groups], "row_groups": [{"rows", "bits", "table_index"}], "trellis_layout": "row"} or a
+    scalar entry {"codes": uint8 [m, n], "scales", "in_seed", "levels": float32} (quantize.py:513-565, 1541-1553), on
+    the CPU; "model": the source model; the evaluation record of a run that skipped evaluation; "text weights";
+    "calibration"; and "row plan" (the validated row plan's manifest) when the build followed one}. Its consumers read
+    saved["matrices"] (compiler_artifact.export_saved_codes, finetune.py:114-115)."""
     saved = {}
     for key, rec in out["codes"].items():
         i, nm = key.split(".", 1)
@@ -495,7 +504,12 @@ def saved_codes(out: dict) -> dict:
             groups.append({"rows": rows, "bits": int(gp["bits"]), "table_index": ti})
         saved[name] = {"states": states, "scales": rec["scales"].float().cpu(), "in_seed": int(rec["in_seed"]),
                        "table": torch.cat(tabs), "row_groups": groups, "trellis_layout": "row"}
-    return saved
+    # (quantize.py:1734: a run without evaluation records it so; this path has no text data to evaluate on)
+    payload = {"matrices": saved, "model": SOURCE_MODEL, "evaluation": "skipped: no evaluation on this path",
+               "eval": 0, "ctx": None, "text weights": None, "calibration": calibration}
+    if row_plan is not None:
+        payload["row plan"] = row_plan
+    return payload
 
 
 def _stage_statistics(xq: list, w: list | None, xr: list | None, classes: list | None = None,
@@ -530,9 +544,17 @@ def _decode(states: torch.Tensor, S: torch.Tensor, groups: list, tables: dict) -
     widths = sorted(tables)
     cat = torch.cat([tables[b] for b in widths])
     size = tables[widths[0]].numel()
-    base = torch.empty(states.shape[0], dtype=torch.int64, pin_memory=True)
+    m = states.shape[0]
+    base = torch.empty(m, dtype=torch.int64, pin_memory=True)
+    seen = np.zeros(m, dtype=np.int64)
     for gp in groups:
-        base.numpy()[np.asarray(gp["rows"], dtype=np.int64)] = widths.index(int(gp["bits"])) * size
+        rows = np.asarray(gp["rows"], dtype=np.int64)
+        if rows.size and (rows.min() < 0 or rows.max() >= m):
+            raise ValueError("row group names a row outside the matrix")
+        np.add.at(seen, rows, 1)
+        base.numpy()[rows] = widths.index(int(gp["bits"])) * size
+    if not (seen == 1).all():  # (quantize.py:530-565: the groups cover every row exactly once)
+        raise ValueError("row groups do not cover every row exactly once")
     base = base.to(dev, non_blocking=True)
     return cat[states.long() + base[:, None]] * S[:, None]
 
@@ -540,7 +562,7 @@ def _decode(states: torch.Tensor, S: torch.Tensor, groups: list, tables: dict) -
 def _reconstruct(states: torch.Tensor, S: torch.Tensor, groups: list, tables: dict, in_seed: int) -> torch.Tensor:
     """W_hat = diag(S) table[states] R_in (codes.py:413-462 with out_rot=False)."""
     dev = states.device
-    dt = {b: torch.as_tensor(np.asarray(t, dtype=np.float64)).to(dev) for b, t in tables.items()}
+    dt = {b: torch.from_numpy(np.array(t, dtype=np.float64)).to(dev) for b, t in tables.items()}
     return E.rht_rows(_decode(states, S, groups, dt), in_seed, inverse=True)
 
 

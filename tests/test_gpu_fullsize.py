@@ -6,18 +6,20 @@ config 3 (one MLP block, quantize.py:1404-1470 and 1530-1560; syntax.py:86-124):
 [2560, 9728] with their 2.3 bpw row plans, both stages' Hessians from 131,072 tokens (10% weighted 10x), one factor per
 stage, the sweeps at L = 12 (the reference's fitted tables) and at L = 16 (the fp16 quantile table).
 
-config 5 (the layer loop, quantize.py:1626-1694): the first two decoder layers of the Qwen3.5-4B-shaped build
-(hidden 2,560, GQA 32/8 x 128, MLP 9,728), 32 x 2,048 calibration tokens through both streams, the QEP cross-Gram and
-targets, every stage's codes.
+config 5 (the layer loop, quantize.py:1626-1694; codes.py:151-181): the first two decoder layers of the
+Qwen3.5-4B-shaped build (hidden 2,560, GQA 32/8 x 128, MLP 9,728), 32 x 2,048 calibration tokens through both streams,
+the QEP cross-Gram and targets, every stage's codes, at L = 12 and at the benchmark's L = 16.
 
 What is checked, at each stage:
   - about 256 entries of H (and D) against float64 dot products over all tokens on the CPU: |err| <= 1e-4 of the
     entry's own scale sqrt(H_ii H_jj), and the largest error <= 1e-4 of max |H|;
   - the stage factor: U upper, U^T U Hd = I within 1e-6, Hd the rotated and damped H;
-  - 4 rows (2 at L = 16) of every row group of every matrix against the C oracle's row-trellis sweep of the same rows
-    under the build's own U and rotation, state for state;
+  - 4 rows (2 at config 3 and 3 at config 5 with L = 16) of every row group of every matrix against the C oracle's
+    row-trellis sweep of the same rows under the build's own U and rotation, state for state;
   - the packed words of every group unpack to its states (a path from state 0), and the device's path flag is clear;
-  - config 5: the reconstruction diag(S) table[states] R_in of the sampled rows against the oracle's (1e-10).
+  - config 5 (L = 12 and the benchmark's L = 16): the reconstruction diag(S) table[states] R_in of the first and last
+    row of every group against the oracle's (1e-10), and the bf16 weights the quantized stream went on with equal to
+    its rounding.
 """
 
 import os
@@ -162,15 +164,20 @@ def test_config3_mlp_block_full_size():
                 check_packed(E, st, plans[nm], packed, L, f"{nm} L={L}")
 
 
-def test_config5_first_two_layers_full_shape():
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("L", [12, 16])
+def test_config5_first_two_layers_full_shape(L):
+    """L = 12: the reference's fitted tables; L = 16: the benchmark's own configuration (the fp16 quantile table of
+    2^16 entries, the merged row-group launch, the device-resident table's decode of the quantized stream)."""
     from lookatmyquant_amd import engine as E
     from lookatmyquant_amd import stack
 
     sh = stack.Shape()
     tok, w = stack.calibration_tokens()
     wn = np.asarray(w, dtype=np.float64).reshape(-1)
-    say("config 5: two layers of the Qwen3.5-4B-shaped build, 32 x 2048 tokens, L=12")
-    out = stack.build(tok, sh, w, L=12, layers=2, keep=2)
+    per_group = 4 if L == 12 else 3
+    say(f"config 5: two layers of the Qwen3.5-4B-shaped build, 32 x 2048 tokens, L={L}")
+    out = stack.build(tok, sh, w, L=L, layers=2, keep=2)
     assert int(out["bad"].item()) == 0 and not out["redamped"]
     shapes = stack.matrix_shapes(sh)
     assert out["weights"] == 2 * sum(m * n for m, n in shapes.values())
@@ -188,10 +195,10 @@ def test_config5_first_two_layers_full_shape():
         for nm, groups in kept["plans"].items():
             rec = out["codes"][f"{i}.{nm}"]
             check_rows(E, kept["targets"][nm], kept["U"], kept["dead"], kept["in_seed"], groups, rec["states"],
-                       out["tables"], 12, 4, rng, f"{i}.{nm}")
-            check_packed(E, rec["states"], groups, rec["packed"], 12, f"{i}.{nm}")
-            # the reconstruction of a few rows: diag(S) table[states] R_in
-            pick = np.asarray(groups[0]["rows"][:3] + groups[-1]["rows"][-3:])
+                       out["tables"], L, per_group, rng, f"{i}.{nm}")
+            check_packed(E, rec["states"], groups, rec["packed"], L, f"{i}.{nm}")
+            # the reconstruction of a few rows of every group: diag(S) table[states] R_in
+            pick = np.unique(np.concatenate([np.asarray(g["rows"])[[0, -1]] for g in groups]))
             Wh = stack._reconstruct(rec["states"], rec["scales"], groups, out["tables"], kept["in_seed"])
             Wh = Wh[torch.as_tensor(pick).cuda()].cpu().numpy()
             st = rec["states"].cpu().numpy()[pick]
@@ -200,6 +207,11 @@ def test_config5_first_two_layers_full_shape():
             Q *= rec["scales"].cpu().numpy()[pick][:, None]
             ref = O.rht_apply(Q, kept["in_seed"], inverse=True)
             assert np.abs(Wh - ref).max() <= 1e-10 * np.abs(ref).max()
+            # the weights the build's quantized stream went on with: the bf16 rounding of that reconstruction (the
+            # layer loop's own decode through the device-resident tables and inverse rotation)
+            Wq = kept["Wq"][nm][torch.as_tensor(pick).cuda()].float().cpu().numpy().astype(np.float64)
+            assert (np.abs(Wq - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-30).all(), f"{i}.{nm}: quantized stream weights"
+            say(f"  {i}.{nm}: {len(pick)} reconstructed rows and the stream's bf16 weights match the oracle's")
 
 
 def test_config5_build_is_reproducible():

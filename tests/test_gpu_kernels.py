@@ -503,6 +503,46 @@ def test_ldlq_trellis16_groups_in_one_launch_equal_each_group_alone(E):
     assert np.array_equal(merged[36].cpu().numpy(), ref[0])
 
 
+@pytest.mark.parametrize("L", [12, 16])
+def test_ldlq_trellis_nan_row_stays_in_range(E, tables, L):
+    """A row whose target is NaN (every path cost NaN from its first position on) gets states inside the table, so the
+    traceback, the next search's start and any later table lookup stay in bounds: the two-pass final argmin of the
+    16-bit-state searches falls back to state 0, the reference's argmin of an all-NaN row. The other rows of the same
+    launch (groups at k = 1..4, one launch per lazy block at L = 16) equal the oracle's states."""
+    from lookatmyquant_amd.tables import quantile_table
+
+    rng = np.random.default_rng(91)
+    n = 272
+    sizes, widths = [5, 4, 4, 5], [1, 2, 3, 4]
+    m = sum(sizes)
+    Xa = rng.standard_normal((2 * n, n))
+    _, U, _ = O.environment(Xa.T @ Xa / (2 * n))
+    X = rng.standard_normal((m, n))
+    S = O.row_scale(X)
+    nan_rows = [1, 6, 10, 17]  # one row of each width's group
+    X[nan_rows] = np.nan
+    S[nan_rows] = 1.0
+    tabs = {k: (np.array(quantile_table(16, 0)) if L == 16 else np.array(tables[k])) for k in widths}
+    say(f"ldlq trellis L={L}: {m} rows in groups k = 1..4, rows {nan_rows} NaN")
+    if L == 16:
+        tab = cuda(tabs[1])
+        st = E.ldlq_trellis_groups(cuda(X), cuda(S), cuda(U), [(r, k, tab, None) for r, k in zip(sizes, widths)], 16)
+    else:
+        parts, r0 = [], 0
+        for r, k in zip(sizes, widths):
+            parts.append(E.ldlq_trellis(cuda(X[r0:r0 + r]), cuda(S[r0:r0 + r]), cuda(U), cuda(tabs[k]), 12, k))
+            r0 += r
+        st = torch.cat(parts)
+    st = st.cpu().numpy()
+    assert st.min() >= 0 and st.max() < (1 << L)
+    r0 = 0
+    for r, k in zip(sizes, widths):
+        keep = [i for i in range(r0, r0 + r) if i not in nan_rows]
+        ref = O.ldlq_trellis(X[keep], U, S[keep], tabs[k], L, k)
+        assert np.array_equal(st[keep], ref), k
+        r0 += r
+
+
 def test_ldlq_trellis_ragged_matches_oracle(E, tables):
     """n not a multiple of the lazy block or of the width, m not a multiple of anything."""
     rng = np.random.default_rng(11)

@@ -225,7 +225,10 @@ def test_cli_plan_driven_build(tmp_path):
     assert abs(res["bits per weight"] - 2.3) < 0.1
     assert res["row plan"]["matrices"] == 7
     assert res["artifact"]["all_tensor_bytes_verified"] and res["artifact"]["tensor_count"] > 7
-    saved = torch.load(tmp_path / "codes.pt", weights_only=True)
+    payload = torch.load(tmp_path / "codes.pt", weights_only=True)
+    # the reference's --save-codes layout (quantize.py:1737-1739): its consumers read payload["matrices"]
+    assert payload["row plan"]["matrices"] == 7 and payload["model"] and payload["evaluation"].startswith("skipped")
+    saved = payload["matrices"]
     assert sorted(saved) == sorted(f"model.layers.0.{nm}.weight" for nm in shapes)
     for name, e in saved.items():
         m, n = shapes[name.split(".", 3)[3][: -len(".weight")]]
@@ -235,6 +238,19 @@ def test_cli_plan_driven_build(tmp_path):
         for g in e["row_groups"]:
             s = e["states"][g["rows"]].long() - 4096 * g["table_index"]
             assert int(s.min()) >= 0 and int(s.max()) < 4096
+    # the saved file through the reference's consumer (compiler_artifact.export_saved_codes): the same packed words as
+    # the artifact the build wrote from its own packed groups
+    from lookatmyquant_amd import artifact
+
+    dense = {name: np.zeros(tuple(e["states"].shape), dtype=np.float32) for name, e in saved.items()}
+    artifact.export_saved_codes(payload, tmp_path / "art2", dense_tensors=dense)
+    t1, m1 = artifact.read_artifact(tmp_path / "art")
+    t2, m2 = artifact.read_artifact(tmp_path / "art2")
+    assert sorted(m1["matrices"]) == sorted(m2["matrices"]) == sorted(saved)
+    assert sorted(t1) == sorted(t2)
+    for key in t1:
+        if key.endswith((".codes", ".rows", ".scales", ".table", ".signs")):
+            assert np.array_equal(np.asarray(t1[key]), np.asarray(t2[key])), key
     print("quantize --program tr3x, one layer", flush=True)
     main(["--program", "tr3x", *small, "--out", str(tmp_path / "res3.json")])
     res3 = json.loads((tmp_path / "res3.json").read_text())

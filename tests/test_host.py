@@ -293,7 +293,7 @@ def test_trellis_tables_must_have_two_to_the_L_entries():
     t12 = torch.from_numpy(load_table(12, 2).copy())
     X = torch.zeros(4, 64, dtype=torch.float64)
     for L, t64, t32 in ((16, t12, None), (12, t12[:100], None), (12, t12, t12[:4095].float()),
-                        (16, torch.from_numpy(np.asarray(quantile_table(16, 0), dtype=np.float64)), t12.float())):
+                        (16, torch.from_numpy(np.array(quantile_table(16, 0), dtype=np.float64)), t12.float())):
         with pytest.raises(ValueError, match="2\\^L"):
             E.ldlq_trellis_groups(X, torch.ones(4, dtype=torch.float64), torch.eye(64, dtype=torch.float64),
                                   [(4, 2, t64, t32)], L)
