@@ -16,6 +16,9 @@
 #include "common.h"
 
 #define LAMQ_WMAX 16      // widest block the fused kernels settle at once
+#ifndef LAMQ_RAMP_LOG_STATES
+#define LAMQ_RAMP_LOG_STATES 10  // L > 12: the ramp of a fixed start ends at the last position reaching <= 2^this states
+#endif
 #define LAMQ_PRE_MAX 1024  // most earlier columns of a run whose updates a block takes itself (pre)
 
 template <int L, int K, int NT>
@@ -70,16 +73,31 @@ struct TabF32 {
     float v[V::SPT];
     __device__ __forceinline__ void load(const float* __restrict__ C, int t)
     {
+        src = C;
 #pragma unroll
         for (int h = 0; h < V::NB; ++h)
 #pragma unroll
             for (int g = 0; g < V::G; ++g) v[h * V::G + g] = C[h * V::R + V::G * t + g];
     }
+    const float* src;  // the whole table (the ramp of a fixed start reads other threads' states there)
     __device__ __forceinline__ void hold() {}
     __device__ __forceinline__ float dsq(float x, int i) const
     {
         const float d = x - v[i];
         return d * d;
+    }
+    // (x - C[s])^2 of state s, and of the states s, s + 1 (s even), read from memory
+    __device__ __forceinline__ float dsq_at(float x, uint32_t s) const
+    {
+        const float d = x - src[s];
+        return d * d;
+    }
+    __device__ __forceinline__ void dsq_at2(float x, uint32_t s, float& q0, float& q1) const
+    {
+        const float2 c = *reinterpret_cast<const float2*>(src + s);
+        const float d0 = x - c.x, d1 = x - c.y;
+        q0 = d0 * d0;
+        q1 = d1 * d1;
     }
 };
 
@@ -88,7 +106,7 @@ template <class V>
 struct TabF16 {
     static_assert(V::G % 2 == 0, "members in pairs");
     uint32_t v[V::SPT / 2];
-    const uint16_t* src;  // the whole table (the one-wave ramp of a fixed start reads other threads' states there)
+    const uint16_t* src;  // the whole table (the ramp of a fixed start reads other threads' states there)
     __device__ __forceinline__ void load(const uint16_t* __restrict__ C16, int t)
     {
         src = C16;
@@ -109,6 +127,18 @@ struct TabF16 {
         const float d = (i & 1) ? xmc_hi(x, v[i >> 1]) : xmc_lo(x, v[i >> 1]);
         return d * d;
     }
+    __device__ __forceinline__ float dsq_at(float x, uint32_t s) const
+    {
+        const float d = xmc_lo(x, (uint32_t)src[s]);
+        return d * d;
+    }
+    __device__ __forceinline__ void dsq_at2(float x, uint32_t s, float& q0, float& q1) const
+    {
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(src + s);
+        const float d0 = xmc_lo(x, w), d1 = xmc_hi(x, w);
+        q0 = d0 * d0;
+        q1 = d1 * d1;
+    }
 };
 
 // f(IntC<v>{}) for the uniform v in [I, N): a chain of scalar branches, so that f indexes registers statically
@@ -126,11 +156,6 @@ __device__ __forceinline__ void uniform_switch(int v, F& f)
             uniform_switch<I + 1, N>(v, f);
     }
 }
-
-// The one-wave ramp of a fixed start (viterbi_gx): a lane's states at position t (the ancestors of its 2^LQ states at
-// position T0).
-template <int K, int T0, int LQ>
-constexpr int ramp_nts(int t) { return K * (T0 - t) >= LQ ? 1 : ((1 << LQ) >> (K * (T0 - t))); }
 
 // f(IntC<I>{}), f(IntC<I + 1>{}), ..., f(IntC<N - 1>{})
 template <int I, int N, class F>
@@ -398,11 +423,129 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
         }
         if (!DBL) lds_barrier();
     };
+    // The ramp of a fixed start. Position t reaches only the 2^(K (t+1)) states base_t + i (i < 2^(K (t+1))),
+    // base_t = (start << K (t+1)) mod 2^L, each with exactly one reachable predecessor, base_(t-1) + (i >> K), while
+    // the range lies in the slab of one h (K (t+1) <= L - K). The path cost of base_t + i is then that predecessor's
+    // cost plus (x_t - C)^2, the value the full step forms (the minimum over one finite member is that member, and
+    // 0 + (x_0 - C)^2 at position 0). Positions 0 .. T1 are therefore taken by every thread at once with no exchange
+    // and no barrier: thread tid follows the ancestors of the states i0 .. i0 + Q - 1 of T1's range (i0 = Q tid; at
+    // position t the distinct ancestors ((i0 + j) >> K (T1 - t)), j < Q), reading the table from memory, and stores
+    // their costs as the minima of their groups rb + i (T1's range covers groups rb .. rb + SPAN - 1); the owners of
+    // the groups outside it store +inf. Each thread also writes its back-pointer word of every position its groups
+    // reach (winner hl = base_t >> (L - K) in every field, as the one-slab step writes them). Minima buffer 0 then holds
+    // exactly the minima of position T1 and the steps go on from T1 + 1. T1 is the last position whose range fits the
+    // slab (T0) where the table is small (L <= 12: float32, 16 KB), and at most the one whose range holds one state per
+    // thread at L = 16: there a wider ramp reads more of the 128 KB fp16 table from memory than the one-slab steps
+    // (register-held table, one barrier each) that take the positions up to T0 cost.
+    constexpr int LNT = LAMQ_RAMP_LOG_STATES;
+    constexpr int T0 = (L - K) / K - 1;  // the last position whose range fits one slab
+    constexpr int T1 = L <= 12 ? T0 : (LNT / K - 1 < T0 ? LNT / K - 1 : T0);
+    constexpr int LS = K * (T1 + 1);  // log2 of T1's range
+    constexpr bool RAMP = V::R >= NT && T1 >= 1;
+    int tb = 0;
+    if constexpr (RAMP) {
+        if (st0 >= 0 && T1 <= TV - 2) {
+            constexpr int SPAN = 1 << LS;
+            constexpr int Q = SPAN > NT ? SPAN / NT : 1;  // states a thread takes
+            constexpr int CK4 = G < 4 ? G : 4;
+            static_assert(SPAN >= G && SPAN % Q == 0, "T1's range: whole blocks of G groups, Q states a thread");
+            const uint32_t su = (uint32_t)st0;
+            const int rb = (int)((su << LS) & (uint32_t)(R - 1));
+            if (G * tid < rb || G * tid >= rb + SPAN) {
+                float infs[CK4];
+#pragma unroll
+                for (int i = 0; i < CK4; ++i) infs[i] = __builtin_inff();
+#pragma unroll
+                for (int e = 0; e < G / CK4; ++e) lds_store_swz<CK4>(buf, G * tid + e * CK4, infs);
+            }
+            if (Q * tid < SPAN) {
+                // the offset through an opaque move: the addresses below are formed here, not hoisted out of the
+                // caller's loop over searches (held across it, they would take registers the steps need)
+                uint32_t ii = (uint32_t)(Q * tid);
+                asm volatile("" : "+v"(ii));
+                // depth first, to keep few costs live: positions 0 .. TC, where all of this thread's states share one
+                // ancestor, once; then the states in chunks of CH, each chunk's ancestors at TC + 1 .. T1 (at
+                // position t the chunk's distinct ancestors ((i0 + CH c) >> K (T1 - t)) + j)
+                constexpr int LGQ = __builtin_ctz(Q);
+                constexpr int TC = T1 - ((LGQ + K - 1) / K > 1 ? (LGQ + K - 1) / K : 1);  // (T1 itself is a chunk's)
+                constexpr int CH = Q < 8 ? Q : 8;
+                constexpr int CPN = (CH >> K) > 0 ? (CH >> K) : 1;  // a chunk's ancestors at T1 - 1
+                float c0 = 0.0f;  // the start's group minimum
+                const auto common = [&](auto tc) {
+                    constexpr int t = decltype(tc)::value;
+                    const uint32_t idx = ((su << (K * (t + 1))) & (uint32_t)(V::NS - 1)) + (ii >> (K * (T1 - t)));
+                    c0 = c0 + tab.dsq_at(xs[t], idx);
+                };
+                static_for<0, TC + 1>(common);
+#pragma unroll
+                for (int cc = 0; cc < Q / CH; ++cc) {
+                    // one chunk's table loads at a time (issued all at once they take a register each)
+                    __builtin_amdgcn_sched_barrier(0);
+                    const uint32_t ic = ii + (uint32_t)(CH * cc);
+                    float cp[CPN];
+                    cp[0] = c0;
+                    const auto pos = [&](auto tc) {
+                        constexpr int t = decltype(tc)::value;
+                        constexpr int SH = K * (T1 - t);
+                        constexpr int NTS = (CH >> SH) > 0 ? (CH >> SH) : 1;
+                        const uint32_t idx = ((su << (K * (t + 1))) & (uint32_t)(V::NS - 1)) + (ic >> SH);
+                        const float xt = xs[t];
+                        float cn[NTS];
+                        if constexpr (NTS == 1) {
+                            cn[0] = cp[0] + tab.dsq_at(xt, idx);
+                        } else {
+#pragma unroll
+                            for (int j = 0; j < NTS; j += 2) {
+                                float q0, q1;
+                                tab.dsq_at2(xt, idx + j, q0, q1);
+                                cn[j] = cp[j >> K] + q0;
+                                cn[j + 1] = cp[(j + 1) >> K] + q1;
+                            }
+                        }
+                        if constexpr (t < T1) {
+#pragma unroll
+                            for (int j = 0; j < NTS; ++j) cp[j] = cn[j];
+                        } else {
+                            lds_store_swz<CH>(buf, rb + (int)ic, cn);
+                        }
+                    };
+                    static_for<TC + 1, T1 + 1>(pos);
+                }
+            }
+            // the back-pointer words of positions 0 .. T1: thread tid's, where its groups are reached (the word's address
+            // formed from an opaque copy of tid, so that the T1 + 1 addresses are not hoisted out of the caller's loop
+            // over searches and held across it)
+            int to = tid;
+            asm volatile("" : "+v"(to));
+            BackT* const bw = back + to;
+            const auto words = [&](auto tc) {
+                constexpr int t = decltype(tc)::value;
+                constexpr int span = 1 << (K * (t + 1));
+                constexpr int no = span >= G ? span / G : 1;
+                const uint32_t base = (su << (K * (t + 1))) & (uint32_t)(V::NS - 1);
+                const int olo = (int)(base & (uint32_t)(R - 1)) / G;
+                if (tid >= olo && tid < olo + no) bw[t * V::ACT] = (BackT)((base >> (L - K)) * REP);
+            };
+            static_for<0, T1 + 1>(words);
+            lds_barrier();
+            dirty0 = wave_live(T1);
+            dirty1 = true;
+            cur = 0;
+            x = xs[T1 + 1];
+            live = wave_live(T1 + 1);
+            if (act && live) {
+#pragma unroll
+                for (int h = 0; h < NB; ++h) load_minima(buf, h);
+            }
+            if (!DBL) lds_barrier();
+            tb = T1 + 1;
+        }
+    }
+    if (tb == 0) start_minima();
     if constexpr (L <= 12 && DBL) {
-        start_minima();
         // a step at L <= 12 is short: two steps per iteration, each with its buffer a constant (immediate LDS offsets
-        // instead of addresses formed every step)
-        int t = 0;
+        // instead of addresses formed every step); step t reads buffer (t - tb) & 1
+        int t = tb;
         for (; t + 1 < TV - 1; t += 2) {
             int c0 = 0, c1 = 1;
             step(t, c0);
@@ -412,111 +555,8 @@ __device__ int viterbi_gx(const float* xs, int TV, Tab& tab, int start, float* b
             int c0 = 0;
             step(t, c0);
         }
-        cur = (TV - 1) & 1;
+        cur = (TV - 1 - tb) & 1;
     } else {
-        int tb = 0;
-        if constexpr (SKIP && (K == 2 || K == 3)) {
-            // From a fixed start the first positions reach few states: position t the 2^(K (t+1)) states
-            // base_t + i (i < 2^(K (t+1))), base_t = (start << K (t+1)) mod 2^L, each with exactly one reachable
-            // predecessor, base_(t-1) + (i >> K). While that holds (one slab, K (t+1) <= L - K) the path cost of
-            // base_t + i is the cost of that predecessor plus (x_t - C)^2, the value the full step forms (the group
-            // minimum over one finite member is that member). Positions 0 .. T0 (at most 1,024 states at T0) are
-            // therefore taken by wave 0 alone, each lane following the ancestors of its Q states at T0
-            // (Q l .. Q l + Q - 1) with no exchange between lanes and no barrier, the table entries read from
-            // memory; it writes those states' costs as the group minima of position T0 and the back-pointer
-            // words of the groups each position reaches (winner hl = base_t >> (L - K) in every field, as the
-            // one-slab step writes them). Every other thread stores +inf into its own entries outside that range,
-            // so minima buffer 0 holds exactly the minima of position T0 and the steps go on from T0 + 1. For
-            // k = 2 and 3 (k = 2: positions 0-4, k = 3: 0-2); at k = 1 the second path costs the kernel spilled
-            // registers, at k = 4 it would replace two steps only.
-            constexpr int LS = 10 < L - K ? 10 : L - K;
-            constexpr int T0 = LS / K - 1;
-            constexpr int LQ = K * (T0 + 1) - 6;
-            constexpr int Q = 1 << LQ;
-            static_assert(LQ >= 2 && Q <= 16 && 64 * Q >= G && (1 << (K * (T0 + 1))) <= R, "one-wave ramp shape");
-            if (st0 >= 0 && T0 <= TV - 2) {
-                constexpr int SPAN = 64 * Q;
-                const uint32_t su = (uint32_t)st0;
-                const int rb = (int)((su << (K * (T0 + 1))) & (uint32_t)(R - 1));
-                if (act && !(G * tid >= rb && G * tid < rb + SPAN)) {
-                    constexpr int CKI = G < 4 ? G : 4;
-                    float infs[CKI];
-#pragma unroll
-                    for (int i = 0; i < CKI; ++i) infs[i] = __builtin_inff();
-#pragma unroll
-                    for (int e = 0; e < G / CKI; ++e) lds_store_swz<CKI>(buf, G * tid + e * CKI, infs);
-                }
-                if (tid < 64) {
-                    // the lane index through an opaque move: the addresses below are formed here, not hoisted out of
-                    // the caller's loop over searches (held across it, they would take registers the steps need)
-                    uint32_t ln = (uint32_t)tid;
-                    asm volatile("" : "+v"(ln));
-                    // the path costs of this lane's ancestors, position by position (at most Q / NB of them before
-                    // T0); position T0 in chunks of four states, each stored as soon as it is formed (few registers
-                    // live at once: the search loop's allocation is the kernel's)
-                    float cp[Q / NB > 0 ? Q / NB : 1];
-                    cp[0] = 0.0f;  // the start's group minimum
-                    const auto back_words = [&](int t, uint32_t base) {  // the owners of the groups t reaches
-                        const int span = 1 << (K * (t + 1));
-                        const int no = span >= G ? span / G : 1;
-                        const int olo = (int)(base & (uint32_t)(R - 1)) / G;
-                        if ((int)ln < no) back[t * V::ACT + olo + (int)ln] = (BackT)((base >> (L - K)) * REP);
-                    };
-                    const auto pos = [&](auto tc) {
-                        constexpr int t = decltype(tc)::value;
-                        constexpr int SH = K * (T0 - t);
-                        constexpr int NTS = ramp_nts<K, T0, LQ>(t);  // this lane's states at position t
-                        const uint32_t base = (su << (K * (t + 1))) & (uint32_t)(V::NS - 1);
-                        const uint16_t* c16 = tab.src + base + (((uint32_t)Q * ln) >> SH);
-                        const float xt = xs[t];
-                        float cn[NTS];
-#pragma unroll
-                        for (int j = 0; j < NTS; j += 2) {
-                            const uint32_t w = NTS == 1 ? (uint32_t)c16[0] : *reinterpret_cast<const uint32_t*>(c16 + j);
-                            const float d0 = xmc_lo(xt, w);
-                            cn[j] = cp[j >> K] + d0 * d0;
-                            if (j + 1 < NTS) {
-                                const float d1 = xmc_hi(xt, w);
-                                cn[j + 1] = cp[(j + 1) >> K] + d1 * d1;
-                            }
-                        }
-#pragma unroll
-                        for (int j = 0; j < NTS; ++j) cp[j] = cn[j];
-                        back_words(t, base);
-                    };
-                    static_for<0, T0>(pos);
-                    {
-                        const uint32_t base = (su << (K * (T0 + 1))) & (uint32_t)(V::NS - 1);
-                        const uint16_t* c16 = tab.src + base + (uint32_t)Q * ln;
-                        const float xt = xs[T0];
-#pragma unroll
-                        for (int c = 0; c < Q; c += 4) {
-                            const uint32_t w0 = *reinterpret_cast<const uint32_t*>(c16 + c);
-                            const uint32_t w1 = *reinterpret_cast<const uint32_t*>(c16 + c + 2);
-                            const float d[4] = {xmc_lo(xt, w0), xmc_hi(xt, w0), xmc_lo(xt, w1), xmc_hi(xt, w1)};
-                            float cn[4];
-#pragma unroll
-                            for (int j = 0; j < 4; ++j) cn[j] = cp[(c + j) >> K] + d[j] * d[j];
-                            lds_store_swz<4>(buf, rb + Q * (int)ln + c, cn);
-                        }
-                        back_words(T0, base);
-                    }
-                }
-                lds_barrier();
-                dirty0 = wave_live(T0);
-                dirty1 = true;
-                cur = 0;
-                x = xs[T0 + 1];
-                live = wave_live(T0 + 1);
-                if (act && live) {
-#pragma unroll
-                    for (int h = 0; h < NB; ++h) load_minima(buf, h);
-                }
-                if (!DBL) lds_barrier();
-                tb = T0 + 1;
-            }
-        }
-        if (tb == 0) start_minima();
         for (int t = tb; t < TV - 1; ++t) step(t, cur);
     }
     int* redi = reinterpret_cast<int*>(red + NT / 64);
