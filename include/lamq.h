@@ -151,6 +151,23 @@ int lamq_ldlq_trellis16_block_groups(double* T, int64_t m, int64_t n, int64_t ld
                                      int64_t b0, int64_t b1, int width, int look, int32_t* state, int32_t* states,
                                      int64_t lds, double* Z, int64_t ldZ, int64_t pre, void* stream);
 
+/* The same batched block for the 12-bit-state trellis (L = 12, the reference's fitted tables; 1 <= k <= 4): group g
+ * is the rows [r0, r0 + rows) of T, S, state, states and Z, swept at its k with its float64 and float32 tables (each
+ * 4,096 entries), exactly as lamq_ldlq_trellis_block sweeps that group alone (the same states, Z and T, bit for bit);
+ * one launch over all the rows leaves no idle tail between the groups' launches. At most LAMQ_TRELLIS_MAX_GROUPS
+ * groups; their row ranges lie in [0, m) and do not overlap. L other than 12: LAMQ_EUNSUP. */
+typedef struct {
+    int64_t r0;
+    int64_t rows;
+    int k;
+    const double* table64;
+    const float* table32;
+} lamq_trellis_group32;
+int lamq_ldlq_trellis_block_groups(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU,
+                                   const double* S, int L, const lamq_trellis_group32* groups, int ngroups,
+                                   int64_t b0, int64_t b1, int width, int look, int32_t* state, int32_t* states,
+                                   int64_t lds, double* Z, int64_t ldZ, int64_t pre, void* stream);
+
 /* ------------------------------------------------------------------------------------------------
  * The lazy trailing update T[:, b1:n] -= Z @ U[b0:b1, b1:n] on fp64 MFMA.
  * Replaces opgraph/syntax.py:122-123 (and opgraph/ldlq_gpu.py:48).

@@ -36,6 +36,8 @@ SIGNATURES = {
                                               ctypes.c_size_t, _p]),
     "lamq_ldlq_trellis16_block_groups": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _c_int, _p, _c_int,
                                                   _c_i64, _c_i64, _c_int, _c_int, _p, _p, _c_i64, _p, _c_i64, _c_i64, _p]),
+    "lamq_ldlq_trellis_block_groups": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _c_int, _p, _c_int, _c_i64,
+                                                _c_i64, _c_int, _c_int, _p, _p, _c_i64, _p, _c_i64, _c_i64, _p]),
     "lamq_trailing_update_f64": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _c_i64, _c_i64, _c_i64, _p]),
     "lamq_gemm_sub_f64": (_c_int, [_p, _c_i64, _p, _c_i64, _p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _p]),
     "lamq_refit_step": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _c_i64, _p, _c_i64, _c_i64, _c_int, _c_i64, _c_i64, _p,
@@ -72,6 +74,12 @@ class TrellisGroup(ctypes.Structure):
 
     _fields_ = [("r0", _c_i64), ("rows", _c_i64), ("k", _c_int), ("table64", _p), ("table16", _p), ("workspace", _p),
                 ("workspace_bytes", _c_size)]
+
+
+class TrellisGroup32(ctypes.Structure):
+    """lamq_trellis_group32 of include/lamq.h: one row group of lamq_ldlq_trellis_block_groups (L = 12)."""
+
+    _fields_ = [("r0", _c_i64), ("rows", _c_i64), ("k", _c_int), ("table64", _p), ("table32", _p)]
 
 
 _LIB = None

@@ -17,7 +17,7 @@
 
 #define LAMQ_WMAX 16      // widest block the fused kernels settle at once
 #ifndef LAMQ_RAMP_LOG_STATES
-#define LAMQ_RAMP_LOG_STATES 10  // L > 12: the ramp of a fixed start ends at the last position reaching <= 2^this states
+#define LAMQ_RAMP_LOG_STATES 13  // L > 12: the ramp of a fixed start ends at the last position reaching <= 2^this states
 #endif
 #define LAMQ_PRE_MAX 1024  // most earlier columns of a run whose updates a block takes itself (pre)
 

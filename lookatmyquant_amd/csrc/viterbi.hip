@@ -84,26 +84,31 @@ extern "C" int lamq_viterbi_rows(const float* x, int64_t B, int T, int64_t ldx, 
 // values are table64[states] * S; columns >= b1 get the trailing update from Z afterwards).
 // ------------------------------------------------------------------------------------------------
 template <int L, int K>
-__global__ __launch_bounds__(LAMQ_NT) void ldlq_trellis_block_kernel(
-    const double* __restrict__ T, int64_t n, int64_t ldT, const double* __restrict__ U, int64_t ldU,
-    const double* __restrict__ S, const double* __restrict__ table64, const float* __restrict__ table32,
-    int64_t b0, int64_t b1, int width, int look, int32_t* __restrict__ state, int32_t* __restrict__ states,
-    int64_t lds, double* __restrict__ Z, int64_t ldZ, int pre)
+struct alignas(16) BlkSmem {
+    using V = VX<L, K, LAMQ_NT>;
+    float buf[2 * V::R];
+    uint8_t back[(LAMQ_TV_BLK - 1) * V::ACT];
+    double trow[LAMQ_LAZY_MAX + LAMQ_TV_BLK];
+    double urows[LAMQ_WMAX][LAMQ_LAZY_MAX];
+    double zs[LAMQ_WMAX];
+    float xs[LAMQ_TV_BLK];
+    int path[LAMQ_TV_BLK];
+    float red[2 * (LAMQ_NT / 64)];
+};
+
+// One row's lazy block [b0, b1): `row` indexes T, S, state, states and Z.
+template <int L, int K>
+__device__ __forceinline__ void trellis_block_row(BlkSmem<L, K>& sm, int64_t row, const double* __restrict__ T, int64_t n,
+                                                  int64_t ldT, const double* __restrict__ U, int64_t ldU,
+                                                  const double* __restrict__ S, const double* __restrict__ table64,
+                                                  const float* __restrict__ table32, int64_t b0, int64_t b1, int width,
+                                                  int look, int32_t* __restrict__ state, int32_t* __restrict__ states,
+                                                  int64_t lds, double* __restrict__ Z, int64_t ldZ, int pre)
 {
     using V = VX<L, K, LAMQ_NT>;
-    __shared__ __align__(16) float buf[2 * V::R];
-    __shared__ uint8_t back[(LAMQ_TV_BLK - 1) * V::ACT];
-    __shared__ __align__(16) double trow[LAMQ_LAZY_MAX + LAMQ_TV_BLK];
-    __shared__ __align__(16) double urows[LAMQ_WMAX][LAMQ_LAZY_MAX];
-    __shared__ double zs[LAMQ_WMAX];
-    __shared__ float xs[LAMQ_TV_BLK];
-    __shared__ int path[LAMQ_TV_BLK];
-    __shared__ float red[2 * (LAMQ_NT / 64)];
-
-    const int64_t row = blockIdx.x;
     const int tid = threadIdx.x;
     const int64_t cend = (b1 + look < n) ? b1 + look : n;
-    load_block_row<LAMQ_NT>(trow, T + row * ldT, b0, (int)(b1 - b0), (int)(cend - b0), Z + row * ldZ - pre, pre, U,
+    load_block_row<LAMQ_NT>(sm.trow, T + row * ldT, b0, (int)(b1 - b0), (int)(cend - b0), Z + row * ldZ - pre, pre, U,
                             ldU);
     TabF32<V> tab;
     if (tid < V::ACT) tab.load(table32, tid);
@@ -118,15 +123,27 @@ __global__ __launch_bounds__(LAMQ_NT) void ldlq_trellis_block_kernel(
         const int TV = w + a;
         const int jo = (int)(j - b0);
         const int nc = (int)(b1 - j - w);
-        refit_fetch_lds<LAMQ_NT, LAMQ_LAZY_MAX>(urows, U, ldU, j, w, b1);
-        if (tid < TV) xs[tid] = (float)(trow[jo + tid] / Sr);
+        refit_fetch_lds<LAMQ_NT, LAMQ_LAZY_MAX>(sm.urows, U, ldU, j, w, b1);
+        if (tid < TV) sm.xs[tid] = (float)(sm.trow[jo + tid] / Sr);
         lds_barrier();
-        const int pv = viterbi_gx<L, K, LAMQ_NT, true, false, true>(xs, TV, tab, st, buf, back, path, red);
-        refit_apply_lds<LAMQ_NT, LAMQ_LAZY_MAX>(urows, trow, jo, w, nc, pv, table64, Sr, states + row * lds + j,
-                                                Z + row * ldZ + jo, zs);
-        st = path[w - 1];
+        const int pv = viterbi_gx<L, K, LAMQ_NT, true, false, true>(sm.xs, TV, tab, st, sm.buf, sm.back, sm.path, sm.red);
+        refit_apply_lds<LAMQ_NT, LAMQ_LAZY_MAX>(sm.urows, sm.trow, jo, w, nc, pv, table64, Sr, states + row * lds + j,
+                                                Z + row * ldZ + jo, sm.zs);
+        st = sm.path[w - 1];
     }
     if (tid == 0) state[row] = st;
+}
+
+template <int L, int K>
+__global__ __launch_bounds__(LAMQ_NT) void ldlq_trellis_block_kernel(
+    const double* __restrict__ T, int64_t n, int64_t ldT, const double* __restrict__ U, int64_t ldU,
+    const double* __restrict__ S, const double* __restrict__ table64, const float* __restrict__ table32,
+    int64_t b0, int64_t b1, int width, int look, int32_t* __restrict__ state, int32_t* __restrict__ states,
+    int64_t lds, double* __restrict__ Z, int64_t ldZ, int pre)
+{
+    __shared__ BlkSmem<L, K> sm;
+    trellis_block_row<L, K>(sm, blockIdx.x, T, n, ldT, U, ldU, S, table64, table32, b0, b1, width, look, state, states,
+                            lds, Z, ldZ, pre);
 }
 
 template <int L, int K>
@@ -157,4 +174,109 @@ extern "C" int lamq_ldlq_trellis_block(double* T, int64_t m, int64_t n, int64_t 
     if (m == 0) return LAMQ_OK;
     return dispatch_lk<TrellisBlock>(L, k, T, m, n, ldT, U, ldU, S, table64, table32, b0, b1, width, look, state,
                                      states, lds, Z, ldZ, (int)pre, as_stream(stream));
+}
+
+// ------------------------------------------------------------------------------------------------ row groups at once
+// One launch for every row group of a stage at L = 12 (the reference's fitted tables): a launch per group ends in a
+// tail of partly idle CUs (four 256-thread rows per CU, so ceil(rows / 1024) rounds), which one launch over all their
+// rows does not have. Workgroup b takes row b of the concatenated groups (in the table's order), finds its group (a
+// uniform scan of at most LAMQ_TRELLIS_MAX_GROUPS entries) and runs that width's block in that width's LDS layout
+// over one shared array (the widest layout's size: four workgroups per CU as for each width alone).
+#define LAMQ_GROUPS_L 12
+struct BlkGroup {
+    int64_t r0, rows;
+    const double* table64;
+    const float* table32;
+    int k;
+};
+struct BlkGroups {
+    BlkGroup g[LAMQ_TRELLIS_MAX_GROUPS];
+    int count;
+};
+
+template <int L>
+constexpr int blk_groups_smem_bytes()
+{
+    int b = (int)sizeof(BlkSmem<L, 1>);
+    b = (int)sizeof(BlkSmem<L, 2>) > b ? (int)sizeof(BlkSmem<L, 2>) : b;
+    b = (int)sizeof(BlkSmem<L, 3>) > b ? (int)sizeof(BlkSmem<L, 3>) : b;
+    b = (int)sizeof(BlkSmem<L, 4>) > b ? (int)sizeof(BlkSmem<L, 4>) : b;
+    return b;
+}
+
+template <int L>
+__global__ __launch_bounds__(LAMQ_NT) void ldlq_trellis_groups_kernel(
+    const double* __restrict__ T, int64_t n, int64_t ldT, const double* __restrict__ U, int64_t ldU,
+    const double* __restrict__ S, int64_t b0, int64_t b1, int width, int look, int32_t* __restrict__ state,
+    int32_t* __restrict__ states, int64_t lds, double* __restrict__ Z, int64_t ldZ, int pre, BlkGroups groups)
+{
+    static_assert(blk_groups_smem_bytes<L>() * 4 <= 160 * 1024, "four workgroups per CU");
+    __shared__ __align__(16) uint8_t raw[blk_groups_smem_bytes<L>()];
+    int64_t b = blockIdx.x;
+    int i = 0;
+    while (i + 1 < groups.count && b >= groups.g[i].rows) {
+        b -= groups.g[i].rows;
+        ++i;
+    }
+    const BlkGroup& G = groups.g[i];
+    const int64_t row = G.r0 + b;
+    switch (G.k) {
+    case 1:
+        trellis_block_row<L, 1>(*reinterpret_cast<BlkSmem<L, 1>*>(raw), row, T, n, ldT, U, ldU, S, G.table64, G.table32,
+                                b0, b1, width, look, state, states, lds, Z, ldZ, pre);
+        break;
+    case 2:
+        trellis_block_row<L, 2>(*reinterpret_cast<BlkSmem<L, 2>*>(raw), row, T, n, ldT, U, ldU, S, G.table64, G.table32,
+                                b0, b1, width, look, state, states, lds, Z, ldZ, pre);
+        break;
+    case 3:
+        trellis_block_row<L, 3>(*reinterpret_cast<BlkSmem<L, 3>*>(raw), row, T, n, ldT, U, ldU, S, G.table64, G.table32,
+                                b0, b1, width, look, state, states, lds, Z, ldZ, pre);
+        break;
+    default:
+        trellis_block_row<L, 4>(*reinterpret_cast<BlkSmem<L, 4>*>(raw), row, T, n, ldT, U, ldU, S, G.table64, G.table32,
+                                b0, b1, width, look, state, states, lds, Z, ldZ, pre);
+        break;
+    }
+}
+
+extern "C" int lamq_ldlq_trellis_block_groups(double* T, int64_t m, int64_t n, int64_t ldT, const double* U,
+                                              int64_t ldU, const double* S, int L,
+                                              const lamq_trellis_group32* groups, int ngroups, int64_t b0, int64_t b1,
+                                              int width, int look, int32_t* state, int32_t* states, int64_t lds,
+                                              double* Z, int64_t ldZ, int64_t pre, void* stream)
+{
+    if (!T || !U || !S || !state || !states || !Z || !groups) return LAMQ_EINVAL;
+    if (ngroups < 1 || ngroups > LAMQ_TRELLIS_MAX_GROUPS) return LAMQ_EINVAL;
+    if (m < 0 || n < 1 || ldT < n || ldU < n || lds < n || b0 < 0 || b1 <= b0 || b1 > n || width < 1 || look < 0)
+        return LAMQ_EINVAL;
+    if (pre < 0 || pre > b0 || ldZ < pre + (b1 - b0)) return LAMQ_EINVAL;
+    if (pre > LAMQ_PRE_MAX) return LAMQ_EUNSUP;
+    if (width > LAMQ_WMAX || width + look > LAMQ_TV_BLK || b1 - b0 > LAMQ_LAZY_MAX || m > 0x7fffffff)
+        return LAMQ_EUNSUP;
+    if (L != LAMQ_GROUPS_L) return LAMQ_EUNSUP;
+    BlkGroups gg{};
+    int64_t total = 0;
+    for (int i = 0; i < ngroups; ++i) {
+        const lamq_trellis_group32& g = groups[i];
+        if (g.r0 < 0 || g.rows < 0 || g.r0 > m - g.rows) return LAMQ_EINVAL;
+        if (!g.table64 || !g.table32) return LAMQ_EINVAL;
+        if (g.k < 1 || g.k > 4) return LAMQ_EUNSUP;
+        for (int j = 0; j < i; ++j)  // the row ranges do not overlap
+            if (g.rows && groups[j].rows && g.r0 < groups[j].r0 + groups[j].rows && groups[j].r0 < g.r0 + g.rows)
+                return LAMQ_EINVAL;
+        gg.g[i].r0 = g.r0;
+        gg.g[i].rows = g.rows;
+        gg.g[i].table64 = g.table64;
+        gg.g[i].table32 = g.table32;
+        gg.g[i].k = g.k;
+        total += g.rows;
+    }
+    gg.count = ngroups;
+    if (total == 0) return LAMQ_OK;
+    hipLaunchKernelGGL((ldlq_trellis_groups_kernel<LAMQ_GROUPS_L>), dim3((unsigned)total), dim3(LAMQ_NT), 0,
+                       as_stream(stream), T, n, ldT, U, ldU, S, b0, b1, width, look, state, states, lds, Z, ldZ, (int)pre,
+                       gg);
+    LAMQ_LAUNCH_CHECK();
+    return LAMQ_OK;
 }

@@ -24,6 +24,7 @@ class LinAlgError(torch.linalg.LinAlgError if hasattr(torch.linalg, "LinAlgError
 
 
 BIG_L = 13  # tables of 2^13 states and more go to the 1024-thread kernels (fp16-exact tables)
+MERGED_SMALL_L = 12  # below BIG_L, the state width whose row groups go through one launch per lazy block
 
 
 def half_bits(C: torch.Tensor) -> torch.Tensor:
@@ -208,12 +209,12 @@ def ldlq_trellis_groups(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, group
                         events: dict | None = None, concurrent: bool | None = None) -> torch.Tensor:
     """ldlq_trellis over consecutive row groups that share U but not the code: groups = [(rows, k, table64,
     table32 or None)] in row order, summing to X's rows. Rows do not interact (the block kernel and the trailing
-    update work row by row), so each group's sweep is independent of the others. With 16-bit states (L >= BIG_L) all
-    groups go through one launch per lazy block (lamq_ldlq_trellis16_block_groups) and one trailing product over all
-    rows. Below that, with `concurrent` (the default without events) every group runs its whole sweep, block kernels
-    and its own trailing updates, on a stream of its own, and the groups' VALU-bound searches and fp64 MFMA products
-    overlap on the chip. Either way the results are those of sweeping the groups one after the other. With events
-    every launch is timed on the caller's stream in turn."""
+    update work row by row), so each group's sweep is independent of the others. With 16-bit states (L >= BIG_L) and
+    at L = 12 (MERGED_SMALL_L) all groups go through one launch per lazy block (lamq_ldlq_trellis16_block_groups,
+    lamq_ldlq_trellis_block_groups) and one trailing product over all rows. At other L, with `concurrent` (the
+    default without events) every group runs its whole sweep, block kernels and its own trailing updates, on a stream
+    of its own. Either way the results are those of sweeping the groups one after the other. With events every
+    launch is timed on the caller's stream in turn."""
     check_tables(groups, L)
     need(X, torch.float64, "X", 2)
     need(U, torch.float64, "U", 2)
@@ -264,15 +265,21 @@ def ldlq_trellis_groups(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, group
     # the 16-bit-state groups go through one launch per lazy block (lamq_ldlq_trellis16_block_groups): every group's
     # rows in one grid, so no group's launch ends in a tail of idle CUs and no stream per group is needed
     merged = None
-    if L >= BIG_L and len(parts) > 1:
+    if (L >= BIG_L or L == MERGED_SMALL_L) and len(parts) > 1:
         # the grid takes the groups in the table's order, widest first: the costliest rows are dispatched first, so
         # the launch ends on its cheapest rows (a shorter tail of partly idle CUs); rows are independent, so the
         # order changes no result
-        merged = (_abi.TrellisGroup * len(parts))()
-        for i, (r0, rows, k, table64, t32) in enumerate(sorted(parts, key=lambda p: -p[2])):
-            w = ws.get(r0)
-            merged[i] = _abi.TrellisGroup(r0, rows, k, table64.data_ptr(), t32.data_ptr(),
-                                          None if w is None else w.data_ptr(), 0 if w is None else w.numel())
+        order = sorted(parts, key=lambda p: -p[2])
+        if L >= BIG_L:
+            merged = (_abi.TrellisGroup * len(parts))()
+            for i, (r0, rows, k, table64, t32) in enumerate(order):
+                w = ws.get(r0)
+                merged[i] = _abi.TrellisGroup(r0, rows, k, table64.data_ptr(), t32.data_ptr(),
+                                              None if w is None else w.data_ptr(), 0 if w is None else w.numel())
+        else:
+            merged = (_abi.TrellisGroup32 * len(parts))()
+            for i, (r0, rows, k, table64, t32) in enumerate(order):
+                merged[i] = _abi.TrellisGroup32(r0, rows, k, table64.data_ptr(), t32.data_ptr())
     if concurrent is None:
         concurrent = events is None
     main = torch.cuda.current_stream(dev)
@@ -293,10 +300,10 @@ def ldlq_trellis_groups(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, group
             pre = b0 - B0 if b1 == B1 else 0
             if merged is not None:
                 ev = _event_pair(events, "block")
-                check(lib().lamq_ldlq_trellis16_block_groups(
-                    ptr(T), m, n, n, ptr(U), ld(U), ptr(S), L, ctypes.addressof(merged), len(parts), b0, b1, width,
-                    look, ptr(state), ptr(states), n, vp(Z.data_ptr() + 8 * (b0 - B0)), outer, pre, stream(dev)),
-                    "ldlq_trellis16_block_groups")
+                fn = lib().lamq_ldlq_trellis16_block_groups if L >= BIG_L else lib().lamq_ldlq_trellis_block_groups
+                check(fn(ptr(T), m, n, n, ptr(U), ld(U), ptr(S), L, ctypes.addressof(merged), len(parts), b0, b1, width,
+                         look, ptr(state), ptr(states), n, vp(Z.data_ptr() + 8 * (b0 - B0)), outer, pre, stream(dev)),
+                      "ldlq_trellis_block_groups")
                 _event_end(ev)
             for p, (r0, rows, k, table64, t32) in enumerate(parts if merged is None else ()):
                 Tp, Zp = views[p]

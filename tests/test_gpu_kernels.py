@@ -473,14 +473,16 @@ def test_ldlq_trellis16_without_workspace_matches_oracle(E, monkeypatch, k):
     assert np.array_equal(without, ref)
 
 
-def test_ldlq_trellis16_groups_in_one_launch_equal_each_group_alone(E):
-    """lamq_ldlq_trellis16_block_groups (every row group of a stage in one launch per lazy block, each workgroup taking
-    its group's width) against each group swept on its own through lamq_ldlq_trellis16_block(_ws): the same states,
-    bit for bit, for groups at k = 4, 1, 3, 2 (k = 1 with its back-pointers in a workspace) in that row order, with an
-    empty group among them; n = 600 (two outer runs, the look-ahead past the first taken in the kernel)."""
+@pytest.mark.parametrize("L", [12, 16])
+def test_ldlq_trellis_groups_in_one_launch_equal_each_group_alone(E, tables, L):
+    """lamq_ldlq_trellis16_block_groups (L = 16) and lamq_ldlq_trellis_block_groups (L = 12): every row group of a stage
+    in one launch per lazy block, each workgroup taking its group's width, against each group swept on its own through
+    lamq_ldlq_trellis16_block(_ws) or lamq_ldlq_trellis_block: the same states, bit for bit, for groups at k = 4, 1, 3,
+    2 (at L = 16, k = 1 with its back-pointers in a workspace) in that row order, with an empty group among them;
+    n = 600 (two outer runs, the look-ahead past the first taken in the kernel)."""
     from lookatmyquant_amd.tables import quantile_table
 
-    rng = np.random.default_rng(77)
+    rng = np.random.default_rng(77 + L)
     n = 600
     sizes, widths = [37, 90, 0, 65, 130], [4, 1, 2, 3, 2]
     m = sum(sizes)
@@ -488,19 +490,20 @@ def test_ldlq_trellis16_groups_in_one_launch_equal_each_group_alone(E):
     _, U, _ = O.environment(Xa.T @ Xa / (2 * n))
     X = rng.standard_normal((m, n))
     S = O.row_scale(X)
-    tab = cuda(np.array(quantile_table(16, 0)))
-    say(f"ldlq_trellis_groups L=16: {m} rows, groups in one launch")
-    merged = E.ldlq_trellis_groups(cuda(X), cuda(S), cuda(U), [(r, k, tab, None) for r, k in zip(sizes, widths)], 16)
+    tabs = {k: cuda(np.array(quantile_table(16, 0) if L == 16 else tables[k])) for k in (1, 2, 3, 4)}
+    say(f"ldlq_trellis_groups L={L}: {m} rows, groups in one launch")
+    merged = E.ldlq_trellis_groups(cuda(X), cuda(S), cuda(U), [(r, k, tabs[k], None) for r, k in zip(sizes, widths)],
+                                   L)
     torch.cuda.synchronize()
     r0 = 0
     for r, k in zip(sizes, widths):
         if r:
             say(f"  group of {r} rows at k={k} alone")
-            alone = E.ldlq_trellis(cuda(X[r0 : r0 + r]), cuda(S[r0 : r0 + r]), cuda(U), tab, 16, k)
+            alone = E.ldlq_trellis(cuda(X[r0 : r0 + r]), cuda(S[r0 : r0 + r]), cuda(U), tabs[k], L, k)
             assert torch.equal(merged[r0 : r0 + r], alone), k
         r0 += r
-    ref = O.ldlq_trellis(X[[36]], U, S[[36]], tab.cpu().numpy(), 16, 4)
-    assert np.array_equal(merged[36].cpu().numpy(), ref[0])
+    for i, k in ((36, 4), (37, 1), (130, 3), (200, 2)):  # one row of each width against the oracle
+        assert np.array_equal(merged[i].cpu().numpy(), O.ldlq_trellis(X[[i]], U, S[[i]], tabs[k].cpu().numpy(), L, k)[0])
 
 
 @pytest.mark.parametrize("L", [12, 16])
@@ -581,9 +584,8 @@ def test_ldlq_trellis_full_width_matches_oracle(E, tables):
 
 @pytest.mark.parametrize("L", [12, 16])
 def test_ldlq_trellis_groups_concurrent_equals_serial_and_oracle(E, tables, L):
-    """Four row groups of different widths (and a fifth, empty one) swept together (L = 12: each on its own stream;
-    L = 16: one launch per lazy block for all groups) give the states of the same sweep run group after group on one
-    stream, bit for bit, and each group's states are the oracle's for its rows alone (n = 1,100: three outer runs, a
+    """Four row groups of different widths (and a fifth, empty one) swept together (one launch per lazy block for all
+    groups) in the production schedule and with every launch in turn on one stream give the same states, bit for bit, and each group's states are the oracle's for its rows alone (n = 1,100: three outer runs, a
     ragged last lazy block)."""
     rng = np.random.default_rng(12 + L)
     n = 1100
