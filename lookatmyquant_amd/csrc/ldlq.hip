@@ -20,6 +20,14 @@
 // row r of the staged triangle (columns r .. SC_MAXW - 1) starts at sc_tri(r)
 __host__ __device__ constexpr int sc_tri(int r) { return r * SC_MAXW - r * (r - 1) / 2; }
 #define SC_REGK 16  // level sets up to this size are searched from registers
+template <bool B>
+struct BoolC {
+    static constexpr bool value = B;
+};
+template <int I>
+struct IntK {
+    static constexpr int value = I;
+};
 // P: 0 (levels read from LDS), or a power of two >= K (levels held in registers, P of them)
 template <int P, int R, int MODE>
 __global__ __launch_bounds__(64 * R) void ldlq_scalar_block_kernel(const double* __restrict__ T, int64_t m, int64_t ldT,
@@ -51,8 +59,10 @@ __global__ __launch_bounds__(64 * R) void ldlq_scalar_block_kernel(const double*
         }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i + 1 < K; i += NTH) mid[i] = (lv[i + 1] + lv[i]) / 2;
-    __syncthreads();
+    if constexpr (MODE == 1) {
+        for (int i = threadIdx.x; i + 1 < K; i += NTH) mid[i] = (lv[i + 1] + lv[i]) / 2;
+        __syncthreads();
+    }
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * R + (threadIdx.x >> 6);
     if (row >= m) return;
@@ -79,6 +89,154 @@ __global__ __launch_bounds__(64 * R) void ldlq_scalar_block_kernel(const double*
         u0 = Uj[lane];
         u1 = Uj[lane + 64];
     };
+    if constexpr (MODE == 0 && REG) {
+        // The search from registers: levels past K are +inf (distance +inf, never strictly below another), so no
+        // step needs K
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            lr[i] = i < K ? lr[i] : __builtin_inf();
+            // held as vector registers (opaque to the uniformity analysis): the tournament's selects are then
+            // v_cndmask on the compares' lane masks, not scalar selects fed back and forth between the vector and
+            // scalar units
+            asm volatile("" : "+v"(lr[i]));
+        }
+        // z = (t - q) / U[j][j] through the hardware division's own sequence split at its divisor: the reciprocal
+        // refinement of U[j][j] (it depends on the divisor alone) before the steps, then on the chain the quotient
+        // q0 = E r, the exact residual fma(-d, q0, E) and the corrected quotient: the values the division E / d forms
+        // wherever its operand scaling is the identity and its final fix-up passes the quotient through, as for every
+        // divisor and nonzero residual within 2^-300 .. 2^300. Divisors outside that range send the block to the plain
+        // division below before it starts; a residual outside it (zero and subnormal included) is noted (the
+        // extremes of its biased exponents, no branch on the chain) and the block is then done again with the plain
+        // division.
+        const auto recip = [](double d) {
+            double r = __builtin_amdgcn_rcp(d);
+            r = fma(r, fma(-d, r, 1.0), r);
+            r = fma(r, fma(-d, r, 1.0), r);
+            return r;
+        };
+        const auto in_range = [](double v) {
+            const double a = __builtin_fabs(v);
+            return a >= 0x1p-300 && a <= 0x1p300;
+        };
+        // every divisor U[j][j] of the block and its reciprocal, formed before the steps: lane l holds those of
+        // columns l and l + 64, and step c reads them with readlane (no step waits on the reciprocal's chain)
+        const double dg0 = lane < bw ? ub[sc_tri(lane)] : 1.0;
+        const double dg1 = lane + 64 < bw ? ub[sc_tri(lane + 64)] : 1.0;
+        const double rc0 = recip(dg0), rc1 = recip(dg1);
+        const bool dg_ok = __builtin_amdgcn_ballot_w64(!(in_range(dg0) && in_range(dg1))) == 0;
+        if (dg_ok) {
+            double zk0 = 0.0, zk1 = 0.0;  // z of this lane's columns (lane, lane + 64)
+            int ik0 = 0, ik1 = 0;
+            uint32_t bmin = 0x7FFu, bmax = 0u;  // extremes of the residuals' biased binary exponents
+            // the U row of step c + 2 is read from LDS during step c (its two columns of each lane), into a ring of
+            // three register pairs: step c's row in slot c % 3 (the steps unrolled by three, so no row is moved)
+            double us[3][2];
+            const auto urow2 = [&](int c, double (&u)[2]) {
+                const double* Uj = ub + sc_tri(c) - c;
+                u[0] = Uj[lane];
+                u[1] = Uj[lane + 64];
+            };
+            urow2(0, us[0]);
+            urow2(bw > 1 ? 1 : 0, us[1]);
+            // step c: a tournament over the squared distances with strict comparisons, the left (lower) index keeping
+            // a tie: the first argmin, as the sequential scan finds it (a NaN t: index 0, as the reference's argmin);
+            // the winner's index (the same in every lane) then reads its level from the register array. LO: columns
+            // below 64 still open (their lanes' first registers take the refit).
+            const auto step = [&](auto slot_c, auto lo_c, const int c) {
+                constexpr int SL = decltype(slot_c)::value;
+                constexpr bool LO = decltype(lo_c)::value;
+                const double t = LO ? readlane_f64(t0, c) : readlane_f64(t1, c - 64);
+                const double ud = LO ? readlane_f64(dg0, c) : readlane_f64(dg1, c - 64);
+                const double rd = LO ? readlane_f64(rc0, c) : readlane_f64(rc1, c - 64);
+                const double u0 = us[SL][0], u1 = us[SL][1];
+                if (c + 2 < bw) urow2(c + 2, us[(SL + 2) % 3]);
+                double d[NR];
+                int bi[NR];
+#pragma unroll
+                for (int i = 0; i < NR; ++i) {
+                    const double e = t - lr[i];
+                    d[i] = e * e;
+                    bi[i] = i;
+                }
+#pragma unroll
+                for (int span = 1; span < NR; span *= 2)
+#pragma unroll
+                    for (int i = 0; i + span < NR; i += 2 * span)
+                        if (d[i + span] < d[i]) {
+                            d[i] = d[i + span];
+                            bi[i] = bi[i + span];
+                        }
+                const int best = __builtin_amdgcn_readfirstlane(bi[0]);
+                const double E = t - lr[best];
+                const double q0 = E * rd;
+                const double r = fma(-ud, q0, E);
+                // div_fmas without its scaling flag is this fma, and div_fixup returns the quotient unchanged for
+                // finite operands whose quotient neither overflows nor underflows (both within 2^-300 .. 2^300)
+                const double zj = fma(r, rd, q0);
+                const uint32_t be = ((uint32_t)(__double_as_longlong(E) >> 52)) & 0x7FFu;  // 0: zero or subnormal
+                bmin = be < bmin ? be : bmin;
+                bmax = be > bmax ? be : bmax;
+                // every lane's open columns take the refit: those at or left of c are settled and those past the
+                // block unused, so their values (formed from entries of the staged triangle outside this row) are
+                // never read
+                if constexpr (LO) {
+                    const double p0 = zj * u0;
+                    t0 = t0 - p0;
+                }
+                {
+                    const double p1 = zj * u1;
+                    t1 = t1 - p1;
+                }
+                if constexpr (LO) {
+                    zk0 = lane == c ? zj : zk0;
+                    ik0 = lane == c ? best : ik0;
+                } else {
+                    zk1 = lane + 64 == c ? zj : zk1;
+                    ik1 = lane + 64 == c ? best : ik1;
+                }
+            };
+            // steps cb .. ce - 1 (slot c % 3 for step c)
+            const auto run = [&](const int cb, const int ce, auto lo_c) {
+                int c = cb;
+                for (; c < ce && c % 3 != 0; ++c) {
+                    if (c % 3 == 1)
+                        step(IntK<1>{}, lo_c, c);
+                    else
+                        step(IntK<2>{}, lo_c, c);
+                }
+                for (; c + 3 <= ce; c += 3) {
+                    step(IntK<0>{}, lo_c, c);
+                    step(IntK<1>{}, lo_c, c + 1);
+                    step(IntK<2>{}, lo_c, c + 2);
+                }
+                for (; c < ce; ++c) {
+                    if (c % 3 == 0)
+                        step(IntK<0>{}, lo_c, c);
+                    else if (c % 3 == 1)
+                        step(IntK<1>{}, lo_c, c);
+                    else
+                        step(IntK<2>{}, lo_c, c);
+                }
+            };
+            run(0, bw < 64 ? bw : 64, BoolC<true>{});
+            run(64, bw, BoolC<false>{});
+            // every |E| in 2^-300 .. 2^300 (biased exponent 723 .. 1322): no zero, subnormal or extreme residual
+            if (bmin >= 723u && bmax <= 1322u) {
+                if (lane < bw) {
+                    idx[row * ldi + b0 + lane] = ik0;
+                    Z[row * ldZ + lane] = zk0;
+                }
+                if (lane + 64 < bw) {
+                    idx[row * ldi + b0 + lane + 64] = ik1;
+                    Z[row * ldZ + lane + 64] = zk1;
+                }
+                return;
+            }
+            // a residual out of the fast quotient's range: the block again with the plain division
+            t0 = lane < bw ? Tr[lane] : 0.0;
+            t1 = lane + 64 < bw ? Tr[lane + 64] : 0.0;
+        }
+    }
     double ud_n, u0_n, u1_n;
     urow(0, ud_n, u0_n, u1_n);
     for (int c = 0; c < bw; ++c) {
@@ -88,39 +246,14 @@ __global__ __launch_bounds__(64 * R) void ldlq_scalar_block_kernel(const double*
         int best = 0;
         double q;
         if constexpr (MODE == 0) {
-            if (REG) {
-                // a tournament over the squared distances with strict comparisons, the left (lower) index keeping a
-                // tie: the first argmin, as the sequential scan finds it
-                double d[NR], lq[NR];
-                int bi[NR];
-#pragma unroll
-                for (int i = 0; i < NR; ++i) {
-                    const double e = t - lr[i];
-                    d[i] = i < K ? e * e : __builtin_inf();
-                    bi[i] = i;
-                    lq[i] = lr[i];
-                }
-#pragma unroll
-                for (int span = 1; span < NR; span *= 2)
-#pragma unroll
-                    for (int i = 0; i + span < NR; i += 2 * span)
-                        if (d[i + span] < d[i]) {
-                            d[i] = d[i + span];
-                            bi[i] = bi[i + span];
-                            lq[i] = lq[i + span];
-                        }
-                best = bi[0];
-                q = lq[0];
-            } else {
-                const double d0 = t - lv[0];
-                double bd = d0 * d0;
-                for (int i = 1; i < K; ++i) {
-                    double d = t - lv[i];
-                    d = d * d;
-                    if (d < bd) { bd = d; best = i; }
-                }
-                q = lv[best];
+            const double d0 = t - lv[0];
+            double bd = d0 * d0;
+            for (int i = 1; i < K; ++i) {
+                double d = t - lv[i];
+                d = d * d;
+                if (d < bd) { bd = d; best = i; }
             }
+            q = lv[best];
         } else {
             const double ts = t / Sr;
             if (REG) {

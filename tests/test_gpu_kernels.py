@@ -663,6 +663,41 @@ def test_ldlq_scalar_level_counts_match_oracle(E, K, m):
                           O.ldlq_scalar(X, U, lv, 1, S))
 
 
+@pytest.mark.parametrize("K,m,bw", [(8, 40, 128), (8, 130, 100), (4, 40, 50), (16, 40, 128)])
+def test_ldlq_scalar_block_z_is_the_ieee_quotient(E, K, m, bw):
+    """One lazy block of the width-1 kernel (lamq_ldlq_scalar_block, the first block, before any trailing update) through
+    the C ABI: its indices are the oracle's and each refit coefficient z = (t - q) / U[j][j] is numpy's IEEE quotient
+    of the oracle's pre-settlement value t (syntax.py:117-118), bit for bit, including the columns whose residual is
+    exactly zero (t on a level) and a row whose values lie far outside 2^-300 .. 2^300 (the plain division's cases)."""
+    import ctypes
+
+    rng = np.random.default_rng(200 + K + m + bw)
+    n = 160
+    Xa = rng.standard_normal((2 * n, n))
+    _, U, _ = O.environment(Xa.T @ Xa / (2 * n))
+    T0 = rng.standard_normal((m, n))
+    lv = np.sort(rng.standard_normal(K)) * 1.5
+    T0[1, :5] = lv[K // 2]  # t on a level: a zero residual in the first column
+    T0[2, [0, 3, 7]] = lv[0]
+    T0[3] *= 1e95  # residuals beyond 2^300
+    T0[4, 0] = 1e-310  # a subnormal column value
+    idx_ref, before = O.ldlq_scalar(T0, U, lv, 0, want_before=True)
+    lib = E._abi.lib()
+    Tg, Ug, lvg = cuda(T0), cuda(U), cuda(lv)
+    idx = torch.zeros(m, n, dtype=torch.int32, device="cuda")
+    Z = torch.zeros(m, 128, dtype=torch.float64, device="cuda")
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    say(f"lamq_ldlq_scalar_block K={K} m={m} bw={bw}")
+    rc = lib.lamq_ldlq_scalar_block(p(Tg), m, n, n, p(Ug), n, None, p(lvg), K, 0, 0, bw, p(idx), n, p(Z), 128,
+                                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(idx.cpu().numpy()[:, :bw], idx_ref[:, :bw])
+    zr = (before[:, :bw] - lv[idx_ref[:, :bw]]) / np.diag(U)[:bw]
+    zg = Z.cpu().numpy()[:, :bw]
+    assert np.array_equal(zg.view(np.int64), zr.view(np.int64))
+
+
 def test_end_to_end_gpu_factor_config2(E, golden, tables, config12):
     """Hessian rotation and U on the GPU too: the reference states at config 2, bit for bit."""
     W, H = config12
