@@ -61,20 +61,27 @@ __global__ void prep_kernel(const double* __restrict__ H, int64_t n, int64_t ldH
 }
 
 // The nb x nb diagonal block at (k0, k0) of A (lower): its Cholesky factor Lkk and Lkk^-1 (lower, ld NBK, written
-// into Linv). One workgroup of four waves with the block in LDS, in four steps of 16
-// columns p:
-//   (1) wave 0 factors the 16 x 16 diagonal block D_p in registers (lane i holds row i; column values move
-//       between lanes by readlane): column c, d = a[c][c], r = 1/sqrt(d), l[c][c] = d r, l[i][c] = a[i][c] r
+// into Linv), and the panel rows below it. One workgroup of four waves keeps the block's ten lower 16 x 16 tiles in
+// LDS (21.8 KB: a workgroup fits on a CU beside two workgroups of the 128-tile product, which hold 128 of its 160 KB,
+// so the first step of a panel need not wait for the inverse's deep product on the side stream to drain; with the
+// whole 64 x 64 block, its inverse and the panel rows in LDS, 108 KB, it waited 200-350 us at n = 9,728), in four
+// steps of 16 columns p:
+//   (1) wave 0 factors the 16 x 16 diagonal tile D_p in registers (lane i holds row i; column values move
+//       between lanes by DPP row broadcasts): column c, d = a[c][c], r = 1/sqrt(d), l[c][c] = d r, l[i][c] = a[i][c] r
 //       (a reciprocal scaling, as LAPACK's unblocked potf2 scales by 1/l[c][c]), a[i][j] -= l[i][c] l[j][c];
-//       then inverts the factor (lane c holds column c of D_p^-1, forward substitution with the same r);
+//       then inverts the factor (lane c holds column c of D_p^-1, forward substitution with the same r) and
+//       overwrites the tile with D_p^-1 (nothing reads D_p itself);
 //   (2) the tiles below it become L_Ip = A_Ip D_p^-T (one MFMA tile per wave);
 //   (3) the lower trailing tiles take A_IJ -= L_Ip L_Jp^T (MFMA).
-// Then Lkk^-1 by block rows: Linv_pp = D_p^-1, Linv_pq = -D_p^-1 sum_{q<=r<p} L_pr Linv_rq, one level per p.
-// Every workgroup of the launch factors the block for itself (the same arithmetic, the same result) and then solves
-// its 64 rows of the panel below the block, L_ik = A_ik Lkk^-T (MFMA); workgroup 0 writes Lkk^-1. The panel
-// solve thus needs no launch of its own after the factor. A block shorter than NBK is padded with the identity. The loops over p run at run time, so the code stays a few
-// KB (a fully unrolled 64-step kernel spends most of its time fetching instructions).
-#define DB_LD 65  // LDS row stride of the block, in doubles
+// Then Lkk^-1 in place, by block rows: Linv_pq = -D_p^-1 sum_{q<=r<p} L_pr Linv_rq, one level per p (tile (p, q) holds
+// L_pq until its row's level has read it). Every workgroup of the launch factors the block for itself (the same
+// arithmetic, the same result) and then solves its 64 rows of the panel below the block, L_ik = A_ik Lkk^-T (MFMA, the
+// rows straight from memory into the operand registers); workgroup 0 writes Lkk^-1. The panel solve thus needs no
+// launch of its own after the factor. A block shorter than NBK is padded with the identity. The loops over p run at
+// run time, so the code stays a few KB (a fully unrolled 64-step kernel spends most of its time fetching
+// instructions).
+#define DT_LD 17            // row stride of a 16 x 16 tile in LDS, in doubles
+#define DT_SZ (16 * DT_LD)  // doubles of one tile
 
 // 1/sqrt(d) for a positive normal d: the hardware estimate and two Newton steps y <- y + y/2 (1 - d y^2), within a
 // few units in the last place
@@ -89,51 +96,92 @@ __device__ __forceinline__ double rsqrt_f64(double d)
     return y;
 }
 
+// v of lane 16 (lane / 16) + J in every lane of each row of 16 (DPP row_newbcast, one VALU move of 64 bits: no
+// scalar registers, no wait states between the moves)
+template <int J>
+__device__ __forceinline__ double row_bcast_f64(double v)
+{
+    return __longlong_as_double(__builtin_amdgcn_update_dpp(0ll, __double_as_longlong(v), 0x150 + J, 0xf, 0xf, false));
+}
+__device__ __forceinline__ double row_bcast_f64(double v, int j)  // j a constant once the loops are unrolled
+{
+    switch (j) {
+        case 0: return row_bcast_f64<0>(v);
+        case 1: return row_bcast_f64<1>(v);
+        case 2: return row_bcast_f64<2>(v);
+        case 3: return row_bcast_f64<3>(v);
+        case 4: return row_bcast_f64<4>(v);
+        case 5: return row_bcast_f64<5>(v);
+        case 6: return row_bcast_f64<6>(v);
+        case 7: return row_bcast_f64<7>(v);
+        case 8: return row_bcast_f64<8>(v);
+        case 9: return row_bcast_f64<9>(v);
+        case 10: return row_bcast_f64<10>(v);
+        case 11: return row_bcast_f64<11>(v);
+        case 12: return row_bcast_f64<12>(v);
+        case 13: return row_bcast_f64<13>(v);
+        case 14: return row_bcast_f64<14>(v);
+        default: return row_bcast_f64<15>(v);
+    }
+}
+
 __global__ __launch_bounds__(256) void diag_block_kernel(double* __restrict__ A, int64_t n, int64_t k0, int nb,
                                                         int64_t rest, double* __restrict__ Linv,
                                                         int32_t* __restrict__ info)
 {
-    __shared__ double blk[NBK * DB_LD];  // the block, then L
-    __shared__ double inv[NBK * DB_LD];  // Lkk^-1
-    __shared__ double prow[NBK * DB_LD]; // this workgroup's 64 rows of the panel below the block
-    __shared__ double dinv[4][16 * 17];  // D_p^-1, [row * 17 + col]
+    __shared__ double tl[10 * DT_SZ];  // tile (I, J), J <= I, at (I (I + 1) / 2 + J) DT_SZ
     __shared__ int sfail;
     if (*info != 0) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int li = lane & 15, lk = lane >> 4;
     const int64_t pr0 = k0 + nb + (int64_t)blockIdx.x * NBK;  // first panel row of this workgroup
     const int prows = (int)(rest - (int64_t)blockIdx.x * NBK < NBK ? rest - (int64_t)blockIdx.x * NBK : NBK);
-    {  // all loads of a thread in flight at once, then the LDS writes
-        double v[NBK * NBK / 256], w[NBK * NBK / 256];
+    // entry (i, j) of the block, for (i, j) in a lower tile (i / 16 >= j / 16)
+    auto T = [&](int i, int j) -> double& {
+        return tl[((i >> 4) * ((i >> 4) + 1) / 2 + (j >> 4)) * DT_SZ + (i & 15) * DT_LD + (j & 15)];
+    };
+    // this wave's 16 panel rows as MFMA A operands, pa[kk] = A_rows[16 wave + li][4 kk + lk]: loaded first, used last
+    double pa[16];
+    {
+        const int r = 16 * wave + li;
+        const bool rok = r < prows;
+        const double* src = A + (rok ? pr0 + r : (int64_t)0) * n + k0;
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) {
+            const int c = 4 * kk + lk;
+            pa[kk] = (rok && c < nb) ? src[c] : 0.0;
+        }
+    }
+    {  // the block's lower tiles, all loads of a thread in flight at once (rows past nb: the identity's)
+        double v[NBK * NBK / 256];
 #pragma unroll
         for (int q = 0; q < NBK * NBK / 256; ++q) {
             const int e = tid + 256 * q, i = e >> 6, j = e & 63;
-            const bool ld = i < nb && j <= i;  // j <= i < nb
-            v[q] = ld ? A[(k0 + i) * n + k0 + j] : 0.0;
-            w[q] = (i < prows && j < nb) ? A[(pr0 + i) * n + k0 + j] : 0.0;
+            v[q] = (j <= i && i < nb) ? A[(k0 + i) * n + k0 + j] : 0.0;
         }
 #pragma unroll
         for (int q = 0; q < NBK * NBK / 256; ++q) {
             const int e = tid + 256 * q, i = e >> 6, j = e & 63;
-            blk[i * DB_LD + j] = (i < nb && j < nb) ? v[q] : (i == j ? 1.0 : 0.0);
-            inv[i * DB_LD + j] = 0.0;
-            prow[i * DB_LD + j] = w[q];
+            if ((j >> 4) <= (i >> 4)) T(i, j) = i < nb ? v[q] : (i == j ? 1.0 : 0.0);
         }
     }
     if (tid == 0) sfail = 0;
     __syncthreads();
-    auto B = [&](int i, int j) -> double& { return blk[i * DB_LD + j]; };
     for (int p = 0; p < 4; ++p) {
         const int c0 = 16 * p;
-        if (wave == 0) {  // (1); lanes 16..63 repeat lanes 0..15
+        if (wave == 0) {  // (1); lanes 16..63 repeat lanes 0..15, so a row broadcast of lane j gives row j's value
             double r[16];
+            // row li of the tile, read whole (its upper part holds finite values) and then masked, so the reads need
+            // no branches
 #pragma unroll
-            for (int j = 0; j < 16; ++j) r[j] = j <= li ? B(c0 + li, c0 + j) : 0.0;
+            for (int j = 0; j < 16; ++j) r[j] = T(c0 + li, c0 + j);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) r[j] = j <= li ? r[j] : 0.0;
             double rc[16];  // 1 / l[c][c], the same in every lane
             int fail = 0;   // the first non-positive pivot (the same in every lane)
             // the pivots form the serial chain; each is formed from lane-uniform values with exactly the operations
-            // lane c + 1 applies to its own entry, so the chain never waits on a lane-to-lane move
-            double d = readlane_f64(r[0], 0);
+            // lane c + 1 applies to its own entry, so the chain never waits on the column's update
+            double d = row_bcast_f64(r[0], 0);
 #pragma unroll
             for (int c = 0; c < 16; ++c) {
                 fail = (fail == 0 && !(d > 0.0)) ? (int)(k0 + c0 + c + 1) : fail;
@@ -142,20 +190,22 @@ __global__ __launch_bounds__(256) void diag_block_kernel(double* __restrict__ A,
                 rc[c] = rs;
                 double dn = 0.0;
                 if (c < 15) {  // the next pivot: a[c+1][c+1] - l[c+1][c]^2
-                    const double l1 = readlane_f64(r[c], c + 1) * rs;
-                    dn = fma(-l1, l1, readlane_f64(r[c + 1], c + 1));
+                    const double l1 = row_bcast_f64(r[c], c + 1) * rs;
+                    dn = fma(-l1, l1, row_bcast_f64(r[c + 1], c + 1));
                 }
                 const double lic = li > c ? r[c] * rs : (li == c ? sd : 0.0);
                 r[c] = lic;
 #pragma unroll
-                for (int j = c + 1; j < 16; ++j) r[j] = fma(-lic, readlane_f64(lic, j), r[j]);
+                for (int j = c + 1; j < 16; ++j) r[j] = fma(-lic, row_bcast_f64(lic, j), r[j]);
                 d = dn;
             }
             if (lane < 16) {
 #pragma unroll
-                for (int j = 0; j < 16; ++j) B(c0 + li, c0 + j) = j <= li ? r[j] : 0.0;
+                for (int j = 0; j < 16; ++j) T(c0 + li, c0 + j) = j <= li ? r[j] : 0.0;
             }
-            // the inverse reads the factor back from LDS (the same value in every lane)
+            // the inverse reads the factor back from LDS (the same value in every lane), lane c holding column c of
+            // D_p^-1 (x[i] = D_p^-1[i][c]); a wave's LDS accesses take effect in the order it issues them, so the tile
+            // can then become D_p^-1 (nothing reads D_p itself)
             double x[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i) x[i] = i == li ? 1.0 : 0.0;
@@ -163,14 +213,11 @@ __global__ __launch_bounds__(256) void diag_block_kernel(double* __restrict__ A,
             for (int l = 0; l < 16; ++l) {
                 x[l] = x[l] * rc[l];
 #pragma unroll
-                for (int i = l + 1; i < 16; ++i) x[i] = fma(-B(c0 + i, c0 + l), x[l], x[i]);
+                for (int i = l + 1; i < 16; ++i) x[i] = fma(-T(c0 + i, c0 + l), x[l], x[i]);
             }
             if (lane < 16) {
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    dinv[p][i * 17 + li] = x[i];
-                    inv[(c0 + i) * DB_LD + c0 + li] = x[i];
-                }
+                for (int i = 0; i < 16; ++i) T(c0 + i, c0 + li) = x[i];
             }
             if (lane == 0 && fail != 0) sfail = fail;
         }
@@ -187,18 +234,18 @@ __global__ __launch_bounds__(256) void diag_block_kernel(double* __restrict__ A,
                 lamq_d4 acc = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
                 for (int kk = 0; kk < 4; ++kk)
-                    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(B(16 * I + li, c0 + 4 * kk + lk),
-                                                               dinv[p][li * 17 + 4 * kk + lk], acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(T(16 * I + li, c0 + 4 * kk + lk),
+                                                               T(c0 + li, c0 + 4 * kk + lk), acc, 0, 0, 0);
 #pragma unroll
-                for (int v = 0; v < 4; ++v) B(16 * I + 4 * v + lk, c0 + li) = acc[v];
+                for (int v = 0; v < 4; ++v) T(16 * I + 4 * v + lk, c0 + li) = acc[v];
             }
         }
         __syncthreads();
         // (3) tiles (I, J), p < J <= I < 4, round-robin over the waves
         {
             const int m = 3 - p;
-            const int T = m * (m + 1) / 2;
-            for (int t = wave; t < T; t += 4) {
+            const int nt = m * (m + 1) / 2;
+            for (int t = wave; t < nt; t += 4) {
                 int ii = 0, jj = t;
                 while (jj > ii) {
                     jj -= ii + 1;
@@ -208,47 +255,51 @@ __global__ __launch_bounds__(256) void diag_block_kernel(double* __restrict__ A,
                 lamq_d4 acc = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
                 for (int kk = 0; kk < 4; ++kk)
-                    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(B(16 * I + li, c0 + 4 * kk + lk),
-                                                               B(16 * J + li, c0 + 4 * kk + lk), acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(T(16 * I + li, c0 + 4 * kk + lk),
+                                                               T(16 * J + li, c0 + 4 * kk + lk), acc, 0, 0, 0);
 #pragma unroll
-                for (int v = 0; v < 4; ++v) B(16 * I + 4 * v + lk, 16 * J + li) -= acc[v];
+                for (int v = 0; v < 4; ++v) T(16 * I + 4 * v + lk, 16 * J + li) -= acc[v];
             }
         }
         __syncthreads();
     }
-    // Lkk^-1 below the diagonal blocks: level p, wave q < p
+    // Lkk^-1 below the diagonal tiles: level p, wave q < p; tile (p, q) is overwritten only once every wave of the
+    // level has read row p's tiles of L
     for (int p = 1; p < 4; ++p) {
         const int q = wave;
+        lamq_d4 o = {0.0, 0.0, 0.0, 0.0};
         if (q < p) {
             lamq_d4 t = {0.0, 0.0, 0.0, 0.0};
             for (int r = q; r < p; ++r) {
 #pragma unroll
                 for (int kk = 0; kk < 4; ++kk)
-                    t = __builtin_amdgcn_mfma_f64_16x16x4f64(B(16 * p + li, 16 * r + 4 * kk + lk),
-                                                             inv[(16 * r + 4 * kk + lk) * DB_LD + 16 * q + li], t, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f64_16x16x4f64(T(16 * p + li, 16 * r + 4 * kk + lk),
+                                                             T(16 * r + 4 * kk + lk, 16 * q + li), t, 0, 0, 0);
             }
             // the result layout of t is the B-operand layout of its k-steps: register kk holds rows 4kk + l / 16
-            lamq_d4 o = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk)
-                o = __builtin_amdgcn_mfma_f64_16x16x4f64(dinv[p][li * 17 + 4 * kk + lk], t[kk], o, 0, 0, 0);
+                o = __builtin_amdgcn_mfma_f64_16x16x4f64(T(16 * p + li, 16 * p + 4 * kk + lk), t[kk], o, 0, 0, 0);
+        }
+        __syncthreads();
+        if (q < p) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) inv[(16 * p + 4 * v + lk) * DB_LD + 16 * q + li] = -o[v];
+            for (int v = 0; v < 4; ++v) T(16 * p + 4 * v + lk, 16 * q + li) = -o[v];
         }
         __syncthreads();
     }
-    // the panel rows: P = A_rows Lkk^-T, wave w rows 16w..16w+15, four column tiles (B[k][j] = Lkk^-1[j][k]; past nb
-    // the rows hold zeros and Lkk^-1 the identity)
+    // the panel rows: P = A_rows Lkk^-T, wave w rows 16w..16w+15, four column tiles (B[k][j] = Lkk^-1[j][k], zero for
+    // k / 16 > j / 16; past nb the rows hold zeros and Lkk^-1 the identity)
     if (prows > 0) {
         lamq_d4 acc[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) acc[t] = lamq_d4{0.0, 0.0, 0.0, 0.0};
 #pragma unroll
         for (int kk = 0; kk < 16; ++kk) {
-            const double a = prow[(16 * wave + li) * DB_LD + 4 * kk + lk];
 #pragma unroll
             for (int t = 0; t < 4; ++t)
-                acc[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, inv[(16 * t + li) * DB_LD + 4 * kk + lk], acc[t], 0, 0, 0);
+                if ((kk >> 2) <= t)
+                    acc[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(pa[kk], T(16 * t + li, 4 * kk + lk), acc[t], 0, 0, 0);
         }
 #pragma unroll
         for (int t = 0; t < 4; ++t)
@@ -264,7 +315,7 @@ __global__ __launch_bounds__(256) void diag_block_kernel(double* __restrict__ A,
     if (blockIdx.x != 0) return;
     for (int e = tid; e < NBK * NBK; e += 256) {
         const int i = e >> 6, j = e & 63;
-        Linv[i * NBK + j] = j <= i ? inv[i * DB_LD + j] : 0.0;
+        Linv[i * NBK + j] = j <= i ? T(i, j) : 0.0;
     }
 }
 
@@ -313,6 +364,17 @@ static int chol_steps(double* A, int64_t n, double* Linv, double* U, int64_t ldU
     // X = L^-1 into U (right-looking solve of L X = I): X_k = Lkk^-1 B_k, then B_i -= L_ik X_k below, inside the
     // panel at once and below it once per panel (X is lower triangular, so the panel's rows are zero right of
     // their diagonal and one product of depth NB2 carries the panel's steps).
+    // The inverse's step k needs Lkk^-1 and the panel L_ik of the factor's step k, nothing the factor writes later: on a
+    // side stream it follows the factor one step behind (an event after each step's diagonal block).
+    auto inverse_step = [&](int64_t k0, int64_t pe) -> int {
+        const int nb = (int)(n - k0 < NBK ? n - k0 : NBK);
+        const double* Lk = Linv + (k0 / NBK) * NBK * NBK;
+        const double* P = A + (k0 + nb) * n + k0;
+        const int64_t pc = pe - (k0 + nb);
+        int rc = gemm_sub_f64<false, false, true>(U + k0 * ldU, ldU, Lk, NBK, U + k0 * ldU, ldU, nb, k0 + nb, nb, info, si);
+        if (rc || pc <= 0) return rc;
+        return gemm_sub_f64<false, false>(U + (k0 + nb) * ldU, ldU, P, n, U + k0 * ldU, ldU, pc, k0 + nb, nb, info, si);
+    };
     for (int64_t K0 = 0; K0 < n; K0 += NB2) {
         const int64_t pe = (K0 + NB2 < n) ? K0 + NB2 : n;
         for (int64_t k0 = K0; k0 < pe; k0 += NBK) {
@@ -325,25 +387,17 @@ static int chol_steps(double* A, int64_t n, double* Linv, double* U, int64_t ldU
             const unsigned pg = rest > 0 ? (unsigned)cdiv(rest, NBK) : 1u;
             hipLaunchKernelGGL(diag_block_kernel, dim3(pg), dim3(256), 0, s, A, n, k0, nb, rest, Lk, info);
             LAMQ_LAUNCH_CHECK();
-            int rc;
             if (si != s) {
                 LAMQ_HIP_CHECK(hipEventRecord(step, s));
                 LAMQ_HIP_CHECK(hipStreamWaitEvent(si, step, 0));
             }
             const int64_t pc = pe - (k0 + nb);
             if (rest > 0 && pc > 0) {
-                rc = gemm_sub_f64<true, true>(A + (k0 + nb) * n + k0 + nb, n, P, n, P, n, rest, pc, nb, info, s);
+                int rc = gemm_sub_f64<true, true>(A + (k0 + nb) * n + k0 + nb, n, P, n, P, n, rest, pc, nb, info, s);
                 if (rc) return rc;
             }
-            // the inverse's step k
-            rc = gemm_sub_f64<false, false, true>(U + k0 * ldU, ldU, Lk, NBK, U + k0 * ldU, ldU, nb, k0 + nb, nb, info,
-                                                  si);
+            int rc = inverse_step(k0, pe);
             if (rc) return rc;
-            if (pc > 0) {
-                rc = gemm_sub_f64<false, false>(U + (k0 + nb) * ldU, ldU, P, n, U + k0 * ldU, ldU, pc, k0 + nb, nb, info,
-                                                si);
-                if (rc) return rc;
-            }
         }
         const int64_t rest = n - pe;
         if (rest > 0) {
@@ -366,6 +420,10 @@ extern "C" size_t lamq_chol_inv_upper_workspace_size(int64_t n)
 
 // Events of one factorization whose inverse runs on a side stream, made and released by the call (the library keeps
 // no state between calls). A released event that is still recorded on a stream lives until the stream reaches it.
+// The step event orders the two streams of one device, so it records with a device-scope fence only: a system-scope
+// release (HIP's default) writes the caches back and costs about 6 us between a step's kernels, once per 64 columns.
+// The fork and join events (once a call) keep the default.
+static constexpr unsigned kStepEventFlags = hipEventDisableTiming | hipEventDisableSystemFence;
 struct CholEvents {
     hipEvent_t fork = nullptr, step = nullptr, join = nullptr;
     ~CholEvents()
@@ -391,7 +449,7 @@ extern "C" int lamq_chol_inv_upper_ex(const double* H, int64_t n, int64_t ldH, d
     CholEvents ev;
     if (fork) {
         LAMQ_HIP_CHECK(hipEventCreateWithFlags(&ev.fork, hipEventDisableTiming));
-        LAMQ_HIP_CHECK(hipEventCreateWithFlags(&ev.step, hipEventDisableTiming));
+        LAMQ_HIP_CHECK(hipEventCreateWithFlags(&ev.step, kStepEventFlags));
         LAMQ_HIP_CHECK(hipEventCreateWithFlags(&ev.join, hipEventDisableTiming));
     }
     double* A = reinterpret_cast<double*>(workspace);
