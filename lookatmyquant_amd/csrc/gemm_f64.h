@@ -142,7 +142,16 @@ gemm128_f64_kernel(double* __restrict__ C, int64_t ldc, const double* __restrict
     constexpr int IPW = BK / 4;          // load instructions per wave, operand and stage
     __shared__ __align__(16) uint8_t lds[2][2][ASZ];  // [buffer][operand]
     if (info && *info != 0) return;
-    const int64_t tr = (int64_t)blockIdx.y * G8_BM, tc = (int64_t)blockIdx.x * G8_BM;
+    int64_t tr = (int64_t)blockIdx.y * G8_BM, tc = (int64_t)blockIdx.x * G8_BM;
+    if (TRI != 0) {
+        // a triangular op(B) gives each tile column its own k-range: the tiles go out column by column, the longest
+        // k-ranges first (workgroups start in the order of their linear index), so that the last round holds the
+        // shortest tiles rather than a full-depth one that starts late
+        const int64_t gx = gridDim.x, gy = gridDim.y, lin = (int64_t)blockIdx.y * gx + blockIdx.x;
+        const int64_t cr = lin / gy;
+        tr = (lin % gy) * G8_BM;
+        tc = (TRI == LAMQ_TRI_KGE ? cr : gx - 1 - cr) * G8_BM;
+    }
     if (LOWER && tc > tr + G8_BM - 1) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
