@@ -1,6 +1,6 @@
 """Benchmark of the per-matrix quantization hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--L 16|12] [--no-cpu] [--workload c5|c1|c2|c3|c4] [--copy-probe MiB]
+    python bench.py [--steps K] [--warmup W] [--L 16|12] [--no-cpu] [--workload c5|c1|c2|c3|c4|l2] [--copy-probe MiB]
 
 The default workload is config 5, the build of a random-initialised Qwen3.5-4B-shaped stack (36 layers x 7 linears:
 q/k/v/o [4096|1024|1024 x 2560, 2560 x 4096], gate/up [9728 x 2560], down [2560 x 9728]), and a step is one decoder
@@ -26,6 +26,8 @@ The other workloads (one JSON line each):
   --workload c3  config 3, one Qwen3.5-4B-shaped MLP block: Hessians of [131072, 2560] and [131072, 9728] with digit
                  token weights, one factor per stage, the row-plan sweeps of gate/up and down, packed codes
   --workload c4  config 4, one KL evaluation over paired bf16 logits [8192, 151936] per step
+  --workload l2  the Gram kernels' operand delivery beside the ceiling of their global->LDS load path (a measurement
+                 for the profiles, not a config)
 --copy-probe M ends the run with one device-to-device copy of M MiB, the known-size reference for the HBM byte
 counters of a profiler run.
 """
@@ -754,6 +756,75 @@ def run_c3(args):
     print(json.dumps(line))
 
 
+# ----------------------------------------------------------------------------- L2-to-CU delivery
+
+
+def run_l2(args):
+    """The Gram kernels' operand delivery against the ceiling of their load path: lamq_probe_l2_delivery (one workgroup
+    a CU streaming 32 KB stages global->LDS from L2-resident regions, nothing else) beside the unweighted Hessian and
+    cross-Gram base passes at the config-5 widths over 65,536 tokens. A 256-tile Gram workgroup loads 32 KB of operands
+    per 32-token stage (256 features x 32 tokens x 2 bytes, two operands), so its delivered bytes are tiles x splits x
+    stages x 32 KB. Rates per CU per clock at the 2.4 GHz peak clock (the ratio does not depend on the clock)."""
+    import torch
+
+    from lookatmyquant_amd import engine as E
+    from lookatmyquant_amd._abi import check, ld, lib, ptr, stream
+
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    cus, clk = 256, 2.4e9
+
+    def timed(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps * 1e-3
+
+    region, stages, wgs = 2 << 20, 4096, 256
+    buf = torch.zeros(8 * region, dtype=torch.uint8, device=dev)
+    st = stream(dev)
+    t = timed(lambda: check(lib().lamq_probe_l2_delivery(ptr(buf), region, stages, wgs, st), "probe"), args.steps)
+    probe = wgs * stages * 32768 / t
+    out = {"probe": {"bytes_per_s": round(probe, 1), "bytes_per_clk_per_cu": round(probe / cus / clk, 2),
+                     "workgroups": wgs, "stages": stages, "region_bytes_per_xcd": region}}
+    del buf
+    N = 65536
+    for n in (2560, 9728):
+        X = torch.randn(N, n, device=dev).bfloat16()
+        Y = torch.randn(N, n, device=dev).bfloat16()
+        H = torch.zeros(n, n, device=dev)
+        nt = -(-n // 256)
+        for sym in (1, 0):
+            nb = lib().lamq_gram_workspace_size(N, n, sym)
+            ws = E.workspace(nb, dev)
+            if sym:
+                fn = lambda: check(lib().lamq_hessian_accum(ptr(X), N, n, ld(X), None, 1.0, ptr(H), ld(H), ptr(ws), nb,
+                                                            st), "hessian")
+            else:
+                fn = lambda: check(lib().lamq_cross_gram(ptr(Y), ptr(X), N, n, ld(X), None, 1.0, ptr(H), ld(H), ptr(ws),
+                                                         nb, st), "cross_gram")
+            t = timed(fn, args.steps)
+            tiles = nt * (nt + 1) // 2 if sym else nt * nt
+            delivered = tiles * -(-N // 32) * 32768 / t  # every split's workgroups cover the N tokens once per tile
+            flops = N * n * (n + 1) if sym else 2.0 * N * n * n
+            out[f"{'hessian' if sym else 'cross_gram'}_n{n}"] = {
+                "bytes_per_s": round(delivered, 1), "bytes_per_clk_per_cu": round(delivered / cus / clk, 2),
+                "of_probe": round(delivered / probe, 3), "ms": round(t * 1e3, 3),
+                "frac_of_bf16_peak": round(flops / t / (MFMA_BF16_PEAK_TFLOPS * 1e12), 3)}
+            del ws
+        del X, Y, H
+        torch.cuda.empty_cache()
+    print(json.dumps({"metric": "L2-to-CU delivery of the Gram kernels' load path", "value": out["probe"][
+        "bytes_per_clk_per_cu"], "unit": "bytes/clk/CU (at 2.4 GHz)", "n_gpus": 1, "steps": args.steps,
+        "warmup": 1, "higher_is_better": True, "data": "synthetic", "config": {"workload": "l2 delivery probe"},
+        "results": out}))
+
+
 # ----------------------------------------------------------------------------- config 4
 
 
@@ -848,7 +919,7 @@ def main():
                          "reference's production trellis)")
     ap.add_argument("--k", type=int, default=2, help="c2: bits per weight")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", choices=("c1", "c2", "c3", "c4", "c5"), default="c5")
+    ap.add_argument("--workload", choices=("c1", "c2", "c3", "c4", "c5", "l2"), default="c5")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MiB")
     ap.add_argument("--no-extra", action="store_true",
                     help="c5: skip the extra layers timed in the production schedule and at the other state width")
@@ -867,7 +938,7 @@ def main():
     # stalls the host for tens of ms, and where the GPU has drained its queue by then, the stall lands inside a span
     gc.collect()
     gc.disable()
-    {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c4": run_c4, "c5": run_c5}[args.workload](args)
+    {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c4": run_c4, "c5": run_c5, "l2": run_l2}[args.workload](args)
     if args.copy_probe:
         copy_probe(args.copy_probe)
 

@@ -379,6 +379,15 @@ int lamq_attention_causal_bf16(const uint16_t* q, int64_t sqb, int64_t sqh, int6
                                int64_t svt, uint16_t* out, int64_t sob, int64_t soh, int64_t sot, int64_t B, int64_t H,
                                int64_t Hkv, int64_t T, int64_t D, float scale, void* stream);
 
+/* ----------------------------------------------------------------------------------------------
+ * Measurement only; no counterpart in the reference. The L2-to-CU delivery ceiling of the direct global->LDS load path
+ * the Gram kernels feed their MFMAs through: `workgroups` workgroups (one a CU: 160 KB of LDS each) stream `stages`
+ * stages of 32 KB each (1 KB loads of 16 bytes a lane, a five-buffer LDS ring, one barrier a stage) from the
+ * region_bytes-long region (region_bytes a multiple of 1,024, at least 65,536) of buf that belongs to their XCD:
+ * workgroup b reads region b % 8, so buf holds 8 regions. Bytes delivered: workgroups * stages * 32,768.
+ * ---------------------------------------------------------------------------------------------- */
+int lamq_probe_l2_delivery(const void* buf, int64_t region_bytes, int stages, int workgroups, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

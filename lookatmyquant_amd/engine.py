@@ -493,22 +493,31 @@ def swiglu(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     return y
 
 
-def rms_norm(x: torch.Tensor, g: torch.Tensor, eps: float) -> torch.Tensor:
+def rms_norm(x: torch.Tensor, g: torch.Tensor, eps: float, pad: int = 0) -> torch.Tensor:
     """bf16(bf16(x rsqrt(mean(x^2) + eps)) g) over the last dim of a bf16 x (float32 inside), one pass
-    (lamq_rms_norm_bf16). x's rows may be strided (the last dim contiguous, one row stride); returns a new contiguous
-    tensor of x's shape."""
+    (lamq_rms_norm_bf16). x's rows may be strided (the last dim contiguous, one row stride); returns a new tensor of
+    x's shape, contiguous, or with `pad` > 0 (a multiple of 8) a view of rows n + pad elements apart (row_pad)."""
     need(x, torch.bfloat16, "x")
     need(g, torch.bfloat16, "g", 1)
     n = x.shape[-1]
     if g.numel() != n:
         raise ValueError("g must have the last dim of x")
+    if pad < 0 or pad % 8:
+        raise ValueError("pad must be a non-negative multiple of 8")
     X = x.reshape(-1, n)
     if X.dim() == 2 and X.shape[0] > 1 and X.stride(1) != 1:
         raise ValueError("x must have a contiguous last dim")
-    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    y = torch.empty(*x.shape[:-1], n + pad, dtype=x.dtype, device=x.device)[..., :n]
     check(lib().lamq_rms_norm_bf16(ptr(X), X.shape[0], n, X.stride(0) if X.shape[0] > 1 else n, ptr(g.contiguous()),
-                                   ptr(y), n, float(eps), stream(x.device)), "rms_norm")
+                                   ptr(y), n + pad, float(eps), stream(x.device)), "rms_norm")
     return y
+
+
+def row_pad(n: int) -> int:
+    """Elements of padding after each row of bf16 activations whose Gram (lamq_hessian_accum, lamq_cross_gram) is
+    taken: 192 at n = 2,560, whose 5,120-byte rows measured 15-20% slower in the Gram kernels than 5,504-byte ones (a
+    channel effect of that stride); 0 elsewhere (no difference at n = 9,728)."""
+    return 192 if n == 2560 else 0
 
 
 def attention_causal(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,

@@ -69,9 +69,10 @@ def layer_weights(i: int, sh: Shape, dev, seed: int = 5000) -> dict:
     return w
 
 
-def rms_norm(x: torch.Tensor, g: torch.Tensor, eps: float) -> torch.Tensor:
-    """Qwen3's RMSNorm in float32 and back: bf16(bf16(x rsqrt(mean(x^2) + eps)) g), one kernel (engine.rms_norm)."""
-    return E.rms_norm(x, g, eps)
+def rms_norm(x: torch.Tensor, g: torch.Tensor, eps: float, pad: bool = False) -> torch.Tensor:
+    """Qwen3's RMSNorm in float32 and back: bf16(bf16(x rsqrt(mean(x^2) + eps)) g), one kernel (engine.rms_norm).
+    pad: a stage input, whose rows are laid out engine.row_pad(n) elements apart for the Gram kernels."""
+    return E.rms_norm(x, g, eps, E.row_pad(x.shape[-1]) if pad else 0)
 
 
 def rope_tables(T: int, sh: Shape, dev):
@@ -264,10 +265,10 @@ class StackBuild:
         xr = {s: [] for s in range(4)}
         hr_next = []
         for h in self.hr:
-            x1 = rms_norm(h, wr["input_layernorm"], sh.eps)
+            x1 = rms_norm(h, wr["input_layernorm"], sh.eps, pad=True)
             a = attention_input_to_o(x1, wr, sh, self.rope)
             h1 = h + _lin(a, wr["self_attn.o_proj"])
-            x2 = rms_norm(h1, wr["post_attention_layernorm"], sh.eps)
+            x2 = rms_norm(h1, wr["post_attention_layernorm"], sh.eps, pad=True)
             m = E.swiglu(_lin(x2, wr["mlp.gate_proj"]), _lin(x2, wr["mlp.up_proj"]))
             hr_next.append(h1 + _lin(m, wr["mlp.down_proj"]))
             for s, x in enumerate((x1, a, x2, m)):
@@ -280,12 +281,12 @@ class StackBuild:
         for s, names in enumerate(STAGES):
             t1 = timer.mark()
             if s == 0:
-                xq = x1q = [rms_norm(h, wq["input_layernorm"], sh.eps) for h in hq]
+                xq = x1q = [rms_norm(h, wq["input_layernorm"], sh.eps, pad=True) for h in hq]
             elif s == 1:
                 xq = aq = [attention_input_to_o(x, wq, sh, self.rope) for x in x1q]
             elif s == 2:
                 h1q = [h + _lin(a, wq["self_attn.o_proj"]) for h, a in zip(hq, aq)]
-                xq = x2q = [rms_norm(h, wq["post_attention_layernorm"], sh.eps) for h in h1q]
+                xq = x2q = [rms_norm(h, wq["post_attention_layernorm"], sh.eps, pad=True) for h in h1q]
             else:
                 xq = [E.swiglu(_lin(x, wq["mlp.gate_proj"]), _lin(x, wq["mlp.up_proj"])) for x in x2q]
             xqf = [_flat(x) for x in xq]
@@ -523,14 +524,19 @@ def _stage_statistics(xq: list, w: list | None, xr: list | None, classes: list |
     D = None if xr is None else torch.zeros(n, n, dtype=torch.float32, device=dev)
     ntok = 0
     for c, a in enumerate(xq):
-        a = a.contiguous()
+        if a.stride(-1) != 1:
+            a = a.contiguous()  # rows may stay strided (padded stage inputs), the elements of a row not
         N = a.shape[0]
         wc = None if w is None else w[c]
         cc = None if classes is None else classes[c]
+        b = None
+        if D is not None:
+            b = xr[c]
+            if b.stride(-1) != 1 or b.stride(0) != a.stride(0):  # the cross-Gram reads both with one row stride
+                a, b = a.contiguous(), b.contiguous()
         with E.span(kt, "hessian", float(N) * n * (n + 1)):
             E.hessian_accum(H, a, wc, classes=cc)
         if D is not None:
-            b = xr[c].contiguous()
             with E.span(kt, "cross_gram", 2.0 * N * n * n):
                 E.cross_gram_accum(D, b, a, wc, classes=cc)
         ntok += N
