@@ -288,17 +288,18 @@ class StackBuild:
                 h1q = [h + _lin(a, wq["self_attn.o_proj"]) for h, a in zip(hq, aq)]
                 xq = x2q = [rms_norm(h, wq["post_attention_layernorm"], sh.eps, pad=True) for h in h1q]
             else:
-                xq = [E.swiglu(_lin(x, wq["mlp.gate_proj"]), _lin(x, wq["mlp.up_proj"])) for x in x2q]
+                xq = mq = [E.swiglu(_lin(x, wq["mlp.gate_proj"]), _lin(x, wq["mlp.up_proj"])) for x in x2q]
             xqf = [_flat(x) for x in xq]
             timer.add("forward", t1, timer.mark())
             self._stage(i, s, names, xqf, xr[s], wr, wq)
             del xq, xqf
-        # both streams through the layer (the quantized one with its last matrix now quantized)
+        # both streams through the layer (the quantized one with its last matrix now quantized); the MLP's gate and up
+        # were quantized before the down stage, so its input (the down stage's) is the quantized stream's MLP
+        # activation as it stands
         t4 = timer.mark()
-        self.hq = [h1 + _lin(E.swiglu(_lin(x, wq["mlp.gate_proj"]), _lin(x, wq["mlp.up_proj"])),
-                             wq["mlp.down_proj"]) for h1, x in zip(h1q, x2q)]
+        self.hq = [h1 + _lin(m, wq["mlp.down_proj"]) for h1, m in zip(h1q, mq)]
         self.hr = hr_next
-        del xr, wr, wq, h1q, x2q
+        del xr, wr, wq, h1q, x2q, mq
         timer.add("forward", t4, timer.mark())
         self.next_layer = i + 1
         return i

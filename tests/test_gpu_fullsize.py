@@ -150,7 +150,7 @@ def test_config3_mlp_block_full_size():
         assert int(info.item()) == 0
         check_factor(E, H, in_seed, U, dead)
         sub = {nm: W.double() for nm, W in targets.items()}
-        for L, per_group in ((12, 4), (16, 2)):
+        for L, per_group in ((12, 4), (16, 4)):
             tables = {b: (quantile_table(16, 0) if L == 16 else load_table(12, b)) for b in (1, 2, 3, 4)}
             say(f"stage n={n}: row-plan sweeps at L={L}")
             res = quantize_stage_row_groups(sub, {nm: plans[nm] for nm in sub}, H, in_seed, L=L, tables=tables,

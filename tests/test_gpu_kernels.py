@@ -860,6 +860,32 @@ def test_kl_rows(E, T, V):
     assert abs(s[0] / s[1] - mean) < 1e-4 * abs(mean)
 
 
+def test_kl_rows_config4_full_size(E):
+    """Config 4's shape, [8192, 151936] bf16 logit pairs with token weights: the launch's fixed-order sums over all
+    8,192 tokens equal the float64 sums of its own per-token values, and 64 sampled tokens equal the oracle's KL."""
+    T, V = 8192, 151936
+    g1 = torch.Generator(device="cuda").manual_seed(401)
+    g2 = torch.Generator(device="cuda").manual_seed(402)
+    ref = (torch.randn(T, V, generator=g1, device="cuda") * 3.0).bfloat16()
+    q = (ref.float() + 0.3 * torch.randn(T, V, generator=g2, device="cuda")).bfloat16()
+    w = torch.rand(T, generator=g1, device="cuda") * 1.5 + 0.5
+    say(f"kl T={T} V={V} (config 4), weighted")
+    kl, sums = E.kl_rows(ref, q, w)
+    k64 = kl.double().cpu().numpy()
+    w64 = w.double().cpu().numpy()
+    s = sums.double().cpu().numpy()
+    assert abs(s[0] - (w64 * k64).sum()) <= 1e-5 * abs(s[0])
+    assert abs(s[1] - w64.sum()) <= 1e-5 * abs(s[1])
+    pick = np.sort(np.random.default_rng(4).choice(T, 64, replace=False))
+    idx = torch.as_tensor(pick, device="cuda")
+    r16 = ref[idx].view(torch.int16).cpu().numpy().view(np.uint16)
+    q16 = q[idx].view(torch.int16).cpu().numpy().view(np.uint16)
+    ref_kl, _ = O.kl_rows(r16, q16, None)
+    err = (np.abs(k64[pick] - ref_kl) / np.abs(ref_kl)).max()
+    say(f"  sampled tokens: largest relative KL error {err:.3e}; mean KL {s[0] / s[1]:.5f}")
+    assert np.all(np.abs(k64[pick] - ref_kl) <= 1e-4 * np.abs(ref_kl) + 1e-9)
+
+
 def test_pack_trellis_matches_reference(E, golden):
     g = golden("misc")
     for bits in (1, 2, 3, 4):
