@@ -1,12 +1,15 @@
 // Causal grouped-query attention of the calibration forwards, fused: the score matrix never reaches memory.
 //
-// One workgroup per (sequence, head, block of 128 queries); its four waves take 32 queries each and walk the key
-// blocks of 32 up to their own diagonal, independently (no barrier: a wave stops where its queries end). Per key
-// block a wave forms S^T = K Q^T (32 keys x 32 queries: the head dim, 128, as eight 16-deep steps of
-// v_mfma_f32_32x32x16_bf16, float32 sums), masks it causally, updates each query's running maximum and sum (the
-// online softmax: exp2 with the scale and log2(e) folded into the scores), rounds the probabilities to bf16 and
-// accumulates O^T += V^T P^T (128 x 32, float32) with the earlier sums rescaled. At the end O = O^T / sum, rounded
-// to bf16 (nearest, ties to even).
+// One workgroup per (sequence, head, block of 128 queries); its four waves take 32 queries each. The workgroup walks
+// the key blocks of 64 up to its last query: each block's K and V rows (16 KB each) go straight from memory into LDS
+// (global_load_lds, 16 bytes a lane, no registers), double-buffered, the next block's loads issued as soon as the
+// current one is published (one barrier a block), so the four waves share one copy and no wave waits on a global
+// load. Per 32-key half of a block a wave forms S^T = K Q^T (32 keys x 32 queries: the head dim, 128, as eight
+// 16-deep steps of v_mfma_f32_32x32x16_bf16, float32 sums), masks it causally, updates each query's running maximum
+// and sum (the online softmax: exp2 with the scale and log2(e) folded into the scores), rounds the probabilities to
+// bf16 and accumulates O^T += V^T P^T (128 x 32, float32) with the earlier sums rescaled; a wave past its own last
+// query skips the half (its key blocks still arrive for the others). At the end O = O^T / sum, rounded to bf16
+// (nearest, ties to even).
 //
 // Operand layouts (32x32x16 bf16 MFMA): A[m][k] has lane l holding m = l % 32 and k = 8 (l / 32) .. + 7; B[k][n]
 // has lane l holding n = l % 32 and the same k; the result has lane l holding column l % 32 and rows
@@ -14,150 +17,170 @@
 // (keys {0-3, 8-11} in lanes 0-31 and {4-7, 12-15} in lanes 32-63 for the first 16 keys, +16 for the second): the
 // V^T operand takes the same order, as two transposing LDS reads (ds_read_b64_tr_b16: a 16-lane group reads a 4 x 16
 // block, lane i receiving the four rows of column i) of four consecutive keys each. Q's fragments (B of S^T: eight
-// consecutive head-dim values of one query) stay in registers; K's (A of S^T) come straight from memory as 16-byte
-// loads. Each wave keeps its own copy of the key block's V rows in LDS: 256-byte rows whose 16-byte chunks are
-// XOR-swizzled by 4 (row & 3), so the 32 lanes a transposing read serves at once touch 16 different chunks of four
-// rows (all 64 banks once).
+// consecutive head-dim values of one query) stay in registers; K's (A of S^T: eight consecutive head-dim values of
+// one key) are 16-byte LDS reads. LDS rows are 256 bytes; K's 16-byte chunks are XOR-swizzled by (row & 15), so the
+// 16 keys a fragment read serves at once touch 16 different chunks (all 64 banks once); V's by 4 (row & 3), so the
+// 32 lanes a transposing read serves at once touch 16 different chunks of four rows. The loads place each chunk where
+// the swizzle puts it (a lane fetches the chunk that belongs in its 16-byte slot).
 #include "common.h"
 
 typedef __bf16 lamq_at_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float lamq_at_f32x16 __attribute__((ext_vector_type(16)));
 
-#define AT_D 128   // head dim
-#define AT_QW 32   // queries per wave
-#define AT_KB 32   // keys per block
-#define AT_QB 128  // queries per workgroup
+#define AT_D 128                        // head dim
+#define AT_QW 32                        // queries per wave
+#define AT_KB 32                        // keys per half block (one S^T tile)
+#define AT_KB2 64                       // keys per block in LDS
+#define AT_QB 128                       // queries per workgroup
+#define AT_OPB (AT_KB2 * AT_D * 2)      // bytes of one operand's block (16 KB)
 
+// byte offset of 16-byte chunk `chunk` (0..15) of row `row` in a V block, and in a K block
 __device__ __forceinline__ uint32_t at_sw(int row, int chunk)
 {
     return (uint32_t)(row * (AT_D * 2) + ((chunk ^ (4 * (row & 3))) << 4));
 }
+__device__ __forceinline__ uint32_t at_ksw(int row, int chunk)
+{
+    return (uint32_t)(row * (AT_D * 2) + ((chunk ^ (row & 15)) << 4));
+}
 
-__global__ __launch_bounds__(256) void attention_causal_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_causal_kernel(
     const uint16_t* __restrict__ Q, int64_t sqb, int64_t sqh, int64_t sqt, const uint16_t* __restrict__ K,
     int64_t skb, int64_t skh, int64_t skt, const uint16_t* __restrict__ V, int64_t svb, int64_t svh, int64_t svt,
     uint16_t* __restrict__ O, int64_t sob, int64_t soh, int64_t sot, int rep, int T, float scale_log2)
 {
-    __shared__ __align__(16) uint8_t lds[4][AT_KB * AT_D * 2];
+    __shared__ __align__(16) uint8_t lds[2][2][AT_OPB];  // [buffer][K, V]
     const int nqb = (T + AT_QB - 1) / AT_QB;
     const int qb = nqb - 1 - (int)blockIdx.x;  // the longest query blocks first
     const int h = (int)blockIdx.y, b = (int)blockIdx.z;
     const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
     const int q0 = qb * AT_QB + AT_QW * wave;
-    if (q0 >= T) return;  // the whole wave
     const int li = lane & 31, hi = lane >> 5, g = lane >> 4, i16 = lane & 15;
     const uint16_t* Qp = Q + b * sqb + (int64_t)h * sqh;
     const uint16_t* Kp = K + b * skb + (int64_t)(h / rep) * skh;
     const uint16_t* Vp = V + b * svb + (int64_t)(h / rep) * svh;
+    const uint32_t base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
+    // every wave takes part in the loads and barriers up to the workgroup's last query; a wave's own work ends at its
+    // last query (none for a wave wholly past T)
+    const int wg_last = (qb * AT_QB + AT_QB < T ? qb * AT_QB + AT_QB : T) - 1;
+    const int nblk = wg_last / AT_KB2 + 1;
+    const int my_last = q0 < T ? (q0 + AT_QW < T ? q0 + AT_QW : T) - 1 : -1;
+    // block kb's rows (keys past T read row T - 1: finite values that meet zero probabilities) into buffer kb & 1:
+    // instruction i (four a wave and operand) covers rows 4i .. 4i + 3, lane l row 4i + l / 16, slot l % 16
+    auto load_block = [&](int kb) {
+        const int k0 = kb * AT_KB2;
+        const uint32_t kbuf = base + (uint32_t)((kb & 1) * 2 * AT_OPB), vbuf = kbuf + AT_OPB;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int i = 4 * wv + q;
+            const int row = 4 * i + (lane >> 4), slot = lane & 15;
+            const int64_t key = k0 + row < T ? k0 + row : T - 1;
+            load_lds16(Kp + key * skt + 8 * (slot ^ (row & 15)), kbuf + (uint32_t)(i * 1024));
+            load_lds16(Vp + key * svt + 8 * (slot ^ (4 * (row & 3))), vbuf + (uint32_t)(i * 1024));
+        }
+    };
+    load_block(0);
     const int myq = q0 + li;  // this lane's query (past T: computed, not stored)
     const int qrow = myq < T ? myq : T - 1;
     lamq_at_bf16x8 qf[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) qf[j] = *reinterpret_cast<const lamq_at_bf16x8*>(Qp + qrow * sqt + 16 * j + 8 * hi);
+    // the Q fragments as operands of an empty asm: the compiler waits for their loads here, before the loop. The
+    // loop's own waits are asm, invisible to it, so without this it would wait on the Q loads inside the loop, where
+    // its counts would cover the next block's loads as well and stall their prefetch
+    asm volatile("" : "+v"(qf[0]), "+v"(qf[1]), "+v"(qf[2]), "+v"(qf[3]), "+v"(qf[4]), "+v"(qf[5]), "+v"(qf[6]),
+                 "+v"(qf[7]));
     lamq_at_f32x16 o[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int v = 0; v < 16; ++v) o[t][v] = 0.0f;
     float mrun = -__builtin_inff(), lrun = 0.0f;
-    const int last = (q0 + AT_QW < T ? q0 + AT_QW : T) - 1;  // the wave's last query
-    const int nkb = last / AT_KB + 1;
-    uint8_t* vl = lds[wave];
-    const uint32_t vbase = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)vl;
     using v2u = uint32_t __attribute__((ext_vector_type(2)));
-    // K fragments (A of S^T): key k0 + li, head dims 16 j + 8 hi .. + 7 (rows past T read row T - 1: finite values
-    // that meet zero probabilities)
-    auto load_k = [&](int k0, lamq_at_bf16x8 (&kf)[8]) {
-        const int krow = k0 + li < T ? k0 + li : T - 1;
+    for (int kb = 0; kb < nblk; ++kb) {
+        wait_vm<0>();     // this wave's loads of block kb have landed
+        __syncthreads();  // everyone's; the other buffer (block kb - 1) is free
+        if (kb + 1 < nblk) load_block(kb + 1);
+        const uint8_t* kl = lds[kb & 1][0];
+        const uint32_t vbase = base + (uint32_t)(((kb & 1) * 2 + 1) * AT_OPB);
+        for (int hf = 0; hf < 2; ++hf) {
+            const int k0 = kb * AT_KB2 + AT_KB * hf;
+            if (k0 > my_last) break;  // uniform: this wave's queries end before these keys
+            // K fragments (A of S^T): key 32 hf + li of the block, head dims 16 j + 8 hi .. + 7 (chunk 2 j + hi)
+            lamq_at_bf16x8 kf[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) kf[j] = *reinterpret_cast<const lamq_at_bf16x8*>(Kp + krow * skt + 16 * j + 8 * hi);
-    };
-    // (the next block's K loaded during this block would take 64 more registers and one wave per SIMD: 8.1 ms
-    // instead of 4.8 at the config-5 shape)
-    for (int kb = 0; kb < nkb; ++kb) {
-        const int k0 = kb * AT_KB;
-        lamq_at_bf16x8 kf[8];
-        load_k(k0, kf);
-        // V rows: chunk c = lane + 64 i is row c / 16, 16-byte chunk c % 16
-        uint4 vr[8];
+            for (int j = 0; j < 8; ++j)
+                kf[j] = *reinterpret_cast<const lamq_at_bf16x8*>(kl + at_ksw(AT_KB * hf + li, 2 * j + hi));
+            lamq_at_f32x16 s;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int c = lane + 64 * i, r = c >> 4;
-            const int row = k0 + r < T ? k0 + r : T - 1;
-            vr[i] = *reinterpret_cast<const uint4*>(Vp + row * svt + 8 * (c & 15));
-        }
-        lamq_at_f32x16 s;
+            for (int v = 0; v < 16; ++v) s[v] = 0.0f;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) s[v] = 0.0f;
+            for (int j = 0; j < 8; ++j) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[j], qf[j], s, 0, 0, 0);
+            // causal mask, scale, the running maximum of each query (its 32 keys: 16 here, 16 in lane l ^ 32)
+            float mx = -__builtin_inff();
 #pragma unroll
-        for (int j = 0; j < 8; ++j) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[j], qf[j], s, 0, 0, 0);
-        // causal mask, scale, the running maximum of each query (its 32 keys: 16 here, 16 in lane l ^ 32)
-        float mx = -__builtin_inff();
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int key = k0 + 8 * (v >> 2) + 4 * hi + (v & 3);
-            const float x = (key <= myq && key < T) ? s[v] * scale_log2 : -__builtin_inff();
-            s[v] = x;
-            mx = fmaxf(mx, x);
-        }
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float mnew = fmaxf(mrun, mx);  // finite from the first block on: key 0 is never masked
-        const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);  // 0 on the first block
-        float ps = 0.0f;
-        lamq_at_bf16x8 pf[2];
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const float p = __builtin_amdgcn_exp2f(s[v] - mnew);  // masked: exp2(-inf) = 0
-            ps += p;
-            pf[v >> 3][v & 7] = (__bf16)p;
-        }
-        ps += __shfl_xor(ps, 32);
-        lrun = lrun * alpha + ps;
-        mrun = mnew;
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) o[t][v] *= alpha;
-        // the block's V rows into this wave's LDS copy; the wave's own reads below come after them in order
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int c = lane + 64 * i;
-            *reinterpret_cast<uint4*>(vl + at_sw(c >> 4, c & 15)) = vr[i];
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        // all sixteen transposing reads first, one wait, then the eight MFMAs. Lane: head dim 32 t + li; keys
-        // 16 mi + 4 hi + {0..3} and + 8 (the P^T order); the group's lane i16 points at row 16 mi + 4 hi + i16 / 4,
-        // columns 32 t + 16 (g & 1) + 4 (i16 % 4) .. + 3
-        v2u lo[4][2], hi2[4][2];
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int mi = 0; mi < 2; ++mi) {
-                const int row = 16 * mi + 4 * hi + (i16 >> 2);
-                const int col = 32 * t + 16 * (g & 1) + 4 * (i16 & 3);
-                const uint32_t a0 = vbase + at_sw(row, col >> 3) + 8 * ((col >> 2) & 1);
-                const uint32_t a1 = vbase + at_sw(row + 8, col >> 3) + 8 * ((col >> 2) & 1);
-                asm volatile("ds_read_b64_tr_b16 %0, %2\n\tds_read_b64_tr_b16 %1, %3"
-                             : "=v"(lo[t][mi]), "=v"(hi2[t][mi])
-                             : "v"(a0), "v"(a1)
-                             : "memory");
+            for (int v = 0; v < 16; ++v) {
+                const int key = k0 + 8 * (v >> 2) + 4 * hi + (v & 3);
+                const float x = (key <= myq && key < T) ? s[v] * scale_log2 : -__builtin_inff();
+                s[v] = x;
+                mx = fmaxf(mx, x);
             }
-        asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(lo[0][0]), "+v"(lo[0][1]), "+v"(lo[1][0]), "+v"(lo[1][1]), "+v"(lo[2][0]), "+v"(lo[2][1]),
-                       "+v"(lo[3][0]), "+v"(lo[3][1]), "+v"(hi2[0][0]), "+v"(hi2[0][1]), "+v"(hi2[1][0]),
-                       "+v"(hi2[1][1]), "+v"(hi2[2][0]), "+v"(hi2[2][1]), "+v"(hi2[3][0]), "+v"(hi2[3][1])
-                     :
-                     : "memory");
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float mnew = fmaxf(mrun, mx);  // finite from the first half on: key 0 is never masked
+            const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);  // 0 on the first half
+            float ps = 0.0f;
+            lamq_at_bf16x8 pf[2];
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int mi = 0; mi < 2; ++mi) {
-                const uint32_t __attribute__((ext_vector_type(4))) w = {lo[t][mi][0], lo[t][mi][1], hi2[t][mi][0],
-                                                                        hi2[t][mi][1]};
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(lamq_at_bf16x8, w), pf[mi], o[t], 0, 0,
-                                                               0);
+            for (int v = 0; v < 16; ++v) {
+                const float p = __builtin_amdgcn_exp2f(s[v] - mnew);  // masked: exp2(-inf) = 0
+                ps += p;
+                pf[v >> 3][v & 7] = (__bf16)p;
             }
-        // the next block rewrites the LDS copy: every read of this one has returned (waited above)
+            ps += __shfl_xor(ps, 32);
+            lrun = lrun * alpha + ps;
+            mrun = mnew;
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) o[t][v] *= alpha;
+            // all sixteen transposing reads first, one wait, then the eight MFMAs. Lane: head dim 32 t + li; keys
+            // 16 mi + 4 hi + {0..3} and + 8 of the half (the P^T order); the group's lane i16 points at row
+            // 32 hf + 16 mi + 4 hi + i16 / 4, columns 32 t + 16 (g & 1) + 4 (i16 % 4) .. + 3
+            v2u lo[4][2], hi2[4][2];
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int mi = 0; mi < 2; ++mi) {
+                    const int row = AT_KB * hf + 16 * mi + 4 * hi + (i16 >> 2);
+                    const int col = 32 * t + 16 * (g & 1) + 4 * (i16 & 3);
+                    const uint32_t a0 = vbase + at_sw(row, col >> 3) + 8 * ((col >> 2) & 1);
+                    const uint32_t a1 = vbase + at_sw(row + 8, col >> 3) + 8 * ((col >> 2) & 1);
+                    // early-clobber outputs: the first read's destination may not share the second's address
+                    // register (the first can return into it before the second read leaves the wave)
+                    asm volatile("ds_read_b64_tr_b16 %0, %2\n\tds_read_b64_tr_b16 %1, %3"
+                                 : "=&v"(lo[t][mi]), "=&v"(hi2[t][mi])
+                                 : "v"(a0), "v"(a1)
+                                 : "memory");
+                }
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(lo[0][0]), "+v"(lo[0][1]), "+v"(lo[1][0]), "+v"(lo[1][1]), "+v"(lo[2][0]),
+                           "+v"(lo[2][1]), "+v"(lo[3][0]), "+v"(lo[3][1]), "+v"(hi2[0][0]), "+v"(hi2[0][1]),
+                           "+v"(hi2[1][0]), "+v"(hi2[1][1]), "+v"(hi2[2][0]), "+v"(hi2[2][1]), "+v"(hi2[3][0]),
+                           "+v"(hi2[3][1])
+                         :
+                         : "memory");
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int mi = 0; mi < 2; ++mi) {
+                    const uint32_t __attribute__((ext_vector_type(4))) w = {lo[t][mi][0], lo[t][mi][1], hi2[t][mi][0],
+                                                                            hi2[t][mi][1]};
+                    o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(lamq_at_bf16x8, w), pf[mi], o[t], 0,
+                                                                   0, 0);
+                }
+        }
+        // the next iteration's barrier comes after every wave's reads of this buffer (their results are used above)
     }
     if (myq >= T) return;
     const float inv = 1.0f / lrun;

@@ -128,21 +128,23 @@ __device__ __forceinline__ void wait_vm()
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// One direct global->LDS load (16 bytes per lane into m0 + 16 * lane). M0 is saved and restored around it.
+// One direct global->LDS load (16 bytes per lane into m0 + 16 * lane). M0 is saved and restored around it. A load
+// to LDS that reads M0 needs one wait state after a scalar write of M0 (the compiler inserts it for its own code, not
+// inside inline asm): the s_nop 0. Without it the load can take the previous M0 and land in the wrong LDS rows.
 __device__ __forceinline__ void load_lds16(const void* g, uint32_t m)
 {
     uint32_t keep;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
                  : "=&s"(keep)
                  : "v"(g), "s"(m)
                  : "memory");
 }
 
-// One direct global->LDS load of 4 bytes per lane (into m0 + 4 * lane).
+// One direct global->LDS load of 4 bytes per lane (into m0 + 4 * lane), with the same wait state after the M0 write.
 __device__ __forceinline__ void load_lds4(const void* g, uint32_t m)
 {
     uint32_t keep;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
                  : "=&s"(keep)
                  : "v"(g), "s"(m)
                  : "memory");

@@ -315,12 +315,14 @@ __global__ __launch_bounds__(256) void gram256_kernel(const uint16_t* __restrict
     }
     // The fragment reads are issued from asm with immediate offsets (+2048 for the second read of a fragment,
     // +8192 per k-step) off one address per fragment and stage; asm reads are invisible to the compiler's wait
-    // insertion, so frag_wait takes the fragments as operands: nothing that uses them can move above it.
+    // insertion, so frag_wait takes the fragments as operands: nothing that uses them can move above it. The outputs
+    // are early-clobber: the second read takes its address after the first has been issued, and a first read whose
+    // destination shared the address register could return into it before the second read leaves the wave.
     using v2u = uint32_t __attribute__((ext_vector_type(2)));
     auto tr_read = [&](uint32_t addr, v2u& lo, v2u& hi, auto ks_tag) {
         constexpr int ks = decltype(ks_tag)::value;
         asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"
-                     : "=v"(lo), "=v"(hi)
+                     : "=&v"(lo), "=&v"(hi)
                      : "v"(addr), "n"(ks * 16 * 512), "n"(ks * 16 * 512 + 4 * 512)
                      : "memory");
     };
