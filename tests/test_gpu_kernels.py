@@ -800,6 +800,36 @@ def test_hessian_large_against_float32(E, N, n, weighted):
     assert err < 1e-4
 
 
+@pytest.mark.parametrize("n", [2560, 9728])
+def test_gram_kernels_repeat_bit_for_bit_under_load(E, n):
+    """The Gram kernels at the config-5 statistics' size (65,536 tokens with digit weights, so the 256-tile kernel
+    class by class; hundreds of tiles keep every CU's LDS busy): H and the cross-Gram four times over from the same
+    inputs, bit for bit equal, and H within 1e-4 of a float32 product. The kernels reduce in a fixed order, so a
+    repeat that differs is a fragment read that took a wrong LDS address under contention (the paired transposing
+    reads' asm once let the first read's destination share the second's address register: runs then differed now
+    and then, only at full size)."""
+    from lookatmyquant_amd import synthetic
+
+    N = 65536
+    g = torch.Generator(device="cuda").manual_seed(n + 7)
+    X = torch.randn(N, n, generator=g, device="cuda").bfloat16()
+    Xq = (X.float() + 0.05 * torch.randn(N, n, generator=g, device="cuda")).bfloat16()
+    w = torch.from_numpy(synthetic.digit_weights(N, 41)).cuda()
+    say(f"gram kernels repeated: N={N} n={n}")
+    H0 = E.hessian(X, w)
+    D0 = E.cross_gram_accum(torch.zeros(n, n, dtype=torch.float32, device="cuda"), X, Xq, w, scale=1.0 / N)
+    for rep in range(3):
+        assert torch.equal(E.hessian(X, w), H0), f"hessian repeat {rep}"
+        D = E.cross_gram_accum(torch.zeros(n, n, dtype=torch.float32, device="cuda"), X, Xq, w, scale=1.0 / N)
+        assert torch.equal(D, D0), f"cross-Gram repeat {rep}"
+    rows = torch.arange(0, n, max(1, n // 64), device="cuda")
+    Xf = X.float()
+    ref = (Xf[:, rows].T @ (Xf * w[:, None])) / N
+    err = ((H0[rows].float() - ref).abs().max() / ref.abs().max()).item()
+    say(f"  max |H - ref| / max |ref| over {rows.numel()} rows = {err:.3e}")
+    assert err < 1e-4
+
+
 def test_hessian_accum_rows(E):
     """lamq_hessian_accum_rows over a row list (repeats allowed, ragged count): scale * sum over the listed rows."""
     from lookatmyquant_amd import synthetic
