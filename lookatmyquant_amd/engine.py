@@ -67,15 +67,39 @@ def viterbi_rows(x: torch.Tensor, C: torch.Tensor, L: int, k: int, start: torch.
 # ----------------------------------------------------------------------------- randomized Hadamard transforms
 
 
-@lru_cache(maxsize=64)
+_UPLOADS: dict = {}  # key -> (device tensors, event after their copy), oldest first
+_UPLOADS_MAX = 512
+
+
+def _uploaded(key, make, dev: str) -> tuple:
+    """Small host-made tables (int8 signs and Hadamard factors) on the device, cached by key: the first use copies
+    them from pinned memory without making the host wait (a blocking copy would wait for the current stream and,
+    through it, for every stream it waits on); every use makes the current stream wait for that copy (an event, no
+    host wait) and marks the tensors as used by it, so an evicted entry's memory is not reused while a kernel on
+    that stream may still read it."""
+    cur = torch.cuda.current_stream(torch.device(dev))
+    hit = _UPLOADS.get(key)
+    if hit is None:
+        ts = tuple(t.to(dev, non_blocking=True) for t in (x.to(torch.int8).contiguous().pin_memory() for x in make()))
+        ev = torch.cuda.Event()
+        ev.record(cur)
+        hit = (ts, ev)
+        while len(_UPLOADS) >= _UPLOADS_MAX:
+            _UPLOADS.pop(next(iter(_UPLOADS)))
+        _UPLOADS[key] = hit
+    else:
+        cur.wait_event(hit[1])
+        for t in hit[0]:
+            t.record_stream(cur)
+    return hit[0]
+
+
 def _factors(n: int, dev: str):
-    A, B = hadamard_factors(n)
-    return A.to(torch.int8).to(dev).contiguous(), B.to(torch.int8).to(dev).contiguous()
+    return _uploaded(("factors", n, dev), lambda: hadamard_factors(n), dev)
 
 
-@lru_cache(maxsize=256)
 def _signs(n: int, seed: int, dev: str):
-    return rht_signs(n, seed).to(torch.int8).to(dev).contiguous()
+    return _uploaded(("signs", n, seed, dev), lambda: (rht_signs(n, seed),), dev)[0]
 
 
 def rht_rows(X: torch.Tensor, seed: int, inverse: bool = False, want_rms: bool = False, out: torch.Tensor | None = None):
