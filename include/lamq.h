@@ -358,6 +358,19 @@ int lamq_causal_softmax_bf16(const uint16_t* S, uint16_t* P, int64_t rows, int T
 int lamq_rms_norm_bf16(const uint16_t* X, int64_t rows, int64_t n, int64_t ldx, const uint16_t* g, uint16_t* Y,
                        int64_t ldy, float eps, void* stream);
 
+/* The per-head RMSNorm of q and k and the rotary embedding after it, fused (the calibration model's q_norm / k_norm
+ * and apply_rotary_pos_emb, quantize.py:1029, in the roundings of the unfused bf16 chain):
+ *   y = bf16( float(bf16(x * rsqrt(mean(x^2) + eps))) * float(g) )        (a row of lamq_rms_norm_bf16)
+ *   Y[r, i] = bf16( float(bf16(y[i] * cos[t, i])) + float(bf16(rot[i] * sin[t, i])) ),
+ *   rot[i] = -y[i + 64] (i < 64), y[i - 64] (i >= 64),  t = (r / heads) % T
+ *   X [rows, n] (row stride ldx), Y [rows, n] (ldy), g [n], cos and sin [T, n] (row stride ldcs), bf16 bits, rows
+ *   ordered (sequence, token, head), rows a multiple of heads * T; n = 128 (LAMQ_EUNSUP otherwise); strides
+ *   multiples of 8, pointers 16-byte aligned. Replaces q_norm / k_norm followed by q * cos + rotate_half(q) * sin
+ *   (a negation, a concatenation, two products and a sum over q and over k) in the forwards. */
+int lamq_rms_norm_rope_bf16(const uint16_t* X, int64_t rows, int64_t n, int64_t ldx, const uint16_t* g,
+                            const uint16_t* cosT, const uint16_t* sinT, int64_t ldcs, int64_t heads, int64_t T,
+                            uint16_t* Y, int64_t ldy, float eps, void* stream);
+
 /* The MLP gate of the forwards (silu(gate) * up, in float32 with the bf16 rounding after each of the two as the
  * unfused chain rounds): y = bf16(float(bf16(a / (1 + exp(-a)))) * float(b)), n elements (a multiple of 8) of
  * 16-byte aligned contiguous bf16 a, b, y. */

@@ -64,6 +64,8 @@ SIGNATURES = {
     "lamq_causal_softmax_bf16": (_c_int, [_p, _p, _c_i64, _c_int, _c_i64, _c_i64, _c_flt, _p]),
     "lamq_swiglu_bf16": (_c_int, [_p, _p, _p, _c_i64, _p]),
     "lamq_rms_norm_bf16": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _p, _c_i64, _c_flt, _p]),
+    "lamq_rms_norm_rope_bf16": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _p, _p, _c_i64, _c_i64, _c_i64, _p, _c_i64,
+                                         _c_flt, _p]),
     "lamq_attention_causal_bf16": (_c_int, [_p] + [_c_i64] * 3 + [_p] + [_c_i64] * 3 + [_p] + [_c_i64] * 3 + [_p]
                                    + [_c_i64] * 3 + [_c_i64] * 5 + [_c_flt, _p]),
     "lamq_probe_l2_delivery": (_c_int, [_p, _c_i64, _c_int, _c_int, _p]),

@@ -192,6 +192,100 @@ extern "C" int lamq_rms_norm_bf16(const uint16_t* X, int64_t rows, int64_t n, in
     return LAMQ_OK;
 }
 
+// The per-head RMSNorm of q or k and the rotary embedding after it, in one pass over 128-wide rows:
+//   y = bf16( float(bf16(x r)) g ),  r = rsqrt(mean(x^2) + eps)          (a row of lamq_rms_norm_bf16)
+//   out[i] = bf16( float(bf16(y[i] cos[t][i])) + float(bf16(rot[i] sin[t][i])) ),
+//   rot[i] = -y[i + 64] for i < 64, y[i - 64] for i >= 64,
+// each product and the sum rounded to bf16 as the unfused chain (q * cos + rotate_half(q) * sin) rounds them.
+// Sixteen lanes a row, eight elements a lane: the partner element i +- 64 sits in lane +- 8 of the row's sixteen,
+// one exchange of the row's packed values. Rows are ordered (sequence, token, head): token t = (row / heads) % T.
+__global__ __launch_bounds__(256) void rms_norm_rope_bf16_kernel(
+    const uint16_t* __restrict__ X, int64_t rows, int64_t ldx, const uint16_t* __restrict__ g,
+    const uint16_t* __restrict__ cosT, const uint16_t* __restrict__ sinT, int64_t ldcs, int heads, int T,
+    uint16_t* __restrict__ Y, int64_t ldy, float eps)
+{
+    const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int64_t row = wave * 4 + lane / 16;
+    const int sl = lane % 16;
+    const bool live = row < rows;  // lanes past the last row still take part in the reductions and the exchange
+    uint4 u = make_uint4(0u, 0u, 0u, 0u);
+    if (live) u = *reinterpret_cast<const uint4*>(X + row * ldx + 8 * sl);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    float v[8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        v[e] = bf16_bits_to_f32((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+        ss += v[e] * v[e];
+    }
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    const float r = rsqrtf(ss / 128.0f + eps);
+    const uint4 gu = *reinterpret_cast<const uint4*>(g + 8 * sl);
+    const uint32_t gw[4] = {gu.x, gu.y, gu.z, gu.w};
+    uint32_t yb[4];  // y as packed bf16 pairs
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        uint32_t pair = 0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int k = 2 * e + h;
+            const float t = bf16_bits_to_f32(f32_to_bf16_bits(v[k] * r));
+            const float gv = bf16_bits_to_f32((gw[k >> 1] >> (16 * (k & 1))) & 0xFFFFu);
+            pair |= f32_to_bf16_bits(t * gv) << (16 * h);
+        }
+        yb[e] = pair;
+    }
+    uint32_t pb[4];  // the partner lane's y (elements i +- 64)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pb[e] = (uint32_t)__shfl_xor((int)yb[e], 8);
+    if (!live) return;
+    const int64_t tok = (row / heads) % T;
+    const uint4 cu = *reinterpret_cast<const uint4*>(cosT + tok * ldcs + 8 * sl);
+    const uint4 su = *reinterpret_cast<const uint4*>(sinT + tok * ldcs + 8 * sl);
+    const uint32_t cw[4] = {cu.x, cu.y, cu.z, cu.w}, sw[4] = {su.x, su.y, su.z, su.w};
+    const float sgn = sl < 8 ? -1.0f : 1.0f;  // rot = -y[i + 64] in the first half, y[i - 64] in the second
+    uint32_t out[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        uint32_t pair = 0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int sh = 16 * h;
+            const float y = bf16_bits_to_f32((yb[e] >> sh) & 0xFFFFu);
+            const float rot = sgn * bf16_bits_to_f32((pb[e] >> sh) & 0xFFFFu);
+            const float c = bf16_bits_to_f32((cw[e] >> sh) & 0xFFFFu), s = bf16_bits_to_f32((sw[e] >> sh) & 0xFFFFu);
+            const float a = bf16_bits_to_f32(f32_to_bf16_bits(y * c));
+            const float b = bf16_bits_to_f32(f32_to_bf16_bits(rot * s));
+            pair |= f32_to_bf16_bits(a + b) << sh;
+        }
+        out[e] = pair;
+    }
+    *reinterpret_cast<uint4*>(Y + row * ldy + 8 * sl) = make_uint4(out[0], out[1], out[2], out[3]);
+}
+
+extern "C" int lamq_rms_norm_rope_bf16(const uint16_t* X, int64_t rows, int64_t n, int64_t ldx, const uint16_t* g,
+                                       const uint16_t* cosT, const uint16_t* sinT, int64_t ldcs, int64_t heads,
+                                       int64_t T, uint16_t* Y, int64_t ldy, float eps, void* stream)
+{
+    if (!X || !g || !cosT || !sinT || !Y || rows < 0 || n < 1 || heads < 1 || T < 1 || !(eps >= 0.0f))
+        return LAMQ_EINVAL;
+    if (n != 128) return LAMQ_EUNSUP;
+    if (ldx < n || ldy < n || ldcs < n || ldx % 8 || ldy % 8 || ldcs % 8 || rows % (heads * T)) return LAMQ_EINVAL;
+    if (((uintptr_t)X % 16) || ((uintptr_t)Y % 16) || ((uintptr_t)g % 16) || ((uintptr_t)cosT % 16) ||
+        ((uintptr_t)sinT % 16))
+        return LAMQ_EINVAL;
+    if (heads > 0x7fffffff || T > 0x7fffffff) return LAMQ_EUNSUP;
+    if (rows == 0) return LAMQ_OK;
+    const int64_t blocks = cdiv(rows, 16);  // four waves of four rows
+    if (blocks > 0x7fffffff) return LAMQ_EUNSUP;
+    hipLaunchKernelGGL(rms_norm_rope_bf16_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), X, rows,
+                       ldx, g, cosT, sinT, ldcs, (int)heads, (int)T, Y, ldy, eps);
+    LAMQ_LAUNCH_CHECK();
+    return LAMQ_OK;
+}
+
 // The MLP's gate of the forwards, fused: Y = bf16( float(bf16(silu(a))) * float(b) ), silu(a) = a / (1 + exp(-a)) in
 // float32, for bf16 a (the gate product) and b (the up product), eight elements a thread.
 __global__ __launch_bounds__(256) void swiglu_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ Bm,

@@ -537,6 +537,33 @@ def rms_norm(x: torch.Tensor, g: torch.Tensor, eps: float, pad: int = 0) -> torc
     return y
 
 
+def rms_norm_rope(x: torch.Tensor, g: torch.Tensor, eps: float, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """The per-head RMSNorm of q or k and the rotary embedding after it, one pass (lamq_rms_norm_rope_bf16): for x
+    [B, T, heads, 128] bf16 (rows of 128 one stride apart) and cos, sin [T, 128] bf16, y = rms_norm(x, g, eps) then
+    y * cos + rotate_half(y) * sin with the bf16 roundings of that chain (transformers' apply_rotary_pos_emb).
+    Returns a new contiguous [B, T, heads, 128] tensor."""
+    need(x, torch.bfloat16, "x", 4)
+    need(g, torch.bfloat16, "g", 1)
+    B, T, heads, n = x.shape
+    if n != 128 or g.numel() != n:
+        raise ValueError("x must be [B, T, heads, 128] and g [128]")
+    for t, nm in ((cos, "cos"), (sin, "sin")):
+        need(t, torch.bfloat16, nm, 2)
+        if t.shape != (T, n) or t.stride(1) != 1:
+            raise ValueError(f"{nm} must be [T, 128] with a contiguous last dim")
+    if cos.stride(0) != sin.stride(0):
+        raise ValueError("cos and sin must share one row stride")
+    X = x.reshape(-1, n)
+    if X.stride(1) != 1:
+        raise ValueError("x must have a contiguous last dim")
+    y = torch.empty(B, T, heads, n, dtype=x.dtype, device=x.device)
+    rows = X.shape[0]
+    check(lib().lamq_rms_norm_rope_bf16(ptr(X), rows, n, X.stride(0) if rows > 1 else n, ptr(g.contiguous()), ptr(cos),
+                                        ptr(sin), cos.stride(0), heads, T, ptr(y), n, float(eps), stream(x.device)),
+          "rms_norm_rope")
+    return y
+
+
 def row_pad(n: int) -> int:
     """Elements of padding after each row of bf16 activations whose Gram (lamq_hessian_accum, lamq_cross_gram) is
     taken: 192 at n = 2,560, whose 5,120-byte rows measured 15-20% slower in the Gram kernels than 5,504-byte ones (a

@@ -82,11 +82,6 @@ def rope_tables(T: int, sh: Shape, dev):
     return emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
 
 
-def _rotate_half(x):
-    h = x.shape[-1] // 2
-    return torch.cat([-x[..., h:], x[..., :h]], -1)
-
-
 def _lin(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     """x W^T (x [.., n] bf16, W [m, n]) as a linear layer computes it: one 2-d product with W read transposed in
     place (no batched product, no copy of W per call)."""
@@ -102,18 +97,17 @@ def attention(q, k, v, sh: Shape):
 
 
 def attention_input_to_o(x: torch.Tensor, w: dict, sh: Shape, rope) -> torch.Tensor:
-    """The o_proj input of one chunk [B, T, hidden] (normed hidden states in): q/k/v, per-head RMSNorm of q and k,
-    rotary embedding, causal grouped-query attention."""
+    """The o_proj input of one chunk [B, T, hidden] (normed hidden states in): q/k/v, per-head RMSNorm of q and k
+    with the rotary embedding after it (one kernel each, the roundings of q_norm then q * cos + rotate_half(q) * sin),
+    causal grouped-query attention."""
     B, T, _ = x.shape
     q = _lin(x, w["self_attn.q_proj"]).view(B, T, sh.heads, sh.head_dim)
     k = _lin(x, w["self_attn.k_proj"]).view(B, T, sh.kv_heads, sh.head_dim)
     v = _lin(x, w["self_attn.v_proj"]).view(B, T, sh.kv_heads, sh.head_dim)
-    q = rms_norm(q, w["self_attn.q_norm"], sh.eps).transpose(1, 2)
-    k = rms_norm(k, w["self_attn.k_norm"], sh.eps).transpose(1, 2)
-    v = v.transpose(1, 2)
     cos, sin = rope
-    q = q * cos + _rotate_half(q) * sin
-    k = k * cos + _rotate_half(k) * sin
+    q = E.rms_norm_rope(q, w["self_attn.q_norm"], sh.eps, cos, sin).transpose(1, 2)
+    k = E.rms_norm_rope(k, w["self_attn.k_norm"], sh.eps, cos, sin).transpose(1, 2)
+    v = v.transpose(1, 2)
     out = attention(q, k, v, sh)
     return out.transpose(1, 2).reshape(B, T, sh.heads * sh.head_dim)
 

@@ -174,6 +174,31 @@ def test_fused_attention_shapes_against_float64(B, H, Hkv, T):
     assert torch.isfinite(got).all()
 
 
+@pytest.mark.parametrize("B,T,heads,tables", [(2, 2048, 32, "model"), (2, 2048, 8, "model"), (3, 37, 8, "random"),
+                                               (1, 1, 4, "random")])
+def test_rms_norm_rope_matches_the_unfused_chain(B, T, heads, tables):
+    """engine.rms_norm_rope (lamq_rms_norm_rope_bf16) against the chain it replaces, the per-head RMSNorm kernel and
+    then y * cos + rotate_half(y) * sin in torch's bf16 operations (each product and the sum rounded to bf16): equal
+    bit for bit, at the config-5 q and k shapes with the model's tables and at ragged shapes with random ones."""
+    from lookatmyquant_amd import engine as E, stack
+
+    g0 = torch.Generator(device="cuda").manual_seed(B * 100 + T + heads)
+    x = (torch.randn(B, T, heads, 128, generator=g0, device="cuda") * 2).bfloat16()
+    g = (1 + 0.1 * torch.randn(128, generator=g0, device="cuda")).bfloat16()
+    if tables == "model":
+        cos, sin = stack.rope_tables(T, stack.Shape(), torch.device("cuda"))
+    else:
+        cos = (2 * torch.rand(T, 128, generator=g0, device="cuda") - 1).bfloat16()
+        sin = (2 * torch.rand(T, 128, generator=g0, device="cuda") - 1).bfloat16()
+    say(f"rms_norm_rope B={B} T={T} heads={heads} {tables} tables")
+    got = E.rms_norm_rope(x, g, 1e-6, cos, sin)
+    y = E.rms_norm(x, g, 1e-6).transpose(1, 2)
+    rot = torch.cat([-y[..., 64:], y[..., :64]], -1)
+    ref = (y * cos + rot * sin).transpose(1, 2)
+    assert got.shape == ref.shape
+    assert torch.equal(got, ref), (got.float() - ref.float()).abs().max().item()
+
+
 def test_fused_attention_repeats_bit_for_bit_at_config5_size():
     """The fused attention at the config-5 forward's full size (32 sequences of 2,048 tokens, GQA 32/8: 16,384
     workgroups, two to a CU, so the LDS is busy with both): five calls on the same inputs bit for bit equal, and
