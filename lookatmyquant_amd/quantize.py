@@ -176,16 +176,43 @@ def cross_target(H: torch.Tensor, D: torch.Tensor, alpha: float, lam: float = LA
     return cross_map(H, D, alpha, lam).cpu()
 
 
-def cross_map(H: torch.Tensor, D: torch.Tensor, alpha: float, lam: float = LAM,
-              timer: E.KernelTimer | None = None) -> torch.Tensor:
-    """cross_target's M, float64 on the GPU. timer: spans "chol" (4n^3/3 flops) and "qep_gemm" (the products:
-    2 M N K flops for a full one, M N K for a triangular one)."""
+def qep_factor(H: torch.Tensor, lam: float = LAM, timer: E.KernelTimer | None = None) -> tuple:
+    """(U, info): the upper Cholesky factor of (H + lam mean(diag H) I)^-1, the QEP solve's factor, and the failing
+    pivot as a device value (0 when positive definite; no host synchronisation), for a caller that checks info
+    itself later. timer: span "chol" (4n^3/3 flops)."""
     dev = E._abi.device()
     Hg = torch.as_tensor(H).to(dev, torch.float64).contiguous()
-    Dg = torch.as_tensor(D).to(dev, torch.float64).contiguous()
     n = Hg.shape[0]
     with E.span(timer, "chol", 4.0 * n ** 3 / 3):
-        _, U, _, _ = E.chol_inv_upper(Hg, damp=lam)
+        _, U, _, info = E.chol_inv_upper(Hg, damp=lam, raise_on_fail=False)
+    return U, info
+
+
+def qep_check(info: torch.Tensor) -> None:
+    """Raises LinAlgError, as the factorization does, when qep_factor's info names a failing pivot (one host
+    synchronisation)."""
+    bad = int(info.item())
+    if bad:
+        raise E.LinAlgError(f"linalg.cholesky: the leading minor of order {bad} is not positive-definite")
+
+
+def _qep_u(H: torch.Tensor, lam: float, timer, U: torch.Tensor | None) -> torch.Tensor:
+    """U as given (from qep_factor, its info checked by the caller), else the factor here, checked at once."""
+    if U is not None:
+        return U
+    U, info = qep_factor(H, lam, timer)
+    qep_check(info)
+    return U
+
+
+def cross_map(H: torch.Tensor, D: torch.Tensor, alpha: float, lam: float = LAM,
+              timer: E.KernelTimer | None = None, U: torch.Tensor | None = None) -> torch.Tensor:
+    """cross_target's M, float64 on the GPU. U: qep_factor(H, lam)[0], if the caller has it already. timer: spans
+    "chol" (4n^3/3 flops) and "qep_gemm" (the products: 2 M N K flops for a full one, M N K for a triangular one)."""
+    dev = E._abi.device()
+    Dg = torch.as_tensor(D).to(dev, torch.float64).contiguous()
+    n = Dg.shape[0]
+    U = _qep_u(H, lam, timer, U)
     # (H + d I)^-1 = U^T U, so M = I + alpha ((H + d I)^-1 D^T)^T = I + alpha D U^T U: two triangular products
     with E.span(timer, "qep_gemm", 2.0 * n ** 3):
         P = torch.zeros(n, n, dtype=torch.float64, device=dev)
@@ -202,22 +229,21 @@ def _product(A: torch.Tensor, B: torch.Tensor, scale: float = 1.0) -> torch.Tens
 
 
 def qep_targets(H: torch.Tensor, D: torch.Tensor, alpha: float, Ws: dict, lam: float = LAM,
-                timer: E.KernelTimer | None = None) -> dict:
+                timer: E.KernelTimer | None = None, U: torch.Tensor | None = None) -> dict:
     """W* = W M for every matrix of a stage (quantize.py:1505), M = cross_target(H, D, alpha, lam), float64 on the
     GPU. When the stage has fewer rows than inputs M is not formed: W M = W + alpha (W D) (H + d I)^-1 =
-    W + alpha (W D) U^T U, one product and two triangular ones (4 m n^2 flops against 2 n^3 + 2 m n^2)."""
+    W + alpha (W D) U^T U, one product and two triangular ones (4 m n^2 flops against 2 n^3 + 2 m n^2).
+    U: qep_factor(H, lam)[0], if the caller has made it (and checks its info itself)."""
     dev = E._abi.device()
     n = H.shape[0]
     Wg = {nm: torch.as_tensor(W).to(dev, torch.float64) for nm, W in Ws.items()}
     m = sum(W.shape[0] for W in Wg.values())
     if m >= n:
-        M = cross_map(H, D, alpha, lam, timer)
+        M = cross_map(H, D, alpha, lam, timer, U)
         with E.span(timer, "qep_gemm", 2.0 * m * n * n):
             return {nm: _product(W, M) for nm, W in Wg.items()}
-    Hg = torch.as_tensor(H).to(dev, torch.float64).contiguous()
     Dg = torch.as_tensor(D).to(dev, torch.float64).contiguous()
-    with E.span(timer, "chol", 4.0 * n ** 3 / 3):
-        _, U, _, _ = E.chol_inv_upper(Hg, damp=lam)
+    U = _qep_u(H, lam, timer, U)
     out = {}
     with E.span(timer, "qep_gemm", 4.0 * m * n * n):
         for nm, W in Wg.items():
@@ -269,7 +295,7 @@ def stage_factor(H: torch.Tensor, in_seed: int, damp: float = 0.01, timer: E.Ker
 def quantize_stage_row_groups(targets: dict, groups: dict, H: torch.Tensor, in_seed: int, L: int = 12,
                               width: int = 16, look: int = 8, tables: dict | None = None, events: dict | None = None,
                               chol_events: tuple | None = None, damp: float = 0.01, factor: tuple | None = None,
-                              timer: E.KernelTimer | None = None):
+                              timer: E.KernelTimer | None = None, check: bool = True):
     """Every matrix of a stage, row group by row group, with the row trellis at the group's width: the same result
     as quantize_row_groups(target, groups, round_group) with round_group = the tr<bits> word of (target[rows], H,
     in_seed, out_rot=False), for each matrix. targets: {name: W [m, n]}; groups: {name: [{"rows", "bits"}]};
@@ -277,7 +303,9 @@ def quantize_stage_row_groups(targets: dict, groups: dict, H: torch.Tensor, in_s
     GPU, S float64 [m] on the GPU)}; the codes entries and reconstructions follow from them. events / chol_events
     ((dict, key)): torch.cuda.Event pairs around the sweep kernels / the factorization, for timing. damp: the
     Environment's damping fraction (frame.py:521). factor: stage_factor(H, in_seed, damp), if the caller has made it
-    already (for instance on another stream, next to other work); a non-positive-definite factor raises. timer: an
+    already (for instance on another stream, next to other work); a non-positive-definite factor raises (with
+    check=False the caller checks the factor's info itself, after the sweep is enqueued: no host synchronisation
+    here, the results then to be discarded if it failed). timer: an
     engine.KernelTimer; every launch of the sweep is timed on this stream (one stream for all groups) under "block" and
     "trailing", the row rotations under "rht" (2n(a + b) flops a row), and the factor as in stage_factor."""
     names = list(targets)
@@ -297,7 +325,7 @@ def quantize_stage_row_groups(targets: dict, groups: dict, H: torch.Tensor, in_s
         factor = stage_factor(H, in_seed, damp, timer)
     if factor is not None:
         U, dead, info = factor
-        if int(info.item()):
+        if check and int(info.item()):
             raise E.LinAlgError(f"linalg.cholesky: the leading minor of order {int(info.item())} is not positive-definite")
     else:
         Hr = E.rotate_hessian(torch.as_tensor(H).to(dev, torch.float64).contiguous(), in_seed)

@@ -24,7 +24,8 @@ import torch
 from . import artifact
 from . import engine as E
 from . import synthetic
-from .quantize import LAM, matrix_seeds, parse, qep_targets, quantize_stage_row_groups, stage_factor
+from .quantize import (LAM, matrix_seeds, parse, qep_check, qep_factor, qep_targets, quantize_stage_row_groups,
+                       stage_factor)
 from .tables import load_table, quantile_table
 
 
@@ -316,15 +317,24 @@ class StackBuild:
         t25 = timer.mark()
         timer.add("statistics", t2, t25)
         _, in_seed = matrix_seeds(i, names[0], 0, names[0], self.seed_set)
+        qf = None
         if kt is None:
             # the stage's factor (rotation of H, damped inverse factor) on a second stream, next to the QEP targets
-            # (their own factor of H + lambda I and products) on this one: the two are independent
+            # (their own factor of H + lambda I and products) on this one: the two are independent. Neither factor
+            # is checked until the sweep is enqueued, so the host does not wait for the stream before then.
             self.side.wait_stream(self.main)
             with torch.cuda.stream(self.side):
                 factor = stage_factor(H, in_seed, 0.01)
+                f_bad = _flag_later(factor[2])
+            if cross:
+                qf = qep_factor(H, self.lam)
+                q_bad = _flag_later(qf[1])
         else:
             factor = stage_factor(H, in_seed, 0.01, kt)
-        targets = qep_targets(H, D - H, self.alpha, {nm: wr[nm] for nm in cross}, self.lam, kt) if cross else {}
+        targets = {}
+        if cross:
+            targets = qep_targets(H, D - H, self.alpha, {nm: wr[nm] for nm in cross}, self.lam, kt,
+                                  U=None if qf is None else qf[0])
         for nm in coded:
             if nm not in targets:
                 targets[nm] = wr[nm].double()
@@ -336,11 +346,24 @@ class StackBuild:
         timer.add("qep_targets", t25, t3)
         trellis = [nm for nm in coded if parse(progs[nm])[0] == "tr"]
         plans = {nm: self.groups(i, nm) for nm in trellis}
-        factor = self._factor(H, in_seed, factor, f"{i}.{names[0]}")
-        res = {}
+        key = f"{i}.{names[0]}"
+        if kt is not None:
+            factor = self._factor(H, in_seed, factor, key)
+        sweep = lambda f: quantize_stage_row_groups({nm: targets[nm] for nm in trellis}, plans, H, in_seed, L=L,
+                                                    tables=self.device_tables(), factor=f, timer=kt,
+                                                    check=kt is not None)
+        res = sweep(factor) if trellis else {}
+        if kt is None:
+            # the factors' checks, the sweep already queued behind them: a failed QEP factor raises (as the
+            # factorization does), a failed stage factor is damped more and the stage swept again before anything
+            # reads the results
+            if qf is not None and q_bad():
+                qep_check(qf[1])
+            checked = self._factor(H, in_seed, factor, key, f_bad())
+            if checked is not factor:
+                factor = checked
+                res = sweep(factor) if trellis else {}
         if trellis:
-            res = quantize_stage_row_groups({nm: targets[nm] for nm in trellis}, plans, H, in_seed, L=L,
-                                            tables=self.device_tables(), factor=factor, timer=kt)
             if kt is not None:  # the sweep's algorithmic work: trellis ops and trailing-update flops per width
                 n = shapes[trellis[0]][1]
                 steps = sum(E.trellis_row_steps(n))
@@ -385,11 +408,11 @@ class StackBuild:
             self.n_w += m * n
         timer.add("quantize", t3, timer.mark())
 
-    def _factor(self, H, in_seed, factor, key):
+    def _factor(self, H, in_seed, factor, key, bad: int | None = None):
         """The stage factor at the Environment's damping; with redamp, x10 and x100 more where that is not positive
-        definite (one host synchronisation reads the pivot flag)."""
+        definite (one host synchronisation reads the pivot flag, unless the caller has read it: bad)."""
         U, dead, info = factor
-        if int(info.item()) == 0:
+        if (int(info.item()) if bad is None else bad) == 0:
             return factor
         if not self.redamp:
             raise E.LinAlgError(f"stage {key}: linalg.cholesky: the leading minor of order {int(info.item())} is not "
@@ -506,6 +529,16 @@ def saved_codes(out: dict, row_plan: dict | None = None, calibration: dict | Non
     if row_plan is not None:
         payload["row plan"] = row_plan
     return payload
+
+
+def _flag_later(t: torch.Tensor):
+    """A one-element int32 device flag copied to pinned host memory on the current stream, an event after the copy;
+    the returned function waits for that event only (not for what the stream does later) and gives the value."""
+    h = torch.empty(1, dtype=torch.int32, pin_memory=True)
+    h.copy_(t, non_blocking=True)
+    ev = torch.cuda.Event()
+    ev.record()
+    return lambda: (ev.synchronize(), int(h[0]))[1]
 
 
 def _stage_statistics(xq: list, w: list | None, xr: list | None, classes: list | None = None,
