@@ -285,13 +285,14 @@ gemm128_f64_kernel(double* __restrict__ C, int64_t ldc, const double* __restrict
 // k-row, chunk c of k-row k at c ^ 8*(k & LAMQ_KSW_MASK) (the four k-rows of a fragment read 128 bytes apart). Needs
 // even K, lda, ldb (and N for a [k][col] B) and 16-byte aligned A and B, like the 128-tile kernel.
 #define GP_BK 32
-template <bool TRANSB, bool LOWER, bool OVERWRITE>
+// NS: the most stages, K <= NS GP_BK (the whole k-range sits in LDS, 32 NS KB: two stages for the factor's depth-64
+// products give two workgroups a CU, four 128 KB and one)
+template <bool TRANSB, bool LOWER, bool OVERWRITE, int NS = 128 / GP_BK>
 __global__ __launch_bounds__(256) void gemm64_panel_f64_kernel(double* C, int64_t ldc, const double* A, int64_t lda,
                                                                const double* B, int64_t ldb, int64_t M, int64_t N,
                                                                int64_t K, const int32_t* __restrict__ info)
 {
     constexpr int SB = 64 * GP_BK * 8;  // bytes of one operand stage (A: 64 rows x 256 B; B: 32 k-rows x 512 B)
-    constexpr int NS = 128 / GP_BK;     // most stages
     __shared__ __align__(16) uint8_t lds[NS][2][SB];
     if (info && *info != 0) return;
     const int64_t tr = (int64_t)blockIdx.y * 64, tc = (int64_t)blockIdx.x * 64;
@@ -544,8 +545,12 @@ static int gemm_sub_f64(double* C, int64_t ldc, const double* A, int64_t lda, co
         return LAMQ_OK;
     }
     if (chunks && K <= 128 && (OVERWRITE || tiles128 < LAMQ_PANEL_MAX_TILES128)) {
-        hipLaunchKernelGGL((gemm64_panel_f64_kernel<TRANSB, LOWER, OVERWRITE>), grid, dim3(256), 0, s, C, ldc, A, lda, B,
-                           ldb, M, N, K, info);
+        if (K <= 2 * GP_BK)
+            hipLaunchKernelGGL((gemm64_panel_f64_kernel<TRANSB, LOWER, OVERWRITE, 2>), grid, dim3(256), 0, s, C, ldc, A,
+                               lda, B, ldb, M, N, K, info);
+        else
+            hipLaunchKernelGGL((gemm64_panel_f64_kernel<TRANSB, LOWER, OVERWRITE>), grid, dim3(256), 0, s, C, ldc, A, lda,
+                               B, ldb, M, N, K, info);
         LAMQ_LAUNCH_CHECK();
         return LAMQ_OK;
     }
