@@ -23,6 +23,11 @@
 #define BIG_TV 24       // longest fused search: width + look
 #define BIG_LAZY 128
 #define BIG_GX_MAX_R 16384  // most groups of the minima-exchange search (64 KB of LDS)
+// most groups whose back-pointers the merged row-group kernel keeps in LDS; above, they go to the workspace, and the
+// LDS they leave holds a second minima buffer (one barrier a step instead of two)
+#ifndef BIG_BACK_LDS_MAX_R
+#define BIG_BACK_LDS_MAX_R 8192
+#endif
 
 template <int L, int K>
 struct VBig {
@@ -486,7 +491,7 @@ struct GxGroups {
 
 // back-pointers outside LDS: more groups than LDS holds next to their minima
 template <int L, int K>
-constexpr bool gx_back_global() { return VX<L, K, BIG_NT>::R > BIG_GX_MAX_R; }
+constexpr bool gx_back_global() { return VX<L, K, BIG_NT>::R > BIG_BACK_LDS_MAX_R; }
 
 template <int L, int K>
 constexpr int gx_smem_bytes() { return (int)sizeof(GxSmem<L, K, gx_back_global<L, K>()>); }
@@ -586,7 +591,7 @@ extern "C" int lamq_ldlq_trellis16_block(double* T, int64_t m, int64_t n, int64_
 extern "C" size_t lamq_ldlq_trellis16_block_workspace_size(int64_t m, int L, int k)
 {
     if (m < 1 || L < 13 || L > 16 || k < 1 || k > L - 12 || k > 4) return 0;
-    if ((1 << (L - k)) <= BIG_GX_MAX_R) return 0;  // the back-pointers fit in LDS
+    if ((1 << (L - k)) <= BIG_BACK_LDS_MAX_R) return 0;  // the back-pointers stay in LDS
     return (size_t)m * (size_t)(BIG_TV - 1) * BIG_NT * sizeof(uint32_t);
 }
 
