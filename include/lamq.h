@@ -121,7 +121,9 @@ int lamq_ldlq_trellis16_block(double* T, int64_t m, int64_t n, int64_t ldT, cons
 /* The same fused block with the back-pointers in a caller's workspace: lamq_ldlq_trellis16_block's results, bit for
  * bit. With 2^15 groups (L = 16, k = 1) the minima-exchange search's 128 KB of group minima leave no LDS for the
  * back-pointers; given this workspace, that case runs the minima-exchange kernel (two barriers per step) instead of
- * the quarter-window one (eight). Other (L, k) need none and ignore it.
+ * the quarter-window one (eight). With 2^14 groups (L = 16, k = 2; L = 15, k = 1) the back-pointers (94 KB) fit in
+ * LDS beside one 64 KB buffer of group minima; in the workspace they leave room for a second (one barrier per step
+ * instead of two). Other (L, k) need none and ignore it.
  * workspace: lamq_ldlq_trellis16_block_workspace_size(m, L, k) bytes (0: not needed), 4-byte aligned. */
 size_t lamq_ldlq_trellis16_block_workspace_size(int64_t m, int L, int k);
 int lamq_ldlq_trellis16_block_ws(double* T, int64_t m, int64_t n, int64_t ldT, const double* U, int64_t ldU,
@@ -337,6 +339,29 @@ int lamq_pack_trellis(const int32_t* states, int64_t m, int64_t n, int64_t lds, 
  * ---------------------------------------------------------------------------------------------- */
 int lamq_pack_codes(const int32_t* src, int64_t ld, int64_t src_rows, const int64_t* rows, int64_t m, int64_t n,
                     int32_t base, int k, int L, int trellis, uint32_t* codes, int64_t ldc, int32_t* bad, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * lamq_pack_codes for many row groups in one launch (per 32 groups): every group of a stage's matrices, where a launch
+ * per group (a few hundred rows each) costs more in fixed launch time than its HBM traffic. Replaces the per-group
+ * loop of compiler_artifact.py:328-353 (encode_entry over a matrix's groups) around pack_symbols and pack_trellis
+ * (:225-240, :261-284). Each entry carries one lamq_pack_codes call's src, ld, src_rows, rows, m, base, k, codes and
+ * ldc; n, L and trellis are shared. Every group's code words and bad flags are those lamq_pack_codes gives for it
+ * alone (the same arithmetic); groups must not share code words. Every entry is checked, as lamq_pack_codes checks
+ * its arguments, before anything is launched.
+ * ---------------------------------------------------------------------------------------------- */
+typedef struct {
+    const int32_t* src;
+    int64_t ld;
+    int64_t src_rows;
+    const int64_t* rows;
+    int64_t m;
+    int32_t base;
+    int k;
+    uint32_t* codes;
+    int64_t ldc;
+} lamq_pack_group;
+int lamq_pack_codes_groups(const lamq_pack_group* groups, int ngroups, int64_t n, int L, int trellis, int32_t* bad,
+                           void* stream);
 
 /* ------------------------------------------------------------------------------------------------
  * The causal softmax of the calibration forwards' attention (the forward of the model the reference's capture runs,

@@ -61,6 +61,7 @@ SIGNATURES = {
     "lamq_kl_rows_noalloc": (_c_int, [_p, _p, _c_i64, _c_i64, _c_i64, _c_i64, _p, _p, _p, _p]),
     "lamq_pack_trellis": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _p, _c_i64, _p, _p]),
     "lamq_pack_codes": (_c_int, [_p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _p, _c_i64, _p, _p]),
+    "lamq_pack_codes_groups": (_c_int, [_p, _c_int, _c_i64, _c_int, _c_int, _p, _p]),
     "lamq_causal_softmax_bf16": (_c_int, [_p, _p, _c_i64, _c_int, _c_i64, _c_i64, _c_flt, _p]),
     "lamq_swiglu_bf16": (_c_int, [_p, _p, _p, _c_i64, _p]),
     "lamq_rms_norm_bf16": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _p, _c_i64, _c_flt, _p]),
@@ -83,6 +84,13 @@ class TrellisGroup32(ctypes.Structure):
     """lamq_trellis_group32 of include/lamq.h: one row group of lamq_ldlq_trellis_block_groups (L = 12)."""
 
     _fields_ = [("r0", _c_i64), ("rows", _c_i64), ("k", _c_int), ("table64", _p), ("table32", _p)]
+
+
+class PackGroup(ctypes.Structure):
+    """lamq_pack_group of include/lamq.h: one row group of lamq_pack_codes_groups."""
+
+    _fields_ = [("src", _p), ("ld", _c_i64), ("src_rows", _c_i64), ("rows", _p), ("m", _c_i64), ("base", ctypes.c_int32),
+                ("k", _c_int), ("codes", _p), ("ldc", _c_i64)]
 
 
 _LIB = None

@@ -9,15 +9,14 @@
 // and each code word written once; the kernel is HBM-bound at 4 bytes read and k/8 bytes written per symbol.
 #include "common.h"
 
+// item id = (row r of the group, output group g) of one group's m * ceil(n / 32) items
 template <int K, bool TRELLIS, bool VEC>
-__global__ __launch_bounds__(256) void pack_codes_kernel(const int32_t* __restrict__ src, int64_t ld,
-                                                         int64_t src_rows, const int64_t* __restrict__ rows, int64_t m,
-                                                         int64_t n, int32_t base, int L, uint32_t* __restrict__ codes,
-                                                         int64_t ldc, int32_t* __restrict__ bad)
+__device__ __forceinline__ void pack_item(const int32_t* __restrict__ src, int64_t ld, int64_t src_rows,
+                                          const int64_t* __restrict__ rows, int64_t n, int32_t base, int L,
+                                          uint32_t* __restrict__ codes, int64_t ldc, int32_t* __restrict__ bad,
+                                          int64_t id)
 {
     const int64_t G = (n + 31) / 32;
-    const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (id >= m * G) return;
     const int64_t r = id / G, g = id - r * G;
     const int64_t fg = TRELLIS ? G - 1 - g : g;  // the forward group this output group holds
     const int64_t c0 = fg * 32;
@@ -78,6 +77,17 @@ __global__ __launch_bounds__(256) void pack_codes_kernel(const int32_t* __restri
     if (!ok) atomicOr(bad, 1);
 }
 
+template <int K, bool TRELLIS, bool VEC>
+__global__ __launch_bounds__(256) void pack_codes_kernel(const int32_t* __restrict__ src, int64_t ld,
+                                                         int64_t src_rows, const int64_t* __restrict__ rows, int64_t m,
+                                                         int64_t n, int32_t base, int L, uint32_t* __restrict__ codes,
+                                                         int64_t ldc, int32_t* __restrict__ bad)
+{
+    const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (id >= m * ((n + 31) / 32)) return;
+    pack_item<K, TRELLIS, VEC>(src, ld, src_rows, rows, n, base, L, codes, ldc, bad, id);
+}
+
 template <int K>
 static int launch_pack(const int32_t* src, int64_t ld, int64_t src_rows, const int64_t* rows, int64_t m, int64_t n,
                        int32_t base, int L, int trellis, uint32_t* codes, int64_t ldc, int32_t* bad, hipStream_t st)
@@ -121,6 +131,97 @@ extern "C" int lamq_pack_codes(const int32_t* src, int64_t ld, int64_t src_rows,
         case 7: return launch_pack<7>(src, ld, src_rows, rows, m, n, base, L, trellis, codes, ldc, bad, st);
         default: return launch_pack<8>(src, ld, src_rows, rows, m, n, base, L, trellis, codes, ldc, bad, st);
     }
+}
+
+// ------------------------------------------------------------------------------------------------ many groups at once
+// Workgroup b takes 256 consecutive items of one group: the groups' workgroup ranges are laid end to end, and a
+// uniform scan over at most PACK_GROUPS_PER_LAUNCH entries finds b's group. The arithmetic is pack_item's, so every
+// group's words and flags are those of lamq_pack_codes on that group alone.
+#define PACK_GROUPS_PER_LAUNCH 32
+struct PackGroupArg {
+    const int32_t* src;
+    const int64_t* rows;
+    uint32_t* codes;
+    int64_t ld, src_rows, m, ldc;
+    int32_t base;
+    int k, vec;
+};
+struct PackGroupArgs {
+    PackGroupArg g[PACK_GROUPS_PER_LAUNCH];
+    int64_t first[PACK_GROUPS_PER_LAUNCH + 1];  // first workgroup of each group; first[count] is the grid
+    int count;
+};
+
+template <bool TRELLIS, bool VEC>
+__device__ __forceinline__ void pack_item_k(const PackGroupArg& a, int64_t n, int L, int32_t* bad, int64_t id)
+{
+    switch (a.k) {
+    case 1: pack_item<1, TRELLIS, VEC>(a.src, a.ld, a.src_rows, a.rows, n, a.base, L, a.codes, a.ldc, bad, id); break;
+    case 2: pack_item<2, TRELLIS, VEC>(a.src, a.ld, a.src_rows, a.rows, n, a.base, L, a.codes, a.ldc, bad, id); break;
+    case 3: pack_item<3, TRELLIS, VEC>(a.src, a.ld, a.src_rows, a.rows, n, a.base, L, a.codes, a.ldc, bad, id); break;
+    case 4: pack_item<4, TRELLIS, VEC>(a.src, a.ld, a.src_rows, a.rows, n, a.base, L, a.codes, a.ldc, bad, id); break;
+    case 5: pack_item<5, TRELLIS, VEC>(a.src, a.ld, a.src_rows, a.rows, n, a.base, L, a.codes, a.ldc, bad, id); break;
+    case 6: pack_item<6, TRELLIS, VEC>(a.src, a.ld, a.src_rows, a.rows, n, a.base, L, a.codes, a.ldc, bad, id); break;
+    case 7: pack_item<7, TRELLIS, VEC>(a.src, a.ld, a.src_rows, a.rows, n, a.base, L, a.codes, a.ldc, bad, id); break;
+    default: pack_item<8, TRELLIS, VEC>(a.src, a.ld, a.src_rows, a.rows, n, a.base, L, a.codes, a.ldc, bad, id); break;
+    }
+}
+
+template <bool TRELLIS>
+__global__ __launch_bounds__(256) void pack_codes_groups_kernel(PackGroupArgs args, int64_t n, int L,
+                                                                int32_t* __restrict__ bad)
+{
+    const int64_t b = blockIdx.x;
+    int i = 0;
+    while (i + 1 < args.count && b >= args.first[i + 1]) ++i;
+    const PackGroupArg& a = args.g[i];
+    const int64_t id = (b - args.first[i]) * 256 + threadIdx.x;
+    if (id >= a.m * ((n + 31) / 32)) return;
+    if (a.vec)
+        pack_item_k<TRELLIS, true>(a, n, L, bad, id);
+    else
+        pack_item_k<TRELLIS, false>(a, n, L, bad, id);
+}
+
+extern "C" int lamq_pack_codes_groups(const lamq_pack_group* groups, int ngroups, int64_t n, int L, int trellis,
+                                      int32_t* bad, void* stream)
+{
+    if ((!groups && ngroups > 0) || ngroups < 0 || n < 1 || !bad) return LAMQ_EINVAL;
+    const int64_t G = (n + 31) / 32;
+    for (int i = 0; i < ngroups; ++i) {  // every group checked before anything is launched
+        const lamq_pack_group& g = groups[i];
+        if (!g.src || !g.codes || g.m < 0 || g.ld < n || g.src_rows < 0 || g.k < 1 || g.k > 8) return LAMQ_EINVAL;
+        if (!g.rows && g.m > g.src_rows) return LAMQ_EINVAL;
+        if (trellis && (L <= g.k || L > 16)) return LAMQ_EINVAL;
+        if (g.ldc < G * g.k) return LAMQ_EINVAL;
+        if (g.m * G > (int64_t)256 * 0x7fffffff) return LAMQ_EUNSUP;
+    }
+    hipStream_t st = as_stream(stream);
+    for (int i0 = 0; i0 < ngroups;) {
+        PackGroupArgs args{};
+        int64_t blocks = 0;
+        int c = 0;
+        for (; i0 < ngroups && c < PACK_GROUPS_PER_LAUNCH; ++i0) {
+            const lamq_pack_group& g = groups[i0];
+            const int64_t nb = cdiv(g.m * G, 256);
+            if (nb == 0) continue;
+            if (blocks + nb > 0x7fffffff) break;  // the next launch takes it
+            args.g[c] = PackGroupArg{g.src, g.rows, g.codes, g.ld, g.src_rows, g.m, g.ldc, g.base, g.k,
+                                     (g.ld % 4) == 0 && ((uintptr_t)g.src & 15) == 0 ? 1 : 0};
+            args.first[c] = blocks;
+            blocks += nb;
+            ++c;
+        }
+        if (c == 0) continue;
+        args.first[c] = blocks;
+        args.count = c;
+        if (trellis)
+            hipLaunchKernelGGL((pack_codes_groups_kernel<true>), dim3((unsigned)blocks), dim3(256), 0, st, args, n, L, bad);
+        else
+            hipLaunchKernelGGL((pack_codes_groups_kernel<false>), dim3((unsigned)blocks), dim3(256), 0, st, args, n, L, bad);
+        LAMQ_LAUNCH_CHECK();
+    }
+    return LAMQ_OK;
 }
 
 extern "C" int lamq_pack_trellis(const int32_t* states, int64_t m, int64_t n, int64_t lds, int k, int L, uint32_t* codes,

@@ -555,11 +555,16 @@ struct TrellisBlockBig {
                    int32_t* state, int32_t* states, int64_t lds, double* Z, int64_t ldZ, uint32_t* back_ws, int pre,
                    hipStream_t s)
     {
-        if constexpr (VX<L, K, BIG_NT>::R <= BIG_GX_MAX_R)
-            hipLaunchKernelGGL((ldlq_trellis_block_gx_kernel<L, K, false>), dim3((unsigned)m), dim3(BIG_NT), 0, s, T, n,
-                               ldT, U, ldU, S, table64, table16, b0, b1, width, look, state, states, lds, Z, ldZ, nullptr,
-                               pre);
-        else if (back_ws)
+        if constexpr (VX<L, K, BIG_NT>::R <= BIG_GX_MAX_R) {
+            if (gx_back_global<L, K>() && back_ws)  // the back-pointers in the workspace, two minima buffers in LDS
+                hipLaunchKernelGGL((ldlq_trellis_block_gx_kernel<L, K, true>), dim3((unsigned)m), dim3(BIG_NT), 0, s, T,
+                                   n, ldT, U, ldU, S, table64, table16, b0, b1, width, look, state, states, lds, Z, ldZ,
+                                   back_ws, pre);
+            else
+                hipLaunchKernelGGL((ldlq_trellis_block_gx_kernel<L, K, false>), dim3((unsigned)m), dim3(BIG_NT), 0, s, T,
+                                   n, ldT, U, ldU, S, table64, table16, b0, b1, width, look, state, states, lds, Z, ldZ,
+                                   nullptr, pre);
+        } else if (back_ws)
             hipLaunchKernelGGL((ldlq_trellis_block_gx_kernel<L, K, true>), dim3((unsigned)m), dim3(BIG_NT), 0, s, T, n,
                                ldT, U, ldU, S, table64, table16, b0, b1, width, look, state, states, lds, Z, ldZ, back_ws,
                                pre);

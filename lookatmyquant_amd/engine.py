@@ -1012,3 +1012,37 @@ def pack_codes(src: torch.Tensor, k: int, rows: torch.Tensor | None = None, base
     check(lib().lamq_pack_codes(ptr(src), ld(src), nsrc, ptr(rows), m, n, int(base), k, L, 1 if trellis else 0, ptr(out),
                                 out.stride(0), ptr(bad), stream(src.device)), "pack_codes")
     return out, bad
+
+
+def pack_codes_groups(items: list, L: int = 12, trellis: bool = True, bad: torch.Tensor | None = None):
+    """pack_codes for many row groups in one launch (lamq_pack_codes_groups): items are (src, k, rows, base) with
+    pack_codes's meanings, every src of the same width n and on one device. Returns ([codes of each item], bad), each
+    item's words those pack_codes gives for it alone (an empty group's: no rows, nothing launched for it). Nothing
+    synchronises."""
+    if not items:
+        raise ValueError("no groups to pack")
+    n = items[0][0].shape[1]
+    dev = items[0][0].device
+    descs = (_abi.PackGroup * len(items))()
+    outs, count = [], 0
+    for src, k, rows, base in items:
+        need(src, torch.int32, "src", 2)
+        if src.shape[1] != n or src.device != dev:
+            raise ValueError("every group's source must have the same width and device")
+        if rows is not None:
+            if rows.dtype != torch.int64 or rows.device != dev or rows.dim() != 1 or not rows.is_contiguous():
+                raise ValueError("rows must be a contiguous 1-d int64 tensor on the device of src")
+        m = src.shape[0] if rows is None else rows.shape[0]
+        out = torch.empty(m, (n + 31) // 32 * k, dtype=torch.int32, device=dev)
+        outs.append(out)
+        if m == 0:
+            continue
+        d = descs[count]
+        d.src, d.ld, d.src_rows, d.rows, d.m = ptr(src), ld(src), src.shape[0], ptr(rows), m
+        d.base, d.k, d.codes, d.ldc = int(base), int(k), ptr(out), out.stride(0)
+        count += 1
+    if bad is None:
+        bad = torch.zeros(1, dtype=torch.int32, device=dev)
+    check(lib().lamq_pack_codes_groups(ctypes.addressof(descs), count, n, L, 1 if trellis else 0, ptr(bad),
+                                       stream(dev)), "pack_codes_groups")
+    return outs, bad

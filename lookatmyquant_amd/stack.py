@@ -375,6 +375,7 @@ class StackBuild:
         if i < self.keep:
             self.kept[(i, s)] = {"Xq": torch.cat(xqf), "Xr": torch.cat(xrf), "H": H, "D": D, "targets": targets,
                                  "in_seed": in_seed, "plans": plans, "U": factor[0], "dead": factor[1]}
+        pack_items, pack_work = [], 0.0  # every row group of the stage's matrices, packed in one launch below
         for nm in trellis:
             st, Srow = res[nm]
             m, n = st.shape
@@ -382,17 +383,22 @@ class StackBuild:
             with E.span(kt, "rht", E.rht_flops(m, n)):
                 Wh = E.rht_rows(Q, in_seed, inverse=True)
             wq[nm] = Wh.to(torch.bfloat16)
-            packed = []
             for gp, rows in zip(plans[nm], E.device_rows(plans[nm], dev)):
                 r = len(gp["rows"])
-                with E.span(kt, "pack", 4.0 * r * n + 4.0 * r * ((n + 31) // 32) * gp["bits"]):
-                    packed.append(E.pack_codes(st, gp["bits"], rows=rows, L=L, bad=self.bad)[0])
+                pack_items.append((st, gp["bits"], rows, 0))
+                pack_work += 4.0 * r * n + 4.0 * r * ((n + 31) // 32) * gp["bits"]
                 self.bits += r * n * gp["bits"] + 16 * r
             self.codes[f"{i}.{nm}"] = {"kind": "trellis", "states": st, "scales": Srow, "in_seed": in_seed,
-                                       "groups": plans[nm], "packed": packed}
+                                       "groups": plans[nm], "packed": []}
             self.n_w += shapes[nm][0] * shapes[nm][1]
             if i < self.keep:  # the weights the quantized stream goes on with (bf16 of the decoded reconstruction)
                 self.kept[(i, s)].setdefault("Wq", {})[nm] = wq[nm]
+        if pack_items:
+            with E.span(kt, "pack", pack_work):
+                packed, _ = E.pack_codes_groups(pack_items, L=L, bad=self.bad)
+            for nm in trellis:
+                self.codes[f"{i}.{nm}"]["packed"] = packed[: len(plans[nm])]
+                packed = packed[len(plans[nm]) :]
         for nm in coded:
             if parse(progs[nm])[0] != "lm":
                 continue

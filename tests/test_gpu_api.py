@@ -302,6 +302,92 @@ def test_pack_codes_flags_rows_outside_the_source():
     assert int(codes.abs().sum().item()) == 0
 
 
+def _paths(rng, ks, n, L):
+    """Random row-trellis paths from state 0, row i at width ks[i], states in [0, 2^L)."""
+    ks = np.asarray(ks, dtype=np.int64)
+    st = np.zeros((ks.size, n), dtype=np.int64)
+    s = np.zeros(ks.size, dtype=np.int64)
+    for c in range(n):
+        s = ((s << ks) | rng.integers(0, 1 << ks)) & ((1 << L) - 1)
+        st[:, c] = s
+    return st
+
+
+@pytest.mark.parametrize("n,L", [(33, 12), (600, 16), (2560, 16)])
+def test_pack_codes_groups_equal_each_group_alone(n, L):
+    """lamq_pack_codes_groups: 37 row groups of three code arrays (more than one launch's 32), widths 1-4 at random,
+    gathered row lists, an empty group, one source with a table offset: every group's words equal lamq_pack_codes on
+    that group alone (and, for the first eight groups, the oracle's pack_trellis of its rows), with no flag raised;
+    then a bad path in one group and a row outside its source in another raise both flags (1 and 2), the
+    out-of-source row's words zero."""
+    from lookatmyquant_amd import engine as E
+
+    rng = np.random.default_rng(n + L)
+    srcs = []  # each row of a source is a path at the width of the groups that read it
+    for si, m in enumerate((200, 96, 130)):
+        ks = rng.integers(1, 5, m)
+        base = 8192 if si == 1 else 0
+        st = _paths(rng, ks, n, L) + base
+        srcs.append((torch.from_numpy(st).int().cuda(), st, ks, base))
+    items, picked = [], []
+    for gi in range(37):
+        src_t, st, ks, base = srcs[gi % 3]
+        k = int(rng.integers(1, 5))
+        cand = np.flatnonzero(ks == k)
+        r = 0 if gi == 5 else int(rng.integers(1, min(40, cand.size) + 1))
+        rows = rng.choice(cand, r, replace=False) if r else cand[:0]
+        items.append((src_t, k, torch.from_numpy(rows.astype(np.int64)).cuda(), base))
+        picked.append((st, rows))
+    say(f"pack_codes_groups n={n} L={L}: 37 groups")
+    outs, bad = E.pack_codes_groups(items, L=L)
+    assert int(bad.item()) == 0
+    for gi, ((src_t, k, rows_t, base), out, (st, rows)) in enumerate(zip(items, outs, picked)):
+        assert out.shape == (rows.size, (n + 31) // 32 * k)
+        if rows.size == 0:  # the empty group: no words, nothing launched for it
+            continue
+        alone, bad1 = E.pack_codes(src_t, k, rows=rows_t, base=base, L=L)
+        assert int(bad1.item()) == 0
+        assert torch.equal(out, alone)
+        if gi < 8 and rows.size:
+            assert np.array_equal(out.cpu().numpy().view(np.uint32), O.pack_trellis(st[rows] - base, k, L))
+    # the flags: a state whose high bit no shift made (a bad path) and a row index past its source
+    src_t, st, ks, base = srcs[0]
+    broken = st.copy()
+    row = int(np.flatnonzero(ks == 2)[0])
+    broken[row, n // 2] ^= 1 << (L - 1)
+    b_t = torch.from_numpy(broken).int().cuda()
+    rows_ok = torch.tensor([row], dtype=torch.int64, device="cuda")
+    rows_out = torch.tensor([0, 200], dtype=torch.int64, device="cuda")
+    outs, bad = E.pack_codes_groups([(b_t, 2, rows_ok, 0), (src_t, 1, rows_out, 0)], L=L)
+    assert int(bad.item()) == 3
+    assert int(outs[1][1].abs().sum().item()) == 0
+    alone, bad1 = E.pack_codes(b_t, 2, rows=rows_ok, L=L)
+    assert int(bad1.item()) == 1 and torch.equal(outs[0], alone)
+
+
+def test_pack_codes_groups_scalar_symbols():
+    """The scalar layout (column order, widths 5-8, no trellis check) through lamq_pack_codes_groups against
+    lamq_pack_codes group by group and the oracle's pack_symbols."""
+    from lookatmyquant_amd import engine as E
+
+    rng = np.random.default_rng(9)
+    n = 70
+    q = rng.integers(0, 256, (60, n))
+    for k in (5, 6, 7):  # a few rows whose symbols fit each narrower width
+        q[4 * k : 4 * k + 3] %= 1 << k
+    src = torch.from_numpy(q).int().cuda()
+    rows = {k: np.flatnonzero(q.max(axis=1) < (1 << k)) for k in (5, 6, 7, 8)}
+    items = [(src, k, torch.from_numpy(rows[k].astype(np.int64)).cuda(), 0) for k in (5, 6, 7, 8)]
+    say("pack_codes_groups, scalar symbols at widths 5-8")
+    outs, bad = E.pack_codes_groups(items, trellis=False)
+    assert int(bad.item()) == 0
+    for (_, k, rows_t, _), out in zip(items, outs):
+        assert rows[k].size >= 3
+        alone, _ = E.pack_codes(src, k, rows=rows_t, trellis=False)
+        assert torch.equal(out, alone)
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), O.pack_symbols(q[rows[k]], k))
+
+
 def test_environment_and_covariance(config12):
     from lookatmyquant_amd import synthetic
     from lookatmyquant_amd.frame import Environment, covariance

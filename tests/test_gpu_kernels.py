@@ -448,11 +448,12 @@ def test_ldlq_trellis_L16_other_widths_match_oracle(E, k):
     assert np.array_equal(st, ref)
 
 
-@pytest.mark.parametrize("k", [1])
+@pytest.mark.parametrize("k", [1, 2])
 def test_ldlq_trellis16_without_workspace_matches_oracle(E, monkeypatch, k):
-    """lamq_ldlq_trellis16_block at L = 16, the entry point without a workspace, for the width whose fused search
+    """lamq_ldlq_trellis16_block at L = 16, the entry point without a workspace, for the widths whose fused search
     otherwise keeps its back-pointers in one (k = 1: the quarter-window kernel, full path costs exchanged through
-    LDS): the same states as the oracle and as the workspace kernel, 3 rows x 272 columns."""
+    LDS; k = 2: the back-pointers in LDS beside one buffer of group minima instead of in the workspace beside two):
+    the same states as the oracle and as the workspace kernel, 3 rows x 272 columns."""
     from lookatmyquant_amd.tables import quantile_table
 
     assert E._abi.lib().lamq_ldlq_trellis16_block_workspace_size(3, 16, k) > 0

@@ -2,6 +2,7 @@
 declares (no compute calls), the host tables (Hadamard factors, rotation signs, Lloyd-Max levels) equal the
 reference's, and the plan/row-plan/program validation behaves like the reference's."""
 
+import ctypes
 import json
 import re
 import subprocess
@@ -104,12 +105,27 @@ def test_argument_errors_are_reported_without_a_gpu():
     assert L.lamq_pack_codes(ptr(q), 8, 8, None, 8, 8, 0, 4, 12, 0, ptr(q), 3, ptr(q), None) == -1
     assert L.lamq_pack_codes(ptr(q), 8, 4, None, 8, 8, 0, 2, 12, 1, ptr(q), 8, ptr(q), None) == -1
     assert L.lamq_pack_codes(None, 8, 8, None, 8, 8, 0, 2, 12, 1, ptr(q), 8, ptr(q), None) == -1
+    # many groups at once: each entry is checked as lamq_pack_codes checks its arguments, before any launch (the
+    # valid first entry is not packed when a later one is refused)
+    good = dict(src=ptr(q), ld=8, src_rows=8, rows=None, m=8, base=0, k=2, codes=ptr(q), ldc=8)
+    for bad_fields in ({"k": 9}, {"k": 12}, {"ldc": 1}, {"src_rows": 4}, {"src": None}, {"codes": None}, {"ld": 4},
+                       {"m": -1}):
+        descs = (_abi.PackGroup * 2)(_abi.PackGroup(**good), _abi.PackGroup(**dict(good, **bad_fields)))
+        assert L.lamq_pack_codes_groups(ctypes.addressof(descs), 2, 8, 12, 1, ptr(q), None) == -1, bad_fields
+    assert L.lamq_pack_codes_groups(None, 1, 8, 12, 1, ptr(q), None) == -1
+    descs = (_abi.PackGroup * 1)(_abi.PackGroup(**good))
+    assert L.lamq_pack_codes_groups(ctypes.addressof(descs), 1, 8, 12, 1, None, None) == -1
+    assert L.lamq_pack_codes_groups(ctypes.addressof(descs), 1, 0, 12, 1, ptr(q), None) == -1
+    assert L.lamq_pack_codes_groups(ctypes.addressof(descs), -1, 8, 12, 1, ptr(q), None) == -1
     assert L.lamq_chol_inv_upper_workspace_size(10) >= 800
     assert L.lamq_viterbi_workspace_size(3, 100, 12, 2) == 3 * 100 * 256
     # the fused 16-bit-state search keeps its back-pointers (23 steps x 1024 words a row) in a workspace where LDS
-    # cannot hold them (k = 1, 2^15 groups); k = 2, 3, 4 keep them in LDS
-    for k, words in ((1, 23 * 1024), (2, 0), (3, 0), (4, 0)):
+    # cannot hold them (k = 1, 2^15 groups) or where the LDS they would take holds a second buffer of group minima
+    # instead (k = 2, 2^14 groups); k = 3, 4 keep them in LDS
+    for k, words in ((1, 23 * 1024), (2, 23 * 1024), (3, 0), (4, 0)):
         assert L.lamq_ldlq_trellis16_block_workspace_size(5, 16, k) == 5 * 4 * words
+    assert L.lamq_ldlq_trellis16_block_workspace_size(5, 15, 1) == 5 * 4 * 23 * 1024
+    assert L.lamq_ldlq_trellis16_block_workspace_size(5, 14, 1) == 0
 
 
 def test_hadamard_factors_and_signs_equal_the_reference(golden):
