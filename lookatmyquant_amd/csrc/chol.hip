@@ -97,11 +97,12 @@ __device__ __forceinline__ double rsqrt_f64(double d)
 }
 
 // v of lane 16 (lane / 16) + J in every lane of each row of 16 (DPP row_newbcast, one VALU move of 64 bits: no
-// scalar registers, no wait states between the moves)
+// scalar registers, no wait states between the moves). Every lane is written, so the move has no old value to keep
+// (mov_dpp: an old operand of 0 would cost a zeroing move before each broadcast)
 template <int J>
 __device__ __forceinline__ double row_bcast_f64(double v)
 {
-    return __longlong_as_double(__builtin_amdgcn_update_dpp(0ll, __double_as_longlong(v), 0x150 + J, 0xf, 0xf, false));
+    return __longlong_as_double(__builtin_amdgcn_mov_dpp(__double_as_longlong(v), 0x150 + J, 0xf, 0xf, false));
 }
 __device__ __forceinline__ double row_bcast_f64(double v, int j)  // j a constant once the loops are unrolled
 {
@@ -171,12 +172,10 @@ __global__ __launch_bounds__(256) void diag_block_kernel(double* __restrict__ A,
         const int c0 = 16 * p;
         if (wave == 0) {  // (1); lanes 16..63 repeat lanes 0..15, so a row broadcast of lane j gives row j's value
             double r[16];
-            // row li of the tile, read whole (its upper part holds finite values) and then masked, so the reads need
-            // no branches
+            // row li of the tile, read whole: its upper part (j > li) holds finite values that are updated below but
+            // never read by a pivot or a lower entry, and the store after the loop writes zeros there
 #pragma unroll
             for (int j = 0; j < 16; ++j) r[j] = T(c0 + li, c0 + j);
-#pragma unroll
-            for (int j = 0; j < 16; ++j) r[j] = j <= li ? r[j] : 0.0;
             double rc[16];  // 1 / l[c][c], the same in every lane
             int fail = 0;   // the first non-positive pivot (the same in every lane)
             // the pivots form the serial chain; each is formed from lane-uniform values with exactly the operations
@@ -186,14 +185,16 @@ __global__ __launch_bounds__(256) void diag_block_kernel(double* __restrict__ A,
             for (int c = 0; c < 16; ++c) {
                 fail = (fail == 0 && !(d > 0.0)) ? (int)(k0 + c0 + c + 1) : fail;
                 const double rs = rsqrt_f64(d);
-                const double sd = d * rs;
                 rc[c] = rs;
                 double dn = 0.0;
                 if (c < 15) {  // the next pivot: a[c+1][c+1] - l[c+1][c]^2
                     const double l1 = row_bcast_f64(r[c], c + 1) * rs;
                     dn = fma(-l1, l1, row_bcast_f64(r[c + 1], c + 1));
                 }
-                const double lic = li > c ? r[c] * rs : (li == c ? sd : 0.0);
+                // l[li][c] for li >= c: lane c's own r[c] is d bit for bit (the same operations on the same operands
+                // as the chain above), so its entry is d rs, the diagonal; lanes li < c compute an upper entry nothing
+                // reads
+                const double lic = r[c] * rs;
                 r[c] = lic;
 #pragma unroll
                 for (int j = c + 1; j < 16; ++j) r[j] = fma(-lic, row_bcast_f64(lic, j), r[j]);
