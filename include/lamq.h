@@ -42,8 +42,10 @@ int lamq_abi_version(void);
  *   start   NULL (first state free) or [B] int32 previous states (codes.py:165-167)
  *   states  [B, T] int32 output (row stride lds)
  * Ties: the lowest predecessor h and the lowest final state win, as torch's min/argmin do.
- * Supported: 2 <= L <= 12 with 1 <= k <= min(4, L-1). Paths longer than 32 steps keep their
- * back-pointers in the workspace: lamq_viterbi_workspace_size(B, T, L, k) bytes (0 otherwise).
+ * Supported: 2 <= L <= 12 with 1 <= k <= min(4, L-1), where paths longer than 32 steps keep their
+ * back-pointers in the workspace; and every other 1 <= k <= min(8, L) with L <= 14 (the reference's
+ * uint8 back-pointers allow k <= 8) on a wide search that always keeps them there, a byte per group of
+ * 2^k predecessors and position. Workspace: lamq_viterbi_workspace_size(B, T, L, k) bytes (0: none).
  * ---------------------------------------------------------------------------------------------- */
 size_t lamq_viterbi_workspace_size(int64_t B, int T, int L, int k);
 int lamq_viterbi_rows(const float* x, int64_t B, int T, int64_t ldx, const float* C, int L, int k,

@@ -48,9 +48,10 @@ def TRELLIS(values, L: int, k: int, axis: str = "t", fixed_start: bool = False) 
 # ----------------------------------------------------------------------------- the trellis
 
 
-def _rows_per_pass(T: int, L: int, k: int) -> int:
-    """Rows per kernel launch so that long paths' back-pointer workspace stays within 1 GiB."""
-    per = E.lib().lamq_viterbi16_workspace_size(1, T, L, k) if L >= E.BIG_L else E.lib().lamq_viterbi_workspace_size(1, T, L, k)
+def _rows_per_pass(T: int, L: int, k: int, big: bool) -> int:
+    """Rows per kernel launch so that long paths' back-pointer workspace stays within 1 GiB (big: the 2^13..2^16-state
+    kernels take the search)."""
+    per = E.lib().lamq_viterbi16_workspace_size(1, T, L, k) if big else E.lib().lamq_viterbi_workspace_size(1, T, L, k)
     return max(1, (1 << 30) // per) if per else 1 << 20
 
 
@@ -62,12 +63,12 @@ def viterbi(X: torch.Tensor, values: torch.Tensor, L: int, k: int, chunk: int | 
     dev = E._abi.device()
     values = torch.as_tensor(values)
     C = values.to(dev, torch.float64).to(torch.float32).contiguous()
-    C16 = E.half_bits(C) if L >= E.BIG_L else None
+    C16 = E.half_bits(C) if E.search16(L, k, C) else None
     x = X.to(dev).to(torch.float32).contiguous()
     st = None if start is None else torch.as_tensor(start).to(dev, torch.int32).contiguous()
     B, T = x.shape
     out = torch.empty(B, T, dtype=torch.int64, device=X.device)
-    step = min(chunk or (1 << 30), _rows_per_pass(T, L, k))
+    step = min(chunk or (1 << 30), _rows_per_pass(T, L, k, C16 is not None))
     for b in range(0, B, step):
         e = min(b + step, B)
         s = E.viterbi_rows(x[b:e], C, L, k, None if st is None else st[b:e], C16=C16)
@@ -226,11 +227,39 @@ def _nets(Ws, seeds, X_codes, values, S, domain, rows_label, rin, out_rot, incoh
     return nets
 
 
+def _row_trellis_sweep(X: torch.Tensor, S: torch.Tensor, Hr: torch.Tensor, code, table: torch.Tensor) -> torch.Tensor:
+    """States of a row trellis the fused kernels do not take (k = 5..8, other widths and look-aheads): the generic
+    sweep (syntax.sweep: the refit and the lazy trailing update on the GPU), each block settled as
+    RowTrellisCode.step settles it (codes.py:397-404, driven by the project of codes.py:441-448): the standalone search
+    over the block's columns and the next `look` as they stand, divided by the row scale, from each row's state."""
+    from .frame import Environment
+    from .syntax import sweep
+
+    m, n = X.shape
+    codes = torch.empty(m, n, dtype=torch.int32, device=X.device)
+    state = torch.zeros(m, dtype=torch.long, device=X.device)
+
+    def project(j, x, T):
+        xs = x[:, None] if x.dim() == 1 else x
+        w = xs.shape[1]
+        seq = torch.cat([xs, T[:, j + w : j + w + code.look]], 1) / S[:, None]
+        path = viterbi(seq, code.values, code.L, code.k, start=state)[:, :w]
+        state.copy_(path[:, -1])
+        codes[:, j : j + w] = path.to(torch.int32)
+        q = table[path] * S[:, None]
+        return q[:, 0] if x.dim() == 1 else q
+
+    sweep(X, Environment(Hr), project, width=code.width)
+    return codes
+
+
 def ldlq_words(Ws: list, H: torch.Tensor | None, code, seeds: list[int], incoherent: bool = True,
                in_seed: int | None = None, out_rot: bool = True) -> list[Net]:
     """(incoherence ->) per-row RMS scale -> (block LDLQ under H ->) the code, for matrices that read the same input
     (codes.py:413-462). With H the columns are settled code.width at a time and the later ones re-solved under U;
-    without H the code is applied directly. Row trellis and scalar codes run on the fused GPU sweep kernels."""
+    without H the code is applied directly. Row trellis and scalar codes run on the fused GPU sweep kernels; row
+    trellises those do not take (k = 5..8, other block widths and look-aheads) on the generic sweep with the standalone
+    search (_row_trellis_sweep)."""
     if not isinstance(code, (RowTrellisCode, ScalarCode, TrellisCode)):
         raise NotImplementedError(f"{type(code).__name__} is not one of the codes this path implements")
     if isinstance(code, TrellisCode) and any(torch.as_tensor(W).shape[0] % code.T for W in Ws):
@@ -275,8 +304,11 @@ def ldlq_words(Ws: list, H: torch.Tensor | None, code, seeds: list[int], incoher
         else:
             Hr = E.rotate_hessian(torch.as_tensor(H).to(dev, torch.float64).contiguous(), rin) if incoherent else \
                 torch.as_tensor(H).to(dev, torch.float64).contiguous()
-            _, U, dead, _ = E.chol_inv_upper(Hr)
-            codes = E.ldlq_trellis(X, S, U, table, code.L, code.k, code.width, code.look, 128, dead=dead)
+            if E.fused_trellis(code.L, code.k, code.width, code.look, table):
+                _, U, dead, _ = E.chol_inv_upper(Hr)
+                codes = E.ldlq_trellis(X, S, U, table, code.L, code.k, code.width, code.look, 128, dead=dead)
+            else:
+                codes = _row_trellis_sweep(X, S, Hr, code, table)
         codes = codes.cpu()
         values = code.values.double()[codes.long()]
         domain = Domain("trellis", float(code.k), levels=code.domain.levels, axis=cols_label, state_bits=code.L,

@@ -54,24 +54,180 @@ struct ActOf {
     static int run(size_t* out) { *out = VX<L, K, LAMQ_NT>::ACT; return LAMQ_OK; }
 };
 
-extern "C" size_t lamq_viterbi_workspace_size(int64_t B, int T, int L, int k)
+// ------------------------------------------------------------------------------------------------
+// viterbi_wide: the same search for the (L, k) the kernels above are not built for: k = 5..8 (and k = L), with
+// 2^L <= 2^LAMQ_WIDE_MAX_L states. One 256-thread workgroup per row; the 2^L path costs live in LDS. Per position
+// the R = 2^(L-k) group minima over h (cost[h R + g], h < 2^k) are formed first: with R < 256 groups, 256 / R
+// consecutive threads share a group, each scanning its members h = j, j + 256/R, ... in increasing order (a strict
+// compare keeps the lowest h), and the group's first thread combines their (value, h) pairs, the lower h winning a
+// tie; with R >= 256 a thread scans whole groups. The new cost of state s is then best[s >> k] + (x - C[s])^2 with
+// the reference's three rounded operations (opgraph/codes.py:170-173), and the winning h of each group is its
+// back-pointer byte (uint8, as the reference keeps them), in the workspace: T * R bytes per row. The final state is
+// the lowest one of least cost; the traceback is s = (s >> k) + back[t][s >> k] * R (codes.py:175-178).
+// ------------------------------------------------------------------------------------------------
+#define LAMQ_WIDE_MAX_L 14
+#define LAMQ_WIDE_NT 256
+
+__device__ __forceinline__ bool wide_better(float v, int h, float bv, int bh)
 {
-    if (B < 0 || T <= LAMQ_TV_LDS) return 0;
-    size_t act = 0;
-    if (dispatch_lk<ActOf>(L, k, &act) != LAMQ_OK) return 0;
-    return (size_t)B * (size_t)T * act;
+    return v < bv || (v == bv && h < bh);
 }
 
-extern "C" int lamq_viterbi_rows(const float* x, int64_t B, int T, int64_t ldx, const float* C, int L, int k,
-                                 const int32_t* start, int32_t* states, int64_t lds, void* workspace,
-                                 size_t workspace_bytes, void* stream)
+__global__ __launch_bounds__(LAMQ_WIDE_NT) void viterbi_wide_kernel(const float* __restrict__ x, int T, int64_t ldx,
+                                                                    const float* __restrict__ C, int L, int k,
+                                                                    const int32_t* __restrict__ start,
+                                                                    int32_t* __restrict__ states, int64_t lds,
+                                                                    uint8_t* __restrict__ back_ws)
 {
-    if (B < 0 || T < 1 || ldx < T || lds < T || !C || !states || !x) return LAMQ_EINVAL;
-    if (B == 0) return LAMQ_OK;
-    if (B > 0x7fffffff) return LAMQ_EUNSUP;
-    return dispatch_lk<ViterbiRows>(L, k, x, B, T, ldx, C, start, states, lds, workspace, workspace_bytes,
-                                    as_stream(stream));
+    __shared__ float cost[1 << LAMQ_WIDE_MAX_L];
+    __shared__ float pv[LAMQ_WIDE_NT];
+    __shared__ int ph[LAMQ_WIDE_NT];
+    __shared__ float best[LAMQ_WIDE_NT];  // group minima (R < 256), or the final reduction's values
+    __shared__ int arg_s;
+    const int tid = threadIdx.x;
+    const int64_t row = blockIdx.x;
+    const float* xr = x + row * ldx;
+    const int NS = 1 << L, NB = 1 << k, R = 1 << (L - k);
+    uint8_t* back = back_ws + row * (int64_t)T * R;
+    // position 0: every state (a free first state), or the 2^k successors of the given start
+    const int st0 = start ? start[row] : -1;
+    {
+        const float x0 = xr[0];
+        for (int s = tid; s < NS; s += LAMQ_WIDE_NT) {
+            const float d = x0 - C[s];
+            const float q = d * d;
+            cost[s] = (st0 < 0 || (s >> k) == (st0 & (R - 1))) ? q : __builtin_inff();
+        }
+    }
+    const int tpg = R < LAMQ_WIDE_NT ? LAMQ_WIDE_NT / R : 1;  // threads per group
+    for (int t = 1; t < T; ++t) {
+        __syncthreads();  // cost of position t - 1 complete
+        if (R < LAMQ_WIDE_NT) {
+            const int g = tid / tpg, j = tid - g * tpg;
+            float bv = __builtin_inff();
+            int bh = NB;
+            for (int h = j; h < NB; h += tpg) {
+                const float v = cost[h * R + g];
+                if (v < bv || bh == NB) {  // the first member, then strictly smaller ones: the lowest h of a tie
+                    bv = v;
+                    bh = h;
+                }
+            }
+            pv[tid] = bv;
+            ph[tid] = bh;
+            __syncthreads();
+            if (j == 0) {
+                for (int i = 1; i < tpg; ++i)
+                    if (wide_better(pv[tid + i], ph[tid + i], bv, bh)) {
+                        bv = pv[tid + i];
+                        bh = ph[tid + i];
+                    }
+                best[g] = bv;
+                back[(int64_t)t * R + g] = (uint8_t)bh;
+            }
+            __syncthreads();  // every read of cost and pv done, best complete
+            const float xt = xr[t];
+            for (int s = tid; s < NS; s += LAMQ_WIDE_NT) {
+                const float d = xt - C[s];
+                const float q = d * d;
+                cost[s] = best[s >> k] + q;
+            }
+        } else {
+            // R >= 256 groups (k small against L): each thread scans its groups whole; the minima go to the
+            // registers of the states' owners through the cost array itself, group g's minimum written over its
+            // member h = 0 (cost[g]) once every thread has read its groups
+            // (register arrays with compile-time bounds, the loops unrolled and guarded: no scratch)
+            constexpr int MAXI = (1 << LAMQ_WIDE_MAX_L) / LAMQ_WIDE_NT;
+            float gm[MAXI / 2];
+            const int gpt = R / LAMQ_WIDE_NT;
+#pragma unroll
+            for (int i = 0; i < MAXI / 2; ++i) {
+                if (i < gpt) {
+                    const int g = tid + LAMQ_WIDE_NT * i;
+                    float bv = cost[g];
+                    int bh = 0;
+                    for (int h = 1; h < NB; ++h) {
+                        const float v = cost[h * R + g];
+                        if (v < bv) {
+                            bv = v;
+                            bh = h;
+                        }
+                    }
+                    gm[i] = bv;
+                    back[(int64_t)t * R + g] = (uint8_t)bh;
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < MAXI / 2; ++i)
+                if (i < gpt) cost[tid + LAMQ_WIDE_NT * i] = gm[i];
+            __syncthreads();
+            // every state's new cost reads a minimum (cost[s >> k], s >> k < R) before any is overwritten (a barrier
+            // between)
+            const float xt = xr[t];
+            float nc[MAXI];
+            const int spt = NS / LAMQ_WIDE_NT;
+#pragma unroll
+            for (int i = 0; i < MAXI; ++i) {
+                if (i < spt) {
+                    const int s = tid + LAMQ_WIDE_NT * i;
+                    const float d = xt - C[s];
+                    nc[i] = cost[s >> k] + d * d;
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < MAXI; ++i)
+                if (i < spt) cost[tid + LAMQ_WIDE_NT * i] = nc[i];
+        }
+    }
+    __syncthreads();
+    // the final state: the lowest state of least cost
+    {
+        float bv = __builtin_inff();
+        int bs = NS;
+        for (int s = tid; s < NS; s += LAMQ_WIDE_NT) {
+            const float v = cost[s];
+            if (v < bv || bs == NS) {
+                bv = v;
+                bs = s;
+            }
+        }
+        pv[tid] = bv;
+        ph[tid] = bs;
+        __syncthreads();
+        if (tid == 0) {
+            for (int i = 1; i < LAMQ_WIDE_NT; ++i)
+                if (ph[i] < NS && wide_better(pv[i], ph[i], bv, bs)) {
+                    bv = pv[i];
+                    bs = ph[i];
+                }
+            arg_s = bs;
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        int32_t* out = states + row * lds;
+        int s = arg_s;
+        out[T - 1] = s;
+        for (int t = T - 1; t > 0; --t) {
+            const int r = s >> k;
+            s = r + (int)back[(int64_t)t * R + r] * R;
+            out[t - 1] = s;
+        }
+    }
 }
+
+// (L, k) the wide search takes: what dispatch_lk has no kernel for, up to k = 8 (the reference's uint8
+// back-pointers) and 2^LAMQ_WIDE_MAX_L states
+static bool wide_lk(int L, int k)
+{
+    size_t act = 0;
+    return L >= 1 && L <= LAMQ_WIDE_MAX_L && k >= 1 && k <= 8 && k <= L &&
+           dispatch_lk<ActOf>(L, k, &act) == LAMQ_EUNSUP;
+}
+
+
 
 // ------------------------------------------------------------------------------------------------
 // ldlq_trellis_block: one workgroup per row walks the steps j = b0, b0+width, ... of the lazy block
@@ -279,4 +435,32 @@ extern "C" int lamq_ldlq_trellis_block_groups(double* T, int64_t m, int64_t n, i
                        gg);
     LAMQ_LAUNCH_CHECK();
     return LAMQ_OK;
+}
+
+extern "C" size_t lamq_viterbi_workspace_size(int64_t B, int T, int L, int k)
+{
+    if (B < 0 || T < 1) return 0;
+    if (wide_lk(L, k)) return (size_t)B * (size_t)T * ((size_t)1 << (L - k));  // a byte per group and position
+    if (T <= LAMQ_TV_LDS) return 0;
+    size_t act = 0;
+    if (dispatch_lk<ActOf>(L, k, &act) != LAMQ_OK) return 0;
+    return (size_t)B * (size_t)T * act;
+}
+
+extern "C" int lamq_viterbi_rows(const float* x, int64_t B, int T, int64_t ldx, const float* C, int L, int k,
+                                 const int32_t* start, int32_t* states, int64_t lds, void* workspace,
+                                 size_t workspace_bytes, void* stream)
+{
+    if (B < 0 || T < 1 || ldx < T || lds < T || !C || !states || !x) return LAMQ_EINVAL;
+    if (B == 0) return LAMQ_OK;
+    if (B > 0x7fffffff) return LAMQ_EUNSUP;
+    if (wide_lk(L, k)) {
+        if (!workspace || workspace_bytes < lamq_viterbi_workspace_size(B, T, L, k)) return LAMQ_EINVAL;
+        hipLaunchKernelGGL(viterbi_wide_kernel, dim3((unsigned)B), dim3(LAMQ_WIDE_NT), 0, as_stream(stream), x, T, ldx,
+                           C, L, k, start, states, lds, (uint8_t*)workspace);
+        LAMQ_LAUNCH_CHECK();
+        return LAMQ_OK;
+    }
+    return dispatch_lk<ViterbiRows>(L, k, x, B, T, ldx, C, start, states, lds, workspace, workspace_bytes,
+                                    as_stream(stream));
 }

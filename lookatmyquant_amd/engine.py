@@ -36,9 +36,20 @@ def half_bits(C: torch.Tensor) -> torch.Tensor:
     return h.view(torch.int16).contiguous()
 
 
+def search16(L: int, k: int, C: torch.Tensor) -> bool:
+    """Whether the standalone search at (L, k) goes to the 2^13..2^16-state kernels (lamq_viterbi16_rows: k <= L - 12
+    and k <= 4, a table exact in fp16); otherwise lamq_viterbi_rows takes it (L <= 12 with k <= 4 on the kernels built
+    per (L, k); k = 5..8, or up to 2^14 states with any float32 table, on its wide search)."""
+    if L < BIG_L or k > min(4, L - 12):
+        return False
+    c32 = C.to(torch.float32)
+    return bool(torch.equal(c32.to(torch.float16).to(torch.float32), c32))
+
+
 def viterbi_rows(x: torch.Tensor, C: torch.Tensor, L: int, k: int, start: torch.Tensor | None = None,
                  C16: torch.Tensor | None = None) -> torch.Tensor:
-    """x [B, T] float32, C [2^L] float32, start None or [B] int32 -> states [B, T] int32."""
+    """x [B, T] float32, C [2^L] float32, start None or [B] int32 -> states [B, T] int32. C16: C's fp16 bit patterns,
+    given when the caller has them (the 2^13..2^16-state kernels read those)."""
     need(x, torch.float32, "x", 2)
     need(C, torch.float32, "C", 1)
     if C.numel() != 1 << L:
@@ -50,7 +61,7 @@ def viterbi_rows(x: torch.Tensor, C: torch.Tensor, L: int, k: int, start: torch.
         st = start.to(device=x.device, dtype=torch.int32).contiguous()
         if st.numel() != B:
             raise ValueError("one start state per row")
-    if L >= BIG_L:
+    if C16 is not None or search16(L, k, C):
         h = half_bits(C) if C16 is None else C16
         nbytes = lib().lamq_viterbi16_workspace_size(B, T, L, k)
         ws = workspace(nbytes, x.device)
@@ -217,6 +228,20 @@ def chol_inv_upper(H: torch.Tensor, damp: float = 0.01, raise_on_fail: bool = Tr
 
 
 # ----------------------------------------------------------------------------- the sweeps (syntax.py:86-124)
+
+
+FUSED_WMAX, FUSED_TV = 16, 24  # the fused block kernels' widest block and longest search (width + look)
+
+
+def fused_trellis(L: int, k: int, width: int, look: int, table64: torch.Tensor) -> bool:
+    """Whether the fused row-trellis block kernels take (L, k, width, look) with this table: L <= 12 with k <=
+    min(4, L - 1), or 13 <= L <= 16 with k <= min(4, L - 12) and a table exact in fp16; width <= 16 and width + look
+    <= 24. Other row trellises go through the generic sweep with the standalone search (codes.ldlq_words)."""
+    if not (1 <= width <= FUSED_WMAX and look >= 0 and width + look <= FUSED_TV):
+        return False
+    if L <= 12:
+        return 1 <= k <= min(4, L - 1)
+    return search16(L, k, table64) and L <= 16
 
 
 def ldlq_trellis(X: torch.Tensor, S: torch.Tensor, U: torch.Tensor, table64: torch.Tensor, L: int, k: int,

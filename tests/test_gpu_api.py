@@ -522,11 +522,36 @@ def test_error_paths():
         Environment(-torch.eye(16, dtype=torch.float64))
     with pytest.raises(NotImplementedError):  # a 17-bit state is beyond the kernels
         C.viterbi(torch.zeros(2, 4), torch.zeros(1 << 17), 17, 2)
-    with pytest.raises(NotImplementedError):  # search longer than the fused kernel's window
-        C.ldlq_words([torch.randn(4, 64, dtype=torch.float64)], torch.eye(64, dtype=torch.float64),
-                     C.RowTrellisCode(12, 2, width=16, look=20), [1], in_seed=2, out_rot=False)
     with pytest.raises(NotImplementedError):  # a 16-bit table that fp16 cannot hold
         C.viterbi(torch.zeros(2, 4), torch.randn(1 << 16, dtype=torch.float64), 16, 2)
+
+
+@pytest.mark.parametrize("L,k,width,look", [(12, 5, 16, 8), (10, 7, 8, 4), (12, 2, 16, 20), (12, 3, 32, 8)])
+def test_row_trellis_outside_the_fused_kernels_matches_oracle(L, k, width, look):
+    """Row trellises the fused block kernels do not take (k past 4, a window longer than 24, a block wider than 16)
+    go through codes.ldlq_words on the generic sweep, each block settled by the standalone search from each row's
+    state with the look-ahead as it stands (codes.py:397-404, 441-448): the oracle's states for the same factor and
+    row scales, 3 rows x 200 columns (two lazy blocks and a partial one)."""
+    from lookatmyquant_amd import codes as C
+    from lookatmyquant_amd import engine as E
+    from lookatmyquant_amd.frame import Environment
+
+    rng = np.random.default_rng(40 * L + k + look)
+    n = 200
+    Xa = rng.standard_normal((600, n))
+    H = Xa.T @ Xa / 600
+    W = rng.standard_normal((3, n))
+    tab = rng.standard_normal(1 << L)
+    code = C.RowTrellisCode(L, k, width=width, look=look, values=tab)
+    assert not E.fused_trellis(L, k, width, look, torch.from_numpy(tab))
+    say(f"row trellis on the generic sweep: L={L} k={k} width={width} look={look}")
+    net = C.ldlq_words([torch.from_numpy(W)], torch.from_numpy(H), code, [1], incoherent=False, out_rot=False)[0]
+    env = Environment(torch.from_numpy(H).cuda())
+    S = net.cores["W.S"].data.numpy()
+    ref = O.ldlq_trellis(W, env.U.cpu().numpy(), S, tab, L, k, width=width, look=look,
+                         dead=env.dead.cpu().numpy().astype(np.uint8))
+    assert np.array_equal(net.codes.numpy(), ref)
+    assert C.is_trellis_path(net.codes, L, k)
 
 
 def test_ldlq_noise_matches_the_oracle():

@@ -138,6 +138,35 @@ def test_viterbi_long_paths_use_workspace(E, tables):
     assert np.array_equal(got, O.viterbi(x, tables[2], 12, 2))
 
 
+@pytest.mark.parametrize("L,k", [(12, 5), (12, 6), (12, 7), (12, 8), (8, 8), (6, 5), (4, 4), (13, 2), (14, 3),
+                                 (13, 6)])
+def test_viterbi_wide_widths_match_oracle(E, L, k):
+    """The wide search (k = 5..8, k = L, and up to 2^14 states with a float32 table fp16 cannot hold) against the C
+    oracle, whose rules brute force pins at these widths on short paths: random tables and targets, 5 rows of 40
+    positions from given starts and 3 free rows, also through codes.viterbi (the reference's signature); then a
+    table of three values with targets on and between them, where every group's winner and the final state are
+    decided by the tie rules."""
+    from lookatmyquant_amd import codes as Cd
+
+    rng = np.random.default_rng(500 + 16 * L + k)
+    tab = rng.standard_normal(1 << L)
+    x = rng.standard_normal((5, 40)).astype(np.float32)
+    st = rng.integers(0, 1 << L, 5)
+    C = cuda(tab.astype(np.float32))
+    say(f"viterbi wide L={L} k={k}")
+    got = E.viterbi_rows(cuda(x), C, L, k, start=cuda(st, torch.int32)).cpu().numpy()
+    assert np.array_equal(got, O.viterbi(x, tab, L, k, start=st))
+    free = E.viterbi_rows(cuda(x[:3]), C, L, k).cpu().numpy()
+    assert np.array_equal(free, O.viterbi(x[:3], tab, L, k))
+    api = Cd.viterbi(torch.from_numpy(x[:3].astype(np.float64)), torch.from_numpy(tab), L, k)
+    assert np.array_equal(api.cpu().numpy(), free)
+    tab3 = rng.choice([-1.0, 0.0, 1.0], 1 << L)
+    x3 = rng.choice([-1.0, -0.5, 0.0, 0.25, 0.5, 1.0], (4, 30)).astype(np.float32)
+    say(f"viterbi wide L={L} k={k}, three-valued table")
+    got3 = E.viterbi_rows(cuda(x3), cuda(tab3.astype(np.float32)), L, k).cpu().numpy()
+    assert np.array_equal(got3, O.viterbi(x3, tab3, L, k))
+
+
 # ----------------------------------------------------------------------------- fp64 building blocks
 
 

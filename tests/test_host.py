@@ -97,8 +97,14 @@ def test_argument_errors_are_reported_without_a_gpu():
                                        None) == -1
     assert L.lamq_ldlq_trellis16_block(ptr(p), 1, 8, 8, ptr(p), 8, ptr(p), ptr(p), ptr(p), 16, 2, 4, 8, 4, 4, ptr(q),
                                        ptr(q), 8, ptr(p), 4, 4, None) == -1
-    # a trellis width the kernels are not built for
-    assert L.lamq_viterbi_rows(ptr(p), 1, 4, 4, ptr(p), 12, 7, None, ptr(q), 4, None, 0, None) == -2
+    # widths past the reference's uint8 back-pointers, or more states than the wide search holds, are unsupported; a
+    # wide search (k = 5..8) keeps a byte per group and position in its workspace and refuses to run without it
+    assert L.lamq_viterbi_rows(ptr(p), 1, 4, 4, ptr(p), 12, 9, None, ptr(q), 4, None, 0, None) == -2
+    assert L.lamq_viterbi_rows(ptr(p), 1, 4, 4, ptr(p), 15, 5, None, ptr(q), 4, None, 0, None) == -2
+    assert L.lamq_viterbi_rows(ptr(p), 1, 4, 4, ptr(p), 12, 7, None, ptr(q), 4, None, 0, None) == -1
+    assert L.lamq_viterbi_workspace_size(3, 10, 12, 7) == 3 * 10 * 32
+    assert L.lamq_viterbi_workspace_size(3, 10, 5, 5) == 3 * 10
+    assert L.lamq_viterbi_workspace_size(3, 10, 12, 2) == 0
     # packing: widths beyond 8, a trellis no wider than its symbols, too few code words, more rows than the source
     assert L.lamq_pack_codes(ptr(q), 8, 8, None, 8, 8, 0, 9, 12, 1, ptr(q), 8, ptr(q), None) == -1
     assert L.lamq_pack_codes(ptr(q), 8, 8, None, 8, 8, 0, 4, 4, 1, ptr(q), 8, ptr(q), None) == -1

@@ -63,13 +63,14 @@ def test_viterbi_is_optimal_by_brute_force():
         assert all((st[r][t] >> k) == (st[r][t - 1] & ((1 << (L - k)) - 1)) for t in range(1, T))
 
 
-@pytest.mark.parametrize("L,k,start", [(4, 1, None), (5, 2, None), (4, 2, 9), (6, 2, 17)])
-def test_viterbi_ties_by_brute_force(L, k, start):
+@pytest.mark.parametrize("L,k,start,T", [(4, 1, None, 6), (5, 2, None, 6), (4, 2, 9, 6), (6, 2, 17, 6),
+                                         (6, 5, None, 3), (6, 5, 45, 3), (5, 5, None, 3), (7, 6, 100, 3)])
+def test_viterbi_ties_by_brute_force(L, k, start, T):
     """With small-integer values every float32 sum is exact, so the path the search keeps is determined by its
     rules alone: among minimal-cost paths the lowest final state, then at each earlier step the predecessor with
-    the lowest top bits (torch's min returns the first minimum). Brute force over all paths with that order."""
+    the lowest top bits (torch's min returns the first minimum). Brute force over all paths with that order; the
+    widths past 4 (k up to 8 in the reference, its back-pointers uint8) and k = L (one group) on short paths."""
     rng = np.random.default_rng(L * 100 + k)
-    T = 6
     v = rng.integers(-2, 3, 1 << L).astype(np.float64)
     R = 1 << (L - k)
     for _ in range(6):
