@@ -197,6 +197,23 @@ int lamq_refit_step(double* T, int64_t m, int64_t n, int64_t ldT, const double* 
 /* T[:, dead] = 0 before a sweep (opgraph/syntax.py:101); dead [n] uint8. */
 int lamq_zero_columns(double* T, int64_t m, int64_t n, int64_t ldT, const uint8_t* dead, void* stream);
 
+/* Output shaping: the projection of multirate_sweep with G, one rate (opgraph/nested.py:104-147). Within a column
+ * the rows are settled `block` at a time: each entry of rows [a, b) on its nearest level (the first least |u - level|,
+ * nested.py:131), then the later rows re-solved, u[b:] -= (u[a:b] - q[a:b]) M_q (nested.py:132-133), with
+ * M_q = V[a:b, a:b]^-1 V[a:b, b:] (nested.py:126-127) and V the upper factor of the damped output sensitivity
+ * (frame.Environment(G, damp=0.03).U, an lamq_chol_inv_upper factor).
+ *   lamq_shaping_feedback: every block's M_q but the last's (empty), packed in block order, each row-major
+ *     [(b - a) x (m - b)]: lamq_shaping_feedback_size(m, block) bytes. V [m, m] upper (row stride ldV).
+ *   lamq_ldlq_shaped_column: column j of T [m, n] settled so (T is only read): idx[:, j] (int32, row stride ldi >= n)
+ *     and the settled levels Q [m] (the projection the caller's refit step subtracts). levels [K], K <= 256.
+ * m <= LAMQ_SHAPE_MAX_M (the column lives in LDS), block <= LAMQ_SHAPE_MAX_BLOCK. */
+#define LAMQ_SHAPE_MAX_M 16384
+#define LAMQ_SHAPE_MAX_BLOCK 64
+size_t lamq_shaping_feedback_size(int64_t m, int block);
+int lamq_shaping_feedback(const double* V, int64_t m, int64_t ldV, int block, double* M, void* stream);
+int lamq_ldlq_shaped_column(const double* T, int64_t m, int64_t n, int64_t ldT, int64_t j, const double* M, int block,
+                            const double* levels, int K, int32_t* idx, int64_t ldi, double* Q, void* stream);
+
 /* ------------------------------------------------------------------------------------------------
  * Damped Hessian and the upper Cholesky factor of its inverse.
  * Replaces opgraph/frame.py:515-522 (Environment.__init__):

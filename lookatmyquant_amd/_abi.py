@@ -62,6 +62,10 @@ SIGNATURES = {
     "lamq_pack_trellis": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _p, _c_i64, _p, _p]),
     "lamq_pack_codes": (_c_int, [_p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _p, _c_i64, _p, _p]),
     "lamq_pack_codes_groups": (_c_int, [_p, _c_int, _c_i64, _c_int, _c_int, _p, _p]),
+    "lamq_shaping_feedback_size": (_c_size, [_c_i64, _c_int]),
+    "lamq_shaping_feedback": (_c_int, [_p, _c_i64, _c_i64, _c_int, _p, _p]),
+    "lamq_ldlq_shaped_column": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _c_i64, _p, _c_int, _p, _c_int, _p, _c_i64, _p,
+                                         _p]),
     "lamq_causal_softmax_bf16": (_c_int, [_p, _p, _c_i64, _c_int, _c_i64, _c_i64, _c_flt, _p]),
     "lamq_swiglu_bf16": (_c_int, [_p, _p, _p, _c_i64, _p]),
     "lamq_rms_norm_bf16": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _p, _p, _c_i64, _c_flt, _p]),

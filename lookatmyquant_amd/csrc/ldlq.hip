@@ -557,3 +557,113 @@ extern "C" int lamq_refit_step(double* T, int64_t m, int64_t n, int64_t ldT, con
     LAMQ_LAUNCH_CHECK();
     return LAMQ_OK;
 }
+
+// ------------------------------------------------------------------------------------------------
+// Output shaping (opgraph/nested.py:104-147, multirate_sweep with G, one rate): within a column the rows are settled
+// `block` at a time, each block's entries on their nearest levels, and the later rows re-solved for the block's
+// error through the factor V of the damped output sensitivity: u[b:] -= (u[a:b] - q[a:b]) M_q with
+// M_q = V[a:b, a:b]^-1 V[a:b, b:] (nested.py:127-136).
+//
+// lamq_shaping_feedback: every block's M_q (rows a..b of V's upper factor), packed one after the other, M_q row-major
+// [(b - a) x (m - b)]. One workgroup per block but the last (whose M is empty); thread c solves the columns c, c + 256,
+// ... of V[a:b, a:b] M = V[a:b, b:] by back substitution (rows from b - 1 down, an fma chain over the rows solved,
+// then the division by the diagonal), reading the rows it has solved back from memory.
+// ------------------------------------------------------------------------------------------------
+extern "C" size_t lamq_shaping_feedback_size(int64_t m, int block)
+{
+    if (m < 1 || block < 1) return 0;
+    const int64_t nb = cdiv(m, (int64_t)block), B = block;
+    return (size_t)(B * ((nb - 1) * m - B * (nb - 1) * nb / 2)) * sizeof(double);
+}
+
+__global__ __launch_bounds__(256) void shaping_feedback_kernel(const double* __restrict__ V, int64_t m, int64_t ldV,
+                                                               int block, double* __restrict__ M)
+{
+    const int64_t q = blockIdx.x, B = block;
+    const int64_t a = q * B, b = a + B;  // a full block: every block but the last is
+    const int64_t w = m - b;
+    double* Mq = M + B * (q * m - B * q * (q + 1) / 2);
+    for (int64_t c = threadIdx.x; c < w; c += 256) {
+        for (int64_t r = b - 1; r >= a; --r) {
+            double acc = V[r * ldV + b + c];
+            for (int64_t s = r + 1; s < b; ++s) acc = fma(-V[r * ldV + s], Mq[(s - a) * w + c], acc);
+            Mq[(r - a) * w + c] = acc / V[r * ldV + r];
+        }
+    }
+}
+
+extern "C" int lamq_shaping_feedback(const double* V, int64_t m, int64_t ldV, int block, double* M, void* stream)
+{
+    if (!V || !M || m < 1 || ldV < m || block < 1) return LAMQ_EINVAL;
+    if (block > LAMQ_SHAPE_MAX_BLOCK) return LAMQ_EUNSUP;
+    const int64_t nb = cdiv(m, (int64_t)block);
+    if (nb < 2) return LAMQ_OK;
+    hipLaunchKernelGGL(shaping_feedback_kernel, dim3((unsigned)(nb - 1)), dim3(256), 0, as_stream(stream), V, m, ldV,
+                       block, M);
+    LAMQ_LAUNCH_CHECK();
+    return LAMQ_OK;
+}
+
+// lamq_ldlq_shaped_column: column j of T, settled row block by row block (the projection of multirate_sweep with G):
+// one 1024-thread workgroup, the column in LDS. Per block the first b - a threads take their entry's nearest level
+// (the first least |u - level|, as argmin of the absolute difference), write its index into idx[:, j] and its level into
+// Q, and leave the error in LDS; then every later row r subtracts sum_rows e M_q[., r] (an fma chain from 0 in row
+// order). T is only read.
+__global__ __launch_bounds__(1024) void ldlq_shaped_column_kernel(const double* __restrict__ T, int64_t m, int64_t ldT,
+                                                                  int64_t j, const double* __restrict__ M, int block,
+                                                                  const double* __restrict__ levels, int K,
+                                                                  int32_t* __restrict__ idx, int64_t ldi,
+                                                                  double* __restrict__ Q)
+{
+    __shared__ double u[LAMQ_SHAPE_MAX_M];
+    __shared__ double lv[256];
+    __shared__ double e[LAMQ_SHAPE_MAX_BLOCK];
+    const int tid = threadIdx.x;
+    for (int64_t r = tid; r < m; r += 1024) u[r] = T[r * ldT + j];
+    for (int l = tid; l < K; l += 1024) lv[l] = levels[l];
+    __syncthreads();
+    const int64_t B = block;
+    for (int64_t a = 0, q = 0; a < m; a += B, ++q) {
+        const int64_t b = a + B < m ? a + B : m;
+        if (tid < b - a) {
+            const double x = u[a + tid];
+            int bi = 0;
+            double bd = fabs(x - lv[0]);
+            for (int l = 1; l < K; ++l) {
+                const double d = fabs(x - lv[l]);
+                if (d < bd) {
+                    bd = d;
+                    bi = l;
+                }
+            }
+            idx[(a + tid) * ldi + j] = bi;
+            Q[a + tid] = lv[bi];
+            e[tid] = x - lv[bi];
+        }
+        __syncthreads();
+        if (b < m) {
+            const int64_t w = m - b;
+            const double* Mq = M + B * (q * m - B * q * (q + 1) / 2);
+            for (int64_t c = tid; c < w; c += 1024) {
+                double acc = 0.0;
+                for (int64_t r = 0; r < b - a; ++r) acc = fma(e[r], Mq[r * w + c], acc);
+                u[b + c] = u[b + c] - acc;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+extern "C" int lamq_ldlq_shaped_column(const double* T, int64_t m, int64_t n, int64_t ldT, int64_t j, const double* M,
+                                       int block, const double* levels, int K, int32_t* idx, int64_t ldi, double* Q,
+                                       void* stream)
+{
+    if (!T || !levels || !idx || !Q || m < 1 || n < 1 || ldT < n || j < 0 || j >= n || block < 1 || K < 1 || ldi < n)
+        return LAMQ_EINVAL;
+    if (!M && cdiv(m, (int64_t)block) > 1) return LAMQ_EINVAL;
+    if (m > LAMQ_SHAPE_MAX_M || block > LAMQ_SHAPE_MAX_BLOCK || K > 256) return LAMQ_EUNSUP;
+    hipLaunchKernelGGL(ldlq_shaped_column_kernel, dim3(1), dim3(1024), 0, as_stream(stream), T, m, ldT, j, M, block,
+                       levels, K, idx, ldi, Q);
+    LAMQ_LAUNCH_CHECK();
+    return LAMQ_OK;
+}

@@ -772,6 +772,29 @@ def refit_step(T: torch.Tensor, U: torch.Tensor, Q: torch.Tensor, j: int, b0: in
     return T
 
 
+def shaping_feedback(V: torch.Tensor, block: int) -> torch.Tensor:
+    """The packed row-block feedback M_q = V[a:b, a:b]^-1 V[a:b, b:] of output shaping (nested.py:126-127), V the
+    upper factor of the damped output sensitivity (lamq_shaping_feedback)."""
+    need(V, torch.float64, "V", 2)
+    m = V.shape[0]
+    M = torch.empty(max(1, lib().lamq_shaping_feedback_size(m, block) // 8), dtype=torch.float64, device=V.device)
+    check(lib().lamq_shaping_feedback(ptr(V), m, ld(V), block, ptr(M), stream(V.device)), "shaping_feedback")
+    return M
+
+
+def shaped_column(T: torch.Tensor, j: int, M: torch.Tensor, block: int, levels: torch.Tensor, idx: torch.Tensor,
+                  Q: torch.Tensor) -> torch.Tensor:
+    """Column j of T settled row block by row block under the feedback M (lamq_ldlq_shaped_column): its indices into
+    idx[:, j], its levels into Q [m] (returned); T is only read."""
+    need(T, torch.float64, "T", 2)
+    need(idx, torch.int32, "idx", 2)
+    m, n = T.shape
+    lv = levels.to(device=T.device, dtype=torch.float64).contiguous()
+    check(lib().lamq_ldlq_shaped_column(ptr(T), m, n, ld(T), j, ptr(M), block, ptr(lv), lv.numel(), ptr(idx), ld(idx),
+                                        ptr(Q), stream(T.device)), "ldlq_shaped_column")
+    return Q
+
+
 def zero_columns(T: torch.Tensor, dead: torch.Tensor):
     need(T, torch.float64, "T", 2)
     m, n = T.shape

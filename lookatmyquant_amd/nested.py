@@ -91,18 +91,52 @@ def multirate_sweep(X: torch.Tensor, H: torch.Tensor | None, tables: torch.Tenso
                     G: torch.Tensor | None = None, block: int = 32) -> torch.Tensor:
     """One index per entry of X (already in units of the row scale) for R rates at once (nested.py:104-147): the first
     minimum of sum_r w_r (t_r - tables[r, i])^2, each rate's copy of the row keeping its own running target; with H,
-    the width-1 LDLQ sweep under U; without H, every column alone. Returns int64 indices on the CPU."""
-    if G is not None:
-        raise NotImplementedError("output shaping (G) is not part of this path")
+    the width-1 LDLQ sweep under U; without H, every column alone. With G (one rate), the output sensitivity in units
+    of the row scale, each column's rows are settled `block` at a time and the later rows re-solved under G's damped
+    factor (_shaped_sweep). Returns int64 indices on the CPU."""
     dev = E._abi.device()
     tables = torch.as_tensor(tables, dtype=torch.float64)
     if tables.dim() != 2:
         raise ValueError("tables must be [rates, levels]")
+    if G is not None:
+        if tables.shape[0] != 1:
+            raise ValueError("output shaping takes one rate")
+        Hg = None if H is None else torch.as_tensor(H).to(dev, torch.float64).contiguous()
+        return _shaped_sweep(torch.as_tensor(X).to(dev, torch.float64), Hg, tables[0].to(dev),
+                             torch.as_tensor(G).to(dev, torch.float64).contiguous(), block).to(torch.int64).cpu()
     x = torch.as_tensor(X).to(dev, torch.float64).contiguous()
     U = dead = None
     if H is not None:
         _, U, dead, _ = E.chol_inv_upper(torch.as_tensor(H).to(dev, torch.float64).contiguous())
     return _sweep(x, U, dead, tables.to(dev), torch.as_tensor(weights, dtype=torch.float64).to(dev)).to(torch.int64).cpu()
+
+
+def _shaped_sweep(x: torch.Tensor, H: torch.Tensor | None, levels: torch.Tensor, G: torch.Tensor,
+                  block: int) -> torch.Tensor:
+    """The index array [m, n] int32 on the device of multirate_sweep with G (nested.py:121-144): V the upper factor of
+    G damped by OUTPUT_DAMP (frame.Environment), its row blocks' feedback packed once (lamq_shaping_feedback); each
+    column settled by lamq_ldlq_shaped_column, inside the width-1 generic sweep under H (syntax.sweep: the refit and
+    the lazy trailing update) or, without H, every column alone."""
+    from .frame import Environment
+    from .syntax import sweep
+
+    m, n = x.shape
+    V = Environment(G, damp=OUTPUT_DAMP).U
+    M = E.shaping_feedback(V, block)
+    idx = torch.empty(m, n, dtype=torch.int32, device=x.device)
+    Q = torch.empty(m, 1, dtype=torch.float64, device=x.device)
+
+    def project(j, col, T):
+        E.shaped_column(T, j, M, block, levels, idx, Q)
+        return Q[:, 0]
+
+    if H is None:
+        X = x.contiguous()
+        for j in range(n):
+            project(j, None, X)
+    else:
+        sweep(x, Environment(H), project)
+    return idx
 
 
 def _sweep(x, U, dead, tables, weights):
@@ -124,21 +158,28 @@ def nested_words(Ws: list, H: torch.Tensor | None, seeds: list[int], top: int, r
     `rates` at once (weights price the rates' squared errors) -> {rate: [Net per matrix]}, each rate reading the shared
     indices with its own levels (nested.py:155-192). With `levels` (one rate only) the code is that set (a dedicated
     code, as quantize.word's lm<b>)."""
-    if G is not None:
-        raise NotImplementedError("output shaping (G) is not part of this path")
     if levels is not None and len(rates) != 1:
         raise ValueError("a dedicated code has one rate")
+    if G is not None and (len(Ws) > 1 or len(rates) > 1 or out_rot):
+        raise ValueError("output shaping is for one matrix at one rate, with its rows not rotated")
     dev, X, S, rin = _prepare(Ws, seeds, True, in_seed, out_rot)
     if levels is None:
         tables = nested_tables(top, rates, alpha)
     else:
         tables = torch.as_tensor(levels, dtype=torch.float64)[None]
     x = (X / S[:, None]).contiguous()
-    U = dead = None
+    Hr = None
     if H is not None:
         Hr = E.rotate_hessian(torch.as_tensor(H).to(dev, torch.float64).contiguous(), rin)
-        _, U, dead, _ = E.chol_inv_upper(Hr)
-    idx = _sweep(x, U, dead, tables.to(dev), torch.as_tensor(weights, dtype=torch.float64).to(dev)).cpu()
+    if G is not None:
+        # the output sensitivity in units of the row scale (nested.py:180): Gs = diag(S) G diag(S)
+        Gs = (S[:, None] * torch.as_tensor(G).to(dev, torch.float64) * S[None, :]).contiguous()
+        idx = _shaped_sweep(x, Hr, tables[0].to(dev), Gs, block).cpu()
+    else:
+        U = dead = None
+        if Hr is not None:
+            _, U, dead, _ = E.chol_inv_upper(Hr)
+        idx = _sweep(x, U, dead, tables.to(dev), torch.as_tensor(weights, dtype=torch.float64).to(dev)).cpu()
     rows_label = "u" if out_rot else "o"
     out = {}
     for r, b in enumerate(rates):

@@ -227,6 +227,44 @@ def multirate_sweep(X, H, tables, weights, lazy: int = 128) -> np.ndarray:
     return idx
 
 
+OUTPUT_DAMP = 0.03  # opgraph/nested.py:101
+
+
+def shaped_sweep(X, H, levels, G, block: int = 32, lazy: int = 128) -> np.ndarray:
+    """opgraph/nested.py:104-147 with output shaping (one rate; G the output sensitivity in units of the row scale):
+    V = Environment(G, damp=0.03).U (:121); within each column the rows are settled `block` at a time, each entry on its
+    nearest level (the first least |u - level|, :131), and the later rows re-solved, u[b:] -= (u[a:b] - q[a:b]) M with
+    M = V[a:b, a:b]^-1 V[a:b, b:] (:123-133); with H the width-1 sweep under Environment(H)'s U (:144), without H every
+    column alone (:140-143). Indices int64."""
+    from scipy.linalg import solve_triangular
+
+    X = np.asarray(X, dtype=np.float64)
+    lv = np.asarray(levels, dtype=np.float64)
+    m = X.shape[0]
+    _, V, _ = environment(G, damp=OUTPUT_DAMP)
+    rows = [(a, min(a + block, m)) for a in range(0, m, block)]
+    feedback = [solve_triangular(V[a:b, a:b], V[a:b, b:]) for a, b in rows]  # upper V[a:b, a:b] M = V[a:b, b:]
+    idx = np.empty(X.shape, dtype=np.int64)
+
+    def project(j, col, T):
+        u = np.array(col, dtype=np.float64).reshape(-1)
+        i = np.empty(m, dtype=np.int64)
+        for (a, b), M in zip(rows, feedback):
+            i[a:b] = np.abs(u[a:b, None] - lv[None, :]).argmin(1)
+            if b < m:
+                u[b:] -= (u[a:b] - lv[i[a:b]]) @ M
+        idx[:, j] = i
+        return lv[i].reshape(-1, 1)
+
+    if H is None:
+        for j in range(X.shape[1]):
+            project(j, X[:, j], None)
+        return idx
+    _, U, dead = environment(H)
+    sweep(X, U, project, width=1, lazy=lazy, dead=dead if dead.any() else None)
+    return idx
+
+
 def column_trellis_states(X, table64, L: int, k: int, T: int) -> np.ndarray:
     """TrellisCode's search (opgraph/codes.py:371-378): each column cut into sequences of T consecutive rows, each
     sequence the nearest path from a free first state; the states in X's layout."""

@@ -685,6 +685,53 @@ def test_multirate_sweep_matches_the_reference(golden, case):
     assert np.array_equal(idx.numpy(), g[f"{case}_idx"])
 
 
+@pytest.mark.parametrize("m,n,block,with_h", [(96, 160, 32, True), (100, 130, 8, True), (70, 40, 16, False),
+                                              (300, 150, 32, True)])
+def test_output_shaping_matches_the_oracle(m, n, block, with_h):
+    """nested.multirate_sweep with G (one rate, nested.py:104-147): each column's rows settled `block` at a time and
+    the later rows re-solved under G's damped factor (lamq_shaping_feedback, lamq_ldlq_shaped_column), inside the
+    width-1 sweep under H (two lazy runs at n = 160 and 150) or every column alone: the oracle's indices, whose
+    block rule the generic block sweep and the isotropic G pin; partial last row blocks at m = 100, 70 and 300."""
+    from lookatmyquant_amd import nested as N
+
+    rng = np.random.default_rng(m + n + block)
+    X = rng.standard_normal((m, n))
+    Xa = rng.standard_normal((2 * n, n))
+    H = Xa.T @ Xa / (2 * n) if with_h else None
+    Ga = rng.standard_normal((3 * m, m)) * np.abs(rng.standard_t(4, m))
+    G = Ga.T @ Ga / (3 * m)
+    lv = N.lloyd_max(3)
+    say(f"output shaping {m} x {n}, block {block}, H {with_h}")
+    idx = N.multirate_sweep(torch.from_numpy(X), None if H is None else torch.from_numpy(H), lv[None],
+                            torch.tensor([1.0], dtype=torch.float64), G=torch.from_numpy(G), block=block)
+    assert np.array_equal(idx.numpy(), O.shaped_sweep(X, H, lv.numpy(), G, block=block))
+
+
+def test_lm_word_with_output_shaping_matches_the_oracle(config12):
+    """quantize.word("lm3", ..., G=G) (quantize.py:332-344 -> nested_words with G, nested.py:155-192): the input
+    rotation, the row scales, G in units of the row scale (S G S) and the shaped sweep under R H R^T, against the
+    oracle's indices from the same rotated rows; one matrix, rows not rotated, as the reference requires."""
+    from lookatmyquant_amd import nested as N
+    from lookatmyquant_amd import quantize as Q
+
+    W, H = config12
+    W = W[:128].astype(np.float64)
+    rng = np.random.default_rng(5)
+    Ga = rng.standard_normal((400, 128))
+    G = Ga.T @ Ga / 400
+    say("lm3 word with output shaping, 128 x 960")
+    net = Q.word("lm3", torch.from_numpy(W), torch.from_numpy(H), 200, None, in_seed=201, out_rot=False,
+                 G=torch.from_numpy(G))
+    S = net.cores["W.S"].data.numpy()
+    X = W @ O.rht(960, 201).T
+    Hr = O.rht(960, 201) @ H @ O.rht(960, 201).T
+    ref = O.shaped_sweep(X / S[:, None], Hr, N.lloyd_max(3).numpy(), S[:, None] * G * S[None, :], block=32)
+    assert np.array_equal(net.codes.numpy(), ref)
+    with pytest.raises(ValueError, match="one matrix at one rate"):
+        N.nested_words([torch.from_numpy(W)], torch.from_numpy(H), [200], 3, [3], 0.4, [1.0], N.lloyd_max(3),
+                       in_seed=201, out_rot=True, G=torch.from_numpy(G))
+
+
 def test_multirate_kernel_matches_the_oracle_across_runs():
     """lamq_ldlq_multirate_block over two outer runs and several workgroups (300 rows x 700 columns, two rates of a
     4-bit nested code with unequal weights) against the oracle, and nested_words' three rates reading the shared

@@ -123,6 +123,16 @@ def test_argument_errors_are_reported_without_a_gpu():
     assert L.lamq_pack_codes_groups(ctypes.addressof(descs), 1, 8, 12, 1, None, None) == -1
     assert L.lamq_pack_codes_groups(ctypes.addressof(descs), 1, 0, 12, 1, ptr(q), None) == -1
     assert L.lamq_pack_codes_groups(ctypes.addressof(descs), -1, 8, 12, 1, ptr(q), None) == -1
+    # output shaping: the packed feedback's size (blocks of 32 rows over 100: 32 x (68 + 36 + 4) doubles), a block
+    # past 64 or a column past LDS unsupported, missing arrays invalid
+    assert L.lamq_shaping_feedback_size(100, 32) == 32 * (68 + 36 + 4) * 8
+    assert L.lamq_shaping_feedback_size(30, 32) == 0
+    assert L.lamq_shaping_feedback(None, 100, 100, 32, ptr(p), None) == -1
+    assert L.lamq_shaping_feedback(ptr(p), 100, 100, 65, ptr(p), None) == -2
+    assert L.lamq_ldlq_shaped_column(None, 8, 8, 8, 0, ptr(p), 4, ptr(p), 4, ptr(q), 8, ptr(p), None) == -1
+    assert L.lamq_ldlq_shaped_column(ptr(p), 8, 8, 8, 8, ptr(p), 4, ptr(p), 4, ptr(q), 8, ptr(p), None) == -1
+    assert L.lamq_ldlq_shaped_column(ptr(p), 20000, 8, 8, 0, ptr(p), 4, ptr(p), 4, ptr(q), 8, ptr(p), None) == -2
+    assert L.lamq_ldlq_shaped_column(ptr(p), 8, 8, 8, 0, ptr(p), 4, ptr(p), 300, ptr(q), 8, ptr(p), None) == -2
     assert L.lamq_chol_inv_upper_workspace_size(10) >= 800
     assert L.lamq_viterbi_workspace_size(3, 100, 12, 2) == 3 * 100 * 256
     # the fused 16-bit-state search keeps its back-pointers (23 steps x 1024 words a row) in a workspace where LDS

@@ -427,6 +427,45 @@ def test_multirate_sweep_matches_the_reference(golden, case):
     assert np.array_equal(idx, g[f"{case}_idx"])
 
 
+@pytest.mark.parametrize("with_h", [True, False])
+def test_shaped_sweep_with_isotropic_g_is_plain_rounding(with_h):
+    """Output shaping under G = c I: the damped factor V is diagonal, every block's feedback V[a:b, a:b]^-1 V[a:b, b:]
+    is zero, and each entry takes its nearest level, so the sweep is the one-rate multirate sweep's."""
+    rng = np.random.default_rng(11)
+    m, n = 40, 90
+    X = rng.standard_normal((m, n))
+    Xa = rng.standard_normal((300, n))
+    H = Xa.T @ Xa / 300 if with_h else None
+    lv = np.sort(rng.standard_normal(8))
+    got = O.shaped_sweep(X, H, lv, 2.5 * np.eye(m), block=8)
+    assert np.array_equal(got, O.multirate_sweep(X, H, lv[None], [1.0]))
+
+
+@pytest.mark.parametrize("block", [1, 4, 8, 16])
+def test_shaped_rows_are_the_block_sweep_of_the_column(block):
+    """Within a column, output shaping settles the rows `block` at a time on their nearest levels and re-solves the
+    later rows through M = V[a:b, a:b]^-1 V[a:b, b:]: the generic block sweep (width = block, the triangular solve
+    z U_BB = E and T -= z U) run along the column, the rows as its columns and V as its factor. Checked against that
+    sweep, written separately, on 42 rows (a partial last block for 4, 8 and 16) with a dense G."""
+    rng = np.random.default_rng(20 + block)
+    m = 42
+    Ga = rng.standard_normal((200, m))
+    G = Ga.T @ Ga / 200
+    u = rng.standard_normal(m)
+    lv = np.sort(rng.standard_normal(16))
+    got = O.shaped_sweep(u[:, None], None, lv, G, block=block)[:, 0]
+    _, V, _ = O.environment(G, damp=O.OUTPUT_DAMP)
+    want = np.empty(m, dtype=np.int64)
+
+    def nearest(j, cols, T):
+        i = np.abs(cols[0][:, None] - lv[None, :]).argmin(1)
+        want[j : j + len(i)] = i
+        return lv[i][None, :]
+
+    O.sweep(u[None, :], V, nearest, width=block, lazy=block * (-(-m // block)))
+    assert np.array_equal(got, want)
+
+
 def test_one_rate_multirate_is_the_scalar_sweep():
     """One rate at weight 1: the joint cost is the squared distance, so the sweep is ldlq_scalar's (mode 0)."""
     rng = np.random.default_rng(3)
