@@ -83,15 +83,16 @@ __global__ void prep_kernel(const double* __restrict__ H, int64_t n, int64_t ldH
 #define DT_LD 17            // row stride of a 16 x 16 tile in LDS, in doubles
 #define DT_SZ (16 * DT_LD)  // doubles of one tile
 
-// 1/sqrt(d) for a positive normal d: the hardware estimate and two Newton steps y <- y + y/2 (1 - d y^2), within a
-// few units in the last place
+// 1/sqrt(d) for a positive normal d: the hardware estimate and two Newton steps y <- y + y (1/2 - (d/2) y^2), within
+// a few units in the last place (d/2 formed once; halving is exact, so each step rounds as y + (y/2)(1 - d y^2) would)
 __device__ __forceinline__ double rsqrt_f64(double d)
 {
     double y = __builtin_amdgcn_rsq(d);
+    const double h = 0.5 * d;
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
-        const double e = fma(-(d * y), y, 1.0);
-        y = fma(0.5 * y, e, y);
+        const double e = fma(-(h * y), y, 0.5);
+        y = fma(y, e, y);
     }
     return y;
 }
@@ -177,13 +178,11 @@ __global__ __launch_bounds__(256) void diag_block_kernel(double* __restrict__ A,
 #pragma unroll
             for (int j = 0; j < 16; ++j) r[j] = T(c0 + li, c0 + j);
             double rc[16];  // 1 / l[c][c], the same in every lane
-            int fail = 0;   // the first non-positive pivot (the same in every lane)
             // the pivots form the serial chain; each is formed from lane-uniform values with exactly the operations
             // lane c + 1 applies to its own entry, so the chain never waits on the column's update
             double d = row_bcast_f64(r[0], 0);
 #pragma unroll
             for (int c = 0; c < 16; ++c) {
-                fail = (fail == 0 && !(d > 0.0)) ? (int)(k0 + c0 + c + 1) : fail;
                 const double rs = rsqrt_f64(d);
                 rc[c] = rs;
                 double dn = 0.0;
@@ -204,6 +203,12 @@ __global__ __launch_bounds__(256) void diag_block_kernel(double* __restrict__ A,
 #pragma unroll
                 for (int j = 0; j < 16; ++j) T(c0 + li, c0 + j) = j <= li ? r[j] : 0.0;
             }
+            // the first failing pivot, read off the diagonal once: l[c][c] = d rs is positive for a positive finite d,
+            // and NaN for a pivot that is not (rs is NaN for d < 0 and infinite for d = 0, and an earlier failure
+            // leaves every later pivot NaN), so the lowest lane of the 16 whose diagonal is not positive names it
+            const double diag = T(c0 + li, c0 + li);
+            const uint64_t badl = __builtin_amdgcn_ballot_w64(!(diag > 0.0)) & 0xffffull;
+            const int fail = badl ? (int)(k0 + c0 + __builtin_ctzll(badl) + 1) : 0;
             // the inverse reads the factor back from LDS (the same value in every lane), lane c holding column c of
             // D_p^-1 (x[i] = D_p^-1[i][c]); a wave's LDS accesses take effect in the order it issues them, so the tile
             // can then become D_p^-1 (nothing reads D_p itself)
