@@ -59,9 +59,9 @@ VALU_ISSUE_TOPS = 256 * 4 * 16 * 2.4e9 / 1e12
 
 # HBM bytes per launch of the dominant kernel from two rocprofv3 counter runs (FETCH_SIZE, WRITE_SIZE), scaled by a
 # 1 GiB copy's readings; keyed by (workload, kernel, L)
-MEASURED_TRAFFIC = {("c2", "ldlq_trellis_block_gx_kernel", 16): 421035178,
-                    ("c5", "ldlq_trellis_groups_gx_kernel", 16): 1394557914,
-                    ("c5", "ldlq_trellis_groups_kernel", 12): 21661751}
+MEASURED_TRAFFIC = {("c2", "ldlq_trellis_block_gx_kernel", 16): 423926181,
+                    ("c5", "ldlq_trellis_groups_gx_kernel", 16): 1394276752,
+                    ("c5", "ldlq_trellis_groups_kernel", 12): 21661290}
 
 
 def kernel_line(ms: float, work: float, peak: float, unit: str, bound: str, scale: float, launches: int = 0) -> dict:
