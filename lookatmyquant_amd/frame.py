@@ -143,17 +143,23 @@ def covariance(x: torch.Tensor, w: torch.Tensor | None = None) -> torch.Tensor:
 class Environment:
     """What the rest of the network sees through a linear core's input bond (opgraph/frame.py:508-522):
     dead columns (zero diagonal) get a unit diagonal, H += damp * mean(diag H) * I, and U is the upper Cholesky
-    factor of H^-1. Computed on the GPU; .H, .U, .dead live there."""
+    factor of H^-1. Computed on the GPU; .H, .U, .dead live there. G, the output-side sensitivity (a square matrix
+    over the output rows, frame.py:516), is kept in float64 beside them and weights error()."""
 
     def __init__(self, H: torch.Tensor, damp: float = 0.01, G: torch.Tensor | None = None):
-        if G is not None:
-            raise NotImplementedError("output-side sensitivity G is not part of this path")
-        self.G = None
         dev = E._abi.device()
+        if G is not None and (G.dim() != 2 or G.shape[0] != G.shape[1]):
+            raise ValueError("G must be a square matrix over the output rows")
+        self.G = None if G is None else G.to(dev, torch.float64).contiguous()
         Hd, U, dead, _ = E.chol_inv_upper(H.to(dev, torch.float64).contiguous(), damp)
         self.H, self.U, self.dead = Hd, U, dead
 
     def error(self, D: torch.Tensor) -> float:
-        """tr(D H D^T), the local objective (opgraph/frame.py:534-537)."""
+        """tr(D H D^T), or tr(G D H D^T) with G, the local objective (opgraph/frame.py:534-537)."""
         D = D.to(self.H.device, torch.float64)
-        return float(((D @ self.H) * D).sum())
+        DH = D @ self.H
+        if self.G is None:
+            return float((DH * D).sum())
+        if self.G.shape[0] != D.shape[0]:
+            raise ValueError("G and D must have the same number of rows")
+        return float(((self.G @ DH) * D).sum())

@@ -5,14 +5,15 @@ gfx950 kernels.
     lloyd_max(bits, iters=500), lloyd_max_levels(n, iters=500)                nested.py:71-82
     nested_tables(top, rates, alpha)                                          nested.py:150-152
     multirate_sweep(X, H, tables, weights, G=None, block=32)                  nested.py:104-147
-    nested_words(Ws, H, seeds, top, rates, alpha, weights, levels=None, in_seed=None, out_rot=True)   nested.py:155
+    nested_words(Ws, H, seeds, top, rates, alpha, weights, levels=None, in_seed=None, out_rot=True, G=None)
+                                                                              nested.py:155
 
 The level tables are small host computations in float64 with torch's special functions, as the reference does
 them (so the levels are the same bits). The sweep is the width-1 LDLQ kernel: each column's index is the first
 minimum of (t - level)^2 over the levels (one rate at weight 1), or of sum_r w_r (t_r - tables[r, i])^2 over the
 rates' copies of the row (several rates: lamq_ldlq_multirate_block), then the later columns are re-solved under U.
-Output-side shaping (G, one matrix at one rate with its rows settled against each other) is not part of this path
-and raises NotImplementedError."""
+With output-side shaping (G: one matrix at one rate) each column's rows are settled a block at a time and the later
+rows re-solved under G's damped factor (lamq_ldlq_shaped_column), inside the generic width-1 sweep under H."""
 
 from __future__ import annotations
 

@@ -393,7 +393,7 @@ def main(argv=None):
     ap.add_argument("--plan", default="", help="with --program plan: a plan JSON ({\"linears\": {\"i.name\": program}})")
     ap.add_argument("--row-plan", default="", help="rowgroup-plan-1 JSON: original row ids and widths by full parameter "
                                                    "name; requires --rot in-shared and --trellis-rows")
-    ap.add_argument("--trellis-rows", default="16,8", help="width,look of the row trellis (16,8)")
+    ap.add_argument("--trellis-rows", default="16,8", help="width,look of the row trellis (quantize.py's --trellis-rows): width 1-16 dividing 128, width + look <= 24")
     ap.add_argument("--rot", choices=["in-shared"], default="in-shared",
                     help="one input rotation per stage, none on the output (the only rotation of this path)")
     ap.add_argument("--cross-alpha", type=float, default=1.0, help="QEP's alpha for cross-term programs")
@@ -414,8 +414,13 @@ def main(argv=None):
     ap.add_argument("--artifact", default="", help="write the codes as an opgraph-packed-1 artifact in this new directory")
     ap.add_argument("--out", required=True)
     args = ap.parse_args(argv)
-    if args.trellis_rows != "16,8":
-        raise NotImplementedError("the fused row-trellis kernels settle 16 columns and look 8 ahead")
+    try:
+        window = tuple(int(v) for v in args.trellis_rows.split(","))
+    except ValueError:
+        window = ()
+    if len(window) != 2:
+        ap.error("--trellis-rows takes width,look")
+    stack.trellis_window(window)
     if not 1 <= args.calib_len <= 0x7FFFFF:
         raise NotImplementedError("the forwards' fused attention takes sequence lengths of 1 to 8388607 tokens")
     sh = stack.Shape()
@@ -436,7 +441,7 @@ def main(argv=None):
     timer = stack.Timer()
     out = stack.build(tokens, sh, w if args.token_weights else None, alpha=args.cross_alpha, L=args.state_bits,
                       plan=plan, row_plan=row_plan, chunk=args.chunk, layers=layers, timer=timer, redamp=args.redamp,
-                      lam=args.lam, seed_set=args.seed_set)
+                      lam=args.lam, seed_set=args.seed_set, window=window)
     torch.cuda.synchronize()
     secs = time.perf_counter() - t0
     res = {"program": args.program, "layers": layers, "weights": out["weights"],

@@ -164,6 +164,16 @@ def active_shapes(sh: Shape, plan: dict, layers: int) -> dict:
             if parse(plan["linears"][f"{i}.{nm}"])[0] == "tr"}
 
 
+def trellis_window(window) -> tuple:
+    """(width, look) of the stages' row trellis (quantize.py's --trellis-rows) as the fused row-group sweep takes it:
+    1 to 16 columns settled at a time, dividing the 128-column lazy block, and width + look <= 24."""
+    width, look = (int(v) for v in window)
+    if not (1 <= width <= E.FUSED_WMAX and look >= 0 and width + look <= E.FUSED_TV and 128 % width == 0):
+        raise NotImplementedError(f"the fused row-trellis kernels settle 1 to {E.FUSED_WMAX} columns dividing the "
+                                  f"128-column block, width + look at most {E.FUSED_TV}; not ({width}, {look})")
+    return width, look
+
+
 class StackBuild:
     """The build of a random-initialised stack on calibration token ids [S, T], one decoder layer per call of
     layer(): per stage, the two streams' statistics, the QEP target of the matrices whose program asks for it, the
@@ -192,7 +202,8 @@ class StackBuild:
                  alpha: float = 0.5, L: int = 12, plan: dict | None = None, row_plan: dict | None = None,
                  plan_seed: int = 7000, chunk: int = 32, layers: int | None = None, weight_seed: int = 5000,
                  timer: Timer | None = None, keep: int = 0, redamp: bool = False, lam: float = LAM,
-                 seed_set: int = 0, kernels: E.KernelTimer | None = None):
+                 seed_set: int = 0, kernels: E.KernelTimer | None = None, window: tuple = (16, 8)):
+        self.width, self.look = trellis_window(window)
         dev = E._abi.device()
         self.dev, self.sh, self.alpha, self.L, self.keep, self.redamp = dev, sh, alpha, L, keep, redamp
         self.lam, self.seed_set, self.kernels = lam, seed_set, kernels
@@ -350,6 +361,7 @@ class StackBuild:
         if kt is not None:
             factor = self._factor(H, in_seed, factor, key)
         sweep = lambda f: quantize_stage_row_groups({nm: targets[nm] for nm in trellis}, plans, H, in_seed, L=L,
+                                                    width=self.width, look=self.look,
                                                     tables=self.device_tables(), factor=f, timer=kt,
                                                     check=kt is not None)
         res = sweep(factor) if trellis else {}
@@ -439,7 +451,7 @@ class StackBuild:
 def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | None = None, alpha: float = 0.5,
           L: int = 12, plan: dict | None = None, row_plan: dict | None = None, plan_seed: int = 7000, chunk: int = 32,
           layers: int | None = None, weight_seed: int = 5000, timer: Timer | None = None, keep: int = 0,
-          redamp: bool = False, lam: float = LAM, seed_set: int = 0) -> dict:
+          redamp: bool = False, lam: float = LAM, seed_set: int = 0, window: tuple = (16, 8)) -> dict:
     """The whole build of a random-initialised stack (StackBuild, layer after layer). Returns {"codes": {"i.name":
     {"kind": "trellis" | "scalar", "states": int32 [m, n] (trellis states, or Lloyd-Max level indices), "scales":
     float64 [m], "in_seed", "groups": the row groups, "packed": per group the code words (engine.pack_codes, read in
@@ -448,7 +460,7 @@ def build(tokens: torch.Tensor, sh: Shape = Shape(), token_w: torch.Tensor | Non
     export_codes writes the codes as an opgraph-packed-1 artifact and saved_codes as the reference's --save-codes
     dictionary."""
     b = StackBuild(tokens, sh, token_w, alpha, L, plan, row_plan, plan_seed, chunk, layers, weight_seed, timer, keep,
-                   redamp, lam, seed_set)
+                   redamp, lam, seed_set, window=window)
     for _ in range(b.layers):
         b.layer()
     return b.result()

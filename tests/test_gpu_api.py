@@ -402,6 +402,34 @@ def test_environment_and_covariance(config12):
     assert np.abs(env.U.cpu().numpy() - U).max() < 1e-9 * np.abs(U).max()
 
 
+def test_environment_output_sensitivity_weights_the_error():
+    """Environment(H, G).error(D) = tr(G D H D^T) (opgraph/frame.py:534-537): G = I gives the unweighted error, a
+    diagonal G the g-weighted sum of the rows' d_i Hd d_i^T, a full G numpy's trace, on the oracle's damped H."""
+    from lookatmyquant_amd.frame import Environment
+
+    rng = np.random.default_rng(41)
+    X = rng.standard_normal((400, 24))
+    H = X.T @ X / 400
+    D = rng.standard_normal((10, 24))
+    A = rng.standard_normal((10, 10))
+    Hd, _, _ = O.environment(H)
+    rows = np.einsum("ij,jk,ik->i", D, Hd, D)
+    Ht, Dt = torch.from_numpy(H), torch.from_numpy(D)
+    e0 = Environment(Ht).error(Dt)
+    assert abs(e0 - rows.sum()) < 1e-12 * rows.sum()
+    assert abs(Environment(Ht, G=torch.eye(10, dtype=torch.float64)).error(Dt) - e0) < 1e-12 * e0
+    g = rng.uniform(0.5, 2.0, 10)
+    eg = Environment(Ht, G=torch.from_numpy(np.diag(g))).error(Dt)
+    assert abs(eg - (g * rows).sum()) < 1e-12 * (g * rows).sum()
+    G = A @ A.T
+    ref = np.trace(G @ D @ Hd @ D.T)
+    assert abs(Environment(Ht, G=torch.from_numpy(G)).error(Dt) - ref) < 1e-12 * ref
+    with pytest.raises(ValueError):
+        Environment(Ht, G=torch.ones(3, 4, dtype=torch.float64))
+    with pytest.raises(ValueError):
+        Environment(Ht, G=torch.eye(9, dtype=torch.float64)).error(Dt)
+
+
 def test_cross_target_is_the_damped_solve():
     from lookatmyquant_amd.quantize import cross_target
 

@@ -88,6 +88,31 @@ def test_small_stack_build(tmp_path):
             assert np.array_equal(stored[k + ".scales"], rec["scales"].float().cpu().numpy()[rows])
 
 
+def test_small_stack_build_at_another_trellis_window():
+    """The stages' row trellis at width 8, look 4 (quantize.py's --trellis-rows 8,4): sampled rows of two row groups
+    of every matrix equal the oracle's row-trellis LDLQ at that window."""
+    from lookatmyquant_amd import stack
+    from lookatmyquant_amd.tables import load_table
+
+    sh = stack.Shape(hidden=512, heads=8, kv_heads=4, head_dim=128, inter=1024, layers=1, vocab=1000)
+    tok, w = stack.calibration_tokens(sequences=4, T=256, vocab=1000, seed=11)
+    say("stack build: 1 layer, hidden 512, window (8, 4)")
+    out = stack.build(tok, sh, w, alpha=0.5, chunk=2, keep=1, window=(8, 4))
+    assert int(out["bad"].item()) == 0
+    tables = {b: np.array(load_table(12, b)) for b in (1, 2, 3, 4)}
+    for (i, s), kept in out["stages"].items():
+        H = kept["H"].cpu().numpy()
+        for nm, groups in kept["plans"].items():
+            target = kept["targets"][nm].cpu().numpy()
+            states = out["codes"][f"{i}.{nm}"]["states"].cpu().numpy()
+            for g in groups[:2]:
+                rows = np.asarray(g["rows"])[:16]
+                ref, _, _ = O.ldlq_words_trellis(target[rows], H, tables[g["bits"]], 12, g["bits"], kept["in_seed"],
+                                                 width=8, look=4)
+                say(f"layer {i} stage {s} {nm} group {g['group']} bits {g['bits']}")
+                assert np.array_equal(states[rows], ref)
+
+
 @pytest.mark.parametrize("T", [8, 64, 520, 2048, 4096])
 def test_causal_softmax_matches_a_float64_reference(T):
     """engine.causal_softmax on bf16 scores [2, 3, T, T]: every kept entry within one bf16 rounding (2^-8 relative)

@@ -365,16 +365,33 @@ def test_synthetic_plans_are_valid_row_plans(tmp_path):
 
 
 def test_cli_checks_its_arguments(tmp_path):
-    """quantize.py's entry point: the row trellis is width 16, look 8; --program plan needs --plan; unknown programs
-    are refused before any work (no GPU is touched)."""
+    """quantize.py's entry point: a row-trellis window the fused kernels do not take, a malformed window, --program
+    plan without --plan and unknown programs are refused before any work (no GPU is touched)."""
     from lookatmyquant_amd.quantize import main
 
-    with pytest.raises(NotImplementedError):
-        main(["--program", "tr2x", "--trellis-rows", "8,4", "--out", str(tmp_path / "o.json")])
+    for window in ("16,12", "12,4", "0,8", "17,0"):
+        with pytest.raises(NotImplementedError):
+            main(["--program", "tr2x", "--trellis-rows", window, "--out", str(tmp_path / "o.json")])
+    for window in ("8", "8,4,2", "a,b"):
+        with pytest.raises(SystemExit):
+            main(["--program", "tr2x", "--trellis-rows", window, "--out", str(tmp_path / "o.json")])
     with pytest.raises(SystemExit):
         main(["--program", "plan", "--out", str(tmp_path / "o.json")])
     with pytest.raises(ValueError):
         main(["--program", "tr9y", "--out", str(tmp_path / "o.json")])
+
+
+def test_stack_trellis_windows():
+    """The windows the stages' fused row-group sweep takes: width 1-16 dividing the 128-column block, width + look
+    <= 24."""
+    from lookatmyquant_amd.stack import trellis_window
+
+    for w in (1, 2, 4, 8, 16):
+        for look in (0, 4, 24 - w):
+            assert trellis_window((w, look)) == (w, look)
+    for bad in ((16, 9), (3, 8), (32, 0), (0, 0), (8, -1)):
+        with pytest.raises(NotImplementedError):
+            trellis_window(bad)
 
 
 def test_trellis_fit_checks_its_arguments():
