@@ -316,6 +316,12 @@ size_t lamq_kl_workspace_size(int64_t T);
 int lamq_kl_rows(const uint16_t* ref, const uint16_t* q, int64_t T, int64_t V, int64_t ldr, int64_t ldq,
                  const float* w, float* kl, double* sums, void* workspace, size_t workspace_bytes, void* stream);
 
+/* The same on float32 logits: the reference takes the model's logits as .logits.float() (compiler.py:180,185), so a
+ * float32 model's logits enter unrounded. Same arguments, workspace and results; on logits bf16 holds exactly the
+ * results equal lamq_kl_rows' bit for bit (the same float32 arithmetic in the same order). */
+int lamq_kl_rows_f32(const float* ref, const float* q, int64_t T, int64_t V, int64_t ldr, int64_t ldq,
+                     const float* w, float* kl, double* sums, void* workspace, size_t workspace_bytes, void* stream);
+
 /* lamq_kl_rows without a workspace and without any allocation: no counterpart in the reference. For callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving or measurement loops, harnesses that
  * forbid hipMalloc). The per-token partials live in a static device array of LAMQ_KL_NOALLOC_MAX_T * 2 float64

@@ -58,6 +58,7 @@ SIGNATURES = {
     "lamq_cross_gram_rows": (_c_int, [_p, _p, _p, _c_i64, _c_i64, _c_i64, _c_flt, _p, _c_i64, _p, _c_size, _p]),
     "lamq_kl_workspace_size": (_c_size, [_c_i64]),
     "lamq_kl_rows": (_c_int, [_p, _p, _c_i64, _c_i64, _c_i64, _c_i64, _p, _p, _p, _p, _c_size, _p]),
+    "lamq_kl_rows_f32": (_c_int, [_p, _p, _c_i64, _c_i64, _c_i64, _c_i64, _p, _p, _p, _p, _c_size, _p]),
     "lamq_kl_rows_noalloc": (_c_int, [_p, _p, _c_i64, _c_i64, _c_i64, _c_i64, _p, _p, _p, _p]),
     "lamq_pack_trellis": (_c_int, [_p, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _p, _c_i64, _p, _p]),
     "lamq_pack_codes": (_c_int, [_p, _c_i64, _c_i64, _p, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _p, _c_i64, _p, _p]),

@@ -5,8 +5,9 @@ kernel, and the LDLQ-shaped noise its noise method adds instead of quantizing.
     kl_per_token(ref_logits, q_logits) -> tensor       per-position KL, as quantize.evaluate / text_kl use it
     ldlq_noise(W, H, d, seed, gen, row_rotation=True)  W plus LDLQ-shaped rounding noise of level d
 
-For each position, KL = sum_v softmax(ref)_v (log_softmax(ref)_v - log_softmax(q)_v) in float32 from bf16 logits
-(the reference casts the model's logits with .float()), in one pass over both logit matrices; positions are
+For each position, KL = sum_v softmax(ref)_v (log_softmax(ref)_v - log_softmax(q)_v) in float32 from bf16 or
+float32 logits (the reference casts the model's logits with .float(); other float dtypes are cast to float32 the
+same way), in one pass over both logit matrices; positions are
 weighted by wpos (the digit weight of compiler.py:170-173) and the result is sum w KL / sum w.
 """
 
@@ -17,24 +18,36 @@ import torch
 from . import engine as E
 
 
-def _as_bf16_rows(x: torch.Tensor) -> torch.Tensor:
+def _as_rows(x: torch.Tensor) -> torch.Tensor:
+    """Logit rows on the device: bf16 as they are (the kernel widens them exactly); any other floating dtype as
+    float32, as the reference's .logits.float() (compiler.py:180,185) takes them."""
     dev = E._abi.device()
     x = torch.as_tensor(x)
+    if not x.is_floating_point():
+        raise ValueError("logits must be a floating-point tensor")
     if x.dtype != torch.bfloat16:
-        raise NotImplementedError("the KL kernel reads bfloat16 logits (the model's output dtype)")
+        x = x.to(dev, torch.float32)
     return x.reshape(-1, x.shape[-1]).to(dev).contiguous()
+
+
+def _pair(ref_logits, q_logits):
+    """Both logit matrices as rows of one dtype: bf16 if both are, else float32 (bf16 widens exactly)."""
+    r, q = _as_rows(ref_logits), _as_rows(q_logits)
+    if r.dtype != q.dtype:
+        r, q = r.float(), q.float()
+    return r, q
 
 
 def kl_per_token(ref_logits: torch.Tensor, q_logits: torch.Tensor) -> torch.Tensor:
     """KL(p_ref || p_q) for every position, float32, shaped like the logits without their last axis."""
     shape = ref_logits.shape[:-1]
-    kl, _ = E.kl_rows(_as_bf16_rows(ref_logits), _as_bf16_rows(q_logits))
+    kl, _ = E.kl_rows(*_pair(ref_logits, q_logits))
     return kl.reshape(shape)
 
 
 def kl(ref_logits: torch.Tensor, q_logits: torch.Tensor, wpos: torch.Tensor | None = None) -> float:
     """sum_pos w_pos KL_pos / sum_pos w_pos (compiler.py:180-188); w = 1 without wpos."""
-    r, q = _as_bf16_rows(ref_logits), _as_bf16_rows(q_logits)
+    r, q = _pair(ref_logits, q_logits)
     w = None if wpos is None else torch.as_tensor(wpos).reshape(-1).to(r.device, torch.float32)
     _, sums = E.kl_rows(r, q, w)
     s = sums.cpu()

@@ -1,4 +1,4 @@
-// Per-token KL(p_ref || p_q) of bf16 logits in one streaming pass (compiler.py:177-188).
+// Per-token KL(p_ref || p_q) of bf16 or float32 logits in one streaming pass (compiler.py:177-188).
 //
 // For a token with logits r (reference) and q (quantized):
 //   KL = sum_v p_v ((r_v - lse_r) - (q_v - lse_q)) = (sum_v e^(r_v - m_r) (r_v - q_v)) / s_r - lse_r + lse_q
@@ -65,7 +65,26 @@ __device__ __forceinline__ void kl_merge(KLPart& a, const KLPart& b)
     a.mq = mq;
 }
 
-__global__ __launch_bounds__(256) void kl_rows_kernel(const uint16_t* __restrict__ ref, const uint16_t* __restrict__ q,
+// Eight logits from 16-byte loads (chunk i of the row, whose start is 16-byte aligned), and one logit, as float32:
+// a bf16 logit widens exactly, so both element types feed the same float32 arithmetic.
+__device__ __forceinline__ void load8(const uint16_t* row, int64_t i, float (&v)[8])
+{
+    const uint4 x = reinterpret_cast<const uint4*>(row)[i];
+    v[0] = bf_lo(x.x); v[1] = bf_hi(x.x); v[2] = bf_lo(x.y); v[3] = bf_hi(x.y);
+    v[4] = bf_lo(x.z); v[5] = bf_hi(x.z); v[6] = bf_lo(x.w); v[7] = bf_hi(x.w);
+}
+__device__ __forceinline__ void load8(const float* row, int64_t i, float (&v)[8])
+{
+    const float4* p = reinterpret_cast<const float4*>(row) + 2 * i;
+    const float4 x = p[0], y = p[1];
+    v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+    v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
+}
+__device__ __forceinline__ float load1(const uint16_t* row, int64_t i) { return __uint_as_float((uint32_t)row[i] << 16); }
+__device__ __forceinline__ float load1(const float* row, int64_t i) { return row[i]; }
+
+template <typename Elt>
+__global__ __launch_bounds__(256) void kl_rows_kernel(const Elt* __restrict__ ref, const Elt* __restrict__ q,
                                                       int64_t V, int64_t ldr, int64_t ldq, const float* __restrict__ w,
                                                       float* __restrict__ kl, double* __restrict__ wkl,
                                                       double* __restrict__ wt, int vec)
@@ -73,8 +92,8 @@ __global__ __launch_bounds__(256) void kl_rows_kernel(const uint16_t* __restrict
     __shared__ KLPart parts[256];
     const int64_t row = blockIdx.x;
     const int tid = threadIdx.x;
-    const uint16_t* r = ref + row * ldr;
-    const uint16_t* p = q + row * ldq;
+    const Elt* r = ref + row * ldr;
+    const Elt* p = q + row * ldq;
     KLPart a;
     a.mr = -__builtin_inff();
     a.mq = -__builtin_inff();
@@ -83,14 +102,9 @@ __global__ __launch_bounds__(256) void kl_rows_kernel(const uint16_t* __restrict
     int64_t done = 0;
     if (vec) {
         const int64_t nv = V / 8;
-        const uint4* r4 = reinterpret_cast<const uint4*>(r);
-        const uint4* q4 = reinterpret_cast<const uint4*>(p);
         for (int64_t i = tid; i < nv; i += 256) {
-            const uint4 x = r4[i], y = q4[i];
-            rv[0] = bf_lo(x.x); rv[1] = bf_hi(x.x); rv[2] = bf_lo(x.y); rv[3] = bf_hi(x.y);
-            rv[4] = bf_lo(x.z); rv[5] = bf_hi(x.z); rv[6] = bf_lo(x.w); rv[7] = bf_hi(x.w);
-            qv[0] = bf_lo(y.x); qv[1] = bf_hi(y.x); qv[2] = bf_lo(y.y); qv[3] = bf_hi(y.y);
-            qv[4] = bf_lo(y.z); qv[5] = bf_hi(y.z); qv[6] = bf_lo(y.w); qv[7] = bf_hi(y.w);
+            load8(r, i, rv);
+            load8(p, i, qv);
             kl_chunk(a, rv, qv, 8);
         }
         done = nv * 8;
@@ -100,8 +114,8 @@ __global__ __launch_bounds__(256) void kl_rows_kernel(const uint16_t* __restrict
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const bool in = i + e < V;
-            rv[e] = in ? __uint_as_float((uint32_t)r[i + e] << 16) : 0.0f;
-            qv[e] = in ? __uint_as_float((uint32_t)p[i + e] << 16) : 0.0f;
+            rv[e] = in ? load1(r, i + e) : 0.0f;
+            qv[e] = in ? load1(p, i + e) : 0.0f;
             cnt += in ? 1 : 0;
         }
         kl_chunk(a, rv, qv, cnt);
@@ -157,12 +171,16 @@ __global__ __launch_bounds__(256) void kl_sum_kernel(const double* __restrict__ 
 extern "C" size_t lamq_kl_workspace_size(int64_t T) { return T > 0 ? (size_t)T * 2 * sizeof(double) : 0; }
 
 // The two launches of both entry points: per-row KL into kl, w*kl and w into wkl[0..T), wkl[T..2T), then their sums.
-static int kl_launch(const uint16_t* ref, const uint16_t* q, int64_t T, int64_t V, int64_t ldr, int64_t ldq,
+template <typename Elt>
+static int kl_launch(const Elt* ref, const Elt* q, int64_t T, int64_t V, int64_t ldr, int64_t ldq,
                      const float* w, float* kl, double* sums, double* wkl, hipStream_t s)
 {
-    const int vec = ((uintptr_t)ref % 16 == 0) && ((uintptr_t)q % 16 == 0) && (ldr % 8 == 0) && (ldq % 8 == 0);
+    // 16-byte loads where every row starts 16-byte aligned
+    constexpr int64_t per16 = 16 / sizeof(Elt);
+    const int vec = ((uintptr_t)ref % 16 == 0) && ((uintptr_t)q % 16 == 0) && (ldr % per16 == 0) && (ldq % per16 == 0);
     double* wt = wkl + T;
-    hipLaunchKernelGGL(kl_rows_kernel, dim3((unsigned)T), dim3(256), 0, s, ref, q, V, ldr, ldq, w, kl, wkl, wt, vec);
+    hipLaunchKernelGGL(kl_rows_kernel<Elt>, dim3((unsigned)T), dim3(256), 0, s, ref, q, V, ldr, ldq, w, kl, wkl, wt,
+                       vec);
     LAMQ_LAUNCH_CHECK();
     if (sums) {
         hipLaunchKernelGGL(kl_sum_kernel, dim3(1), dim3(256), 0, s, wkl, wt, T, sums);
@@ -173,6 +191,17 @@ static int kl_launch(const uint16_t* ref, const uint16_t* q, int64_t T, int64_t 
 
 extern "C" int lamq_kl_rows(const uint16_t* ref, const uint16_t* q, int64_t T, int64_t V, int64_t ldr, int64_t ldq,
                             const float* w, float* kl, double* sums, void* workspace, size_t workspace_bytes, void* stream)
+{
+    if (!ref || !q || !kl || T < 0 || V < 1 || ldr < V || ldq < V) return LAMQ_EINVAL;
+    if (T == 0) return LAMQ_OK;
+    if (!workspace || workspace_bytes < lamq_kl_workspace_size(T)) return LAMQ_EINVAL;
+    if (T > 0x7fffffff) return LAMQ_EUNSUP;
+    return kl_launch(ref, q, T, V, ldr, ldq, w, kl, sums, reinterpret_cast<double*>(workspace), as_stream(stream));
+}
+
+extern "C" int lamq_kl_rows_f32(const float* ref, const float* q, int64_t T, int64_t V, int64_t ldr, int64_t ldq,
+                                const float* w, float* kl, double* sums, void* workspace, size_t workspace_bytes,
+                                void* stream)
 {
     if (!ref || !q || !kl || T < 0 || V < 1 || ldr < V || ldq < V) return LAMQ_EINVAL;
     if (T == 0) return LAMQ_OK;

@@ -970,9 +970,11 @@ def cross_gram_accum(D: torch.Tensor, Xr: torch.Tensor, Xq: torch.Tensor, w: tor
 
 
 def kl_rows(ref: torch.Tensor, q: torch.Tensor, w: torch.Tensor | None = None):
-    """(kl [T] float32, sums [2] float64 = (sum w kl, sum w)) for bf16 logits [T, V]."""
-    need(ref, torch.bfloat16, "ref", 2)
-    need(q, torch.bfloat16, "q", 2)
+    """(kl [T] float32, sums [2] float64 = (sum w kl, sum w)) for logits [T, V], both bf16 (lamq_kl_rows) or both
+    float32 (lamq_kl_rows_f32)."""
+    dt = ref.dtype if ref.dtype in (torch.bfloat16, torch.float32) else torch.bfloat16
+    need(ref, dt, "ref", 2)
+    need(q, dt, "q", 2)
     if ref.shape != q.shape:
         raise ValueError("ref and q must have the same shape")
     T, V = ref.shape
@@ -981,8 +983,9 @@ def kl_rows(ref: torch.Tensor, q: torch.Tensor, w: torch.Tensor | None = None):
     sums = torch.empty(2, dtype=torch.float64, device=ref.device)
     nbytes = lib().lamq_kl_workspace_size(T)
     ws = workspace(nbytes, ref.device)
-    check(lib().lamq_kl_rows(ptr(ref), ptr(q), T, V, ld(ref), ld(q), ptr(wv), ptr(kl), ptr(sums), ptr(ws), nbytes,
-                             stream(ref.device)), "kl_rows")
+    fn = lib().lamq_kl_rows if dt == torch.bfloat16 else lib().lamq_kl_rows_f32
+    check(fn(ptr(ref), ptr(q), T, V, ld(ref), ld(q), ptr(wv), ptr(kl), ptr(sums), ptr(ws), nbytes, stream(ref.device)),
+          "kl_rows")
     return kl, sums
 
 

@@ -452,6 +452,22 @@ def kl_rows(ref_bf16, q_bf16, w=None):
     return kl, (sw.value / st.value if st.value else 0.0)
 
 
+def kl_rows_float(ref, q, w=None):
+    """kl_rows for float logits (the reference's .logits.float(), compiler.py:180,185): the float32 values taken
+    exactly, KL(p_ref || p_q) per token in float64 through log-sum-exp; returns (kl per token, sum_t w_t kl_t /
+    sum_t w_t)."""
+    r = np.asarray(ref, dtype=np.float32).astype(np.float64)
+    p = np.asarray(q, dtype=np.float32).astype(np.float64)
+    mr, mq = r.max(axis=1, keepdims=True), p.max(axis=1, keepdims=True)
+    er = np.exp(r - mr)
+    sr = er.sum(axis=1)
+    lse_r = mr[:, 0] + np.log(sr)
+    lse_q = mq[:, 0] + np.log(np.exp(p - mq).sum(axis=1))
+    kl = (er * (r - p)).sum(axis=1) / sr - lse_r + lse_q
+    ww = np.ones(len(kl)) if w is None else np.asarray(w, dtype=np.float32).astype(np.float64)
+    return kl, (float((ww * kl).sum() / ww.sum()) if ww.sum() else 0.0)
+
+
 def bf16_bits(x) -> np.ndarray:
     """float32 -> bfloat16 bit patterns, round to nearest even (what torch's .to(bfloat16) does)."""
     u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)

@@ -920,6 +920,58 @@ def test_kl_rows(E, T, V):
     assert abs(s[0] / s[1] - mean) < 1e-4 * abs(mean)
 
 
+@pytest.mark.parametrize("T,V", [(33, 1000), (7, 777), (64, 151936)])
+def test_kl_rows_float32_logits(E, T, V):
+    """lamq_kl_rows_f32: on logits bf16 holds exactly, the bf16 kernel's results bit for bit (the same float32
+    arithmetic in the same order, both vector loads at V = 1,000 and 151,936, both scalar at 777); on general float32
+    logits, and through a padded row stride, within 1e-4 of the float oracle."""
+    from lookatmyquant_amd import synthetic
+
+    r, q = synthetic.logits(T, V, 501 + V, 502 + V)
+    w = torch.from_numpy(np.random.default_rng(V).uniform(0.5, 2.0, T).astype(np.float32)).cuda()
+    rb, qb = cuda(r.view(np.int16)).view(torch.bfloat16), cuda(q.view(np.int16)).view(torch.bfloat16)
+    say(f"kl float32 T={T} V={V}")
+    kb, sb = E.kl_rows(rb, qb, w)
+    kf, sf = E.kl_rows(rb.float(), qb.float(), w)
+    assert torch.equal(kb, kf) and torch.equal(sb, sf)
+    g = torch.Generator(device="cuda").manual_seed(V)
+    rf = torch.randn(T, V, generator=g, device="cuda") * 3.0
+    qf = rf + 0.3 * torch.randn(T, V, generator=g, device="cuda")
+    for pad in (0, 3):
+        if pad:
+            rp = torch.zeros(T, V + pad, device="cuda")
+            qp = torch.zeros(T, V + pad, device="cuda")
+            rp[:, :V], qp[:, :V] = rf, qf
+            a, b = rp[:, :V], qp[:, :V]
+        else:
+            a, b = rf, qf
+        kl, sums = E.kl_rows(a, b, w)
+        ref, mean = O.kl_rows_float(rf.cpu().numpy(), qf.cpu().numpy(), w.cpu().numpy())
+        k64 = kl.cpu().numpy().astype(np.float64)
+        assert np.all(np.abs(k64 - ref) <= 1e-4 * np.abs(ref) + 1e-9), pad
+        s = sums.cpu().numpy()
+        assert abs(s[0] / s[1] - mean) < 1e-4 * abs(mean)
+    with pytest.raises(ValueError):
+        E.kl_rows(rf, qf.bfloat16())
+
+
+def test_compiler_kl_takes_any_float_logits():
+    """compiler.kl and kl_per_token take float16, float32 and mixed logits as the reference's .logits.float() does:
+    the float32 results of the cast tensors, exactly."""
+    from lookatmyquant_amd import compiler
+
+    g = torch.Generator(device="cuda").manual_seed(5)
+    r = (torch.randn(2, 3, 500, generator=g, device="cuda") * 3.0).half()
+    q = (r.float() + 0.3 * torch.randn(2, 3, 500, generator=g, device="cuda")).half()
+    ref = compiler.kl_per_token(r.float(), q.float())
+    assert ref.shape == (2, 3)
+    assert torch.equal(compiler.kl_per_token(r, q), ref)
+    assert torch.equal(compiler.kl_per_token(r.float(), q), ref)
+    assert compiler.kl(r, q) == compiler.kl(r.float(), q.float())
+    rb, qb = r.bfloat16(), q.bfloat16()
+    assert torch.equal(compiler.kl_per_token(rb, qb.float()), compiler.kl_per_token(rb, qb))
+
+
 def test_kl_rows_config4_full_size(E):
     """Config 4's shape, [8192, 151936] bf16 logit pairs with token weights: the launch's fixed-order sums over all
     8,192 tokens equal the float64 sums of its own per-token values, and 64 sampled tokens equal the oracle's KL."""

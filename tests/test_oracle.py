@@ -365,6 +365,30 @@ def test_kl_closed_forms():
     assert np.all(kl > 0)
 
 
+def test_kl_float_restatement_matches_the_bf16_oracle():
+    """kl_rows_float (float logits) equals the C bf16 oracle on logits bf16 holds exactly, weighted mean included; on
+    two logits it is the Bernoulli KL; a shift of a row's logits leaves it unchanged."""
+    rng = np.random.default_rng(19)
+    r = O.bf16_bits(rng.standard_normal((6, 777)).astype(np.float32) * 3)
+    q = O.bf16_bits(O.bf16_to_f32(r) + rng.standard_normal(r.shape).astype(np.float32) * 0.5)
+    w = rng.uniform(0.5, 2.0, 6).astype(np.float32)
+    k16, m16 = O.kl_rows(r, q, w)
+    kf, mf = O.kl_rows_float(O.bf16_to_f32(r), O.bf16_to_f32(q), w)
+    assert np.abs(kf - k16).max() < 1e-12 * np.abs(k16).max()
+    assert abs(mf - m16) < 1e-12 * abs(m16)
+    a = np.array([[0.3, -1.7]], dtype=np.float32)
+    b = np.array([[-0.9, 0.4]], dtype=np.float32)
+    p = 1 / (1 + math.exp(-(float(a[0, 0]) - float(a[0, 1]))))
+    qq = 1 / (1 + math.exp(-(float(b[0, 0]) - float(b[0, 1]))))
+    kf, _ = O.kl_rows_float(a, b)
+    assert abs(kf[0] - (p * math.log(p / qq) + (1 - p) * math.log((1 - p) / (1 - qq)))) < 1e-12
+    x = rng.standard_normal((3, 50)).astype(np.float32)
+    y = rng.standard_normal((3, 50)).astype(np.float32)
+    k0, _ = O.kl_rows_float(x, y)
+    k1, _ = O.kl_rows_float(x + np.float32(4.0), y - np.float32(2.0))
+    assert np.abs(k0 - k1).max() < 1e-5 * np.abs(k0).max()
+
+
 @pytest.mark.parametrize("bits", [1, 2, 3, 4])
 def test_pack_trellis_matches_reference_bytes(golden, bits):
     g = golden("misc")
