@@ -21,6 +21,8 @@ Parity status of each function (what pins it is listed in the test named beside 
   rht_apply          equals the products with the dense rht(n, seed) both ways (tests/test_oracle.py)
   hessian            fp64 closed form X^T diag(w) X / N
   kl_rows            fp64 closed form; KL(p||p) = 0; Gaussian-logit closed form
+  kl_rows_float      equals kl_rows on bf16-valued logits; the Bernoulli closed form; shift invariance
+  shaped_sweep       isotropic G equals the one-rate multirate_sweep; one column's row pass equals sweep along the rows
   lloyd_max          Max (1960) MSE table; GAUSS2 levels; reference vectors
   pack_symbols etc.  round trip and the reference's byte layout spelled out bit by bit
   ldlq_noise         A A^T = Hr with A upper; tr(E_r Hr E_r^T) = sum diag(A)^2 eta^2 (QuIP Theorem 1's identity);
